@@ -1,0 +1,315 @@
+"""Pins the oracle's compute functions (oracle/ttlab_oracle.c a3-a13).
+
+Known answers are the reference's own (tenstorrent/tt-lab tests/host_dispatch.cpp:92-127,
+src/tests.cpp:194-234).  Beyond those: brute force in float64 (numpy), exact
+cross-body relations of the reference's two multiversioned bodies, and
+hand-derived answers for the selection sort's tie and NaN rules (model.cpp:296-309).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+lib = O.lib
+N = 2880
+BODIES = [O.BODY_DEFAULT, O.BODY_V4, O.BODY_V4_SIMD]
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def decode_f64(blocks, rows, cols):
+    """Independent float64 decode: E2M1 magnitude, sign bit 3, times 2^(e-127)."""
+    b = blocks.reshape(rows, cols // 32, 17)
+    scale = np.ldexp(1.0, b[:, :, 0].astype(np.int64) - 127)
+    qs = b[:, :, 1:]
+    lo, hi = qs & 15, qs >> 4
+
+    def val(c):
+        v = E2M1[c & 7]
+        return np.where(c & 8, -v, v)
+    w = np.concatenate([val(lo), val(hi)], axis=2) * scale[:, :, None]
+    return w.reshape(rows, cols)
+
+
+def mxfp4_kat_matrix():
+    expert_bytes = N * (N // 32) * 17
+    data = np.zeros(2 * expert_bytes, np.uint8)
+    blocks = data[expert_bytes:].reshape(-1, 17)
+    blocks[:, 0] = 127
+    blocks[:, 1:] = 0x21
+    return data
+
+
+@pytest.mark.parametrize("body", BODIES)
+def test_mxfp4_matvec_reference_kat(body):
+    # tests/host_dispatch.cpp:92-107: expert 1, scale 127, bytes 0x21, x = 0.5, bias 0.25 -> 1080.25
+    data = mxfp4_kat_matrix()
+    bias = np.full(2 * N, 0.25, np.float32)
+    x = np.full(N, 0.5, np.float32)
+    y = O.mxfp4_matvec(data, bias, N, N, x, expert=1, body=body)
+    assert np.all(y == np.float32(1080.25))
+
+
+@pytest.mark.parametrize("body", BODIES)
+@pytest.mark.parametrize("count", [3, 16, 17])
+def test_mxfp4_selected_matmul_reference_kat(body, count):
+    # tests/host_dispatch.cpp:108-126: tokens[s] = count - s, input (s+1)/2,
+    # result 1080 (s+1) + 0.25, token 0's row untouched (-1)
+    data = mxfp4_kat_matrix()
+    bias = np.full(2 * N, 0.25, np.float32)
+    tokens = np.array([count - s for s in range(count)], np.uintp)
+    transposed = np.empty(N * count, np.float32)
+    for s in range(count):
+        transposed[s::count] = (s + 1) * 0.5
+    workspace = np.empty(4 * count + 8, np.float32)
+    out = np.full((count + 1) * N, -1.0, np.float32)
+    lib.orc_matmul_add_mxfp4_selected_transposed(data, bias, N, N, transposed, tokens, count, out, workspace, 1,
+                                                 body)
+    out = out.reshape(count + 1, N)
+    assert np.all(out[0] == -1.0)
+    for s in range(count):
+        assert np.all(out[count - s] == np.float32(1080.0 * (s + 1) + 0.25))
+
+
+def test_f32_matvec_and_rmsnorm_kats():
+    # src/tests.cpp:194-212
+    w = np.array([1, 2, 3, 4], np.float32)
+    bias = np.array([10, 20], np.float32)
+    x = np.array([5, 6], np.float32)
+    y = np.empty(2, np.float32)
+    lib.orc_matvec_add_f32(w, bias, 2, 2, x, y)
+    assert y[0] == 27 and y[1] == 59
+    out = np.empty(2, np.float32)
+    lib.orc_rms_norm(np.array([3, 4], np.float32), np.array([2, 3], np.float32), 2, 0.0, out)
+    scale = 1.0 / np.sqrt(12.5)
+    assert abs(out[0] - 6 * scale) <= 1e-6 and abs(out[1] - 12 * scale) <= 1e-6
+
+
+def test_q8_0_matvec_kats():
+    # src/tests.cpp:214-234
+    data = np.zeros(68, np.uint8)
+    data[0:2] = [0x00, 0x3C]
+    data[34:36] = [0x00, 0x3C]
+    data[2:34] = 1
+    data[36:68] = 0xFF
+    x = np.ones(32, np.float32)
+    y = np.empty(2, np.float32)
+    lib.orc_matvec_q8_0(data, 2, 32, x, y)
+    assert y[0] == 32 and y[1] == -32
+    lib.orc_matvec_add_q8_0(data, np.array([10, 20], np.float32), 2, 32, x, y)
+    assert y[0] == 42 and y[1] == -12
+
+
+def test_mxfp4_matvec_brute_force_all_bodies():
+    rows, cols = 256, N
+    w = O.synth_mxfp4(11, 0, rows * cols // 32)
+    x = O.synth_normal(12, 0, cols)
+    bias = O.synth_normal(13, 0, rows, sigma=0.1)
+    exact = decode_f64(w, rows, cols) @ x.astype(np.float64) + bias
+    outs = [O.mxfp4_matvec(w, bias, rows, cols, x, body=b) for b in BODIES]
+    for y in outs:
+        assert O.rel_l2(y, exact) < 1e-6
+    # v4 restated lane by lane and v4 with AVX-512 intrinsics are the same arithmetic
+    if O.has_avx512():
+        assert np.array_equal(outs[1].view(np.uint32), outs[2].view(np.uint32))
+    # the default and v4 bodies round differently (fused vs unfused), as in the reference
+    assert not np.array_equal(outs[0], outs[1])
+
+
+def test_mxfp4_matvec_default_is_sequential_unfused():
+    """Single-row check: the default body equals a float32 sequential unfused loop over
+    (block, i, low, high) with weights decoded independently."""
+    cols = 96
+    w = O.synth_mxfp4(21, 0, cols // 32)
+    x = O.synth_normal(22, 0, cols)
+    dense = decode_f64(w, 1, cols)[0].astype(np.float32)
+    acc = np.float32(0.125)
+    for b in range(cols // 32):
+        for i in range(16):
+            acc = np.float32(acc + np.float32(dense[32 * b + i] * x[32 * b + i]))
+            acc = np.float32(acc + np.float32(dense[32 * b + 16 + i] * x[32 * b + 16 + i]))
+    y = O.mxfp4_matvec(w, np.array([0.125] * 4, np.float32), 1, cols, x, body=O.BODY_DEFAULT)
+    assert y[0] == acc
+
+
+def test_selected_matmul_matches_matvec_default_and_brute_force():
+    rows, cols, count = 64, 320, 7
+    w = O.synth_mxfp4(31, 0, 2 * rows * cols // 32)
+    bias = O.synth_normal(32, 0, 2 * rows, sigma=0.1)
+    x = O.synth_normal(33, 0, 10 * cols).reshape(10, cols)
+    tokens = np.array([9, 2, 5, 0, 7, 3, 1], np.uintp)
+    tr = np.empty(cols * count, np.float32)
+    lib.orc_transpose_selected(cols, np.ascontiguousarray(x), tokens, count, tr)
+    for body in BODIES:
+        out = np.full(10 * rows, np.nan, np.float32)
+        ws = np.empty(4 * count, np.float32)
+        lib.orc_matmul_add_mxfp4_selected_transposed(w, bias, rows, cols, tr, tokens, count, out, ws, 1, body)
+        out = out.reshape(10, rows)
+        dense = decode_f64(w[rows * cols // 32 * 17:], rows, cols)
+        for t in tokens:
+            exact = dense @ x[t].astype(np.float64) + bias[rows:]
+            assert O.rel_l2(out[t], exact) < 1e-6
+            if body == O.BODY_DEFAULT:
+                # the default matmul walks the same order as the default matvec
+                mv = O.mxfp4_matvec(w, bias, rows, cols, x[t], expert=1, body=O.BODY_DEFAULT)
+                assert np.array_equal(out[t], mv)
+        untouched = [t for t in range(10) if t not in tokens]
+        assert np.all(np.isnan(out[untouched]))
+
+
+def test_router_topk_distinct_values_against_sort():
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        logits = rng.standard_normal(32).astype(np.float32)
+        idx, w = O.router_topk(logits)
+        assert list(idx) == list(np.argsort(-logits.astype(np.float64), kind="stable")[:4])
+        top = logits[idx].astype(np.float64)
+        soft = np.exp(top - top.max())
+        soft /= soft.sum()
+        assert np.allclose(w, soft, rtol=1e-6, atol=0)
+
+
+def test_router_topk_tie_and_nan_rules_hand_derived():
+    def run(values, k):
+        logits = np.full(32, -100.0, np.float32)
+        logits[:len(values)] = values
+        return list(O.router_topk(logits, k)[0])
+    # all equal: nothing is strictly greater, positions are taken in order
+    assert list(O.router_topk(np.zeros(32, np.float32))[0]) == [0, 1, 2, 3]
+    # [5, 5, 9]: step 0 swaps 9 into position 0 and expert 0 into position 2, so the
+    # tie between experts 0 and 1 resolves to expert 1 first (not the lower index)
+    assert run([5, 5, 9], 3) == [2, 1, 0]
+    # a NaN at the current position is never displaced ('x > NaN' is false)
+    assert run([np.nan, 3, 2, 1], 2) == [0, 1]
+    assert run([1, np.nan, 3, 2], 2) == [2, 1]
+    # a NaN elsewhere is never selected ahead of numbers
+    assert run([1, 2, np.nan, 3], 2) == [3, 1]
+
+
+def test_swiglu_against_float64_and_special_values():
+    rng = np.random.default_rng(4)
+    g = (rng.standard_normal(4096) * 6).astype(np.float32)
+    u = (rng.standard_normal(4096) * 6).astype(np.float32)
+    h = np.empty_like(g)
+    lib.orc_swiglu(g, u, g.size, h)
+    x = np.minimum(g.astype(np.float64), 7.0)
+    y = np.clip(u.astype(np.float64), -7.0, 7.0)
+    c = float(np.float32(-1.702))
+    ref = x / (1.0 + np.exp(c * x)) * (y + 1.0)
+    # exp amplifies the rounding of its float32 argument c*x by |c*x|
+    tol = 4e-7 * (4.0 + np.abs(c * x))
+    assert np.all(np.abs(h - ref) <= tol * np.abs(ref) + 1e-37)
+    special_g = np.array([100.0, np.nan, -200.0, 0.0], np.float32)
+    special_u = np.array([100.0, 1.0, 1.0, -100.0], np.float32)
+    h = np.empty(4, np.float32)
+    lib.orc_swiglu(special_g, special_u, 4, h)
+    assert h[0] == np.float32(np.float32(7.0 / (1.0 + np.exp(np.float32(-1.702 * 7.0)))) * 8.0) or \
+        abs(h[0] - 7.0 / (1.0 + np.exp(-1.702 * 7.0)) * 8.0) < 1e-5
+    assert np.isnan(h[1])  # NaN gate propagates through std::min
+    assert h[2] == 0.0     # exp overflow -> x / inf -> -0
+    assert h[3] == 0.0     # x = 0
+
+
+def test_rms_norm_against_float64():
+    x = O.synth_normal(41, 0, N, sigma=3.0)
+    w = O.synth_normal(42, 0, N, mean=1.0, sigma=0.1)
+    out = np.empty(N, np.float32)
+    lib.orc_rms_norm(x, w, N, 1e-5, out)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt(np.mean(xd * xd) + 1e-5) * w
+    assert O.rel_l2(out, ref) < 1e-6
+
+
+def test_q8_0_matvec_and_matmul_against_float64():
+    rows, cols = 128, N
+    q = O.synth_q8_0(51, 0, rows * cols // 32)
+    x = O.synth_normal(52, 0, 3 * cols).reshape(3, cols)
+    bias = O.synth_normal(53, 0, rows, sigma=0.1)
+    blocks = q.reshape(rows, cols // 32, 34)
+    d = blocks[:, :, :2].copy().view(np.uint16)[..., 0].view(np.float16).astype(np.float64)
+    qs = blocks[:, :, 2:].view(np.int8).astype(np.float64)
+    dense = (qs * d[:, :, None]).reshape(rows, cols)
+    y = np.empty(rows, np.float32)
+    lib.orc_matvec_add_q8_0(q, bias, rows, cols, x[0], y)
+    assert O.rel_l2(y, dense @ x[0] + bias) < 1e-6
+    out = np.empty(3 * rows, np.float32)
+    ws = np.empty(3, np.float32)
+    tr = np.empty(3 * cols, np.float32)
+    lib.orc_matmul_add_q8_0(q, bias, rows, cols, np.ascontiguousarray(x), 3, out, ws, tr)
+    assert O.rel_l2(out.reshape(3, rows), (dense @ x.T.astype(np.float64)).T + bias) < 1e-6
+    emb = np.empty(cols, np.float32)
+    lib.orc_load_token_embedding_q8_0(q, cols, 5, emb)
+    assert np.array_equal(emb, dense[5].astype(np.float32))
+
+
+def test_bf16_matvec_against_float64():
+    rows, cols = 64, 512
+    w = O.synth_bf16(61, 0, rows * cols)
+    x = O.synth_normal(62, 0, cols)
+    y = np.empty(rows, np.float32)
+    lib.orc_matvec_bf16(w, rows, cols, x, y)
+    dense = (w.astype(np.uint32) << 16).view(np.float32).reshape(rows, cols).astype(np.float64)
+    assert O.rel_l2(y, dense @ x) < 1e-6
+
+
+def test_greedy_first_max_and_nan():
+    assert lib.orc_greedy(np.array([1, 3, 3, 2], np.float32), 4) == 1
+    assert lib.orc_greedy(np.array([np.nan, 3, 9], np.float32), 3) == 0
+    assert lib.orc_greedy(np.array([1, np.nan, 9, 9], np.float32), 4) == 2
+    assert lib.orc_greedy(np.array([-0.0, 0.0], np.float32), 2) == 0
+
+
+def test_rope_frequencies_against_float64():
+    f = np.empty(32, np.float32)
+    lib.orc_rope_frequencies(f)
+    base, head = 150000.0, 64.0
+    corr = head * np.log(4096 / (32 * 2 * np.pi)) / (2 * np.log(base))
+    corr_slow = head * np.log(4096 / (1 * 2 * np.pi)) / (2 * np.log(base))
+    low, high = max(0.0, np.floor(corr)), min(63.0, np.ceil(corr_slow))
+    pair = np.arange(32)
+    theta = base ** (-(2.0 * pair) / head)
+    ramp = 1 - np.clip((pair - low) / max(0.001, high - low), 0, 1)
+    ref = theta / 32 * (1 - ramp) + theta * ramp
+    assert np.allclose(f, ref, rtol=1e-5)
+    # the extremes are pure extrapolation (pair 0) and pure interpolation (last pair)
+    assert abs(f[0] - 1.0) < 1e-6
+    assert abs(f[31] / (theta[31] / 32) - 1) < 1e-5
+
+
+def test_apply_rope_rotation_property():
+    f = np.empty(32, np.float32)
+    lib.orc_rope_frequencies(f)
+    v = O.synth_normal(71, 0, 8 * 64)
+    r = v.copy()
+    lib.orc_apply_rope(r, 8, 1234, f)
+    mag = 1 + 0.1 * np.log(32.0)
+    v2 = v.reshape(8, 2, 32).astype(np.float64)
+    r2 = r.reshape(8, 2, 32).astype(np.float64)
+    # each (d, d+32) pair is rotated by 1234*f[d] and scaled by 1 + 0.1 ln 32
+    ang = 1234.0 * f.astype(np.float64)
+    ref0 = (v2[:, 0] * np.cos(ang) - v2[:, 1] * np.sin(ang)) * mag
+    ref1 = (v2[:, 0] * np.sin(ang) + v2[:, 1] * np.cos(ang)) * mag
+    assert O.rel_l2(r2[:, 0], ref0) < 1e-5 and O.rel_l2(r2[:, 1], ref1) < 1e-5
+
+
+@pytest.mark.parametrize("layer_index,position", [(0, 5), (1, 5), (0, 300), (1, 300)])
+def test_attention_against_float64(layer_index, position):
+    T = position + 1
+    q = O.synth_normal(81, 0, 64 * 64)
+    k = O.synth_normal(82, 0, T * 512)
+    v = O.synth_normal(83, 0, T * 512)
+    sinks = O.synth_normal(84, 0, 64)
+    out = np.empty(64 * 64, np.float32)
+    scores = np.empty(T, np.float32)
+    lib.orc_attention(q, k, v, sinks, layer_index, position, out, scores)
+    first = position + 1 - 128 if (layer_index % 2 == 0 and position + 1 > 128) else 0
+    K = k.reshape(T, 8, 64)[first:].astype(np.float64)
+    V = v.reshape(T, 8, 64)[first:].astype(np.float64)
+    Q = q.reshape(64, 64).astype(np.float64)
+    ref = np.empty((64, 64))
+    for h in range(64):
+        s = K[:, h // 8] @ Q[h] / 8.0
+        m = max(s.max(), sinks[h])
+        e = np.exp(s - m)
+        ref[h] = (e / (e.sum() + np.exp(sinks[h] - m))) @ V[:, h // 8]
+    assert O.rel_l2(out, ref.ravel()) < 1e-5
