@@ -1,0 +1,132 @@
+/*
+ * ttlab_hip.h -- C ABI of the MI355X (gfx950) backend for tt-lab's quantized decode path.
+ *
+ * This is the drop-in boundary.  Everything behind it is hand-written HIP for
+ * gfx950 in tt-lab_amd/csrc/; everything above it (the C++ facade in
+ * tt-lab_amd/host/, the tests, bench.py) sees plain pointers and sizes only.
+ *
+ * Conventions
+ *  - Every entry point returns 0 (TTL_OK) or a negative TTL_ERR_* code; the
+ *    message of the last failure on the calling thread is ttl_last_error().
+ *    The C++ facade turns a non-zero code into std::runtime_error, the
+ *    reference's error convention (model.cpp:209-228, main.cpp:414-417).
+ *  - Pointers named *_dev are device pointers (from ttl_malloc or a tensor
+ *    handle); all others are host pointers.
+ *  - Work is queued in order on the context's stream and is asynchronous with
+ *    respect to the host, except ttl_memcpy_d2h and ttl_sync, which wait.
+ *  - Shapes are validated on the host before any launch; expert indices that
+ *    live in device memory are bounds-checked by the kernels (an index out of
+ *    range produces NaN outputs, never an out-of-bounds read).
+ *  - One context owns one device and one stream; calls on one context must not
+ *    overlap from several host threads (the reference is single-threaded,
+ *    AGENTS.md:3).
+ */
+#ifndef TTLAB_HIP_H
+#define TTLAB_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTL_OK 0
+#define TTL_ERR_INVALID -1   /* bad argument (null pointer, unsupported type)     */
+#define TTL_ERR_SHAPE -2     /* shape the kernels do not support                  */
+#define TTL_ERR_HIP -3       /* HIP runtime error (message has the HIP string)    */
+#define TTL_ERR_NO_DEVICE -4 /* no gfx950 device at that ordinal                  */
+#define TTL_ERR_MEMORY -5    /* device allocation failed                          */
+
+typedef struct ttl_ctx ttl_ctx;
+typedef struct ttl_mxfp4 ttl_mxfp4;
+
+/* ---- context ---------------------------------------------------------------- */
+
+/* Opens `device` (must be gfx950) and creates the context's stream.  No reference
+ * counterpart: the reference CPU path has no device (the TT path's counterpart is
+ * open_tt_firmware_runtime, tt_backend.cpp:1492-1528). */
+int ttl_create(int device, ttl_ctx **out);
+void ttl_destroy(ttl_ctx *ctx);
+const char *ttl_last_error(void);
+int ttl_sync(ttl_ctx *ctx);
+/* Device name and compute-unit count, for reports. */
+int ttl_device_info(ttl_ctx *ctx, char *name, size_t name_bytes, int *compute_units, double *hbm_bytes);
+
+/* ---- device memory ------------------------------------------------------------ */
+
+int ttl_malloc(ttl_ctx *ctx, size_t bytes, void **dev);
+int ttl_free(ttl_ctx *ctx, void *dev);
+int ttl_memcpy_h2d(ttl_ctx *ctx, void *dst_dev, const void *src, size_t bytes);
+int ttl_memcpy_d2h(ttl_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
+int ttl_memcpy_d2d(ttl_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
+/* Fills with a byte value using a kernel (safe inside HIP graph capture). */
+int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes);
+
+/* ---- timing (HIP events on the context's stream) -------------------------------- */
+
+int ttl_timer_start(ttl_ctx *ctx);
+/* Records the stop event, waits for it, returns milliseconds since ttl_timer_start. */
+int ttl_timer_stop(ttl_ctx *ctx, float *ms);
+
+/* ---- synthetic inputs (same bits as the specification in oracle/ttlab_oracle.h) --- */
+
+int ttl_synth_normal(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t offset, size_t n, float mean,
+                     float sigma, float *out_dev);
+int ttl_synth_normal_bf16(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t offset, size_t n, float sigma,
+                          float *out_dev);
+/* GGUF-layout MXFP4 blocks (17 B each), E8M0 uniform in [emin, emax]. */
+int ttl_synth_mxfp4_gguf(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t block_offset, size_t n,
+                         uint32_t emin, uint32_t emax, uint8_t *out_dev);
+
+/* ---- MXFP4 tensors ---------------------------------------------------------------- *
+ * A ttl_mxfp4 holds `experts` matrices of `rows` x `cols` MXFP4 values, the GGUF
+ * tensor {cols, rows, experts} of type 39 (tensor.h:15-17, model.cpp:160-169):
+ * GGUF stores row r of expert e as cols/32 blocks of 17 bytes (E8M0 scale, then
+ * 16 bytes of packed E2M1 codes; tensor.cpp:136-161, 283-296).  On upload the
+ * blocks are repacked into two planes -- 16-byte code chunks and scale bytes --
+ * tiled by 16 rows so one 64-lane load is 1 KiB of contiguous codes; the decode is
+ * byte-identical.  Supported shapes: cols = 2880 (the reference's only width,
+ * tensor.cpp:76-79), rows a multiple of 16.                                         */
+
+int ttl_mxfp4_upload(ttl_ctx *ctx, const void *gguf_blocks, uint32_t rows, uint32_t cols, uint32_t experts,
+                     ttl_mxfp4 **out);
+/* Same, from GGUF-layout blocks already in device memory. */
+int ttl_mxfp4_upload_dev(ttl_ctx *ctx, const void *gguf_blocks_dev, uint32_t rows, uint32_t cols,
+                         uint32_t experts, ttl_mxfp4 **out);
+/* Generates the tensor on the device: expert e is stream `stream + e` of the MXFP4
+ * generator, so any expert can be regenerated on the host independently. */
+int ttl_mxfp4_synthetic(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, uint64_t seed,
+                        uint64_t stream, uint32_t emin, uint32_t emax, ttl_mxfp4 **out);
+/* Writes the GGUF-layout bytes of the whole tensor back to host memory. */
+int ttl_mxfp4_download(ttl_ctx *ctx, const ttl_mxfp4 *tensor, void *gguf_blocks);
+void ttl_mxfp4_free(ttl_ctx *ctx, ttl_mxfp4 *tensor);
+int ttl_mxfp4_shape(const ttl_mxfp4 *tensor, uint32_t *rows, uint32_t *cols, uint32_t *experts);
+size_t ttl_mxfp4_bytes(const ttl_mxfp4 *tensor);
+
+/* Decodes expert `expert` to f32 [rows][cols] on the device (out_dev).
+ * mode 0: the reference's table, weight = 2^(e-128) * int(code) (tensor.cpp:34-74).
+ * mode 1: the decode the matvec kernels perform: the gfx950 fp4 conversion
+ *         instruction, then the block scale 2^(e-127) applied by ldexp. */
+int ttl_mxfp4_dequantize(ttl_ctx *ctx, const ttl_mxfp4 *tensor, uint32_t expert, int mode, float *out_dev);
+
+/* y = W[expert] x + bias[expert].  Replaces matvec_add_mxfp4_2880
+ * (tensor.h:28-35, tensor.cpp:239-304): bias_dev is f32 [experts][rows] (NULL for
+ * none), x_dev f32 [cols], y_dev f32 [rows]. */
+int ttl_matvec_mxfp4(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev, float *y_dev,
+                     uint32_t expert);
+
+/* Expert-indexed batch of matvecs in one launch: for slot s < n,
+ * y[s] = W[experts[s]] x[s] + bias[experts[s]], reading only the selected experts.
+ * experts_dev is int32 [n] in device memory (so router output feeds it without a
+ * host round trip); x_dev is f32 [n][x_stride] (x_stride 0 = one shared x);
+ * y_dev is f32 [n][rows].  The reference's callers loop over experts instead
+ * (model.cpp:324-337). */
+int ttl_matvec_mxfp4_experts(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
+                             uint32_t x_stride, const int32_t *experts_dev, uint32_t n, float *y_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,192 @@
+// Context, errors, device memory and timing entry points of the C ABI.
+#include "ttl_internal.hpp"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+namespace {
+thread_local char last_error[512] = "";
+
+__global__ void fill_bytes_kernel(uint8_t *dst, uint8_t value, size_t n) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (size_t k = i; k < n; k += stride) {
+        dst[k] = value;
+    }
+}
+}  // namespace
+
+namespace ttl {
+int set_error(int code, const char *fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    std::vsnprintf(last_error, sizeof(last_error), fmt, args);
+    va_end(args);
+    return code;
+}
+
+int hip_fail(hipError_t err, const char *what) {
+    return set_error(err == hipErrorOutOfMemory ? TTL_ERR_MEMORY : TTL_ERR_HIP, "%s: %s", what,
+                     hipGetErrorString(err));
+}
+}  // namespace ttl
+
+extern "C" {
+
+const char *ttl_last_error(void) {
+    return last_error;
+}
+
+int ttl_create(int device, ttl_ctx **out) {
+    TTL_REQUIRE(out != nullptr, TTL_ERR_INVALID, "ttl_create: null output pointer");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= device || device < 0) {
+        return ttl::set_error(TTL_ERR_NO_DEVICE, "ttl_create: no HIP device %d (found %d)", device, count);
+    }
+    hipDeviceProp_t prop;
+    TTL_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        return ttl::set_error(TTL_ERR_NO_DEVICE, "ttl_create: device %d is %s, this library is built for gfx950",
+                              device, prop.gcnArchName);
+    }
+    TTL_HIP(hipSetDevice(device));
+    ttl_ctx *ctx = new ttl_ctx;
+    ctx->device = device;
+    ctx->compute_units = prop.multiProcessorCount;
+    ctx->hbm_bytes = double(prop.totalGlobalMem);
+    std::snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", prop.name, prop.gcnArchName);
+    hipError_t err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (err == hipSuccess) {
+        err = hipEventCreate(&ctx->timer_start);
+    }
+    if (err == hipSuccess) {
+        err = hipEventCreate(&ctx->timer_stop);
+    }
+    if (err == hipSuccess) {
+        err = hipMalloc(&ctx->iota, sizeof(int32_t) * ttl::iota_size);
+    }
+    if (err == hipSuccess) {
+        int32_t host_iota[ttl::iota_size];
+        for (int i = 0; i < ttl::iota_size; ++i) {
+            host_iota[i] = i;
+        }
+        err = hipMemcpy(ctx->iota, host_iota, sizeof(host_iota), hipMemcpyHostToDevice);
+    }
+    if (err != hipSuccess) {
+        ttl_destroy(ctx);
+        return ttl::hip_fail(err, "ttl_create");
+    }
+    *out = ctx;
+    return TTL_OK;
+}
+
+void ttl_destroy(ttl_ctx *ctx) {
+    if (!ctx) {
+        return;
+    }
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) {
+        (void)hipStreamSynchronize(ctx->stream);
+    }
+    if (ctx->timer_start) {
+        (void)hipEventDestroy(ctx->timer_start);
+    }
+    if (ctx->timer_stop) {
+        (void)hipEventDestroy(ctx->timer_stop);
+    }
+    if (ctx->stream) {
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    if (ctx->iota) {
+        (void)hipFree(ctx->iota);
+    }
+    delete ctx;
+}
+
+int ttl_sync(ttl_ctx *ctx) {
+    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_sync: null context");
+    TTL_HIP(hipStreamSynchronize(ctx->stream));
+    return TTL_OK;
+}
+
+int ttl_device_info(ttl_ctx *ctx, char *name, size_t name_bytes, int *compute_units, double *hbm_bytes) {
+    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_device_info: null context");
+    if (name && name_bytes) {
+        std::snprintf(name, name_bytes, "%s", ctx->name);
+    }
+    if (compute_units) {
+        *compute_units = ctx->compute_units;
+    }
+    if (hbm_bytes) {
+        *hbm_bytes = ctx->hbm_bytes;
+    }
+    return TTL_OK;
+}
+
+int ttl_malloc(ttl_ctx *ctx, size_t bytes, void **dev) {
+    TTL_REQUIRE(ctx && dev, TTL_ERR_INVALID, "ttl_malloc: null argument");
+    *dev = nullptr;
+    TTL_HIP(hipSetDevice(ctx->device));
+    TTL_HIP(hipMalloc(dev, bytes ? bytes : 1));
+    return TTL_OK;
+}
+
+int ttl_free(ttl_ctx *ctx, void *dev) {
+    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_free: null context");
+    if (dev) {
+        TTL_HIP(hipStreamSynchronize(ctx->stream));
+        TTL_HIP(hipFree(dev));
+    }
+    return TTL_OK;
+}
+
+int ttl_memcpy_h2d(ttl_ctx *ctx, void *dst_dev, const void *src, size_t bytes) {
+    TTL_REQUIRE(ctx && (bytes == 0 || (dst_dev && src)), TTL_ERR_INVALID, "ttl_memcpy_h2d: null argument");
+    TTL_HIP(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    // The source is pageable host memory owned by the caller; wait so it may be reused.
+    TTL_HIP(hipStreamSynchronize(ctx->stream));
+    return TTL_OK;
+}
+
+int ttl_memcpy_d2h(ttl_ctx *ctx, void *dst, const void *src_dev, size_t bytes) {
+    TTL_REQUIRE(ctx && (bytes == 0 || (dst && src_dev)), TTL_ERR_INVALID, "ttl_memcpy_d2h: null argument");
+    TTL_HIP(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    TTL_HIP(hipStreamSynchronize(ctx->stream));
+    return TTL_OK;
+}
+
+int ttl_memcpy_d2d(ttl_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes) {
+    TTL_REQUIRE(ctx && (bytes == 0 || (dst_dev && src_dev)), TTL_ERR_INVALID, "ttl_memcpy_d2d: null argument");
+    TTL_HIP(hipMemcpyAsync(dst_dev, src_dev, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return TTL_OK;
+}
+
+int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes) {
+    TTL_REQUIRE(ctx && (bytes == 0 || dst_dev), TTL_ERR_INVALID, "ttl_fill_bytes: null argument");
+    if (bytes == 0) {
+        return TTL_OK;
+    }
+    const unsigned threads = 256;
+    const unsigned blocks = unsigned(std::min<size_t>(ttl::blocks_for(bytes, threads), 4096));
+    fill_bytes_kernel<<<blocks, threads, 0, ctx->stream>>>((uint8_t *)dst_dev, value, bytes);
+    TTL_LAUNCHED("fill_bytes_kernel");
+    return TTL_OK;
+}
+
+int ttl_timer_start(ttl_ctx *ctx) {
+    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_timer_start: null context");
+    TTL_HIP(hipEventRecord(ctx->timer_start, ctx->stream));
+    return TTL_OK;
+}
+
+int ttl_timer_stop(ttl_ctx *ctx, float *ms) {
+    TTL_REQUIRE(ctx && ms, TTL_ERR_INVALID, "ttl_timer_stop: null argument");
+    TTL_HIP(hipEventRecord(ctx->timer_stop, ctx->stream));
+    TTL_HIP(hipEventSynchronize(ctx->timer_stop));
+    TTL_HIP(hipEventElapsedTime(ms, ctx->timer_start, ctx->timer_stop));
+    return TTL_OK;
+}
+
+}  // extern "C"

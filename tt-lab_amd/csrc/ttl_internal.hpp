@@ -1,0 +1,105 @@
+// Internal definitions shared by the HIP sources of the gfx950 backend.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/ttlab_hip.h"
+
+struct ttl_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t timer_start = nullptr;
+    hipEvent_t timer_stop = nullptr;
+    int32_t *iota = nullptr;  // device int32 [iota_size] = 0, 1, 2, ... (expert ids for single calls)
+    int compute_units = 0;
+    double hbm_bytes = 0.0;
+    char name[128] = {};
+};
+
+// MXFP4 tensor in the repacked layout (see mx:: constants).
+struct ttl_mxfp4 {
+    uint32_t rows = 0;
+    uint32_t cols = 0;
+    uint32_t experts = 0;
+    uint32_t tiles = 0;          // rows / mx::tile_rows per expert
+    uint8_t *codes = nullptr;    // [experts][tiles][blocks][tile_rows][16 B]
+    uint8_t *scales = nullptr;   // [experts][tiles][lanes_k][tile_rows][scale_pad]
+    size_t code_bytes = 0;
+    size_t scale_bytes = 0;
+};
+
+namespace ttl {
+
+constexpr int iota_size = 1024;
+
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t err, const char *what);
+
+// Launch configuration helper: blocks needed for n items.
+inline unsigned blocks_for(size_t n, unsigned threads) {
+    return unsigned((n + threads - 1) / threads);
+}
+
+}  // namespace ttl
+
+#define TTL_HIP(call)                                  \
+    do {                                               \
+        hipError_t ttl_err_ = (call);                  \
+        if (ttl_err_ != hipSuccess) {                  \
+            return ttl::hip_fail(ttl_err_, #call);     \
+        }                                              \
+    } while (0)
+
+#define TTL_LAUNCHED(what)                             \
+    do {                                               \
+        hipError_t ttl_err_ = hipGetLastError();       \
+        if (ttl_err_ != hipSuccess) {                  \
+            return ttl::hip_fail(ttl_err_, what);      \
+        }                                              \
+    } while (0)
+
+#define TTL_REQUIRE(cond, code, ...)                   \
+    do {                                               \
+        if (!(cond)) {                                 \
+            return ttl::set_error(code, __VA_ARGS__);  \
+        }                                              \
+    } while (0)
+
+// Repacked MXFP4 layout.  A tile is 16 consecutive rows of one expert; within a
+// tile the 16-byte code chunks are ordered [block][row], so the 64 lanes of a
+// wave that read blocks 4i..4i+3 of the tile's 16 rows touch 1 KiB of contiguous
+// memory.  Scale bytes are ordered so that each lane's 23 scales (blocks
+// kl, kl+4, ..., kl+88 of its row) are 24 contiguous bytes.
+namespace mx {
+constexpr int tile_rows = 16;
+constexpr int cols = 2880;
+constexpr int blocks = cols / 32;                             // 90 blocks per row
+constexpr int lanes_k = 4;                                    // lanes sharing a row
+constexpr int iters = (blocks + lanes_k - 1) / lanes_k;       // 23
+constexpr int scale_pad = 24;                                 // per-lane scale bytes
+constexpr size_t tile_code_bytes = size_t(blocks) * tile_rows * 16;          // 23040
+constexpr size_t tile_scale_bytes = size_t(lanes_k) * tile_rows * scale_pad; // 1536
+constexpr uint8_t pad_scale = 127;                            // scale of padding blocks
+
+__host__ __device__ inline size_t code_chunk(size_t tile_index, uint32_t block, uint32_t row) {
+    return (tile_index * blocks + block) * tile_rows + row;
+}
+__host__ __device__ inline size_t scale_offset(size_t tile_index, uint32_t block, uint32_t row) {
+    return tile_index * tile_scale_bytes + (size_t(block % lanes_k) * tile_rows + row) * scale_pad + block / lanes_k;
+}
+}  // namespace mx
+
+// Synthetic-input generator shared with oracle/ttlab_oracle.c (same arithmetic).
+namespace synth {
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__host__ __device__ inline uint64_t hash(uint64_t seed, uint64_t stream, uint64_t index) {
+    return mix64(seed + stream * 0xD1342543DE82EF95ull + (index + 1) * 0x9E3779B97F4A7C15ull);
+}
+}  // namespace synth

@@ -1,0 +1,415 @@
+// MXFP4 tensors (GGUF block layout in, repacked planes on the device) and the
+// expert-indexed MXFP4 matvec.
+//
+// Matvec design (gfx950, wave64):
+//  - One wave owns a tile of 16 rows of one expert.  Lane l works on row l%16
+//    and on the blocks kb = 4*i + l/16, i = 0..22, so each 64-lane load of
+//    16 bytes reads 1 KiB of contiguous codes (blocks 4i..4i+3 of the tile).
+//  - All 23 code chunks and the lane's 24 scale bytes are requested before any
+//    arithmetic, so a wave keeps ~23 KiB in flight from HBM.
+//  - The activation vector is staged once per workgroup in LDS with a padded
+//    stride (36 floats per block) so the four distinct addresses of a
+//    ds_read_b128 fall in different banks.
+//  - Decode happens in registers: v_cvt_scalef32_pk_f32_fp4 turns one byte into
+//    the two E2M1 values it holds (low nibble -> element j, high -> j+16), the
+//    32 products of a block are accumulated in f32 and the block's E8M0 scale is
+//    applied once to that partial as an exact power of two (v_ldexp_f32).
+//  - The four lanes of a row are combined with two cross-lane exchanges.
+#include "ttl_internal.hpp"
+
+#include <cmath>
+#include <vector>
+
+namespace ttl {
+int synth_mxfp4_repacked(ttl_ctx *ctx, ttl_mxfp4 *t, uint64_t seed, uint64_t stream, uint32_t emin, uint32_t emax);
+}
+
+namespace {
+
+constexpr int kWaves = 4;               // tiles (waves) per workgroup
+constexpr int kXStride = 36;            // padded LDS floats per 32-value block
+constexpr int kXBlocks = mx::iters * mx::lanes_k;  // 92: blocks 90 and 91 are zero padding
+
+// ---- layout conversion ------------------------------------------------------
+
+__global__ void repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows, uint32_t experts,
+                              uint4 *__restrict__ codes, uint8_t *__restrict__ scales) {
+    const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t per_expert = size_t(rows) * mx::blocks;
+    if (gid >= per_expert * experts) {
+        return;
+    }
+    const uint32_t e = uint32_t(gid / per_expert);
+    const size_t b = gid % per_expert;
+    const uint32_t row = uint32_t(b / mx::blocks);
+    const uint32_t block = uint32_t(b % mx::blocks);
+    const uint8_t *src = gguf + gid * 17;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        w[i / 4] |= uint32_t(src[1 + i]) << (8 * (i % 4));
+    }
+    const size_t tile_index = size_t(e) * (rows / mx::tile_rows) + row / mx::tile_rows;
+    codes[mx::code_chunk(tile_index, block, row % mx::tile_rows)] = make_uint4(w[0], w[1], w[2], w[3]);
+    scales[mx::scale_offset(tile_index, block, row % mx::tile_rows)] = src[0];
+}
+
+__global__ void unpack_kernel(const uint4 *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows,
+                              uint32_t experts, uint8_t *__restrict__ gguf) {
+    const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t per_expert = size_t(rows) * mx::blocks;
+    if (gid >= per_expert * experts) {
+        return;
+    }
+    const uint32_t e = uint32_t(gid / per_expert);
+    const size_t b = gid % per_expert;
+    const uint32_t row = uint32_t(b / mx::blocks);
+    const uint32_t block = uint32_t(b % mx::blocks);
+    const size_t tile_index = size_t(e) * (rows / mx::tile_rows) + row / mx::tile_rows;
+    const uint4 c = codes[mx::code_chunk(tile_index, block, row % mx::tile_rows)];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    uint8_t *dst = gguf + gid * 17;
+    dst[0] = scales[mx::scale_offset(tile_index, block, row % mx::tile_rows)];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        dst[1 + i] = uint8_t(w[i / 4] >> (8 * (i % 4)));
+    }
+}
+
+// ---- decode ------------------------------------------------------------------
+
+// tensor.cpp:34: the reference's integer for code c (twice its E2M1 value).
+__device__ inline int mxfp4_int(uint32_t code) {
+    const uint32_t m = code & 7u;
+    const int magnitude = m < 4 ? int(m) : int(((m & 1u) ? 3u : 2u) << ((m >> 1) - 1));
+    return (code & 8u) ? -magnitude : magnitude;
+}
+
+// tensor.cpp:36-44: 2^(e-128) from its bit pattern.
+__device__ inline float mxfp4_scale(uint32_t e) {
+    const uint32_t bits = e < 2 ? (0x00200000u << e) : ((e - 1u) << 23);
+    return __uint_as_float(bits);
+}
+
+template <int Sel>
+__device__ inline float2 cvt_fp4x2(uint32_t word) {
+    // Two E2M1 values of byte Sel of `word`: .x from the low nibble, .y from the high.
+    const auto v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, Sel);
+    return make_float2(v[0], v[1]);
+}
+
+__global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows,
+                               uint32_t expert, int mode, float *__restrict__ out) {
+    const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= size_t(rows) * mx::blocks) {
+        return;
+    }
+    const uint32_t row = uint32_t(gid / mx::blocks);
+    const uint32_t block = uint32_t(gid % mx::blocks);
+    const size_t tile_index = size_t(expert) * (rows / mx::tile_rows) + row / mx::tile_rows;
+    const uint4 c = codes[mx::code_chunk(tile_index, block, row % mx::tile_rows)];
+    const uint32_t e = scales[mx::scale_offset(tile_index, block, row % mx::tile_rows)];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    float *dst = out + size_t(row) * mx::cols + block * 32;
+    if (mode == 0) {
+        const float scale = mxfp4_scale(e);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
+            dst[j] = scale * float(mxfp4_int(byte & 15u));
+            dst[j + 16] = scale * float(mxfp4_int(byte >> 4));
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float2 v0 = cvt_fp4x2<0>(w[q]);
+            const float2 v1 = cvt_fp4x2<1>(w[q]);
+            const float2 v2 = cvt_fp4x2<2>(w[q]);
+            const float2 v3 = cvt_fp4x2<3>(w[q]);
+            const int k = int(e) - 127;
+            dst[4 * q + 0] = __builtin_amdgcn_ldexpf(v0.x, k);
+            dst[4 * q + 16] = __builtin_amdgcn_ldexpf(v0.y, k);
+            dst[4 * q + 1] = __builtin_amdgcn_ldexpf(v1.x, k);
+            dst[4 * q + 17] = __builtin_amdgcn_ldexpf(v1.y, k);
+            dst[4 * q + 2] = __builtin_amdgcn_ldexpf(v2.x, k);
+            dst[4 * q + 18] = __builtin_amdgcn_ldexpf(v2.y, k);
+            dst[4 * q + 3] = __builtin_amdgcn_ldexpf(v3.x, k);
+            dst[4 * q + 19] = __builtin_amdgcn_ldexpf(v3.y, k);
+        }
+    }
+}
+
+// ---- matvec ------------------------------------------------------------------
+
+// Sum over one 32-value block: codes (16 bytes) against x[0..31] of the block.
+__device__ inline float block_dot(const uint4 c, const float *__restrict__ xb) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 xl = *reinterpret_cast<const float4 *>(xb + 4 * q);
+        const float4 xh = *reinterpret_cast<const float4 *>(xb + 16 + 4 * q);
+        const float2 v0 = cvt_fp4x2<0>(w[q]);
+        const float2 v1 = cvt_fp4x2<1>(w[q]);
+        const float2 v2 = cvt_fp4x2<2>(w[q]);
+        const float2 v3 = cvt_fp4x2<3>(w[q]);
+        lo = fmaf(v0.x, xl.x, lo);
+        hi = fmaf(v0.y, xh.x, hi);
+        lo = fmaf(v1.x, xl.y, lo);
+        hi = fmaf(v1.y, xh.y, hi);
+        lo = fmaf(v2.x, xl.z, lo);
+        hi = fmaf(v2.y, xh.z, hi);
+        lo = fmaf(v3.x, xl.w, lo);
+        hi = fmaf(v3.y, xh.w, hi);
+    }
+    return lo + hi;
+}
+
+// Stages x (2880 floats) into the padded LDS layout; blocks 90 and 91 are zero.
+__device__ inline void stage_x(const float *__restrict__ x, float *xs) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    for (int i = threadIdx.x; i < kXBlocks * 8; i += blockDim.x) {
+        const int block = i / 8, part = i % 8;
+        const float4 v = block < mx::blocks ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4 *>(xs + block * kXStride + part * 4) = v;
+    }
+}
+
+// One wave = one 16-row tile of the expert selected for slot blockIdx.x / groups.
+__global__ __launch_bounds__(kWaves * 64) void matvec_kernel(
+    const uint4 *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows, uint32_t tiles,
+    uint32_t experts, const float *__restrict__ bias, const float *__restrict__ x, uint32_t x_stride,
+    const int32_t *__restrict__ expert_ids, float *__restrict__ y) {
+    __shared__ __attribute__((aligned(16))) float xs[kXBlocks * kXStride];
+    const uint32_t groups = (tiles + kWaves - 1) / kWaves;
+    const uint32_t slot = blockIdx.x / groups;
+    const uint32_t tile = (blockIdx.x % groups) * kWaves + threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t r = lane % mx::tile_rows;
+    const uint32_t kl = lane / mx::tile_rows;
+
+    stage_x(x + size_t(slot) * x_stride, xs);
+    __syncthreads();
+    if (tile >= tiles) {
+        return;
+    }
+    const uint32_t row = tile * mx::tile_rows + r;
+    const int32_t e = expert_ids[slot];
+    if (e < 0 || uint32_t(e) >= experts) {
+        if (kl == 0) {
+            y[size_t(slot) * rows + row] = __builtin_nanf("");
+        }
+        return;
+    }
+    const size_t tile_index = size_t(e) * tiles + tile;
+    const uint4 *tc = codes + tile_index * mx::blocks * mx::tile_rows + r;
+    const uint2 *ts = reinterpret_cast<const uint2 *>(scales + tile_index * mx::tile_scale_bytes +
+                                                      size_t(lane) * mx::scale_pad);
+    const uint2 s01 = ts[0], s23 = ts[1], s45 = ts[2];
+    const uint32_t sw[6] = {s01.x, s01.y, s23.x, s23.y, s45.x, s45.y};
+
+    uint4 q[mx::iters];
+#pragma unroll
+    for (int i = 0; i < mx::iters; ++i) {
+        const uint32_t kb = 4 * i + kl;
+        q[i] = (i < mx::iters - 1 || kb < mx::blocks) ? tc[size_t(kb) * mx::tile_rows] : make_uint4(0, 0, 0, 0);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < mx::iters; ++i) {
+        const uint32_t kb = 4 * i + kl;
+        const int e8 = int((sw[i / 4] >> (8 * (i % 4))) & 0xffu);
+        const float partial = block_dot(q[i], xs + kb * kXStride);
+        acc += __builtin_amdgcn_ldexpf(partial, e8 - 127);
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (kl == 0) {
+        y[size_t(slot) * rows + row] = bias ? acc + bias[size_t(e) * rows + row] : acc;
+    }
+}
+
+int check_tensor(const ttl_mxfp4 *t, const char *who) {
+    TTL_REQUIRE(t && t->codes && t->scales, TTL_ERR_INVALID, "%s: null tensor", who);
+    return TTL_OK;
+}
+
+int alloc_tensor(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, ttl_mxfp4 **out, const char *who) {
+    TTL_REQUIRE(ctx && out, TTL_ERR_INVALID, "%s: null argument", who);
+    *out = nullptr;
+    TTL_REQUIRE(cols == uint32_t(mx::cols), TTL_ERR_SHAPE, "%s: cols must be %d (got %u)", who, mx::cols, cols);
+    TTL_REQUIRE(rows > 0 && rows % mx::tile_rows == 0, TTL_ERR_SHAPE, "%s: rows must be a positive multiple of %d",
+                who, mx::tile_rows);
+    TTL_REQUIRE(experts > 0, TTL_ERR_SHAPE, "%s: experts must be positive", who);
+    ttl_mxfp4 *t = new ttl_mxfp4;
+    t->rows = rows;
+    t->cols = cols;
+    t->experts = experts;
+    t->tiles = rows / mx::tile_rows;
+    const size_t tiles_total = size_t(t->tiles) * experts;
+    t->code_bytes = tiles_total * mx::tile_code_bytes;
+    t->scale_bytes = tiles_total * mx::tile_scale_bytes;
+    hipError_t err = hipMalloc(&t->codes, t->code_bytes);
+    if (err == hipSuccess) {
+        err = hipMalloc(&t->scales, t->scale_bytes);
+    }
+    if (err != hipSuccess) {
+        (void)hipFree(t->codes);
+        delete t;
+        return ttl::hip_fail(err, who);
+    }
+    // Padding scale bytes must decode to a finite scale (their blocks are zero).
+    const int rc = ttl_fill_bytes(ctx, t->scales, mx::pad_scale, t->scale_bytes);
+    if (rc != TTL_OK) {
+        ttl_mxfp4_free(ctx, t);
+        return rc;
+    }
+    *out = t;
+    return TTL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ttl_mxfp4_upload_dev(ttl_ctx *ctx, const void *gguf_blocks_dev, uint32_t rows, uint32_t cols,
+                         uint32_t experts, ttl_mxfp4 **out) {
+    TTL_REQUIRE(gguf_blocks_dev, TTL_ERR_INVALID, "ttl_mxfp4_upload_dev: null blocks");
+    int rc = alloc_tensor(ctx, rows, cols, experts, out, "ttl_mxfp4_upload_dev");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    ttl_mxfp4 *t = *out;
+    const size_t n = size_t(rows) * mx::blocks * experts;
+    repack_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>((const uint8_t *)gguf_blocks_dev, rows, experts,
+                                                                     (uint4 *)t->codes, t->scales);
+    TTL_LAUNCHED("repack_kernel");
+    return TTL_OK;
+}
+
+int ttl_mxfp4_upload(ttl_ctx *ctx, const void *gguf_blocks, uint32_t rows, uint32_t cols, uint32_t experts,
+                     ttl_mxfp4 **out) {
+    TTL_REQUIRE(ctx && gguf_blocks && out, TTL_ERR_INVALID, "ttl_mxfp4_upload: null argument");
+    TTL_REQUIRE(cols == uint32_t(mx::cols), TTL_ERR_SHAPE, "ttl_mxfp4_upload: cols must be %d", mx::cols);
+    const size_t bytes = size_t(rows) * mx::blocks * 17 * experts;
+    void *staging = nullptr;
+    TTL_HIP(hipMalloc(&staging, bytes ? bytes : 1));
+    int rc = ttl_memcpy_h2d(ctx, staging, gguf_blocks, bytes);
+    if (rc == TTL_OK) {
+        rc = ttl_mxfp4_upload_dev(ctx, staging, rows, cols, experts, out);
+    }
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(staging);
+    return rc;
+}
+
+int ttl_mxfp4_synthetic(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, uint64_t seed,
+                        uint64_t stream, uint32_t emin, uint32_t emax, ttl_mxfp4 **out) {
+    TTL_REQUIRE(emin <= emax && emax <= 255, TTL_ERR_INVALID, "ttl_mxfp4_synthetic: bad exponent range");
+    int rc = alloc_tensor(ctx, rows, cols, experts, out, "ttl_mxfp4_synthetic");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    return ttl::synth_mxfp4_repacked(ctx, *out, seed, stream, emin, emax);
+}
+
+int ttl_mxfp4_download(ttl_ctx *ctx, const ttl_mxfp4 *t, void *gguf_blocks) {
+    TTL_REQUIRE(ctx && gguf_blocks, TTL_ERR_INVALID, "ttl_mxfp4_download: null argument");
+    int rc = check_tensor(t, "ttl_mxfp4_download");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const size_t n = size_t(t->rows) * mx::blocks * t->experts;
+    void *staging = nullptr;
+    TTL_HIP(hipMalloc(&staging, n * 17));
+    unpack_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>((const uint4 *)t->codes, t->scales, t->rows,
+                                                                     t->experts, (uint8_t *)staging);
+    hipError_t err = hipGetLastError();
+    rc = err == hipSuccess ? ttl_memcpy_d2h(ctx, gguf_blocks, staging, n * 17) : ttl::hip_fail(err, "unpack_kernel");
+    (void)hipFree(staging);
+    return rc;
+}
+
+void ttl_mxfp4_free(ttl_ctx *ctx, ttl_mxfp4 *t) {
+    if (!t) {
+        return;
+    }
+    if (ctx) {
+        (void)hipStreamSynchronize(ctx->stream);
+    }
+    (void)hipFree(t->codes);
+    (void)hipFree(t->scales);
+    delete t;
+}
+
+int ttl_mxfp4_shape(const ttl_mxfp4 *t, uint32_t *rows, uint32_t *cols, uint32_t *experts) {
+    TTL_REQUIRE(t, TTL_ERR_INVALID, "ttl_mxfp4_shape: null tensor");
+    if (rows) {
+        *rows = t->rows;
+    }
+    if (cols) {
+        *cols = t->cols;
+    }
+    if (experts) {
+        *experts = t->experts;
+    }
+    return TTL_OK;
+}
+
+size_t ttl_mxfp4_bytes(const ttl_mxfp4 *t) {
+    return t ? t->code_bytes + t->scale_bytes : 0;
+}
+
+int ttl_mxfp4_dequantize(ttl_ctx *ctx, const ttl_mxfp4 *t, uint32_t expert, int mode, float *out_dev) {
+    TTL_REQUIRE(ctx && out_dev, TTL_ERR_INVALID, "ttl_mxfp4_dequantize: null argument");
+    int rc = check_tensor(t, "ttl_mxfp4_dequantize");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(expert < t->experts, TTL_ERR_INVALID, "ttl_mxfp4_dequantize: expert %u out of range", expert);
+    TTL_REQUIRE(mode == 0 || mode == 1, TTL_ERR_INVALID, "ttl_mxfp4_dequantize: mode must be 0 or 1");
+    const size_t n = size_t(t->rows) * mx::blocks;
+    dequant_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>((const uint4 *)t->codes, t->scales, t->rows,
+                                                                      expert, mode, out_dev);
+    TTL_LAUNCHED("dequant_kernel");
+    return TTL_OK;
+}
+
+int ttl_matvec_mxfp4_experts(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
+                             uint32_t x_stride, const int32_t *experts_dev, uint32_t n, float *y_dev) {
+    TTL_REQUIRE(ctx && x_dev && experts_dev && y_dev, TTL_ERR_INVALID, "ttl_matvec_mxfp4_experts: null argument");
+    int rc = check_tensor(w, "ttl_matvec_mxfp4_experts");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(x_stride == 0 || x_stride >= w->cols, TTL_ERR_SHAPE,
+                "ttl_matvec_mxfp4_experts: x_stride %u smaller than cols %u", x_stride, w->cols);
+    TTL_REQUIRE(x_stride % 4 == 0, TTL_ERR_SHAPE, "ttl_matvec_mxfp4_experts: x_stride must be a multiple of 4");
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0, TTL_ERR_INVALID,
+                "ttl_matvec_mxfp4_experts: x must be 16-byte aligned");
+    if (n == 0) {
+        return TTL_OK;
+    }
+    const uint32_t groups = (w->tiles + kWaves - 1) / kWaves;
+    const size_t grid = size_t(groups) * n;
+    TTL_REQUIRE(grid < (1u << 31), TTL_ERR_SHAPE, "ttl_matvec_mxfp4_experts: too many slots");
+    matvec_kernel<<<unsigned(grid), kWaves * 64, 0, ctx->stream>>>((const uint4 *)w->codes, w->scales, w->rows,
+                                                                   w->tiles, w->experts, bias_dev, x_dev, x_stride,
+                                                                   experts_dev, y_dev);
+    TTL_LAUNCHED("matvec_kernel");
+    return TTL_OK;
+}
+
+int ttl_matvec_mxfp4(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev, float *y_dev,
+                     uint32_t expert) {
+    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_matvec_mxfp4: null context");
+    int rc = check_tensor(w, "ttl_matvec_mxfp4");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(expert < w->experts && expert < uint32_t(ttl::iota_size), TTL_ERR_INVALID,
+                "ttl_matvec_mxfp4: expert %u out of range (%u experts)", expert, w->experts);
+    return ttl_matvec_mxfp4_experts(ctx, w, bias_dev, x_dev, 0, ctx->iota + expert, 1, y_dev);
+}
+
+}  // extern "C"

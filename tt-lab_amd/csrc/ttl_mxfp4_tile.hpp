@@ -1,0 +1,98 @@
+// Device building blocks of the MXFP4 matvec kernels (one wave = one 16-row tile).
+//
+//  - Lane l works on row l%16 of the tile and on blocks kb = 4*i + l/16,
+//    i = 0..22, so each 64-lane 16-byte load reads 1 KiB of contiguous codes.
+//  - All 23 code chunks and the lane's 24 scale bytes are requested before any
+//    arithmetic, so a wave keeps ~23 KiB in flight from HBM.
+//  - The activation vector sits in LDS with a padded stride (36 floats per
+//    32-value block), so the four distinct addresses of a ds_read_b128 fall in
+//    different banks.
+//  - Decode happens in registers: v_cvt_scalef32_pk_f32_fp4 turns one byte into
+//    the two E2M1 values it holds (low nibble -> element j, high -> j+16); the 32
+//    products of a block accumulate in f32 and the block's E8M0 scale is applied
+//    once to that partial as an exact power of two (v_ldexp_f32).
+//  - The four lanes of a row are combined with two cross-lane exchanges.
+#pragma once
+
+#include "ttl_internal.hpp"
+
+namespace mxt {
+
+constexpr int x_stride = 36;                       // padded LDS floats per block
+constexpr int x_blocks = mx::iters * mx::lanes_k;  // 92: blocks 90 and 91 are zero
+constexpr int x_floats = x_blocks * x_stride;
+
+template <int Sel>
+__device__ inline float2 cvt_fp4x2(uint32_t word) {
+    // The two E2M1 values of byte Sel of `word`: .x from the low nibble, .y from the high.
+    const auto v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, Sel);
+    return make_float2(v[0], v[1]);
+}
+
+// Unscaled dot product of one block's 32 codes with x[0..31] of the block.
+__device__ inline float block_dot(const uint4 c, const float *__restrict__ xb) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 xl = *reinterpret_cast<const float4 *>(xb + 4 * q);
+        const float4 xh = *reinterpret_cast<const float4 *>(xb + 16 + 4 * q);
+        const float2 v0 = cvt_fp4x2<0>(w[q]);
+        const float2 v1 = cvt_fp4x2<1>(w[q]);
+        const float2 v2 = cvt_fp4x2<2>(w[q]);
+        const float2 v3 = cvt_fp4x2<3>(w[q]);
+        lo = fmaf(v0.x, xl.x, lo);
+        hi = fmaf(v0.y, xh.x, hi);
+        lo = fmaf(v1.x, xl.y, lo);
+        hi = fmaf(v1.y, xh.y, hi);
+        lo = fmaf(v2.x, xl.z, lo);
+        hi = fmaf(v2.y, xh.z, hi);
+        lo = fmaf(v3.x, xl.w, lo);
+        hi = fmaf(v3.y, xh.w, hi);
+    }
+    return lo + hi;
+}
+
+// Copies x (2880 floats, 16-byte aligned) into the padded LDS layout; the two
+// padding blocks are zero.  All threads of the workgroup take part.
+__device__ inline void stage_x(const float *__restrict__ x, float *xs) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    for (int i = threadIdx.x; i < x_blocks * 8; i += blockDim.x) {
+        const int block = i / 8, part = i % 8;
+        const float4 v = block < mx::blocks ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4 *>(xs + block * x_stride + part * 4) = v;
+    }
+}
+
+// Dot products of the 16 rows of one tile with x.  `lane` is the lane in the
+// wave.  The row sum for row lane%16 is returned in every lane (lanes l, l+16,
+// l+32, l+48 hold the same value).
+__device__ inline float tile_dot(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
+                                 size_t tile_index, const float *xs, uint32_t lane) {
+    const uint32_t r = lane % mx::tile_rows;
+    const uint32_t kl = lane / mx::tile_rows;
+    const uint4 *tc = reinterpret_cast<const uint4 *>(codes) + tile_index * mx::blocks * mx::tile_rows + r;
+    const uint2 *ts = reinterpret_cast<const uint2 *>(scales + tile_index * mx::tile_scale_bytes +
+                                                      size_t(lane) * mx::scale_pad);
+    const uint2 s01 = ts[0], s23 = ts[1], s45 = ts[2];
+    const uint32_t sw[6] = {s01.x, s01.y, s23.x, s23.y, s45.x, s45.y};
+
+    uint4 q[mx::iters];
+#pragma unroll
+    for (int i = 0; i < mx::iters; ++i) {
+        const uint32_t kb = 4 * i + kl;
+        q[i] = (i < mx::iters - 1 || kb < mx::blocks) ? tc[size_t(kb) * mx::tile_rows] : make_uint4(0, 0, 0, 0);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < mx::iters; ++i) {
+        const uint32_t kb = 4 * i + kl;
+        const int e8 = int((sw[i / 4] >> (8 * (i % 4))) & 0xffu);
+        acc += __builtin_amdgcn_ldexpf(block_dot(q[i], xs + kb * x_stride), e8 - 127);
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    return acc;
+}
+
+}  // namespace mxt

@@ -1,0 +1,252 @@
+"""ctypes binding of the gfx950 backend's C ABI (include/ttlab_hip.h).
+
+The product is the shared library build/libttlab_hip.so; this module only loads
+it and wraps its entry points for Python callers (tests, bench.py).  There is no
+fallback: if the library is missing or the GPU is absent, calls raise.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(PKG_DIR, "build", "libttlab_hip.so")
+HEADER_PATH = os.path.join(REPO_DIR, "include", "ttlab_hip.h")
+
+TTL_OK = 0
+
+
+class TtlError(RuntimeError):
+    pass
+
+
+class MoeLayerDesc(C.Structure):
+    """Mirror of ttl_moe_layer."""
+    _fields_ = [
+        ("hidden", C.c_uint32),
+        ("expert_hidden", C.c_uint32),
+        ("experts", C.c_uint32),
+        ("used", C.c_uint32),
+        ("router_weight", C.c_void_p),
+        ("router_bias", C.c_void_p),
+        ("gate", C.c_void_p),
+        ("gate_bias", C.c_void_p),
+        ("up", C.c_void_p),
+        ("up_bias", C.c_void_p),
+        ("down", C.c_void_p),
+        ("down_bias", C.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load_library():
+    """Loads build/libttlab_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise TtlError(f"{LIB_PATH} is missing: run __graft_entry__.build() (make -C tt-lab_amd)")
+    lib = C.CDLL(LIB_PATH)
+    vp, u32, u64, sz, f32, i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float, C.c_int
+    sigs = {
+        "ttl_create": (i32, [i32, C.POINTER(vp)]),
+        "ttl_destroy": (None, [vp]),
+        "ttl_last_error": (C.c_char_p, []),
+        "ttl_sync": (i32, [vp]),
+        "ttl_device_info": (i32, [vp, C.c_char_p, sz, C.POINTER(i32), C.POINTER(C.c_double)]),
+        "ttl_malloc": (i32, [vp, sz, C.POINTER(vp)]),
+        "ttl_free": (i32, [vp, vp]),
+        "ttl_memcpy_h2d": (i32, [vp, vp, vp, sz]),
+        "ttl_memcpy_d2h": (i32, [vp, vp, vp, sz]),
+        "ttl_memcpy_d2d": (i32, [vp, vp, vp, sz]),
+        "ttl_fill_bytes": (i32, [vp, vp, C.c_uint8, sz]),
+        "ttl_timer_start": (i32, [vp]),
+        "ttl_timer_stop": (i32, [vp, C.POINTER(f32)]),
+        "ttl_synth_normal": (i32, [vp, u64, u64, sz, sz, f32, f32, vp]),
+        "ttl_synth_normal_bf16": (i32, [vp, u64, u64, sz, sz, f32, vp]),
+        "ttl_synth_mxfp4_gguf": (i32, [vp, u64, u64, sz, sz, u32, u32, vp]),
+        "ttl_mxfp4_upload": (i32, [vp, vp, u32, u32, u32, C.POINTER(vp)]),
+        "ttl_mxfp4_upload_dev": (i32, [vp, vp, u32, u32, u32, C.POINTER(vp)]),
+        "ttl_mxfp4_synthetic": (i32, [vp, u32, u32, u32, u64, u64, u32, u32, C.POINTER(vp)]),
+        "ttl_mxfp4_download": (i32, [vp, vp, vp]),
+        "ttl_mxfp4_free": (None, [vp, vp]),
+        "ttl_mxfp4_shape": (i32, [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(u32)]),
+        "ttl_mxfp4_bytes": (sz, [vp]),
+        "ttl_mxfp4_dequantize": (i32, [vp, vp, u32, i32, vp]),
+        "ttl_matvec_mxfp4": (i32, [vp, vp, vp, vp, vp, u32]),
+        "ttl_matvec_mxfp4_experts": (i32, [vp, vp, vp, vp, u32, vp, u32, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def header_symbols():
+    """Names of the functions include/ttlab_hip.h declares."""
+    import re
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ttl_[a-z0-9_]+)\s*\(", text)))
+
+
+def _check(rc, what):
+    if rc != TTL_OK:
+        msg = load_library().ttl_last_error()
+        raise TtlError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
+
+
+class Buffer:
+    """Device allocation owned by a Device."""
+
+    def __init__(self, dev, nbytes):
+        self.dev = dev
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(dev.lib.ttl_malloc(dev.ctx, self.nbytes, C.byref(p)), "ttl_malloc")
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            self.dev.lib.ttl_free(self.dev.ctx, self.ptr)
+            self.ptr = None
+
+    def offset(self, nbytes):
+        return C.c_void_p(self.ptr + int(nbytes))
+
+    @property
+    def p(self):
+        return C.c_void_p(self.ptr)
+
+    def upload(self, array):
+        a = np.ascontiguousarray(array)
+        assert a.nbytes <= self.nbytes
+        _check(self.dev.lib.ttl_memcpy_h2d(self.dev.ctx, self.ptr, a.ctypes.data, a.nbytes), "ttl_memcpy_h2d")
+        return self
+
+    def download(self, dtype, count=None, offset_bytes=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset_bytes) // dtype.itemsize
+        out = np.empty(count, dtype)
+        _check(self.dev.lib.ttl_memcpy_d2h(self.dev.ctx, out.ctypes.data, self.ptr + offset_bytes, out.nbytes),
+               "ttl_memcpy_d2h")
+        return out
+
+
+class Mxfp4:
+    """Device MXFP4 tensor handle (ttl_mxfp4)."""
+
+    def __init__(self, dev, handle):
+        self.dev = dev
+        self.handle = handle
+        r, c, e = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        _check(dev.lib.ttl_mxfp4_shape(handle, C.byref(r), C.byref(c), C.byref(e)), "ttl_mxfp4_shape")
+        self.rows, self.cols, self.experts = r.value, c.value, e.value
+
+    @property
+    def nbytes(self):
+        return self.dev.lib.ttl_mxfp4_bytes(self.handle)
+
+    def download_gguf(self):
+        out = np.empty(self.rows * self.cols // 32 * 17 * self.experts, np.uint8)
+        _check(self.dev.lib.ttl_mxfp4_download(self.dev.ctx, self.handle, out.ctypes.data), "ttl_mxfp4_download")
+        return out
+
+    def dequantize(self, expert, mode=0):
+        buf = self.dev.alloc(self.rows * self.cols * 4)
+        try:
+            _check(self.dev.lib.ttl_mxfp4_dequantize(self.dev.ctx, self.handle, expert, mode, buf.ptr),
+                   "ttl_mxfp4_dequantize")
+            return buf.download(np.float32).reshape(self.rows, self.cols)
+        finally:
+            buf.free()
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.ttl_mxfp4_free(self.dev.ctx, self.handle)
+            self.handle = None
+
+
+class Device:
+    """One ttl_ctx: a gfx950 device and its stream."""
+
+    def __init__(self, ordinal=0):
+        self.lib = load_library()
+        p = C.c_void_p()
+        _check(self.lib.ttl_create(ordinal, C.byref(p)), "ttl_create")
+        self.ctx = p.value
+
+    def close(self):
+        if self.ctx:
+            self.lib.ttl_destroy(self.ctx)
+            self.ctx = None
+
+    def info(self):
+        name = C.create_string_buffer(128)
+        cu = C.c_int()
+        mem = C.c_double()
+        _check(self.lib.ttl_device_info(self.ctx, name, 128, C.byref(cu), C.byref(mem)), "ttl_device_info")
+        return {"name": name.value.decode(), "compute_units": cu.value, "hbm_bytes": mem.value}
+
+    def sync(self):
+        _check(self.lib.ttl_sync(self.ctx), "ttl_sync")
+
+    def alloc(self, nbytes):
+        return Buffer(self, nbytes)
+
+    def upload(self, array):
+        a = np.ascontiguousarray(array)
+        return Buffer(self, max(a.nbytes, 1)).upload(a)
+
+    def fill(self, buf, value, nbytes=None):
+        _check(self.lib.ttl_fill_bytes(self.ctx, buf.ptr, value, buf.nbytes if nbytes is None else nbytes),
+               "ttl_fill_bytes")
+
+    def timer_start(self):
+        _check(self.lib.ttl_timer_start(self.ctx), "ttl_timer_start")
+
+    def timer_stop(self):
+        ms = C.c_float()
+        _check(self.lib.ttl_timer_stop(self.ctx, C.byref(ms)), "ttl_timer_stop")
+        return ms.value
+
+    # ---- synthetic inputs ----
+    def synth_normal(self, buf, seed, stream, n, sigma=1.0, mean=0.0, offset=0):
+        _check(self.lib.ttl_synth_normal(self.ctx, seed, stream, offset, n, mean, sigma, buf.ptr), "ttl_synth_normal")
+
+    def synth_normal_bf16(self, buf, seed, stream, n, sigma, offset=0):
+        _check(self.lib.ttl_synth_normal_bf16(self.ctx, seed, stream, offset, n, sigma, buf.ptr),
+               "ttl_synth_normal_bf16")
+
+    def synth_mxfp4_gguf(self, buf, seed, stream, nblocks, emin=119, emax=125, block_offset=0):
+        _check(self.lib.ttl_synth_mxfp4_gguf(self.ctx, seed, stream, block_offset, nblocks, emin, emax, buf.ptr),
+               "ttl_synth_mxfp4_gguf")
+
+    # ---- MXFP4 ----
+    def mxfp4_upload(self, gguf_bytes, rows, cols, experts):
+        a = np.ascontiguousarray(gguf_bytes, np.uint8)
+        h = C.c_void_p()
+        _check(self.lib.ttl_mxfp4_upload(self.ctx, a.ctypes.data, rows, cols, experts, C.byref(h)), "ttl_mxfp4_upload")
+        return Mxfp4(self, h.value)
+
+    def mxfp4_synthetic(self, rows, cols, experts, seed, stream, emin=119, emax=125):
+        h = C.c_void_p()
+        _check(self.lib.ttl_mxfp4_synthetic(self.ctx, rows, cols, experts, seed, stream, emin, emax, C.byref(h)),
+               "ttl_mxfp4_synthetic")
+        return Mxfp4(self, h.value)
+
+    def matvec_mxfp4(self, w, bias, x, y, expert):
+        _check(self.lib.ttl_matvec_mxfp4(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, y.ptr, expert),
+               "ttl_matvec_mxfp4")
+
+    def matvec_mxfp4_experts(self, w, bias, x, x_stride, experts, n, y):
+        _check(self.lib.ttl_matvec_mxfp4_experts(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
+                                                 experts.ptr, n, y.ptr), "ttl_matvec_mxfp4_experts")
