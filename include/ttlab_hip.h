@@ -125,6 +125,70 @@ int ttl_matvec_mxfp4(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, co
 int ttl_matvec_mxfp4_experts(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
                              uint32_t x_stride, const int32_t *experts_dev, uint32_t n, float *y_dev);
 
+/* ---- MoE decode (one token) ----------------------------------------------------- */
+
+/* Router logits, top-k experts and their softmax weights.  Replaces the router
+ * matvec_add_f32 call and the selection sort + softmax of GptOssModel::moe
+ * (model.cpp:293-321, tensor.cpp:186-200).  weight_dev is f32 [experts][hidden]
+ * (the GGUF ffn_gate_inp tensor), bias_dev f32 [experts], x_dev f32 [hidden].
+ * Outputs: logits_dev f32 [experts], indices_dev int32 [k] (rank order, exactly the
+ * reference's), weights_dev f32 [k].  hidden must be 2880, experts <= 192, k <= 16.
+ * flags: TTL_ROUTER_FORCE_EXACT makes the kernel take its exact sequential path
+ * (the path it otherwise takes only when a near-tie could change the selection). */
+#define TTL_ROUTER_FORCE_EXACT 1u
+int ttl_router_topk(ttl_ctx *ctx, const float *weight_dev, const float *bias_dev, uint32_t experts, uint32_t hidden,
+                    const float *x_dev, uint32_t k, uint32_t flags, float *logits_dev, int32_t *indices_dev,
+                    float *weights_dev);
+/* Number of router launches on this context that took the exact sequential path. */
+int ttl_router_exact_count(ttl_ctx *ctx, uint64_t *count);
+
+/* One gpt-oss MoE layer's tensors, all in device memory (names as model.cpp:157-169). */
+typedef struct {
+    uint32_t hidden;             /* embedding length, 2880                        */
+    uint32_t expert_hidden;      /* expert feed-forward length, 2880              */
+    uint32_t experts;            /* 32 (20b) or 128 (120b)                        */
+    uint32_t used;               /* experts per token, 4                          */
+    const float *router_weight;  /* ffn_gate_inp.weight, f32 [experts][hidden]    */
+    const float *router_bias;    /* ffn_gate_inp.bias, f32 [experts]              */
+    const ttl_mxfp4 *gate;       /* ffn_gate_exps.weight: experts x expert_hidden x hidden */
+    const float *gate_bias;      /* ffn_gate_exps.bias, f32 [experts][expert_hidden] (may be NULL) */
+    const ttl_mxfp4 *up;         /* ffn_up_exps.weight                            */
+    const float *up_bias;        /* ffn_up_exps.bias (may be NULL)                */
+    const ttl_mxfp4 *down;       /* ffn_down_exps.weight: experts x hidden x expert_hidden */
+    const float *down_bias;      /* ffn_down_exps.bias, f32 [experts][hidden] (may be NULL) */
+} ttl_moe_layer;
+
+/* out = MoE(x) for one token: router + top-k + softmax, then for the k selected
+ * experts only: gate and up matvecs with the clamped SwiGLU fused in, the down
+ * matvec, and out = sum_r w_r * down_r in rank order.  Replaces GptOssModel::moe
+ * (model.cpp:292-338).  indices_dev / weights_dev (int32 [used], f32 [used]) may be
+ * NULL; when given they receive the routing. */
+int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *out_dev,
+                   int32_t *indices_dev, float *weights_dev);
+
+/* The stages of ttl_moe_decode, for callers that fuse the combine elsewhere.
+ * gate/up + SwiGLU: hidden_dev f32 [used][expert_hidden] = swiglu(gate_e x + bg, up_e x + bu)
+ *   for e = indices[r] (model.cpp:326-332);
+ * down: down_dev f32 [used][hidden] = down_e hidden_r + bd (model.cpp:333);
+ * combine: out = sum_r weights[r] * down_r, unfused, r = 0..k-1 (model.cpp:323,334-336). */
+int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
+                          const int32_t *indices_dev, float *hidden_dev);
+int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
+                 float *down_dev);
+int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
+                    float *out_dev);
+
+/* ---- HIP graphs ------------------------------------------------------------------- *
+ * Calls made on the context between ttl_capture_begin and ttl_capture_end are
+ * recorded (not run) into a graph that ttl_graph_launch replays on the stream.
+ * Only launch-only entry points may be captured (no ttl_memcpy_h2d/d2h, ttl_sync,
+ * tensor uploads).  No reference counterpart (the reference runs on the CPU). */
+typedef struct ttl_graph ttl_graph;
+int ttl_capture_begin(ttl_ctx *ctx);
+int ttl_capture_end(ttl_ctx *ctx, ttl_graph **out);
+int ttl_graph_launch(ttl_ctx *ctx, ttl_graph *graph);
+void ttl_graph_free(ttl_graph *graph);
+
 #ifdef __cplusplus
 }
 #endif

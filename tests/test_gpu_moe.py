@@ -1,0 +1,171 @@
+"""GPU parity of the MoE decode path (router + top-k + SwiGLU + combine) against the oracle.
+
+Bit-exact: top-k expert indices (fast certified path and exact path), router logits
+on the exact path.  Tolerance: relative L2 <= 1e-5 for the layer output.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import ttlab_amd
+from moe_fixtures import N, X_SEED, DeviceLayer, HostLayer
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = ttlab_amd.Device(0)
+    yield d
+    d.close()
+
+
+@pytest.fixture(scope="module")
+def layer32(dev):
+    host = HostLayer(32, 4, biases=False)
+    device = DeviceLayer(dev, host)
+    yield host, device
+    device.free()
+
+
+def oracle_router(w, b, x, k):
+    logits = np.empty(b.size, np.float32)
+    O.lib.orc_matvec_add_f32(w, b, b.size, N, np.ascontiguousarray(x, np.float32), logits)
+    idx, wts = O.router_topk(logits, k)
+    return logits, idx, wts
+
+
+def run_router(dev, wbuf, bbuf, experts, x, k, force_exact=False):
+    xb = dev.upload(x)
+    lb, ib, wb = dev.alloc(experts * 4), dev.alloc(k * 4), dev.alloc(k * 4)
+    dev.router_topk(wbuf, bbuf, experts, xb, k, lb, ib, wb, force_exact)
+    out = lb.download(np.float32), ib.download(np.int32), wb.download(np.float32)
+    for b in (xb, lb, ib, wb):
+        b.free()
+    return out
+
+
+@pytest.mark.parametrize("experts", [32, 128])
+def test_router_fast_and_exact_paths_match_reference(dev, experts):
+    w = O.synth_normal_bf16(0x77000009, 20, experts * N, 0.02)
+    b = O.synth_normal(0x77000009, 21, experts, sigma=0.05)
+    wb, bb = dev.upload(w), dev.upload(b)
+    before = dev.router_exact_count()
+    certified = 0
+    for token in range(24):
+        x = O.synth_normal(X_SEED, 100 + token, N)
+        ref_logits, ref_idx, ref_w = oracle_router(w, b, x, 4)
+        logits, idx, wts = run_router(dev, wb, bb, experts, x, 4)
+        assert list(idx) == list(ref_idx), (token, idx, ref_idx)
+        assert np.allclose(wts, ref_w, rtol=1e-5, atol=0)
+        assert O.rel_l2(logits, ref_logits) < 1e-5
+        # the exact path reproduces the reference's sequential f32 sums bit for bit
+        logits_x, idx_x, wts_x = run_router(dev, wb, bb, experts, x, 4, force_exact=True)
+        assert np.array_equal(logits_x.view(np.uint32), ref_logits.view(np.uint32))
+        assert list(idx_x) == list(ref_idx)
+        assert np.allclose(wts_x, ref_w, rtol=5e-7, atol=0)
+    exact_calls = dev.router_exact_count() - before
+    certified = 48 - exact_calls
+    print(f"experts {experts}: {exact_calls - 24} of 24 unforced calls needed the exact path")
+    assert exact_calls >= 24
+    assert certified >= 12  # random logits are rarely within the rounding bound
+    wb.free()
+    bb.free()
+
+
+def test_router_exact_ties_follow_reference_selection_sort(dev):
+    """Rows 3, 5 and 9 are identical and lead the ranking, so their logits tie exactly.
+    The fast path cannot separate them and the kernel falls back to the reference's
+    selection sort, whose swaps order the tie as the reference does."""
+    experts = 32
+    w = O.synth_normal_bf16(0x7700000A, 20, experts * N, 0.02).reshape(experts, N)
+    x = O.synth_normal(X_SEED, 7, N)
+    lead = np.sign(x).astype(np.float32) * np.float32(0.05)
+    for r in (3, 5, 9):
+        w[r] = lead
+    w = np.ascontiguousarray(w.ravel())
+    b = np.zeros(experts, np.float32)
+    b[0] = np.float32(0.0)
+    wb, bb = dev.upload(w), dev.upload(b)
+    before = dev.router_exact_count()
+    ref_logits, ref_idx, ref_w = oracle_router(w, b, x, 4)
+    assert ref_logits[3] == ref_logits[5] == ref_logits[9]
+    logits, idx, wts = run_router(dev, wb, bb, experts, x, 4)
+    assert dev.router_exact_count() == before + 1
+    assert list(idx) == list(ref_idx)
+    assert list(idx[:3]) == [3, 5, 9]
+    assert np.array_equal(logits.view(np.uint32), ref_logits.view(np.uint32))
+    wb.free()
+    bb.free()
+
+
+@pytest.mark.parametrize("body", [O.BODY_V4, O.BODY_DEFAULT])
+def test_moe_layer_config1_matches_oracle(dev, layer32, body):
+    host, device = layer32
+    out = dev.alloc(N * 4)
+    ib, wb = dev.alloc(16), dev.alloc(16)
+    for token in range(4):
+        x = O.synth_normal(X_SEED, token, N)
+        xb = dev.upload(x)
+        dev.moe_decode(device.desc, xb, out, ib, wb)
+        got = out.download(np.float32)
+        ref, _, ref_idx, ref_w = host.oracle_moe(x, body)
+        assert list(ib.download(np.int32)) == list(ref_idx)
+        assert np.allclose(wb.download(np.float32), ref_w, rtol=1e-5, atol=0)
+        err = O.rel_l2(got, ref)
+        print(f"token {token} body {body}: experts {list(ref_idx)} rel_l2 {err:.3e}")
+        assert err <= TOL
+        xb.free()
+    for b in (out, ib, wb):
+        b.free()
+
+
+def test_moe_layer_with_biases_matches_oracle(dev):
+    host = HostLayer(32, 4, biases=True, seed=0x77000002)
+    device = DeviceLayer(dev, host)
+    out = dev.alloc(N * 4)
+    for token in range(3):
+        x = O.synth_normal(X_SEED, 50 + token, N)
+        xb = dev.upload(x)
+        dev.moe_decode(device.desc, xb, out)
+        ref, _, _, _ = host.oracle_moe(x, O.BODY_V4)
+        assert O.rel_l2(out.download(np.float32), ref) <= TOL
+        xb.free()
+    out.free()
+    device.free()
+
+
+def test_moe_rejects_mismatched_layers(dev, layer32):
+    host, device = layer32
+    bad = type(device.desc).from_buffer_copy(device.desc)
+    bad.experts = 16
+    xb, out = dev.upload(np.zeros(N, np.float32)), dev.alloc(N * 4)
+    with pytest.raises(ttlab_amd.TtlError, match="must hold 16 experts"):
+        dev.moe_decode(bad, xb, out)
+    xb.free()
+    out.free()
+
+
+def test_graph_replays_match_eager_bitwise(dev, layer32):
+    """A captured MoE layer replays identically, with eager work between replays."""
+    host, device = layer32
+    x = dev.upload(O.synth_normal(X_SEED, 77, N))
+    eager_out, graph_out = dev.alloc(N * 4), dev.alloc(N * 4)
+    ib, wb = dev.alloc(16), dev.alloc(16)
+    dev.moe_decode(device.desc, x, eager_out, ib, wb)
+    expected = eager_out.download(np.float32)
+    graph = dev.capture(lambda: dev.moe_decode(device.desc, x, graph_out, ib, wb))
+    for replay in range(4):
+        dev.fill(graph_out, 0xFF)
+        graph.launch()
+        got = graph_out.download(np.float32)
+        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), replay
+        # eager work between replays reuses the same workspace
+        other = dev.upload(O.synth_normal(X_SEED, 900 + replay, N))
+        dev.moe_decode(device.desc, other, eager_out)
+        dev.sync()
+        other.free()
+    graph.free()
+    for b in (x, eager_out, graph_out, ib, wb):
+        b.free()

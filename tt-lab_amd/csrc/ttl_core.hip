@@ -74,6 +74,12 @@ int ttl_create(int device, ttl_ctx **out) {
         }
         err = hipMemcpy(ctx->iota, host_iota, sizeof(host_iota), hipMemcpyHostToDevice);
     }
+    if (err == hipSuccess) {
+        err = hipMalloc(&ctx->moe_workspace, ttl::moe_workspace_bytes());
+    }
+    if (err == hipSuccess) {
+        err = hipMemset(ctx->moe_workspace, 0, ttl::moe_workspace_bytes());
+    }
     if (err != hipSuccess) {
         ttl_destroy(ctx);
         return ttl::hip_fail(err, "ttl_create");
@@ -101,6 +107,9 @@ void ttl_destroy(ttl_ctx *ctx) {
     }
     if (ctx->iota) {
         (void)hipFree(ctx->iota);
+    }
+    if (ctx->moe_workspace) {
+        (void)hipFree(ctx->moe_workspace);
     }
     delete ctx;
 }
@@ -173,6 +182,41 @@ int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes) {
     fill_bytes_kernel<<<blocks, threads, 0, ctx->stream>>>((uint8_t *)dst_dev, value, bytes);
     TTL_LAUNCHED("fill_bytes_kernel");
     return TTL_OK;
+}
+
+int ttl_capture_begin(ttl_ctx *ctx) {
+    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_capture_begin: null context");
+    TTL_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return TTL_OK;
+}
+
+int ttl_capture_end(ttl_ctx *ctx, ttl_graph **out) {
+    TTL_REQUIRE(ctx && out, TTL_ERR_INVALID, "ttl_capture_end: null argument");
+    *out = nullptr;
+    hipGraph_t graph = nullptr;
+    TTL_HIP(hipStreamEndCapture(ctx->stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return ttl::hip_fail(err, "hipGraphInstantiate");
+    }
+    *out = new ttl_graph{graph, exec};
+    return TTL_OK;
+}
+
+int ttl_graph_launch(ttl_ctx *ctx, ttl_graph *graph) {
+    TTL_REQUIRE(ctx && graph, TTL_ERR_INVALID, "ttl_graph_launch: null argument");
+    TTL_HIP(hipGraphLaunch(graph->exec, ctx->stream));
+    return TTL_OK;
+}
+
+void ttl_graph_free(ttl_graph *graph) {
+    if (graph) {
+        (void)hipGraphExecDestroy(graph->exec);
+        (void)hipGraphDestroy(graph->graph);
+        delete graph;
+    }
 }
 
 int ttl_timer_start(ttl_ctx *ctx) {

@@ -14,9 +14,15 @@ struct ttl_ctx {
     hipEvent_t timer_start = nullptr;
     hipEvent_t timer_stop = nullptr;
     int32_t *iota = nullptr;  // device int32 [iota_size] = 0, 1, 2, ... (expert ids for single calls)
+    void *moe_workspace = nullptr;  // device ttl::MoeWorkspace, zeroed at creation
     int compute_units = 0;
     double hbm_bytes = 0.0;
     char name[128] = {};
+};
+
+struct ttl_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
 };
 
 // MXFP4 tensor in the repacked layout (see mx:: constants).
@@ -34,6 +40,8 @@ struct ttl_mxfp4 {
 namespace ttl {
 
 constexpr int iota_size = 1024;
+
+size_t moe_workspace_bytes();
 
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t err, const char *what);

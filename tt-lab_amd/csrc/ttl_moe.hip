@@ -1,0 +1,657 @@
+// MoE decode for one token: router + top-k + softmax, gate/up matvecs with the
+// clamped SwiGLU fused in, down matvecs, rank-ordered weighted combine.
+// Reference: GptOssModel::moe (model.cpp:292-338).
+//
+// Router and top-k.  The reference sums each router row sequentially in f32
+// (tensor.cpp:186-200), and the expert indices must match it exactly.  A
+// parallel sum rounds differently, so router_rows_kernel computes every row
+// exactly (products are exact in f64, sums kept in f64) together with a rigorous
+// bound on how far the reference's sequential f32 sum can be from it:
+//     |ref - exact| <= u * (sum_k |w_k x_k| + sum_k |S_k|),  u = 2^-24,
+// where S_k is the exact partial sum after column k (each product and each
+// addition rounds by at most u times its exact result).  route_workgroup() then
+// ranks the exact values; when the top-k order and the k/k+1 boundary are
+// separated by more than the bounds, the reference's selection sort provably
+// returns the same indices.  Otherwise (and for any non-finite value) it
+// recomputes every logit in the reference's sequential order and replays the
+// reference's selection sort (model.cpp:296-309) on them.
+//
+// route_workgroup() runs in the prologue of every gate/up workgroup (each one
+// derives its expert from the same data, deterministically), so routing costs
+// no kernel of its own; workgroup 0 publishes indices, weights and logits.
+#include "ttl_mxfp4_tile.hpp"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kRouterThreads = 192;  // 180 lanes x 16 columns = 2880
+constexpr int kRouterCols = 2880;
+constexpr uint32_t kMaxExperts = 192;
+constexpr uint32_t kMaxUsed = 16;
+constexpr int kPerLane = kMaxExperts / 64;  // candidates per lane in the wave-wide selection
+
+// std::max / std::min as the reference's libstdc++ defines them.
+__device__ inline float std_max(float a, float b) {
+    return (a < b) ? b : a;
+}
+__device__ inline float std_min(float a, float b) {
+    return (b < a) ? b : a;
+}
+
+__device__ inline double wave_inclusive_scan(double v, uint32_t lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const double t = __shfl_up(v, d);
+        if (lane >= uint32_t(d)) {
+            v += t;
+        }
+    }
+    return v;
+}
+
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        v += __shfl_xor(v, d);
+    }
+    return v;
+}
+
+// model.cpp:310-321: softmax over the selected logits in rank order (both arrays
+// in LDS, so no per-thread array needs scratch memory).
+__device__ void softmax_selected(const float *selected, uint32_t k, float *weights) {
+#pragma clang fp contract(off)
+    float maximum = -INFINITY;
+    for (uint32_t i = 0; i < k; ++i) {
+        maximum = std_max(maximum, selected[i]);
+    }
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < k; ++i) {
+        weights[i] = expf(selected[i] - maximum);
+        sum = sum + weights[i];
+    }
+    for (uint32_t i = 0; i < k; ++i) {
+        weights[i] = weights[i] / sum;
+    }
+}
+
+struct RouterScratch {
+    double exact[kMaxExperts];  // exact logit (f64)
+    double bound[kMaxExperts];  // bound on |reference - exact|
+    uint32_t exact_path_count;
+};
+
+// One workgroup per router row: the exact value of the row (f64) and the bound
+// on the reference's sequential-sum error.  180 lanes hold 16 columns each.
+__global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float *__restrict__ weight,
+                                                                     const float *__restrict__ bias,
+                                                                     const float *__restrict__ x,
+                                                                     RouterScratch *scratch) {
+    __shared__ double wave_part[3][3];
+    const uint32_t row = blockIdx.x;
+    const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
+    const bool active = t < kRouterCols / 16;
+
+    double prod[16];
+    double local = 0.0, abs_sum = 0.0;
+    if (active) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols) + 4 * t;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x) + 4 * t;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 w = w4[q], v = x4[q];
+            prod[4 * q + 0] = double(w.x) * double(v.x);
+            prod[4 * q + 1] = double(w.y) * double(v.y);
+            prod[4 * q + 2] = double(w.z) * double(v.z);
+            prod[4 * q + 3] = double(w.w) * double(v.w);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            local += prod[i];
+            abs_sum += fabs(prod[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            prod[i] = 0.0;
+        }
+    }
+    // exclusive prefix of the per-lane sums across the 180 lanes
+    const double incl = wave_inclusive_scan(local, lane);
+    if (lane == 63) {
+        wave_part[0][wave] = incl;
+    }
+    __syncthreads();
+    double offset = incl - local;
+    for (uint32_t w = 0; w < wave; ++w) {
+        offset += wave_part[0][w];
+    }
+    const double b = double(bias[row]);
+    double running = b + offset, partial_abs = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        running += prod[i];
+        partial_abs += fabs(running);
+    }
+    if (!active) {
+        partial_abs = 0.0;
+    }
+    const double s_abs = wave_sum(partial_abs), s_prod = wave_sum(abs_sum);
+    if (lane == 0) {
+        wave_part[1][wave] = s_abs;
+        wave_part[2][wave] = s_prod;
+    }
+    __syncthreads();
+    if (t == 0) {
+        const double total = b + wave_part[0][0] + wave_part[0][1] + wave_part[0][2];
+        const double abs_partials = wave_part[1][0] + wave_part[1][1] + wave_part[1][2];
+        const double abs_products = wave_part[2][0] + wave_part[2][1] + wave_part[2][2];
+        scratch->exact[row] = total;
+        // u = 2^-24; 1.001 covers second-order terms (n u < 2e-4); the 1e-12 term
+        // covers the f64 rounding of the exact sums; 1e-37 covers subnormal steps.
+        scratch->bound[row] = 1.001 * 0x1p-24 * (abs_partials + abs_products) + 1e-12 * abs_products + 1e-37;
+    }
+}
+
+// Routing result shared by a workgroup.
+struct RouteLds {
+    int32_t indices[kMaxUsed];
+    float weights[kMaxUsed];
+    float selected[kMaxUsed];
+    float ref_logits[kMaxExperts];
+    int32_t order[kMaxExperts];
+    int certified;
+};
+
+// Wave-wide (value, bound, index) maximum: larger value, then lower index.
+__device__ inline void wave_argmax(double &v, double &b, int32_t &i) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const double ov = __shfl_xor(v, d), ob = __shfl_xor(b, d);
+        const int32_t oi = __shfl_xor(i, d);
+        if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            b = ob;
+            i = oi;
+        }
+    }
+}
+
+__device__ inline double wave_max(double v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        v = fmax(v, __shfl_xor(v, d));
+    }
+    return v;
+}
+
+// Routing for one token, computed by the whole workgroup (blockDim.x >= experts).
+// Leaves indices/weights in lds; when `logits` is non-null also writes the logits
+// (and bumps the exact-path counter) -- only one workgroup of a launch does that.
+__device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
+                                const float *__restrict__ x, uint32_t experts, uint32_t k, bool force_exact,
+                                RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits) {
+    const uint32_t t = threadIdx.x, lane = t % 64;
+    if (t < 64) {
+        // ---- certified path: wave 0 ranks the exact values -------------------
+        double v[kPerLane], b[kPerLane];
+        bool finite = true;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const uint32_t c = lane + 64 * j;
+            v[j] = c < experts ? scratch->exact[c] : -INFINITY;
+            b[j] = c < experts ? scratch->bound[c] : 0.0;
+            if (c < experts) {
+                finite = finite && isfinite(v[j]) && isfinite(b[j]);
+            }
+        }
+        bool ok = !force_exact && __all(finite);
+        uint32_t taken = 0;
+        for (uint32_t r = 0; r < k && ok; ++r) {
+            double bv = -INFINITY, bb = 0.0;
+            int32_t bi = 0x7fffffff;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const int32_t c = int32_t(lane + 64 * j);
+                if (uint32_t(c) < experts && !(taken >> j & 1u) && (v[j] > bv || (v[j] == bv && c < bi))) {
+                    bv = v[j];
+                    bb = b[j];
+                    bi = c;
+                }
+            }
+            wave_argmax(bv, bb, bi);
+            if (uint32_t(bi) % 64 == lane) {
+                taken |= 1u << (uint32_t(bi) / 64);
+            }
+            double up = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                if (lane + 64 * j < experts && !(taken >> j & 1u)) {
+                    up = fmax(up, v[j] + b[j]);
+                }
+            }
+            up = wave_max(up);
+            ok = bv - bb > up;
+            if (lane == 0) {
+                lds.indices[r] = bi;
+                lds.selected[r] = float(bv);
+            }
+        }
+        if (lane == 0) {
+            lds.certified = ok;
+            if (ok) {
+                softmax_selected(lds.selected, k, lds.weights);
+            }
+        }
+        if (logits && ok) {
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                if (lane + 64 * j < experts) {
+                    logits[lane + 64 * j] = float(v[j]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (lds.certified) {
+        return;
+    }
+
+    // ---- exact path: the reference's sequential sums (tensor.cpp:186-200) ----
+    if (t < experts) {
+#pragma clang fp contract(off)
+        const float *w = weight + size_t(t) * kRouterCols;
+        float sum = bias[t];
+        for (int c = 0; c < kRouterCols; ++c) {
+            sum = sum + w[c] * x[c];
+        }
+        lds.ref_logits[t] = sum;
+        lds.order[t] = int32_t(t);
+        if (logits) {
+            logits[t] = sum;
+        }
+    }
+    __syncthreads();
+    if (t < 64) {
+        // model.cpp:296-309, one step per rank: best starts at position i and moves to
+        // j only if value[j] > value[best].  So best stays at i when value[order[i]] is
+        // NaN, and otherwise is the first position >= i holding the largest non-NaN value.
+        for (uint32_t i = 0; i < k; ++i) {
+            const bool start_nan = isnan(lds.ref_logits[lds.order[i]]);
+            double m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const uint32_t p = lane + 64 * j;
+                if (p >= i && p < experts) {
+                    const float val = lds.ref_logits[lds.order[p]];
+                    if (!isnan(val)) {
+                        m = fmax(m, double(val));
+                    }
+                }
+            }
+            m = wave_max(m);
+            int32_t best = 0x7fffffff;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const uint32_t p = lane + 64 * j;
+                if (p >= i && p < experts && double(lds.ref_logits[lds.order[p]]) == m) {
+                    best = min(best, int32_t(p));
+                }
+            }
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) {
+                best = min(best, __shfl_xor(best, d));
+            }
+            if (start_nan) {
+                best = int32_t(i);
+            }
+            if (lane == 0) {
+                const int32_t tmp = lds.order[i];
+                lds.order[i] = lds.order[best];
+                lds.order[best] = tmp;
+                lds.indices[i] = lds.order[i];
+            }
+            // lane 0's LDS swap must land before the wave reads order[] again
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        if (lane == 0) {
+            for (uint32_t r = 0; r < k; ++r) {
+                lds.selected[r] = lds.ref_logits[lds.indices[r]];
+            }
+            softmax_selected(lds.selected, k, lds.weights);
+            if (logits) {
+                scratch->exact_path_count += 1;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Standalone routing (ttl_router_topk): one workgroup, publishes everything.
+__global__ __launch_bounds__(256) void router_select_kernel(const float *__restrict__ weight,
+                                                            const float *__restrict__ bias, uint32_t experts,
+                                                            const float *__restrict__ x, uint32_t k,
+                                                            uint32_t force_exact, RouterScratch *scratch,
+                                                            float *__restrict__ logits,
+                                                            int32_t *__restrict__ indices,
+                                                            float *__restrict__ weights_out) {
+    __shared__ RouteLds lds;
+    route_workgroup(weight, bias, x, experts, k, force_exact != 0, scratch, lds, logits);
+    if (threadIdx.x < k) {
+        indices[threadIdx.x] = lds.indices[threadIdx.x];
+        weights_out[threadIdx.x] = lds.weights[threadIdx.x];
+    }
+}
+
+// ---- gate/up + SwiGLU -------------------------------------------------------
+
+constexpr int kGateUpWaves = 4;  // waves 0,1: gate tiles 2g, 2g+1; waves 2,3: the same up tiles
+
+// model.cpp:328-332
+__device__ inline float clamped_swiglu(float gate, float up) {
+#pragma clang fp contract(off)
+    const float x = std_min(gate, 7.0f);
+    const float y = (up < -7.0f) ? -7.0f : ((7.0f < up) ? 7.0f : up);
+    return (x / (1.0f + expf(-1.702f * x))) * (y + 1.0f);
+}
+
+struct GateUpArgs {
+    const uint8_t *gate_codes, *gate_scales;
+    const float *gate_bias;
+    const uint8_t *up_codes, *up_scales;
+    const float *up_bias;
+    uint32_t rows, tiles, experts, k;
+    const float *x;
+    // routing: either given (expert_ids) or derived in the prologue from the router
+    const int32_t *expert_ids;
+    const float *router_weight, *router_bias;
+    RouterScratch *scratch;
+    // outputs
+    float *hidden;
+    int32_t *indices_out;
+    float *weights_out, *logits_out;
+};
+
+__global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUpArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
+    __shared__ float result[2][2 * mx::tile_rows];
+    __shared__ RouteLds route;
+    const uint32_t pairs = (a.tiles + 1) / 2;
+    const uint32_t slot = blockIdx.x / pairs;
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t which = wave / 2;  // 0 gate, 1 up
+    const uint32_t tile = (blockIdx.x % pairs) * 2 + wave % 2;
+
+    int32_t e;
+    if (a.expert_ids) {
+        e = a.expert_ids[slot];
+    } else {
+        const bool publish = blockIdx.x == 0;
+        route_workgroup(a.router_weight, a.router_bias, a.x, a.experts, a.k, false, a.scratch, route,
+                        publish ? a.logits_out : nullptr);
+        e = route.indices[slot];
+        if (publish && threadIdx.x < a.k) {
+            a.indices_out[threadIdx.x] = route.indices[threadIdx.x];
+            a.weights_out[threadIdx.x] = route.weights[threadIdx.x];
+        }
+    }
+    const bool valid = e >= 0 && uint32_t(e) < a.experts;
+    mxt::TileRegs regs;
+    const size_t tile_index = size_t(e) * a.tiles + tile;
+    if (valid && tile < a.tiles) {
+        mxt::tile_load(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales, tile_index,
+                       lane, regs);
+    }
+    mxt::stage_x(a.x, xs);
+    __syncthreads();
+    if (valid && tile < a.tiles) {
+        const float acc = mxt::tile_compute(regs, xs, lane);
+        if (lane < mx::tile_rows) {
+            const uint32_t row = tile * mx::tile_rows + lane;
+            const float *b = which == 0 ? a.gate_bias : a.up_bias;
+            result[which][(wave % 2) * mx::tile_rows + lane] = b ? acc + b[size_t(e) * a.rows + row] : acc;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * mx::tile_rows) {
+        const uint32_t row = (blockIdx.x % pairs) * 2 * mx::tile_rows + threadIdx.x;
+        if (row < a.rows) {
+            a.hidden[size_t(slot) * a.rows + row] =
+                valid ? clamped_swiglu(result[0][threadIdx.x], result[1][threadIdx.x]) : __builtin_nanf("");
+        }
+    }
+}
+
+// ---- down matvec (per-slot input) -------------------------------------------
+
+constexpr int kDownWaves = 4;
+
+__global__ __launch_bounds__(kDownWaves * 64) void down_kernel(
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const float *__restrict__ bias,
+    uint32_t rows, uint32_t tiles, uint32_t experts, const float *__restrict__ hidden, uint32_t hidden_stride,
+    const int32_t *__restrict__ expert_ids, float *__restrict__ down) {
+    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
+    const uint32_t groups = (tiles + kDownWaves - 1) / kDownWaves;
+    const uint32_t slot = blockIdx.x / groups;
+    const uint32_t tile = (blockIdx.x % groups) * kDownWaves + threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x % 64;
+    const int32_t e = expert_ids[slot];
+    const bool valid = tile < tiles && e >= 0 && uint32_t(e) < experts;
+    mxt::TileRegs regs;
+    if (valid) {
+        mxt::tile_load(codes, scales, size_t(e) * tiles + tile, lane, regs);
+    }
+    mxt::stage_x(hidden + size_t(slot) * hidden_stride, xs);
+    __syncthreads();
+    if (tile >= tiles) {
+        return;
+    }
+    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
+    if (!valid) {
+        if (lane < mx::tile_rows) {
+            down[size_t(slot) * rows + row] = __builtin_nanf("");
+        }
+        return;
+    }
+    const float acc = mxt::tile_compute(regs, xs, lane);
+    if (lane < mx::tile_rows) {
+        down[size_t(slot) * rows + row] = bias ? acc + bias[size_t(e) * rows + row] : acc;
+    }
+}
+
+// model.cpp:323-337: out = 0; out += w_r * down_r for r = 0..k-1 (unfused).
+__global__ void combine_kernel(const float *__restrict__ down, const float *__restrict__ weights, uint32_t k,
+                               uint32_t n, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < k; ++r) {
+        acc = acc + weights[r] * down[size_t(r) * n + i];
+    }
+    out[i] = acc;
+}
+
+}  // namespace
+
+// ---- per-context MoE workspace ---------------------------------------------------
+
+namespace ttl {
+
+struct MoeWorkspace {
+    RouterScratch router;
+    float logits[kMaxExperts];
+    int32_t indices[kMaxUsed];
+    float weights[kMaxUsed];
+    alignas(256) float hidden[kMaxUsed * 2880];
+    alignas(256) float down[kMaxUsed * 2880];
+};
+
+size_t moe_workspace_bytes() {
+    return sizeof(MoeWorkspace);
+}
+
+}  // namespace ttl
+
+namespace {
+
+ttl::MoeWorkspace *workspace(ttl_ctx *ctx) {
+    return reinterpret_cast<ttl::MoeWorkspace *>(ctx->moe_workspace);
+}
+
+int check_router(const float *weight, const float *bias, uint32_t experts, uint32_t hidden, const float *x,
+                 uint32_t k) {
+    TTL_REQUIRE(weight && bias && x, TTL_ERR_INVALID, "router: null argument");
+    TTL_REQUIRE(hidden == uint32_t(kRouterCols), TTL_ERR_SHAPE, "router: hidden must be %d", kRouterCols);
+    TTL_REQUIRE(experts >= 1 && experts <= kMaxExperts, TTL_ERR_SHAPE, "router: experts must be 1..%u", kMaxExperts);
+    TTL_REQUIRE(k >= 1 && k <= kMaxUsed && k <= experts, TTL_ERR_SHAPE, "router: k must be 1..%u and <= experts",
+                kMaxUsed);
+    TTL_REQUIRE(((uintptr_t)weight & 15) == 0 && ((uintptr_t)x & 15) == 0, TTL_ERR_INVALID,
+                "router: weight and x must be 16-byte aligned");
+    return TTL_OK;
+}
+
+int check_layer(const ttl_moe_layer *layer, const char *who) {
+    TTL_REQUIRE(layer, TTL_ERR_INVALID, "%s: null layer", who);
+    const ttl_moe_layer &L = *layer;
+    TTL_REQUIRE(L.gate && L.up && L.down, TTL_ERR_INVALID, "%s: null expert tensor", who);
+    TTL_REQUIRE(L.hidden == uint32_t(mx::cols) && L.expert_hidden == uint32_t(mx::cols), TTL_ERR_SHAPE,
+                "%s: hidden and expert_hidden must be %d", who, mx::cols);
+    TTL_REQUIRE(L.gate->rows == L.expert_hidden && L.up->rows == L.expert_hidden && L.down->rows == L.hidden,
+                TTL_ERR_SHAPE, "%s: expert tensor rows do not match the layer", who);
+    TTL_REQUIRE(L.gate->experts == L.experts && L.up->experts == L.experts && L.down->experts == L.experts,
+                TTL_ERR_SHAPE, "%s: expert tensors must hold %u experts", who, L.experts);
+    TTL_REQUIRE(L.used >= 1 && L.used <= kMaxUsed && L.used <= L.experts, TTL_ERR_SHAPE,
+                "%s: used must be 1..%u", who, kMaxUsed);
+    return TTL_OK;
+}
+
+int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden,
+                  int32_t *indices_out, float *weights_out) {
+    GateUpArgs a;
+    a.gate_codes = L.gate->codes;
+    a.gate_scales = L.gate->scales;
+    a.gate_bias = L.gate_bias;
+    a.up_codes = L.up->codes;
+    a.up_scales = L.up->scales;
+    a.up_bias = L.up_bias;
+    a.rows = L.expert_hidden;
+    a.tiles = L.expert_hidden / mx::tile_rows;
+    a.experts = L.experts;
+    a.k = L.used;
+    a.x = x;
+    a.expert_ids = expert_ids;
+    a.router_weight = L.router_weight;
+    a.router_bias = L.router_bias;
+    a.scratch = &workspace(ctx)->router;
+    a.hidden = hidden;
+    a.indices_out = indices_out;
+    a.weights_out = weights_out;
+    a.logits_out = workspace(ctx)->logits;
+    const uint32_t pairs = (a.tiles + 1) / 2;
+    gateup_swiglu_kernel<<<pairs * L.used, kGateUpWaves * 64, 0, ctx->stream>>>(a);
+    TTL_LAUNCHED("gateup_swiglu_kernel");
+    return TTL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ttl_router_topk(ttl_ctx *ctx, const float *weight_dev, const float *bias_dev, uint32_t experts, uint32_t hidden,
+                    const float *x_dev, uint32_t k, uint32_t flags, float *logits_dev, int32_t *indices_dev,
+                    float *weights_dev) {
+    TTL_REQUIRE(ctx && logits_dev && indices_dev && weights_dev, TTL_ERR_INVALID, "ttl_router_topk: null argument");
+    int rc = check_router(weight_dev, bias_dev, experts, hidden, x_dev, k);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    RouterScratch *scratch = &workspace(ctx)->router;
+    router_rows_kernel<<<experts, kRouterThreads, 0, ctx->stream>>>(weight_dev, bias_dev, x_dev, scratch);
+    TTL_LAUNCHED("router_rows_kernel");
+    router_select_kernel<<<1, 256, 0, ctx->stream>>>(weight_dev, bias_dev, experts, x_dev, k, flags & 1u, scratch,
+                                                     logits_dev, indices_dev, weights_dev);
+    TTL_LAUNCHED("router_select_kernel");
+    return TTL_OK;
+}
+
+int ttl_router_exact_count(ttl_ctx *ctx, uint64_t *count) {
+    TTL_REQUIRE(ctx && count, TTL_ERR_INVALID, "ttl_router_exact_count: null argument");
+    uint32_t value = 0;
+    TTL_HIP(hipMemcpyAsync(&value, &workspace(ctx)->router.exact_path_count, sizeof(value), hipMemcpyDeviceToHost,
+                           ctx->stream));
+    TTL_HIP(hipStreamSynchronize(ctx->stream));
+    *count = value;
+    return TTL_OK;
+}
+
+int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
+                          const int32_t *indices_dev, float *hidden_dev) {
+    TTL_REQUIRE(ctx && x_dev && indices_dev && hidden_dev, TTL_ERR_INVALID, "ttl_moe_gateup_swiglu: null argument");
+    int rc = check_layer(layer, "ttl_moe_gateup_swiglu");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    return launch_gateup(ctx, *layer, x_dev, indices_dev, hidden_dev, nullptr, nullptr);
+}
+
+int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
+                 float *down_dev) {
+    TTL_REQUIRE(ctx && hidden_dev && indices_dev && down_dev, TTL_ERR_INVALID, "ttl_moe_down: null argument");
+    int rc = check_layer(layer, "ttl_moe_down");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const ttl_moe_layer &L = *layer;
+    const uint32_t down_tiles = L.hidden / mx::tile_rows;
+    const uint32_t groups = (down_tiles + kDownWaves - 1) / kDownWaves;
+    down_kernel<<<groups * L.used, kDownWaves * 64, 0, ctx->stream>>>(L.down->codes, L.down->scales, L.down_bias,
+                                                                       L.hidden, down_tiles, L.experts, hidden_dev,
+                                                                       L.expert_hidden, indices_dev, down_dev);
+    TTL_LAUNCHED("down_kernel");
+    return TTL_OK;
+}
+
+int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
+                    float *out_dev) {
+    TTL_REQUIRE(ctx && down_dev && weights_dev && out_dev, TTL_ERR_INVALID, "ttl_moe_combine: null argument");
+    TTL_REQUIRE(k >= 1 && k <= kMaxUsed && n > 0, TTL_ERR_SHAPE, "ttl_moe_combine: bad k or n");
+    combine_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>(down_dev, weights_dev, k, n, out_dev);
+    TTL_LAUNCHED("combine_kernel");
+    return TTL_OK;
+}
+
+int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *out_dev,
+                   int32_t *indices_dev, float *weights_dev) {
+    TTL_REQUIRE(ctx && x_dev && out_dev, TTL_ERR_INVALID, "ttl_moe_decode: null argument");
+    int rc = check_layer(layer, "ttl_moe_decode");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const ttl_moe_layer &L = *layer;
+    rc = check_router(L.router_weight, L.router_bias, L.experts, L.hidden, x_dev, L.used);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    ttl::MoeWorkspace *ws = workspace(ctx);
+    int32_t *indices = indices_dev ? indices_dev : ws->indices;
+    float *weights = weights_dev ? weights_dev : ws->weights;
+    router_rows_kernel<<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias, x_dev,
+                                                                      &ws->router);
+    TTL_LAUNCHED("router_rows_kernel");
+    rc = launch_gateup(ctx, L, x_dev, nullptr, ws->hidden, indices, weights);
+    if (rc == TTL_OK) {
+        rc = ttl_moe_down(ctx, layer, ws->hidden, indices, ws->down);
+    }
+    if (rc == TTL_OK) {
+        rc = ttl_moe_combine(ctx, ws->down, weights, L.used, L.hidden, out_dev);
+    }
+    return rc;
+}
+
+}  // extern "C"

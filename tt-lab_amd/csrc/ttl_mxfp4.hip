@@ -1,21 +1,6 @@
 // MXFP4 tensors (GGUF block layout in, repacked planes on the device) and the
-// expert-indexed MXFP4 matvec.
-//
-// Matvec design (gfx950, wave64):
-//  - One wave owns a tile of 16 rows of one expert.  Lane l works on row l%16
-//    and on the blocks kb = 4*i + l/16, i = 0..22, so each 64-lane load of
-//    16 bytes reads 1 KiB of contiguous codes (blocks 4i..4i+3 of the tile).
-//  - All 23 code chunks and the lane's 24 scale bytes are requested before any
-//    arithmetic, so a wave keeps ~23 KiB in flight from HBM.
-//  - The activation vector is staged once per workgroup in LDS with a padded
-//    stride (36 floats per block) so the four distinct addresses of a
-//    ds_read_b128 fall in different banks.
-//  - Decode happens in registers: v_cvt_scalef32_pk_f32_fp4 turns one byte into
-//    the two E2M1 values it holds (low nibble -> element j, high -> j+16), the
-//    32 products of a block are accumulated in f32 and the block's E8M0 scale is
-//    applied once to that partial as an exact power of two (v_ldexp_f32).
-//  - The four lanes of a row are combined with two cross-lane exchanges.
-#include "ttl_internal.hpp"
+// expert-indexed MXFP4 matvec.  The per-tile inner loop is in ttl_mxfp4_tile.hpp.
+#include "ttl_mxfp4_tile.hpp"
 
 #include <cmath>
 #include <vector>
@@ -26,9 +11,7 @@ int synth_mxfp4_repacked(ttl_ctx *ctx, ttl_mxfp4 *t, uint64_t seed, uint64_t str
 
 namespace {
 
-constexpr int kWaves = 4;               // tiles (waves) per workgroup
-constexpr int kXStride = 36;            // padded LDS floats per 32-value block
-constexpr int kXBlocks = mx::iters * mx::lanes_k;  // 92: blocks 90 and 91 are zero padding
+constexpr int kWaves = 4;  // tiles (waves) per workgroup
 
 // ---- layout conversion ------------------------------------------------------
 
@@ -91,13 +74,6 @@ __device__ inline float mxfp4_scale(uint32_t e) {
     return __uint_as_float(bits);
 }
 
-template <int Sel>
-__device__ inline float2 cvt_fp4x2(uint32_t word) {
-    // Two E2M1 values of byte Sel of `word`: .x from the low nibble, .y from the high.
-    const auto v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, Sel);
-    return make_float2(v[0], v[1]);
-}
-
 __global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows,
                                uint32_t expert, int mode, float *__restrict__ out) {
     const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -122,10 +98,10 @@ __global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *_
     } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float2 v0 = cvt_fp4x2<0>(w[q]);
-            const float2 v1 = cvt_fp4x2<1>(w[q]);
-            const float2 v2 = cvt_fp4x2<2>(w[q]);
-            const float2 v3 = cvt_fp4x2<3>(w[q]);
+            const float2 v0 = mxt::cvt_fp4x2<0>(w[q]);
+            const float2 v1 = mxt::cvt_fp4x2<1>(w[q]);
+            const float2 v2 = mxt::cvt_fp4x2<2>(w[q]);
+            const float2 v3 = mxt::cvt_fp4x2<3>(w[q]);
             const int k = int(e) - 127;
             dst[4 * q + 0] = __builtin_amdgcn_ldexpf(v0.x, k);
             dst[4 * q + 16] = __builtin_amdgcn_ldexpf(v0.y, k);
@@ -141,90 +117,37 @@ __global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *_
 
 // ---- matvec ------------------------------------------------------------------
 
-// Sum over one 32-value block: codes (16 bytes) against x[0..31] of the block.
-__device__ inline float block_dot(const uint4 c, const float *__restrict__ xb) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float4 xl = *reinterpret_cast<const float4 *>(xb + 4 * q);
-        const float4 xh = *reinterpret_cast<const float4 *>(xb + 16 + 4 * q);
-        const float2 v0 = cvt_fp4x2<0>(w[q]);
-        const float2 v1 = cvt_fp4x2<1>(w[q]);
-        const float2 v2 = cvt_fp4x2<2>(w[q]);
-        const float2 v3 = cvt_fp4x2<3>(w[q]);
-        lo = fmaf(v0.x, xl.x, lo);
-        hi = fmaf(v0.y, xh.x, hi);
-        lo = fmaf(v1.x, xl.y, lo);
-        hi = fmaf(v1.y, xh.y, hi);
-        lo = fmaf(v2.x, xl.z, lo);
-        hi = fmaf(v2.y, xh.z, hi);
-        lo = fmaf(v3.x, xl.w, lo);
-        hi = fmaf(v3.y, xh.w, hi);
-    }
-    return lo + hi;
-}
-
-// Stages x (2880 floats) into the padded LDS layout; blocks 90 and 91 are zero.
-__device__ inline void stage_x(const float *__restrict__ x, float *xs) {
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    for (int i = threadIdx.x; i < kXBlocks * 8; i += blockDim.x) {
-        const int block = i / 8, part = i % 8;
-        const float4 v = block < mx::blocks ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4 *>(xs + block * kXStride + part * 4) = v;
-    }
-}
-
 // One wave = one 16-row tile of the expert selected for slot blockIdx.x / groups.
 __global__ __launch_bounds__(kWaves * 64) void matvec_kernel(
-    const uint4 *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows, uint32_t tiles,
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows, uint32_t tiles,
     uint32_t experts, const float *__restrict__ bias, const float *__restrict__ x, uint32_t x_stride,
     const int32_t *__restrict__ expert_ids, float *__restrict__ y) {
-    __shared__ __attribute__((aligned(16))) float xs[kXBlocks * kXStride];
+    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     const uint32_t groups = (tiles + kWaves - 1) / kWaves;
     const uint32_t slot = blockIdx.x / groups;
     const uint32_t tile = (blockIdx.x % groups) * kWaves + threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
-    const uint32_t r = lane % mx::tile_rows;
-    const uint32_t kl = lane / mx::tile_rows;
 
-    stage_x(x + size_t(slot) * x_stride, xs);
+    const int32_t e = expert_ids[slot];
+    const bool valid = tile < tiles && e >= 0 && uint32_t(e) < experts;
+    mxt::TileRegs regs;
+    if (valid) {
+        mxt::tile_load(codes, scales, size_t(e) * tiles + tile, lane, regs);
+    }
+    mxt::stage_x(x + size_t(slot) * x_stride, xs);
     __syncthreads();
     if (tile >= tiles) {
         return;
     }
-    const uint32_t row = tile * mx::tile_rows + r;
-    const int32_t e = expert_ids[slot];
-    if (e < 0 || uint32_t(e) >= experts) {
-        if (kl == 0) {
+    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
+    if (!valid) {
+        if (lane < mx::tile_rows) {
             y[size_t(slot) * rows + row] = __builtin_nanf("");
         }
         return;
     }
-    const size_t tile_index = size_t(e) * tiles + tile;
-    const uint4 *tc = codes + tile_index * mx::blocks * mx::tile_rows + r;
-    const uint2 *ts = reinterpret_cast<const uint2 *>(scales + tile_index * mx::tile_scale_bytes +
-                                                      size_t(lane) * mx::scale_pad);
-    const uint2 s01 = ts[0], s23 = ts[1], s45 = ts[2];
-    const uint32_t sw[6] = {s01.x, s01.y, s23.x, s23.y, s45.x, s45.y};
-
-    uint4 q[mx::iters];
-#pragma unroll
-    for (int i = 0; i < mx::iters; ++i) {
-        const uint32_t kb = 4 * i + kl;
-        q[i] = (i < mx::iters - 1 || kb < mx::blocks) ? tc[size_t(kb) * mx::tile_rows] : make_uint4(0, 0, 0, 0);
-    }
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < mx::iters; ++i) {
-        const uint32_t kb = 4 * i + kl;
-        const int e8 = int((sw[i / 4] >> (8 * (i % 4))) & 0xffu);
-        const float partial = block_dot(q[i], xs + kb * kXStride);
-        acc += __builtin_amdgcn_ldexpf(partial, e8 - 127);
-    }
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if (kl == 0) {
+    const float acc = mxt::tile_compute(regs, xs, lane);
+    if (lane < mx::tile_rows) {
         y[size_t(slot) * rows + row] = bias ? acc + bias[size_t(e) * rows + row] : acc;
     }
 }
@@ -393,7 +316,7 @@ int ttl_matvec_mxfp4_experts(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias
     const uint32_t groups = (w->tiles + kWaves - 1) / kWaves;
     const size_t grid = size_t(groups) * n;
     TTL_REQUIRE(grid < (1u << 31), TTL_ERR_SHAPE, "ttl_matvec_mxfp4_experts: too many slots");
-    matvec_kernel<<<unsigned(grid), kWaves * 64, 0, ctx->stream>>>((const uint4 *)w->codes, w->scales, w->rows,
+    matvec_kernel<<<unsigned(grid), kWaves * 64, 0, ctx->stream>>>(w->codes, w->scales, w->rows,
                                                                    w->tiles, w->experts, bias_dev, x_dev, x_stride,
                                                                    experts_dev, y_dev);
     TTL_LAUNCHED("matvec_kernel");

@@ -64,31 +64,47 @@ __device__ inline void stage_x(const float *__restrict__ x, float *xs) {
     }
 }
 
-// Dot products of the 16 rows of one tile with x.  `lane` is the lane in the
-// wave.  The row sum for row lane%16 is returned in every lane (lanes l, l+16,
-// l+32, l+48 hold the same value).
-__device__ inline float tile_dot(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
-                                 size_t tile_index, const float *xs, uint32_t lane) {
+// Registers of one lane for one tile: its 23 code chunks and 24 scale bytes.
+struct TileRegs {
+    uint4 q[mx::iters];
+    uint32_t sw[6];
+};
+
+// Issues all of the lane's loads for one tile (they do not depend on x, so
+// callers issue them before staging x into LDS).
+__device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *__restrict__ codes,
+                                                                const uint8_t *__restrict__ scales,
+                                                                size_t tile_index, uint32_t lane, TileRegs &regs) {
     const uint32_t r = lane % mx::tile_rows;
     const uint32_t kl = lane / mx::tile_rows;
     const uint4 *tc = reinterpret_cast<const uint4 *>(codes) + tile_index * mx::blocks * mx::tile_rows + r;
     const uint2 *ts = reinterpret_cast<const uint2 *>(scales + tile_index * mx::tile_scale_bytes +
                                                       size_t(lane) * mx::scale_pad);
     const uint2 s01 = ts[0], s23 = ts[1], s45 = ts[2];
-    const uint32_t sw[6] = {s01.x, s01.y, s23.x, s23.y, s45.x, s45.y};
-
-    uint4 q[mx::iters];
+    regs.sw[0] = s01.x;
+    regs.sw[1] = s01.y;
+    regs.sw[2] = s23.x;
+    regs.sw[3] = s23.y;
+    regs.sw[4] = s45.x;
+    regs.sw[5] = s45.y;
 #pragma unroll
     for (int i = 0; i < mx::iters; ++i) {
         const uint32_t kb = 4 * i + kl;
-        q[i] = (i < mx::iters - 1 || kb < mx::blocks) ? tc[size_t(kb) * mx::tile_rows] : make_uint4(0, 0, 0, 0);
+        regs.q[i] = (i < mx::iters - 1 || kb < mx::blocks) ? tc[size_t(kb) * mx::tile_rows] : make_uint4(0, 0, 0, 0);
     }
+}
+
+// Dot products of the tile's 16 rows with x (in LDS).  The row sum for row
+// lane%16 is returned in every lane (lanes l, l+16, l+32, l+48 agree).
+__device__ __attribute__((always_inline)) inline float tile_compute(const TileRegs &regs, const float *xs,
+                                                                   uint32_t lane) {
+    const uint32_t kl = lane / mx::tile_rows;
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < mx::iters; ++i) {
         const uint32_t kb = 4 * i + kl;
-        const int e8 = int((sw[i / 4] >> (8 * (i % 4))) & 0xffu);
-        acc += __builtin_amdgcn_ldexpf(block_dot(q[i], xs + kb * x_stride), e8 - 127);
+        const int e8 = int((regs.sw[i / 4] >> (8 * (i % 4))) & 0xffu);
+        acc += __builtin_amdgcn_ldexpf(block_dot(regs.q[i], xs + kb * x_stride), e8 - 127);
     }
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);

@@ -24,15 +24,16 @@ __device__ inline uint16_t f32_to_bf16_rne(float value) {
 
 __global__ void normal_kernel(uint64_t seed, uint64_t stream, size_t offset, size_t n, float mean, float sigma,
                               int bf16, float *out) {
+#pragma clang fp contract(off)
     const size_t k = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (k >= n) {
         return;
     }
-    const float z = __fmul_rn(unit_normal(seed, stream, offset + k), sigma);
+    const float z = unit_normal(seed, stream, offset + k) * sigma;
     if (bf16) {
         out[k] = __uint_as_float(uint32_t(f32_to_bf16_rne(z)) << 16);
     } else {
-        out[k] = __fadd_rn(mean, z);
+        out[k] = mean + z;
     }
 }
 

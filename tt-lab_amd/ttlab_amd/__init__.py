@@ -78,6 +78,16 @@ def load_library():
         "ttl_mxfp4_dequantize": (i32, [vp, vp, u32, i32, vp]),
         "ttl_matvec_mxfp4": (i32, [vp, vp, vp, vp, vp, u32]),
         "ttl_matvec_mxfp4_experts": (i32, [vp, vp, vp, vp, u32, vp, u32, vp]),
+        "ttl_router_topk": (i32, [vp, vp, vp, u32, u32, vp, u32, u32, vp, vp, vp]),
+        "ttl_router_exact_count": (i32, [vp, C.POINTER(u64)]),
+        "ttl_moe_decode": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp, vp]),
+        "ttl_moe_gateup_swiglu": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp]),
+        "ttl_moe_down": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp]),
+        "ttl_moe_combine": (i32, [vp, vp, vp, u32, u32, vp]),
+        "ttl_capture_begin": (i32, [vp]),
+        "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
+        "ttl_graph_launch": (i32, [vp, vp]),
+        "ttl_graph_free": (None, [vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name, None)
@@ -175,6 +185,21 @@ class Mxfp4:
             self.handle = None
 
 
+class Graph:
+    """Instantiated HIP graph (ttl_graph)."""
+
+    def __init__(self, dev, handle):
+        self.dev, self.handle = dev, handle
+
+    def launch(self):
+        _check(self.dev.lib.ttl_graph_launch(self.dev.ctx, self.handle), "ttl_graph_launch")
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.ttl_graph_free(self.handle)
+            self.handle = None
+
+
 class Device:
     """One ttl_ctx: a gfx950 device and its stream."""
 
@@ -246,6 +271,42 @@ class Device:
     def matvec_mxfp4(self, w, bias, x, y, expert):
         _check(self.lib.ttl_matvec_mxfp4(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, y.ptr, expert),
                "ttl_matvec_mxfp4")
+
+    def router_topk(self, weight, bias, experts, x, k, logits, indices, weights, force_exact=False):
+        _check(self.lib.ttl_router_topk(self.ctx, weight.ptr, bias.ptr, experts, 2880, x.ptr, k,
+                                        1 if force_exact else 0, logits.ptr, indices.ptr, weights.ptr),
+               "ttl_router_topk")
+
+    def router_exact_count(self):
+        c = C.c_uint64()
+        _check(self.lib.ttl_router_exact_count(self.ctx, C.byref(c)), "ttl_router_exact_count")
+        return c.value
+
+    def moe_decode(self, layer, x, out, indices=None, weights=None):
+        _check(self.lib.ttl_moe_decode(self.ctx, C.byref(layer), x.ptr, out.ptr, indices.ptr if indices else None,
+                                       weights.ptr if weights else None), "ttl_moe_decode")
+
+    def moe_gateup_swiglu(self, layer, x, indices, hidden):
+        _check(self.lib.ttl_moe_gateup_swiglu(self.ctx, C.byref(layer), x.ptr, indices.ptr, hidden.ptr),
+               "ttl_moe_gateup_swiglu")
+
+    def moe_down(self, layer, hidden, indices, down):
+        _check(self.lib.ttl_moe_down(self.ctx, C.byref(layer), hidden.ptr, indices.ptr, down.ptr), "ttl_moe_down")
+
+    def moe_combine(self, down, weights, k, n, out):
+        _check(self.lib.ttl_moe_combine(self.ctx, down.ptr, weights.ptr, k, n, out.ptr), "ttl_moe_combine")
+
+    # ---- graphs ----
+    def capture(self, fn):
+        """Records the launches fn() makes into a replayable graph."""
+        _check(self.lib.ttl_capture_begin(self.ctx), "ttl_capture_begin")
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = self.lib.ttl_capture_end(self.ctx, C.byref(g))
+        _check(rc, "ttl_capture_end")
+        return Graph(self, g.value)
 
     def matvec_mxfp4_experts(self, w, bias, x, x_stride, experts, n, y):
         _check(self.lib.ttl_matvec_mxfp4_experts(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
