@@ -75,6 +75,8 @@ int ttl_synth_normal(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t offset
                      float sigma, float *out_dev);
 int ttl_synth_normal_bf16(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t offset, size_t n, float sigma,
                           float *out_dev);
+/* BF16 bit patterns (random sign and mantissa, exponent 120..123). */
+int ttl_synth_bf16(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t offset, size_t n, uint16_t *out_dev);
 /* GGUF-layout MXFP4 blocks (17 B each), E8M0 uniform in [emin, emax]. */
 int ttl_synth_mxfp4_gguf(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t block_offset, size_t n,
                          uint32_t emin, uint32_t emax, uint8_t *out_dev);
@@ -156,6 +158,11 @@ typedef struct {
     const float *up_bias;        /* ffn_up_exps.bias (may be NULL)                */
     const ttl_mxfp4 *down;       /* ffn_down_exps.weight: experts x hidden x expert_hidden */
     const float *down_bias;      /* ffn_down_exps.bias, f32 [experts][hidden] (may be NULL) */
+    /* If non-NULL, x is the residual stream and the layer input is
+     * rms_norm(x, input_norm, input_norm_epsilon) (post_attention_norm, model.cpp:590),
+     * computed inside the router and gate/up kernels. */
+    const float *input_norm;
+    float input_norm_epsilon;
 } ttl_moe_layer;
 
 /* out = MoE(x) for one token: router + top-k + softmax, then for the k selected
@@ -173,10 +180,101 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
  * combine: out = sum_r weights[r] * down_r, unfused, r = 0..k-1 (model.cpp:323,334-336). */
 int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
                           const int32_t *indices_dev, float *hidden_dev);
+/* Router + top-k + gate/up + SwiGLU in two launches (the routing is derived inside the
+ * gate/up kernel); writes hidden f32 [used][expert_hidden], indices int32 [used] and
+ * weights f32 [used] (model.cpp:293-332). */
+int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                         int32_t *indices_dev, float *weights_dev);
 int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
                  float *down_dev);
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
                     float *out_dev);
+
+/* ---- matvec inputs ----------------------------------------------------------------- *
+ * The vector a matvec reads, with the elementwise steps GptOssModel::forward runs
+ * before it fused in (each workgroup recomputes them; nothing is launched for them):
+ *   v  = base + sum_r add_weights[r] * add[r]   (the MoE combine and residual add,
+ *                                                model.cpp:323-337 and 592-594; add may be NULL)
+ *   in = rms_norm(v, norm_weight, epsilon)      (tensor.cpp:568-580; norm_weight may be NULL)
+ * sum_out, if non-NULL, receives v (the next residual stream value).  All pointers
+ * are device pointers, 16-byte aligned. */
+typedef struct {
+    const float *base;
+    const float *add;            /* f32 [add_count][n] or NULL */
+    const float *add_weights;    /* f32 [add_count]            */
+    uint32_t add_count;
+    const float *norm_weight;    /* f32 [n] or NULL            */
+    float epsilon;
+    float *sum_out;              /* f32 [n] or NULL            */
+} ttl_stage_input;
+
+/* ---- Q8_0 tensors and the attention-side matvecs ----------------------------------- *
+ * A ttl_q8 holds rows x cols Q8_0 values (GGUF type 8: per 32 values an fp16 scale
+ * and 32 int8, tensor.cpp:94-114, 136-157), repacked on upload into 16-row tiles.
+ * row_source (host, may be NULL) maps each repacked row to the GGUF row that fills
+ * it, so several GGUF tensors can be stacked and reordered into one.  cols must be
+ * 2880 or 4096, rows a multiple of 16. */
+typedef struct ttl_q8 ttl_q8;
+int ttl_q8_upload(ttl_ctx *ctx, const void *gguf_blocks, uint32_t rows, uint32_t cols, const int32_t *row_source,
+                  uint32_t source_rows, ttl_q8 **out);
+int ttl_q8_upload_dev(ttl_ctx *ctx, const void *gguf_blocks_dev, uint32_t rows, uint32_t cols,
+                      const int32_t *row_source, ttl_q8 **out);
+/* GGUF bytes of the repacked rows, in repacked row order. */
+int ttl_q8_download(ttl_ctx *ctx, const ttl_q8 *tensor, void *gguf_blocks);
+void ttl_q8_free(ttl_ctx *ctx, ttl_q8 *tensor);
+size_t ttl_q8_bytes(const ttl_q8 *tensor);
+/* GGUF Q8_0 blocks from the synthetic generator (oracle orc_synth_q8_0). */
+int ttl_synth_q8_0_gguf(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t block_offset, size_t n,
+                        uint8_t *out_dev);
+
+/* y = W in (+ bias) (+ residual).  Replaces matvec_q8_0 / matvec_add_q8_0
+ * (tensor.h:26-27, tensor.cpp:202-237); with residual_dev it is the output
+ * projection plus residual add of model.cpp:584-588. */
+int ttl_matvec_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const ttl_stage_input *in,
+                    const float *residual_dev, float *y_dev);
+
+/* The row order ttl_attn_qkv expects of its 5120-row tensor: rows of attn_q (0..4095),
+ * attn_k (4096..4607) and attn_v (4608..5119) stacked, reordered so each RoPE pair
+ * (d, d+32) of a head shares a tile.  Fills row_source[5120]. */
+int ttl_qkv_row_source(int32_t *row_source);
+
+/* Q/K/V projection of one decode token (model.cpp:572-582): in is normally the
+ * residual stream with the attention norm; bias_dev is f32 [5120] = q|k|v biases in
+ * GGUF order; rope_dev is f32 [capacity][32][2] = (cos, sin) * (1 + 0.1 ln 32) per
+ * position and pair, computed on the host exactly as apply_rope does (model.cpp:230-245);
+ * position_dev is int32 [1].  Writes q (after RoPE) to q_dev f32 [4096] and k (after
+ * RoPE), v to the caches f32 [capacity][8][64] at the position. */
+int ttl_attn_qkv(ttl_ctx *ctx, const ttl_q8 *qkv, const float *bias_dev, const ttl_stage_input *in,
+                 const float *rope_dev, const int32_t *position_dev, uint32_t capacity, float *q_dev,
+                 float *k_cache_dev, float *v_cache_dev);
+
+/* ---- attention with sinks --------------------------------------------------------- */
+
+size_t ttl_attention_workspace_bytes(uint32_t capacity);
+/* attention_from_cache (model.cpp:255-290) for the position in position_dev: even
+ * layer_index uses the last 128 positions, odd all; sinks_dev f32 [64]; out_dev
+ * f32 [4096].  workspace_dev holds ttl_attention_workspace_bytes(capacity). */
+int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev, const float *v_cache_dev,
+                         const float *sinks_dev, const int32_t *position_dev, uint32_t capacity, uint32_t layer_index,
+                         float *workspace_dev, float *out_dev);
+
+/* ---- embedding, unembedding, greedy ------------------------------------------------ */
+
+/* load_token_embedding_q8_0 (tensor.cpp:171-184) for the token in token_dev; table_dev
+ * holds the GGUF Q8_0 token_embd rows (vocab x 2880).  An out-of-range token gives NaNs. */
+int ttl_embedding_q8_0(ttl_ctx *ctx, const void *table_dev, uint32_t vocab, const int32_t *token_dev,
+                       float *out_dev);
+size_t ttl_logits_workspace_bytes(uint32_t vocab);
+/* logits = W in for a bf16 unembedding W [vocab][2880] (the synthetic configurations'
+ * output.weight; the reference's is Q8_0, model.cpp:598-599), and per-group argmax
+ * partials in workspace_dev for ttl_argmax. */
+int ttl_logits_bf16(ttl_ctx *ctx, const uint16_t *weight_dev, uint32_t vocab, const ttl_stage_input *in,
+                    float *logits_dev, void *workspace_dev);
+/* greedy (model.cpp:604-612) from ttl_logits_bf16's partials: writes the token to
+ * token_dev and, if position_dev is non-NULL, also history_dev[position] (when
+ * history_dev is non-NULL and position < history_len) and increments the position. */
+int ttl_argmax(ttl_ctx *ctx, uint32_t vocab, const void *workspace_dev, int32_t *token_dev, int32_t *position_dev,
+               int32_t *history_dev, uint32_t history_len);
 
 /* ---- HIP graphs ------------------------------------------------------------------- *
  * Calls made on the context between ttl_capture_begin and ttl_capture_end are

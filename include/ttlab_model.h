@@ -1,0 +1,61 @@
+/*
+ * ttlab_model.h -- C API of the C++ gpt-oss decode model that runs on the gfx950
+ * backend (tt-lab_amd/host/gpt_oss_hip.{hpp,cpp}, class ttlab::HipGptOssModel).
+ *
+ * The model mirrors the reference's GptOssModel (model.h:15-31): construction
+ * allocates everything, forward(token, position) advances one token and returns
+ * logits, greedy() picks the first maximum.  Weights here are synthetic (the
+ * BASELINE configurations 3 and 4), generated on the device from the stream
+ * layout of ttlab::synth_stream().  Every call returns 0 or a negative code;
+ * ttlm_last_error() has the message.
+ */
+#ifndef TTLAB_MODEL_H
+#define TTLAB_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ttlm_model ttlm_model;
+
+/* layers >= 1, experts 32 or 128, vocab >= 1, capacity = KV positions (token capacity). */
+int ttlm_create_synthetic(int device, uint32_t layers, uint32_t experts, uint32_t vocab, uint32_t capacity,
+                          uint64_t seed, ttlm_model **out);
+void ttlm_destroy(ttlm_model *model);
+const char *ttlm_last_error(void);
+
+/* GptOssModel::forward (model.cpp:557-602): logits (host, f32 [vocab]) may be NULL. */
+int ttlm_forward(ttlm_model *model, int32_t token, uint32_t position, float *logits);
+/* GptOssModel::prefill (model.cpp:463-555) as consecutive decode steps: logits of the last token. */
+int ttlm_prefill(ttlm_model *model, const int32_t *tokens, uint32_t count, float *logits);
+/* Greedy decode on the device: feeds token at position, then each step's argmax,
+ * for `steps` steps; tokens (host, int32 [steps]) receives the chosen tokens. */
+int ttlm_generate(ttlm_model *model, int32_t token, uint32_t position, uint32_t steps, int32_t *tokens);
+/* Times `steps` device-resident decode steps (after `warmup` untimed ones) with HIP
+ * events around the graph replays; positions start at `position`. */
+int ttlm_time_decode(ttlm_model *model, int32_t token, uint32_t position, uint32_t warmup, uint32_t steps,
+                     double *ms_per_step);
+
+/* State of the last step, for layer-by-layer checks (host outputs, each may be NULL):
+ * x_in f32 [2880] = input of `layer` (the embedding for layer 0), residual f32 [2880]
+ * after attention, indices int32 [4] / weights f32 [4] its routing. */
+int ttlm_layer_state(ttlm_model *model, uint32_t layer, float *x_in, float *residual, int32_t *indices,
+                     float *weights);
+/* The final residual stream (input of the output norm) of the last step. */
+int ttlm_final_state(ttlm_model *model, float *x_final);
+/* Key and value caches of `layer`, positions [0, positions): f32 [positions][8][64] each. */
+int ttlm_kv_cache(ttlm_model *model, uint32_t layer, uint32_t positions, float *keys, float *values);
+/* Bytes of device memory the model holds. */
+size_t ttlm_device_bytes(const ttlm_model *model);
+/* Algorithmic bytes one decode step reads and writes at this position (weights actually
+ * touched: 4 experts per layer, the attention span per layer, embedding row, unembedding). */
+double ttlm_step_bytes(const ttlm_model *model, uint32_t position);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -8,9 +8,10 @@
  */
 #include "ttlab_oracle.h"
 
-#include <math.h>
-#include <string.h>
 #include <immintrin.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 /* ------------------------------------------------------------------------- */
 /* formats                                                                   */
@@ -456,8 +457,6 @@ void orc_moe(const orc_moe_layer *layer, const float *input, float *output, int 
     }
 }
 
-#include <stdlib.h>
-
 /* model.cpp:340-461.  Router via the F32 matmul, per-token top-k, buckets per
  * expert in token order, then per expert (ascending index): per-token matvecs
  * when at most 4 tokens chose it (model.cpp:22,404), the selected-token matmul
@@ -780,6 +779,49 @@ int32_t orc_greedy(const float *logits, size_t n) {
         }
     }
     return (int32_t)best;
+}
+
+/* ------------------------------------------------------------------------- */
+/* one transformer block                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* model.cpp:572-595 (with model.h:34-44 widths) */
+void orc_layer_forward(const orc_layer *layer, size_t layer_index, size_t position, const float *x_in,
+                       const float *rope_frequencies, float *key_cache, float *value_cache, int body, float *x_out,
+                       float *query_out, float *attended_out, float *residual_out, float *router_out,
+                       int64_t *indices_out, float *weights_out) {
+    enum { H = 2880, QW = ORC_QHEADS * ORC_HEAD, KW = ORC_KVHEADS * ORC_HEAD };
+    static float normalized[H], query[QW], key[KW], value[KW], attended[QW], projected[H], residual[H],
+        moe_out[H];
+    float *scores = malloc(sizeof(float) * (position + 1));
+    orc_rms_norm(x_in, layer->attention_norm, H, 1.0e-5f, normalized);
+    orc_matvec_add_q8_0(layer->query_weight, layer->query_bias, QW, H, normalized, query);
+    orc_matvec_add_q8_0(layer->key_weight, layer->key_bias, KW, H, normalized, key);
+    orc_matvec_add_q8_0(layer->value_weight, layer->value_bias, KW, H, normalized, value);
+    orc_apply_rope(query, ORC_QHEADS, position, rope_frequencies);
+    orc_apply_rope(key, ORC_KVHEADS, position, rope_frequencies);
+    memcpy(key_cache + position * KW, key, sizeof(key));     /* store_kv, model.cpp:247-253 */
+    memcpy(value_cache + position * KW, value, sizeof(value));
+    orc_attention(query, key_cache, value_cache, layer->sinks, layer_index, position, attended, scores);
+    orc_matvec_add_q8_0(layer->output_weight, layer->output_bias, H, QW, attended, projected);
+    for (size_t j = 0; j < H; ++j) {
+        residual[j] = x_in[j] + projected[j];
+    }
+    orc_rms_norm(residual, layer->post_attention_norm, H, 1.0e-5f, normalized);
+    orc_moe(&layer->moe, normalized, moe_out, body, router_out, indices_out, weights_out);
+    for (size_t j = 0; j < H; ++j) {
+        x_out[j] = residual[j] + moe_out[j];
+    }
+    if (query_out) {
+        memcpy(query_out, query, sizeof(query));
+    }
+    if (attended_out) {
+        memcpy(attended_out, attended, sizeof(attended));
+    }
+    if (residual_out) {
+        memcpy(residual_out, residual, sizeof(residual));
+    }
+    free(scores);
 }
 
 /* ------------------------------------------------------------------------- */

@@ -146,6 +146,32 @@ void orc_matvec_bf16(const uint16_t *weights, size_t rows, size_t cols, const fl
 /* ---- a13: greedy (model.cpp:604-612) -------------------------------------- */
 int32_t orc_greedy(const float *logits, size_t n);
 
+/* One gpt-oss transformer block's tensors (GGUF layouts; names as model.cpp:141-169). */
+typedef struct {
+    const float *attention_norm;     /* f32 [2880] */
+    const float *post_attention_norm;
+    const uint8_t *query_weight;     /* Q8_0 4096 x 2880 */
+    const float *query_bias;         /* f32 [4096] */
+    const uint8_t *key_weight;       /* Q8_0 512 x 2880 */
+    const float *key_bias;
+    const uint8_t *value_weight;     /* Q8_0 512 x 2880 */
+    const float *value_bias;
+    const uint8_t *output_weight;    /* Q8_0 2880 x 4096 */
+    const float *output_bias;        /* f32 [2880] */
+    const float *sinks;              /* f32 [64] */
+    orc_moe_layer moe;
+} orc_layer;
+
+/* The body of GptOssModel::forward's layer loop (model.cpp:571-595) for one layer
+ * at `position`: writes key/value for `position` into the caches (f32
+ * [capacity][8][64]), reads positions before it, and writes the layer output
+ * x_out[2880].  Optional outputs (each may be NULL): query[4096] after RoPE,
+ * attended[4096], residual[2880], router[experts], indices[used], weights[used]. */
+void orc_layer_forward(const orc_layer *layer, size_t layer_index, size_t position, const float *x_in,
+                       const float *rope_frequencies, float *key_cache, float *value_cache, int body, float *x_out,
+                       float *query, float *attended, float *residual, float *router, int64_t *indices,
+                       float *weights);
+
 /* ---- synthetic inputs (shared specification with tt-lab_amd/csrc/synth.hip) */
 uint64_t orc_hash(uint64_t seed, uint64_t stream, uint64_t index);
 /* N(0,1) drawn as an Irwin-Hall sum of 12 24-bit uniforms in exact integer arithmetic,

@@ -40,6 +40,23 @@ class MoeLayer(C.Structure):
     ]
 
 
+class OrcLayer(C.Structure):
+    _fields_ = [
+        ("attention_norm", C.c_void_p),
+        ("post_attention_norm", C.c_void_p),
+        ("query_weight", C.c_void_p),
+        ("query_bias", C.c_void_p),
+        ("key_weight", C.c_void_p),
+        ("key_bias", C.c_void_p),
+        ("value_weight", C.c_void_p),
+        ("value_bias", C.c_void_p),
+        ("output_weight", C.c_void_p),
+        ("output_bias", C.c_void_p),
+        ("sinks", C.c_void_p),
+        ("moe", MoeLayer),
+    ]
+
+
 def _load():
     if not os.path.exists(ORACLE_SO):
         subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
@@ -73,6 +90,8 @@ def _load():
         "orc_matmul_add_q8_0": (None, [_u8p, _f32p, _sz, _sz, _f32p, _sz, _f32p, _f32p, _f32p]),
         "orc_matvec_bf16": (None, [_u16p, _sz, _sz, _f32p, _f32p]),
         "orc_greedy": (C.c_int32, [_f32p, _sz]),
+        "orc_layer_forward": (None, [C.POINTER(OrcLayer), _sz, _sz, _f32p, _f32p, _f32p, _f32p, C.c_int, _f32p,
+                                     _f32p, _f32p, _f32p, _f32p, _i64p, _f32p]),
         "orc_hash": (C.c_uint64, [_u64, _u64, _u64]),
         "orc_synth_normal": (None, [_u64, _u64, _sz, _sz, C.c_float, C.c_float, _f32p]),
         "orc_synth_normal_bf16": (None, [_u64, _u64, _sz, _sz, C.c_float, _f32p]),

@@ -1,0 +1,254 @@
+"""GPU parity of the non-expert decode kernels against the CPU oracle:
+Q8_0 matvec (with the fused combine / RMSNorm staging), the fused Q/K/V projection
+with RoPE and the KV-cache store, attention with sinks, the bf16 unembedding,
+greedy argmax and the embedding lookup.  Tolerance: relative L2 <= 1e-5; argmax,
+layout round trips and the staging's combine are bit-exact."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import ttlab_amd
+
+pytestmark = pytest.mark.gpu
+N = 2880
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = ttlab_amd.Device(0)
+    yield d
+    d.close()
+
+
+def q8_dense(blocks, rows, cols):
+    b = blocks.reshape(rows, cols // 32, 34)
+    d = b[:, :, :2].copy().view(np.uint16)[..., 0].view(np.float16).astype(np.float64)
+    return (b[:, :, 2:].view(np.int8).astype(np.float64) * d[:, :, None]).reshape(rows, cols)
+
+
+def test_q8_round_trip_with_row_permutation(dev):
+    rows, cols = 64, 4096
+    blocks = O.synth_q8_0(9, 1, rows * cols // 32)
+    perm = np.random.default_rng(0).permutation(rows).astype(np.int32)
+    t = dev.q8_upload(blocks, rows, cols, perm)
+    got = t.download_gguf().reshape(rows, -1)
+    assert np.array_equal(got, blocks.reshape(rows, -1)[perm])
+    t.free()
+
+
+@pytest.mark.parametrize("cols", [2880, 4096])
+def test_q8_matvec_matches_oracle(dev, cols):
+    rows = 512
+    blocks = O.synth_q8_0(11, cols, rows * cols // 32)
+    x = O.synth_normal(12, cols, cols)
+    bias = O.synth_normal(13, cols, rows, sigma=0.1)
+    resid = O.synth_normal(14, cols, rows, sigma=3.0)
+    t = dev.q8_upload(blocks, rows, cols)
+    xb, bb, rb, yb = dev.upload(x), dev.upload(bias), dev.upload(resid), dev.alloc(rows * 4)
+    dev.matvec_q8_0(t, bb, ttlab_amd.stage_input(xb), None, yb)
+    ref = np.empty(rows, np.float32)
+    O.lib.orc_matvec_add_q8_0(blocks, bias, rows, cols, x, ref)
+    err = O.rel_l2(yb.download(np.float32), ref)
+    print(f"q8_0 {rows}x{cols}: rel_l2 {err:.2e}")
+    assert err <= TOL
+    assert O.rel_l2(yb.download(np.float32), q8_dense(blocks, rows, cols) @ x.astype(np.float64) + bias) < 1e-6
+    dev.matvec_q8_0(t, bb, ttlab_amd.stage_input(xb), rb, yb)
+    assert O.rel_l2(yb.download(np.float32), resid + ref) <= TOL
+    for b in (xb, bb, rb, yb):
+        b.free()
+    t.free()
+
+
+def test_stage_combine_is_exact_and_norm_matches_oracle(dev):
+    """in = rms_norm(base + sum_r w_r add_r): the combine matches the reference's unfused
+    rank-order sum bit for bit (model.cpp:323-337, 592-594); the norm is within tolerance."""
+    rows = 256
+    blocks = O.synth_q8_0(21, 0, rows * 90)
+    base = O.synth_normal(22, 0, N, sigma=40.0)
+    add = O.synth_normal(23, 0, 4 * N, sigma=30.0)
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    norm = O.synth_normal(24, 0, N, mean=1.0, sigma=0.05)
+    t = dev.q8_upload(blocks, rows, N)
+    bb, ab, wb, nb = dev.upload(base), dev.upload(add), dev.upload(w), dev.upload(norm)
+    sb, yb = dev.alloc(N * 4), dev.alloc(rows * 4)
+    dev.matvec_q8_0(t, None, ttlab_amd.stage_input(bb, ab, wb, 4, nb, 1e-5, sb), None, yb)
+    combined = np.zeros(N, np.float32)
+    for r in range(4):
+        combined = (combined + np.float32(w[r]) * add.reshape(4, N)[r]).astype(np.float32)
+    v = (base + combined).astype(np.float32)
+    assert np.array_equal(sb.download(np.float32).view(np.uint32), v.view(np.uint32))
+    normed = np.empty(N, np.float32)
+    O.lib.orc_rms_norm(v, norm, N, 1e-5, normed)
+    ref = np.empty(rows, np.float32)
+    O.lib.orc_matvec_q8_0(blocks, rows, N, normed, ref)
+    assert O.rel_l2(yb.download(np.float32), ref) <= TOL
+    for b in (bb, ab, wb, nb, sb, yb):
+        b.free()
+    t.free()
+
+
+def rope_table(capacity):
+    f = np.empty(32, np.float32)
+    O.lib.orc_rope_frequencies(f)
+    mag = np.float32(1.0) + np.float32(0.1) * np.float32(np.log(np.float32(32.0)))
+    table = np.empty((capacity, 32, 2), np.float32)
+    # the oracle's apply_rope on unit pairs recovers (cos, sin) * magnitude exactly
+    for pos in range(capacity):
+        v = np.zeros(64, np.float32)
+        v[:32] = 1.0
+        O.lib.orc_apply_rope(v, 1, pos, f)
+        table[pos, :, 0] = v[:32]
+        table[pos, :, 1] = v[32:]
+    return table, f
+
+
+@pytest.mark.parametrize("position", [0, 7, 130])
+def test_qkv_rope_kv_store_matches_oracle(dev, position):
+    capacity = 136
+    q = O.synth_q8_0(31, 3, 4096 * 90)
+    k = O.synth_q8_0(31, 4, 512 * 90)
+    v = O.synth_q8_0(31, 5, 512 * 90)
+    bias = O.synth_normal(31, 6, 5120, sigma=0.05)
+    x = O.synth_normal(32, position, N, sigma=20.0)
+    norm = O.synth_normal(33, 0, N, mean=1.0, sigma=0.05)
+    rows = np.empty(5120, np.int32)
+    ttlab_amd.load_library().ttl_qkv_row_source(rows.ctypes.data)
+    qkv = dev.q8_upload(np.concatenate([q, k, v]), 5120, N, rows, 5120)
+    table, freqs = rope_table(capacity)
+    xb, nb, bb, tb = dev.upload(x), dev.upload(norm), dev.upload(bias), dev.upload(table)
+    pb = dev.upload(np.array([position], np.int32))
+    qo = dev.alloc(4096 * 4)
+    kc, vc = dev.alloc(capacity * 512 * 4), dev.alloc(capacity * 512 * 4)
+    dev.fill(kc, 0)
+    dev.fill(vc, 0)
+    dev.attn_qkv(qkv, bb, ttlab_amd.stage_input(xb, norm=nb), tb, pb, capacity, qo, kc, vc)
+    normed = np.empty(N, np.float32)
+    O.lib.orc_rms_norm(x, norm, N, 1e-5, normed)
+    rq, rk, rv = np.empty(4096, np.float32), np.empty(512, np.float32), np.empty(512, np.float32)
+    O.lib.orc_matvec_add_q8_0(q, bias[:4096].copy(), 4096, N, normed, rq)
+    O.lib.orc_matvec_add_q8_0(k, bias[4096:4608].copy(), 512, N, normed, rk)
+    O.lib.orc_matvec_add_q8_0(v, bias[4608:].copy(), 512, N, normed, rv)
+    O.lib.orc_apply_rope(rq, 64, position, freqs)
+    O.lib.orc_apply_rope(rk, 8, position, freqs)
+    assert O.rel_l2(qo.download(np.float32), rq) <= TOL
+    kcache = kc.download(np.float32).reshape(capacity, 512)
+    vcache = vc.download(np.float32).reshape(capacity, 512)
+    assert O.rel_l2(kcache[position], rk) <= TOL
+    assert O.rel_l2(vcache[position], rv) <= TOL
+    others = [p for p in range(capacity) if p != position]
+    assert not kcache[others].any() and not vcache[others].any()
+    for b in (xb, nb, bb, tb, pb, qo, kc, vc):
+        b.free()
+    qkv.free()
+
+
+@pytest.mark.parametrize("layer_index,position", [(0, 0), (1, 0), (0, 63), (1, 64), (0, 127), (0, 128),
+                                                  (0, 129), (1, 129), (0, 300), (1, 300), (1, 1023)])
+def test_attention_with_sinks_matches_oracle(dev, layer_index, position):
+    capacity = 1088
+    T = position + 1
+    q = O.synth_normal(41, position, 4096, sigma=2.0)
+    k = O.synth_normal(42, position, capacity * 512, sigma=2.0)
+    v = O.synth_normal(43, position, capacity * 512)
+    sinks = O.synth_normal(44, 0, 64, sigma=2.0)
+    qb, kb, vb, sb = dev.upload(q), dev.upload(k), dev.upload(v), dev.upload(sinks)
+    pb = dev.upload(np.array([position], np.int32))
+    ws = dev.alloc(dev.lib.ttl_attention_workspace_bytes(capacity))
+    out = dev.alloc(4096 * 4)
+    dev.attention_decode(qb, kb, vb, sb, pb, capacity, layer_index, ws, out)
+    ref = np.empty(4096, np.float32)
+    scores = np.empty(T, np.float32)
+    O.lib.orc_attention(q, k, v, sinks, layer_index, position, ref, scores)
+    err = O.rel_l2(out.download(np.float32), ref)
+    print(f"attention layer {layer_index} position {position}: rel_l2 {err:.2e}")
+    assert err <= TOL
+    for b in (qb, kb, vb, sb, pb, ws, out):
+        b.free()
+
+
+def test_logits_and_greedy_match_oracle(dev):
+    vocab = 5003
+    w = O.synth_bf16(51, 0, vocab * N)
+    x = O.synth_normal(52, 0, N, sigma=7.0)
+    norm = O.synth_normal(53, 0, N, mean=1.0, sigma=0.05)
+    wb, xb, nb = dev.upload(w), dev.upload(x), dev.upload(norm)
+    lb = dev.alloc(vocab * 4)
+    ws = dev.alloc(dev.lib.ttl_logits_workspace_bytes(vocab))
+    tok, pos, hist = dev.upload(np.array([-1], np.int32)), dev.upload(np.array([3], np.int32)), dev.alloc(64)
+    dev.logits_bf16(wb, vocab, ttlab_amd.stage_input(xb, norm=nb), lb, ws)
+    dev.argmax(vocab, ws, tok, pos, hist, 16)
+    normed = np.empty(N, np.float32)
+    O.lib.orc_rms_norm(x, norm, N, 1e-5, normed)
+    ref = np.empty(vocab, np.float32)
+    O.lib.orc_matvec_bf16(w, vocab, N, normed, ref)
+    got = lb.download(np.float32)
+    assert O.rel_l2(got, ref) <= TOL
+    assert tok.download(np.int32)[0] == O.lib.orc_greedy(got, vocab)
+    assert tok.download(np.int32)[0] == O.lib.orc_greedy(ref, vocab)
+    assert pos.download(np.int32)[0] == 4
+    assert hist.download(np.int32, 16)[3] == tok.download(np.int32)[0]
+    for b in (wb, xb, nb, lb, ws, tok, pos, hist):
+        b.free()
+
+
+def test_greedy_ties_and_nan_follow_reference(dev):
+    """Argmax semantics of model.cpp:604-612 on crafted logits: first maximum wins,
+    NaNs never win, and a NaN at index 0 is never displaced."""
+    vocab = 4096
+    ident = np.zeros(vocab * N, np.uint16)
+    ident.reshape(vocab, N)[:, 0] = 0x3F80  # bf16 1.0 in column 0: logit = x[0]
+    wb = dev.upload(ident)
+    lb, ws = dev.alloc(vocab * 4), dev.alloc(dev.lib.ttl_logits_workspace_bytes(vocab))
+    tok = dev.alloc(4)
+    cases = []
+    for fill in ("ties", "nan_first", "nan_mid"):
+        vals = np.full(vocab, -1.0, np.float32)
+        if fill == "ties":
+            vals[[700, 300, 3000]] = 5.0
+            expected = 300
+        elif fill == "nan_first":
+            vals[0] = np.nan
+            vals[10] = 9.0
+            expected = 0
+        else:
+            vals[5] = np.nan
+            vals[1000] = 2.0
+            expected = 1000
+        cases.append((vals, expected))
+    for vals, expected in cases:
+        # logits[i] = W[i] . x with W[i] = e_0 scaled: build a per-row x by making row i's
+        # column 0 hold the value in bf16 and x = e_0 (values are exact in bf16)
+        w = np.zeros((vocab, N), np.uint16)
+        w[:, 0] = (vals.view(np.uint32) >> 16).astype(np.uint16)
+        w[np.isnan(vals), 0] = 0x7FC0
+        wb.upload(w.ravel())
+        e0 = np.zeros(N, np.float32)
+        e0[0] = 1.0
+        xb = dev.upload(e0)
+        dev.logits_bf16(wb, vocab, ttlab_amd.stage_input(xb), lb, ws)
+        dev.argmax(vocab, ws, tok)
+        got = lb.download(np.float32)
+        assert tok.download(np.int32)[0] == expected == O.lib.orc_greedy(got, vocab)
+        xb.free()
+    for b in (wb, lb, ws, tok):
+        b.free()
+
+
+def test_embedding_matches_oracle(dev):
+    vocab = 1000
+    table = O.synth_q8_0(61, 0, vocab * 90)
+    tb = dev.upload(table)
+    out = dev.alloc(N * 4)
+    for token in (0, 17, 999):
+        t = dev.upload(np.array([token], np.int32))
+        dev.embedding_q8_0(tb, vocab, t, out)
+        ref = np.empty(N, np.float32)
+        O.lib.orc_load_token_embedding_q8_0(table, N, token, ref)
+        assert np.array_equal(out.download(np.float32).view(np.uint32), ref.view(np.uint32))
+        t.free()
+    bad = dev.upload(np.array([vocab], np.int32))
+    dev.embedding_q8_0(tb, vocab, bad, out)
+    assert np.all(np.isnan(out.download(np.float32)))
+    for b in (tb, out, bad):
+        b.free()

@@ -37,6 +37,18 @@ struct ttl_mxfp4 {
     size_t scale_bytes = 0;
 };
 
+// Q8_0 tensor in the repacked layout (see q8:: constants in ttl_q8_tile.hpp): rows of
+// GGUF Q8_0 blocks (fp16 scale + 32 int8), optionally permuted at upload.
+struct ttl_q8 {
+    uint32_t rows = 0;
+    uint32_t cols = 0;
+    uint32_t tiles = 0;          // rows / 16
+    uint8_t *codes = nullptr;    // [tiles][blocks][16 rows][32 B]
+    uint16_t *scales = nullptr;  // [tiles][4 lanes_k][16 rows][scale_pad] fp16
+    size_t code_bytes = 0;
+    size_t scale_bytes = 0;
+};
+
 namespace ttl {
 
 constexpr int iota_size = 1024;

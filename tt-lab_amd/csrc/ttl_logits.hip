@@ -1,0 +1,216 @@
+// Token embedding (load_token_embedding_q8_0, tensor.cpp:171-184), the bf16
+// unembedding matvec with a per-workgroup argmax, and the greedy choice
+// (GptOssModel::greedy, model.cpp:604-612).  Token and position live in device
+// memory so a captured decode step can feed its own output back.
+#include <hip/hip_fp16.h>
+
+#include "ttl_internal.hpp"
+#include "ttl_stage.hpp"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerWave = 4;                   // 16 lanes per row
+constexpr int kRowsPerGroup = 4 * kRowsPerWave;   // 16 rows per workgroup
+constexpr int kCols = 2880;
+constexpr int kChunks = kCols / 8;                // 16-byte chunks of 8 bf16 per row
+constexpr int kIters = (kChunks + 15) / 16;       // 23
+constexpr int kXBlocks = kCols / 32;
+
+struct Best {
+    float value;
+    int32_t index;
+    int32_t first_is_nan;  // set by the group holding row 0
+    int32_t pad;
+};
+
+// model.cpp:604-612 as a reduction: the first index holding the largest non-NaN
+// value (NaN never wins a strict '>').
+__device__ inline bool better(float v, int32_t i, float bv, int32_t bi) {
+    if (isnan(v)) {
+        return false;
+    }
+    if (isnan(bv)) {
+        return true;
+    }
+    return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(kThreads) void logits_kernel(const uint16_t *__restrict__ w, uint32_t rows,
+                                                          stage::Input in, float *__restrict__ logits,
+                                                          Best *__restrict__ partial) {
+    __shared__ __attribute__((aligned(16))) float xs[kXBlocks * stage::x_stride];
+    __shared__ float red[stage::red_floats(kXBlocks)];
+    __shared__ float vals[kRowsPerGroup];
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t row = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave + lane / 16;
+    const uint32_t j = lane % 16;
+    const bool valid = row < rows;
+    uint4 q[kIters];
+    const uint4 *src = reinterpret_cast<const uint4 *>(w + size_t(valid ? row : 0) * kCols);
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+        const uint32_t c = j + 16 * i;
+        q[i] = (valid && c < uint32_t(kChunks)) ? src[c] : make_uint4(0, 0, 0, 0);
+    }
+    if (blockIdx.x != 0) {
+        in.v_out = nullptr;
+    }
+    stage::stage(in, kCols, kXBlocks, xs, red);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+        const uint32_t c = j + 16 * i;
+        if (c < uint32_t(kChunks)) {
+            const float *xb = xs + (c / 4) * stage::x_stride + (c % 4) * 8;
+            const float4 x0 = *reinterpret_cast<const float4 *>(xb);
+            const float4 x1 = *reinterpret_cast<const float4 *>(xb + 4);
+            const uint32_t ww[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+            acc = fmaf(__uint_as_float(ww[0] << 16), x0.x, acc);
+            acc = fmaf(__uint_as_float(ww[0] & 0xffff0000u), x0.y, acc);
+            acc = fmaf(__uint_as_float(ww[1] << 16), x0.z, acc);
+            acc = fmaf(__uint_as_float(ww[1] & 0xffff0000u), x0.w, acc);
+            acc = fmaf(__uint_as_float(ww[2] << 16), x1.x, acc);
+            acc = fmaf(__uint_as_float(ww[2] & 0xffff0000u), x1.y, acc);
+            acc = fmaf(__uint_as_float(ww[3] << 16), x1.z, acc);
+            acc = fmaf(__uint_as_float(ww[3] & 0xffff0000u), x1.w, acc);
+        }
+    }
+#pragma unroll
+    for (int d = 8; d >= 1; d >>= 1) {
+        acc += __shfl_xor(acc, d);
+    }
+    if (j == 0) {
+        vals[wave * kRowsPerWave + lane / 16] = acc;
+        if (valid) {
+            logits[row] = acc;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Best b{NAN, 0x7fffffff, 0, 0};
+        for (int r = 0; r < kRowsPerGroup; ++r) {
+            const int32_t idx = int32_t(blockIdx.x * kRowsPerGroup + r);
+            if (uint32_t(idx) < rows && better(vals[r], idx, b.value, b.index)) {
+                b.value = vals[r];
+                b.index = idx;
+            }
+        }
+        b.first_is_nan = blockIdx.x == 0 && isnan(vals[0]);
+        partial[blockIdx.x] = b;
+    }
+}
+
+// Reduces the per-group bests, writes the greedy token and advances the position.
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const Best *__restrict__ partial, uint32_t groups,
+                                                          int32_t *__restrict__ token, int32_t *__restrict__ position,
+                                                          int32_t advance, int32_t *__restrict__ history,
+                                                          uint32_t history_len) {
+    __shared__ float sv[kThreads];
+    __shared__ int32_t si[kThreads];
+    float bv = NAN;
+    int32_t bi = 0x7fffffff;
+    for (uint32_t g = threadIdx.x; g < groups; g += kThreads) {
+        const Best b = partial[g];
+        if (better(b.value, b.index, bv, bi)) {
+            bv = b.value;
+            bi = b.index;
+        }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (uint32_t s = kThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s && better(sv[threadIdx.x + s], si[threadIdx.x + s], sv[threadIdx.x], si[threadIdx.x])) {
+            sv[threadIdx.x] = sv[threadIdx.x + s];
+            si[threadIdx.x] = si[threadIdx.x + s];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        // logits[0] NaN: the reference's loop never moves off index 0
+        const int32_t choice = partial[0].first_is_nan || si[0] == 0x7fffffff ? 0 : si[0];
+        *token = choice;
+        if (advance) {
+            const int32_t p = *position;
+            if (history && p >= 0 && uint32_t(p) < history_len) {
+                history[p] = choice;
+            }
+            *position = p + 1;
+        }
+    }
+}
+
+// tensor.cpp:171-184 for the token held in device memory.
+__global__ __launch_bounds__(kThreads) void embedding_kernel(const uint8_t *__restrict__ table, uint32_t vocab,
+                                                             const int32_t *__restrict__ token,
+                                                             float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int32_t tok = *token;
+    const bool ok = tok >= 0 && uint32_t(tok) < vocab;
+    const uint8_t *row = table + size_t(ok ? tok : 0) * (kCols / 32) * 34;
+    for (uint32_t i = threadIdx.x; i < uint32_t(kCols); i += kThreads) {
+        const uint8_t *blk = row + (i / 32) * 34;
+        const float d = __half2float(__ushort_as_half(uint16_t(blk[0] | (blk[1] << 8))));
+        out[i] = ok ? d * float(int8_t(blk[2 + i % 32])) : __builtin_nanf("");
+    }
+}
+
+}  // namespace
+
+namespace ttl {
+size_t logits_partials(uint32_t rows) {
+    return (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+}
+}  // namespace ttl
+
+extern "C" {
+
+size_t ttl_logits_workspace_bytes(uint32_t vocab) {
+    return ttl::logits_partials(vocab) * sizeof(Best);
+}
+
+int ttl_logits_bf16(ttl_ctx *ctx, const uint16_t *weight_dev, uint32_t vocab, const ttl_stage_input *in,
+                    float *logits_dev, void *workspace_dev) {
+    TTL_REQUIRE(ctx && weight_dev && in && in->base && logits_dev && workspace_dev, TTL_ERR_INVALID,
+                "ttl_logits_bf16: null argument");
+    TTL_REQUIRE(vocab > 0, TTL_ERR_SHAPE, "ttl_logits_bf16: vocab must be positive");
+    TTL_REQUIRE(((uintptr_t)weight_dev & 15) == 0 && ((uintptr_t)in->base & 15) == 0, TTL_ERR_INVALID,
+                "ttl_logits_bf16: weights and input must be 16-byte aligned");
+    stage::Input s;
+    s.base = in->base;
+    s.add = in->add;
+    s.add_w = in->add_weights;
+    s.add_k = in->add_count;
+    s.norm_w = in->norm_weight;
+    s.eps = in->epsilon;
+    s.v_out = in->sum_out;
+    const uint32_t groups = uint32_t(ttl::logits_partials(vocab));
+    logits_kernel<<<groups, kThreads, 0, ctx->stream>>>(weight_dev, vocab, s, logits_dev,
+                                                        reinterpret_cast<Best *>(workspace_dev));
+    TTL_LAUNCHED("logits_kernel");
+    return TTL_OK;
+}
+
+int ttl_argmax(ttl_ctx *ctx, uint32_t vocab, const void *workspace_dev, int32_t *token_dev, int32_t *position_dev,
+               int32_t *history_dev, uint32_t history_len) {
+    TTL_REQUIRE(ctx && workspace_dev && token_dev, TTL_ERR_INVALID, "ttl_argmax: null argument");
+    argmax_kernel<<<1, kThreads, 0, ctx->stream>>>(reinterpret_cast<const Best *>(workspace_dev),
+                                                   uint32_t(ttl::logits_partials(vocab)), token_dev,
+                                                   position_dev ? position_dev : token_dev, position_dev ? 1 : 0,
+                                                   history_dev, history_len);
+    TTL_LAUNCHED("argmax_kernel");
+    return TTL_OK;
+}
+
+int ttl_embedding_q8_0(ttl_ctx *ctx, const void *table_dev, uint32_t vocab, const int32_t *token_dev,
+                       float *out_dev) {
+    TTL_REQUIRE(ctx && table_dev && token_dev && out_dev, TTL_ERR_INVALID, "ttl_embedding_q8_0: null argument");
+    embedding_kernel<<<1, kThreads, 0, ctx->stream>>>((const uint8_t *)table_dev, vocab, token_dev, out_dev);
+    TTL_LAUNCHED("embedding_kernel");
+    return TTL_OK;
+}
+
+}  // extern "C"

@@ -20,6 +20,7 @@
 // derives its expert from the same data, deterministically), so routing costs
 // no kernel of its own; workgroup 0 publishes indices, weights and logits.
 #include "ttl_mxfp4_tile.hpp"
+#include "ttl_stage.hpp"
 
 #include <cmath>
 
@@ -86,21 +87,31 @@ struct RouterScratch {
 // on the reference's sequential-sum error.  180 lanes hold 16 columns each.
 __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float *__restrict__ weight,
                                                                      const float *__restrict__ bias,
-                                                                     const float *__restrict__ x,
-                                                                     RouterScratch *scratch) {
+                                                                     stage::Input in, RouterScratch *scratch) {
     __shared__ double wave_part[3][3];
+    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
+    __shared__ float red[stage::red_floats(mxt::x_blocks)];
     const uint32_t row = blockIdx.x;
     const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
     const bool active = t < kRouterCols / 16;
 
+    float4 wv[4];
+    if (active) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols) + 4 * t;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            wv[q] = w4[q];
+        }
+    }
+    stage::stage(in, kRouterCols, mxt::x_blocks, xs, red);
     double prod[16];
     double local = 0.0, abs_sum = 0.0;
     if (active) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols) + 4 * t;
-        const float4 *x4 = reinterpret_cast<const float4 *>(x) + 4 * t;
+        // lane t holds columns 16t .. 16t+15: half of block t/2 in the padded layout
+        const float *xt = xs + (t / 2) * mxt::x_stride + (t % 2) * 16;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 w = w4[q], v = x4[q];
+            const float4 w = wv[q], v = *reinterpret_cast<const float4 *>(xt + 4 * q);
             prod[4 * q + 0] = double(w.x) * double(v.x);
             prod[4 * q + 1] = double(w.y) * double(v.y);
             prod[4 * q + 2] = double(w.z) * double(v.z);
@@ -189,9 +200,12 @@ __device__ inline double wave_max(double v) {
 // Routing for one token, computed by the whole workgroup (blockDim.x >= experts).
 // Leaves indices/weights in lds; when `logits` is non-null also writes the logits
 // (and bumps the exact-path counter) -- only one workgroup of a launch does that.
+// The exact path stages the router input into xs/red (the same values the router
+// rows saw); the certified path does not touch them.
 __device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
-                                const float *__restrict__ x, uint32_t experts, uint32_t k, bool force_exact,
-                                RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits) {
+                                const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
+                                RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
+                                float *red) {
     const uint32_t t = threadIdx.x, lane = t % 64;
     if (t < 64) {
         // ---- certified path: wave 0 ranks the exact values -------------------
@@ -259,12 +273,13 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     }
 
     // ---- exact path: the reference's sequential sums (tensor.cpp:186-200) ----
+    stage::stage(in, kRouterCols, mxt::x_blocks, xs, red);
     if (t < experts) {
 #pragma clang fp contract(off)
         const float *w = weight + size_t(t) * kRouterCols;
         float sum = bias[t];
         for (int c = 0; c < kRouterCols; ++c) {
-            sum = sum + w[c] * x[c];
+            sum = sum + w[c] * xs[(c / 32) * mxt::x_stride + c % 32];
         }
         lds.ref_logits[t] = sum;
         lds.order[t] = int32_t(t);
@@ -333,13 +348,14 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
 // Standalone routing (ttl_router_topk): one workgroup, publishes everything.
 __global__ __launch_bounds__(256) void router_select_kernel(const float *__restrict__ weight,
                                                             const float *__restrict__ bias, uint32_t experts,
-                                                            const float *__restrict__ x, uint32_t k,
-                                                            uint32_t force_exact, RouterScratch *scratch,
-                                                            float *__restrict__ logits,
+                                                            stage::Input in, uint32_t k, uint32_t force_exact,
+                                                            RouterScratch *scratch, float *__restrict__ logits,
                                                             int32_t *__restrict__ indices,
                                                             float *__restrict__ weights_out) {
     __shared__ RouteLds lds;
-    route_workgroup(weight, bias, x, experts, k, force_exact != 0, scratch, lds, logits);
+    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
+    __shared__ float red[stage::red_floats(mxt::x_blocks)];
+    route_workgroup(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
     if (threadIdx.x < k) {
         indices[threadIdx.x] = lds.indices[threadIdx.x];
         weights_out[threadIdx.x] = lds.weights[threadIdx.x];
@@ -364,7 +380,7 @@ struct GateUpArgs {
     const uint8_t *up_codes, *up_scales;
     const float *up_bias;
     uint32_t rows, tiles, experts, k;
-    const float *x;
+    stage::Input in;  // the layer input (optionally the residual stream + norm)
     // routing: either given (expert_ids) or derived in the prologue from the router
     const int32_t *expert_ids;
     const float *router_weight, *router_bias;
@@ -377,6 +393,7 @@ struct GateUpArgs {
 
 __global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUpArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
+    __shared__ float red[stage::red_floats(mxt::x_blocks)];
     __shared__ float result[2][2 * mx::tile_rows];
     __shared__ RouteLds route;
     const uint32_t pairs = (a.tiles + 1) / 2;
@@ -390,8 +407,8 @@ __global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUp
         e = a.expert_ids[slot];
     } else {
         const bool publish = blockIdx.x == 0;
-        route_workgroup(a.router_weight, a.router_bias, a.x, a.experts, a.k, false, a.scratch, route,
-                        publish ? a.logits_out : nullptr);
+        route_workgroup(a.router_weight, a.router_bias, a.in, a.experts, a.k, false, a.scratch, route,
+                        publish ? a.logits_out : nullptr, xs, red);
         e = route.indices[slot];
         if (publish && threadIdx.x < a.k) {
             a.indices_out[threadIdx.x] = route.indices[threadIdx.x];
@@ -405,8 +422,7 @@ __global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUp
         mxt::tile_load(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales, tile_index,
                        lane, regs);
     }
-    mxt::stage_x(a.x, xs);
-    __syncthreads();
+    stage::stage(a.in, mx::cols, mxt::x_blocks, xs, red);
     if (valid && tile < a.tiles) {
         const float acc = mxt::tile_compute(regs, xs, lane);
         if (lane < mx::tile_rows) {
@@ -531,6 +547,20 @@ int check_layer(const ttl_moe_layer *layer, const char *who) {
     return TTL_OK;
 }
 
+// The MoE input as the staging sees it: x itself, or rms_norm(x) when the layer
+// carries its input norm (x is then the residual stream).
+stage::Input layer_input(const ttl_moe_layer &L, const float *x) {
+    stage::Input in;
+    in.base = x;
+    in.add = nullptr;
+    in.add_w = nullptr;
+    in.add_k = 0;
+    in.norm_w = L.input_norm;
+    in.eps = L.input_norm_epsilon;
+    in.v_out = nullptr;
+    return in;
+}
+
 int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden,
                   int32_t *indices_out, float *weights_out) {
     GateUpArgs a;
@@ -544,7 +574,7 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
     a.tiles = L.expert_hidden / mx::tile_rows;
     a.experts = L.experts;
     a.k = L.used;
-    a.x = x;
+    a.in = layer_input(L, x);
     a.expert_ids = expert_ids;
     a.router_weight = L.router_weight;
     a.router_bias = L.router_bias;
@@ -572,9 +602,11 @@ int ttl_router_topk(ttl_ctx *ctx, const float *weight_dev, const float *bias_dev
         return rc;
     }
     RouterScratch *scratch = &workspace(ctx)->router;
-    router_rows_kernel<<<experts, kRouterThreads, 0, ctx->stream>>>(weight_dev, bias_dev, x_dev, scratch);
+    ttl_moe_layer plain{};
+    const stage::Input in = layer_input(plain, x_dev);
+    router_rows_kernel<<<experts, kRouterThreads, 0, ctx->stream>>>(weight_dev, bias_dev, in, scratch);
     TTL_LAUNCHED("router_rows_kernel");
-    router_select_kernel<<<1, 256, 0, ctx->stream>>>(weight_dev, bias_dev, experts, x_dev, k, flags & 1u, scratch,
+    router_select_kernel<<<1, 256, 0, ctx->stream>>>(weight_dev, bias_dev, experts, in, k, flags & 1u, scratch,
                                                      logits_dev, indices_dev, weights_dev);
     TTL_LAUNCHED("router_select_kernel");
     return TTL_OK;
@@ -617,6 +649,25 @@ int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_d
     return TTL_OK;
 }
 
+int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                         int32_t *indices_dev, float *weights_dev) {
+    TTL_REQUIRE(ctx && x_dev && hidden_dev && indices_dev && weights_dev, TTL_ERR_INVALID,
+                "ttl_moe_route_gateup: null argument");
+    int rc = check_layer(layer, "ttl_moe_route_gateup");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const ttl_moe_layer &L = *layer;
+    rc = check_router(L.router_weight, L.router_bias, L.experts, L.hidden, x_dev, L.used);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    router_rows_kernel<<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias,
+                                                                      layer_input(L, x_dev), &workspace(ctx)->router);
+    TTL_LAUNCHED("router_rows_kernel");
+    return launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
+}
+
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
                     float *out_dev) {
     TTL_REQUIRE(ctx && down_dev && weights_dev && out_dev, TTL_ERR_INVALID, "ttl_moe_combine: null argument");
@@ -641,8 +692,8 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
     ttl::MoeWorkspace *ws = workspace(ctx);
     int32_t *indices = indices_dev ? indices_dev : ws->indices;
     float *weights = weights_dev ? weights_dev : ws->weights;
-    router_rows_kernel<<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias, x_dev,
-                                                                      &ws->router);
+    router_rows_kernel<<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias,
+                                                                      layer_input(L, x_dev), &ws->router);
     TTL_LAUNCHED("router_rows_kernel");
     rc = launch_gateup(ctx, L, x_dev, nullptr, ws->hidden, indices, weights);
     if (rc == TTL_OK) {

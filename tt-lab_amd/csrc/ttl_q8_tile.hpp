@@ -1,0 +1,130 @@
+// Device building blocks of the Q8_0 matvec kernels.
+//
+// Layout (repacked on upload from GGUF Q8_0 rows of 34-byte blocks, fp16 scale
+// then 32 int8, tensor.cpp:94-114): a tile is 16 rows; code chunks are 32 bytes
+// ordered [tile][block][row]; scales are fp16 ordered so each lane's scales are
+// contiguous, [tile][block%4][row][block/4 padded].
+//
+// Work split: one workgroup of 4 waves owns one tile.  Lane l handles row l%16
+// and blocks 4*i + l/16; wave w handles iterations i in [w*P, w*P + P), so the
+// per-wave dependency chain is a quarter of the row and the tile's four partial
+// sums are added in LDS in wave order (deterministic).
+//
+// Decode: the 32 int8 codes are biased to unsigned (xor 0x80), converted with
+// v_cvt_f32_ubyte{0..3} and accumulated against x; the bias is removed with the
+// block sum of x: sum_j q_j x_j = sum_j (q_j + 128) x_j - 128 * sum_j x_j.
+#pragma once
+
+#include "ttl_internal.hpp"
+#include "ttl_stage.hpp"
+
+namespace q8 {
+
+constexpr int tile_rows = 16;
+constexpr int lanes_k = 4;
+constexpr int waves = 4;
+
+template <int K>
+struct Shape {
+    static constexpr int blocks = K / 32;
+    static constexpr int iters = (blocks + lanes_k - 1) / lanes_k;
+    static constexpr int per_wave = (iters + waves - 1) / waves;
+    static constexpr int scale_pad = per_wave * waves;  // fp16 scales per lane
+    static constexpr int x_blocks = iters * lanes_k;
+    static constexpr size_t tile_code_bytes = size_t(blocks) * tile_rows * 32;
+    static constexpr size_t tile_scales = size_t(lanes_k) * tile_rows * scale_pad;
+};
+
+__host__ __device__ inline int blocks_of(int cols) {
+    return cols / 32;
+}
+__host__ __device__ inline int scale_pad_of(int cols) {
+    const int iters = (cols / 32 + lanes_k - 1) / lanes_k;
+    return ((iters + waves - 1) / waves) * waves;
+}
+__host__ __device__ inline size_t code_offset(size_t tile, uint32_t block, uint32_t row, int cols) {
+    return ((tile * blocks_of(cols) + block) * tile_rows + row) * 32;
+}
+__host__ __device__ inline size_t scale_index(size_t tile, uint32_t block, uint32_t row, int cols) {
+    const int pad = scale_pad_of(cols);
+    return tile * lanes_k * tile_rows * pad + (size_t(block % lanes_k) * tile_rows + row) * pad + block / lanes_k;
+}
+
+template <int K>
+struct TileRegs {
+    uint4 c[Shape<K>::per_wave][2];
+    float d[Shape<K>::per_wave];
+};
+
+// Issues the loads of wave `wave`'s share of one tile.
+template <int K>
+__device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *__restrict__ codes,
+                                                                const uint16_t *__restrict__ scales, size_t tile,
+                                                                uint32_t wave, uint32_t lane, TileRegs<K> &regs) {
+    using S = Shape<K>;
+    const uint32_t r = lane % tile_rows, kl = lane / tile_rows;
+    const uint16_t *sp = scales + tile * S::tile_scales + (size_t(kl) * tile_rows + r) * S::scale_pad +
+                         wave * S::per_wave;
+#pragma unroll
+    for (int j = 0; j < S::per_wave; ++j) {
+        const int i = int(wave) * S::per_wave + j;
+        const uint32_t kb = 4 * i + kl;
+        const bool ok = i < S::iters && kb < uint32_t(S::blocks);
+        const uint4 *p = reinterpret_cast<const uint4 *>(codes + ((tile * S::blocks + kb) * tile_rows + r) * 32);
+        regs.c[j][0] = ok ? p[0] : make_uint4(0, 0, 0, 0);
+        regs.c[j][1] = ok ? p[1] : make_uint4(0, 0, 0, 0);
+        regs.d[j] = ok ? __half2float(__ushort_as_half(sp[j])) : 0.0f;
+    }
+}
+
+__device__ inline float block_dot(const uint4 c0, const uint4 c1, const float *__restrict__ xb, float xsum) {
+    const uint32_t w[8] = {c0.x ^ 0x80808080u, c0.y ^ 0x80808080u, c0.z ^ 0x80808080u, c0.w ^ 0x80808080u,
+                           c1.x ^ 0x80808080u, c1.y ^ 0x80808080u, c1.z ^ 0x80808080u, c1.w ^ 0x80808080u};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const float4 x = *reinterpret_cast<const float4 *>(xb + 4 * q);
+        a0 = fmaf(float(w[q] & 0xffu), x.x, a0);
+        a1 = fmaf(float((w[q] >> 8) & 0xffu), x.y, a1);
+        a0 = fmaf(float((w[q] >> 16) & 0xffu), x.z, a0);
+        a1 = fmaf(float(w[q] >> 24), x.w, a1);
+    }
+    return fmaf(-128.0f, xsum, a0 + a1);
+}
+
+// Wave's partial dot products for the tile's 16 rows; valid in lanes 0..15.
+template <int K>
+__device__ __attribute__((always_inline)) inline float tile_compute(const TileRegs<K> &regs, uint32_t wave,
+                                                                   uint32_t lane, const float *xs,
+                                                                   const float *xsum) {
+    using S = Shape<K>;
+    const uint32_t kl = lane / tile_rows;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < S::per_wave; ++j) {
+        const int i = int(wave) * S::per_wave + j;
+        if (i < S::iters) {
+            const uint32_t kb = 4 * i + kl;
+            acc = fmaf(regs.d[j], block_dot(regs.c[j][0], regs.c[j][1], xs + kb * stage::x_stride, xsum[kb]), acc);
+        }
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    return acc;
+}
+
+// Per-block sums of x (in the padded LDS layout), one thread per block.
+__device__ inline void block_sums(const float *xs, uint32_t x_blocks, float *xsum) {
+    for (uint32_t b = threadIdx.x; b < x_blocks; b += blockDim.x) {
+        const float *p = xs + b * stage::x_stride;
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            s += p[j];
+        }
+        xsum[b] = s;
+    }
+    __syncthreads();
+}
+
+}  // namespace q8

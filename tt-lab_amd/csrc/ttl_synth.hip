@@ -63,6 +63,17 @@ __global__ void mxfp4_gguf_kernel(uint64_t seed, uint64_t stream, size_t block_o
     }
 }
 
+// BF16 bits: random sign and mantissa, exponent uniform in 120..123 (orc_synth_bf16).
+__global__ void bf16_kernel(uint64_t seed, uint64_t stream, size_t offset, size_t n, uint16_t *out) {
+    const size_t k = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= n) {
+        return;
+    }
+    const uint64_t i = offset + k;
+    const uint32_t h = uint32_t(synth::hash(seed, stream, i >> 2) >> (16 * (i & 3))) & 0xffffu;
+    out[k] = uint16_t((h & 0x807fu) | ((120u + ((h >> 7) & 3u)) << 7));
+}
+
 // Writes expert e (stream + e) straight into the repacked planes.
 __global__ void mxfp4_repacked_kernel(uint64_t seed, uint64_t stream, uint32_t rows, uint32_t experts,
                                       uint32_t emin, uint32_t span, uint4 *codes, uint8_t *scales) {
@@ -116,6 +127,15 @@ int ttl_synth_normal_bf16(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t o
         normal_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>(seed, stream, offset, n, 0.0f, sigma, 1,
                                                                          out_dev);
         TTL_LAUNCHED("normal_kernel");
+    }
+    return TTL_OK;
+}
+
+int ttl_synth_bf16(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t offset, size_t n, uint16_t *out_dev) {
+    TTL_REQUIRE(ctx && (n == 0 || out_dev), TTL_ERR_INVALID, "ttl_synth_bf16: null argument");
+    if (n) {
+        bf16_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>(seed, stream, offset, n, out_dev);
+        TTL_LAUNCHED("bf16_kernel");
     }
     return TTL_OK;
 }

@@ -1,0 +1,143 @@
+// ttlab::HipGptOssModel -- the gpt-oss decode loop of the reference's GptOssModel
+// (model.h:15-31, model.cpp:557-612) on the gfx950 backend.  Host code only: every
+// device operation goes through the C ABI in include/ttlab_hip.h.
+#pragma once
+
+#include "ttlab_hip.h"
+
+#include <array>
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace ttlab {
+
+// Turns a C ABI status into the reference's error convention (std::runtime_error,
+// model.cpp:209-228).
+void check(int status, const char *what);
+
+// Synthetic weights.  Tensor `kind` of layer l comes from generator stream
+// synth_stream(l, kind) (model-wide tensors use l = -1); MXFP4 expert e of a
+// tensor uses stream synth_stream(l, kind) + e.  Distributions:
+//   norms N(1, 0.05); q/k/v/o Q8_0 (fp16 scale in [2^-12, 2^-11), int8 uniform);
+//   biases N(0, 0.05); sinks N(0, 1); router bf16 N(0, 0.02), bias N(0, 0.02);
+//   experts MXFP4 (E8M0 uniform 119..125, codes uniform); expert biases N(0, 0.05);
+//   embedding Q8_0; unembedding bf16 (exponents 120..123).
+enum SynthKind : uint32_t {
+    kAttnNorm = 1,
+    kPostNorm = 2,
+    kQuery = 3,
+    kKey = 4,
+    kValue = 5,
+    kQkvBias = 6,
+    kAttnOutput = 7,
+    kAttnOutputBias = 8,
+    kSinks = 9,
+    kRouter = 10,
+    kRouterBias = 11,
+    kGate = 12,
+    kUp = 13,
+    kDown = 14,
+    kGateBias = 15,
+    kUpBias = 16,
+    kDownBias = 17,
+    kEmbedding = 1,
+    kOutputNorm = 2,
+    kUnembedding = 3,
+};
+uint64_t synth_stream(int layer, uint32_t kind);
+
+struct SyntheticSpec {
+    uint32_t layers = 24;       // 24 (20b) or 36 (120b); tests use fewer
+    uint32_t experts = 32;      // 32 (20b) or 128 (120b)
+    uint32_t vocab = 201088;
+    uint32_t capacity = 2112;   // token capacity of the KV caches
+    uint64_t seed = 0x77000003;
+};
+
+// YaRN RoPE frequencies exactly as model.cpp:124-139 computes them.
+std::array<float, 32> rope_frequencies();
+
+class HipGptOssModel {
+  public:
+    static constexpr size_t context_length = 131072;      // model.h:17
+    static constexpr size_t embedding_length = 2880;      // model.h:34
+    static constexpr size_t query_heads = 64, kv_heads = 8, head_size = 64;
+    static constexpr size_t experts_used = 4;
+    static constexpr float norm_epsilon = 1.0e-5f;
+
+    explicit HipGptOssModel(const SyntheticSpec &spec, int device = 0);
+    ~HipGptOssModel();
+    HipGptOssModel(const HipGptOssModel &) = delete;
+    HipGptOssModel &operator=(const HipGptOssModel &) = delete;
+
+    // The reference's interface (model.h:26-30).
+    const float *prefill(const int32_t *tokens, size_t count);
+    const float *forward(int32_t token, size_t position);
+    int32_t greedy(const float *logits) const;
+
+    // Greedy decode with the token fed back on the device: `steps` tokens.
+    std::vector<int32_t> generate(int32_t token, size_t position, size_t steps);
+    // Milliseconds per device-resident decode step (HIP events around graph replays).
+    double time_decode(int32_t token, size_t position, size_t warmup, size_t steps);
+
+    // Last step's state, for layer-by-layer checks.
+    void layer_state(size_t layer, float *x_in, float *residual, int32_t *indices, float *weights) const;
+    void final_state(float *x_final) const;
+    void kv_cache(size_t layer, size_t positions, float *keys, float *values) const;
+    size_t device_bytes() const {
+        return device_bytes_;
+    }
+    double step_bytes(size_t position) const;
+    const SyntheticSpec &spec() const {
+        return spec_;
+    }
+
+  private:
+    struct Layer {
+        float *attn_norm = nullptr, *post_norm = nullptr;
+        ttl_q8 *qkv = nullptr;
+        float *qkv_bias = nullptr;
+        ttl_q8 *attn_output = nullptr;
+        float *attn_output_bias = nullptr;
+        float *sinks = nullptr;
+        float *router = nullptr, *router_bias = nullptr;
+        ttl_mxfp4 *gate = nullptr, *up = nullptr, *down = nullptr;
+        float *gate_bias = nullptr, *up_bias = nullptr, *down_bias = nullptr;
+        float *key_cache = nullptr, *value_cache = nullptr;
+        ttl_moe_layer moe{};
+    };
+
+    void *alloc(size_t bytes);
+    void release();
+    void generate_weights();
+    void record_step();
+    void set_position(int32_t token, size_t position);
+    void validate(int32_t token, size_t position) const;
+
+    SyntheticSpec spec_;
+    ttl_ctx *ctx_ = nullptr;
+    std::vector<void *> allocations_;
+    std::vector<Layer> layers_;
+    size_t device_bytes_ = 0;
+    uint8_t *embedding_ = nullptr;   // Q8_0, GGUF rows
+    float *output_norm_ = nullptr;
+    uint16_t *unembedding_ = nullptr;
+    float *rope_ = nullptr;          // [capacity][32][2]
+    // activations
+    int32_t *token_ = nullptr, *position_ = nullptr, *history_ = nullptr;
+    float *x_ = nullptr;             // [layers + 1][2880]: layer inputs, then the final stream
+    float *residual_ = nullptr;      // [layers][2880]
+    float *down_ = nullptr;          // [layers][4][2880]
+    int32_t *indices_ = nullptr;     // [layers][4]
+    float *weights_ = nullptr;       // [layers][4]
+    float *hidden_ = nullptr, *query_ = nullptr, *attended_ = nullptr, *attn_workspace_ = nullptr;
+    float *logits_ = nullptr;
+    void *logits_workspace_ = nullptr;
+    ttl_graph *step_ = nullptr;
+    std::vector<float> host_logits_;
+};
+
+}  // namespace ttlab

@@ -1,0 +1,117 @@
+// C API of ttlab::HipGptOssModel (include/ttlab_model.h): exceptions become status codes.
+#include "gpt_oss_hip.hpp"
+#include "ttlab_model.h"
+
+#include <cstring>
+#include <exception>
+#include <string>
+
+struct ttlm_model {
+    ttlab::HipGptOssModel *model;
+};
+
+namespace {
+
+thread_local std::string last_error;
+
+template <class F>
+int guarded(F &&f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        last_error = e.what();
+    } catch (...) {
+        last_error = "unknown error";
+    }
+    return -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ttlm_last_error(void) {
+    return last_error.c_str();
+}
+
+int ttlm_create_synthetic(int device, uint32_t layers, uint32_t experts, uint32_t vocab, uint32_t capacity,
+                          uint64_t seed, ttlm_model **out) {
+    if (!out) {
+        last_error = "ttlm_create_synthetic: null output pointer";
+        return -1;
+    }
+    *out = nullptr;
+    return guarded([&] {
+        ttlab::SyntheticSpec spec;
+        spec.layers = layers;
+        spec.experts = experts;
+        spec.vocab = vocab;
+        spec.capacity = capacity;
+        spec.seed = seed;
+        auto *m = new ttlab::HipGptOssModel(spec, device);
+        *out = new ttlm_model{m};
+    });
+}
+
+void ttlm_destroy(ttlm_model *model) {
+    if (model) {
+        delete model->model;
+        delete model;
+    }
+}
+
+int ttlm_forward(ttlm_model *model, int32_t token, uint32_t position, float *logits) {
+    return guarded([&] {
+        const float *l = model->model->forward(token, position);
+        if (logits) {
+            std::memcpy(logits, l, sizeof(float) * model->model->spec().vocab);
+        }
+    });
+}
+
+int ttlm_prefill(ttlm_model *model, const int32_t *tokens, uint32_t count, float *logits) {
+    return guarded([&] {
+        const float *l = model->model->prefill(tokens, count);
+        if (logits) {
+            std::memcpy(logits, l, sizeof(float) * model->model->spec().vocab);
+        }
+    });
+}
+
+int ttlm_generate(ttlm_model *model, int32_t token, uint32_t position, uint32_t steps, int32_t *tokens) {
+    return guarded([&] {
+        const std::vector<int32_t> out = model->model->generate(token, position, steps);
+        if (tokens && !out.empty()) {
+            std::memcpy(tokens, out.data(), sizeof(int32_t) * out.size());
+        }
+    });
+}
+
+int ttlm_time_decode(ttlm_model *model, int32_t token, uint32_t position, uint32_t warmup, uint32_t steps,
+                     double *ms_per_step) {
+    return guarded([&] { *ms_per_step = model->model->time_decode(token, position, warmup, steps); });
+}
+
+int ttlm_layer_state(ttlm_model *model, uint32_t layer, float *x_in, float *residual, int32_t *indices,
+                     float *weights) {
+    return guarded([&] { model->model->layer_state(layer, x_in, residual, indices, weights); });
+}
+
+int ttlm_final_state(ttlm_model *model, float *x_final) {
+    return guarded([&] { model->model->final_state(x_final); });
+}
+
+int ttlm_kv_cache(ttlm_model *model, uint32_t layer, uint32_t positions, float *keys, float *values) {
+    return guarded([&] { model->model->kv_cache(layer, positions, keys, values); });
+}
+
+size_t ttlm_device_bytes(const ttlm_model *model) {
+    return model ? model->model->device_bytes() : 0;
+}
+
+double ttlm_step_bytes(const ttlm_model *model, uint32_t position) {
+    return model ? model->model->step_bytes(position) : 0.0;
+}
+
+}  // extern "C"

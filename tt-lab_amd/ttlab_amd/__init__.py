@@ -36,10 +36,142 @@ class MoeLayerDesc(C.Structure):
         ("up_bias", C.c_void_p),
         ("down", C.c_void_p),
         ("down_bias", C.c_void_p),
+        ("input_norm", C.c_void_p),
+        ("input_norm_epsilon", C.c_float),
     ]
 
 
+class StageInput(C.Structure):
+    """Mirror of ttl_stage_input."""
+    _fields_ = [
+        ("base", C.c_void_p),
+        ("add", C.c_void_p),
+        ("add_weights", C.c_void_p),
+        ("add_count", C.c_uint32),
+        ("norm_weight", C.c_void_p),
+        ("epsilon", C.c_float),
+        ("sum_out", C.c_void_p),
+    ]
+
+
+def stage_input(base, add=None, add_weights=None, add_count=0, norm=None, eps=1e-5, sum_out=None):
+    s = StageInput()
+    s.base = base.ptr
+    s.add = add.ptr if add else None
+    s.add_weights = add_weights.ptr if add_weights else None
+    s.add_count = add_count
+    s.norm_weight = norm.ptr if norm else None
+    s.epsilon = eps
+    s.sum_out = sum_out.ptr if sum_out else None
+    return s
+
+
 _lib = None
+_model_lib = None
+MODEL_LIB_PATH = os.path.join(PKG_DIR, "build", "libttlab_model.so")
+
+
+def load_model_library():
+    """Loads build/libttlab_model.so (the C++ HipGptOssModel behind include/ttlab_model.h)."""
+    global _model_lib
+    if _model_lib is not None:
+        return _model_lib
+    load_library()
+    if not os.path.exists(MODEL_LIB_PATH):
+        raise TtlError(f"{MODEL_LIB_PATH} is missing: run __graft_entry__.build()")
+    lib = C.CDLL(MODEL_LIB_PATH)
+    vp, u32, i32 = C.c_void_p, C.c_uint32, C.c_int
+    sigs = {
+        "ttlm_create_synthetic": (i32, [i32, u32, u32, u32, u32, C.c_uint64, C.POINTER(vp)]),
+        "ttlm_destroy": (None, [vp]),
+        "ttlm_last_error": (C.c_char_p, []),
+        "ttlm_forward": (i32, [vp, C.c_int32, u32, vp]),
+        "ttlm_prefill": (i32, [vp, vp, u32, vp]),
+        "ttlm_generate": (i32, [vp, C.c_int32, u32, u32, vp]),
+        "ttlm_time_decode": (i32, [vp, C.c_int32, u32, u32, u32, C.POINTER(C.c_double)]),
+        "ttlm_layer_state": (i32, [vp, u32, vp, vp, vp, vp]),
+        "ttlm_final_state": (i32, [vp, vp]),
+        "ttlm_kv_cache": (i32, [vp, u32, u32, vp, vp]),
+        "ttlm_device_bytes": (C.c_size_t, [vp]),
+        "ttlm_step_bytes": (C.c_double, [vp, u32]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _model_lib = lib
+    return lib
+
+
+def _mcheck(rc, what):
+    if rc != 0:
+        msg = load_model_library().ttlm_last_error()
+        raise TtlError(f"{what} failed: {msg.decode() if msg else ''}")
+
+
+class Model:
+    """ttlab::HipGptOssModel with synthetic weights (BASELINE configurations 3/4)."""
+
+    def __init__(self, layers=24, experts=32, vocab=201088, capacity=2112, seed=0x77000003, device=0):
+        self.lib = load_model_library()
+        p = C.c_void_p()
+        _mcheck(self.lib.ttlm_create_synthetic(device, layers, experts, vocab, capacity, seed, C.byref(p)),
+                "ttlm_create_synthetic")
+        self.h = p.value
+        self.layers, self.experts, self.vocab, self.capacity, self.seed = layers, experts, vocab, capacity, seed
+
+    def close(self):
+        if self.h:
+            self.lib.ttlm_destroy(self.h)
+            self.h = None
+
+    def forward(self, token, position):
+        out = np.empty(self.vocab, np.float32)
+        _mcheck(self.lib.ttlm_forward(self.h, token, position, out.ctypes.data), "ttlm_forward")
+        return out
+
+    def prefill(self, tokens):
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.vocab, np.float32)
+        _mcheck(self.lib.ttlm_prefill(self.h, t.ctypes.data, t.size, out.ctypes.data), "ttlm_prefill")
+        return out
+
+    def generate(self, token, position, steps):
+        out = np.empty(steps, np.int32)
+        _mcheck(self.lib.ttlm_generate(self.h, token, position, steps, out.ctypes.data), "ttlm_generate")
+        return out
+
+    def time_decode(self, token, position, warmup, steps):
+        ms = C.c_double()
+        _mcheck(self.lib.ttlm_time_decode(self.h, token, position, warmup, steps, C.byref(ms)), "ttlm_time_decode")
+        return ms.value
+
+    def layer_state(self, layer):
+        x = np.empty(2880, np.float32)
+        r = np.empty(2880, np.float32)
+        idx = np.empty(4, np.int32)
+        w = np.empty(4, np.float32)
+        _mcheck(self.lib.ttlm_layer_state(self.h, layer, x.ctypes.data, r.ctypes.data, idx.ctypes.data,
+                                          w.ctypes.data), "ttlm_layer_state")
+        return x, r, idx, w
+
+    def final_state(self):
+        x = np.empty(2880, np.float32)
+        _mcheck(self.lib.ttlm_final_state(self.h, x.ctypes.data), "ttlm_final_state")
+        return x
+
+    def kv_cache(self, layer, positions):
+        k = np.empty(positions * 512, np.float32)
+        v = np.empty(positions * 512, np.float32)
+        _mcheck(self.lib.ttlm_kv_cache(self.h, layer, positions, k.ctypes.data, v.ctypes.data), "ttlm_kv_cache")
+        return k, v
+
+    @property
+    def device_bytes(self):
+        return self.lib.ttlm_device_bytes(self.h)
+
+    def step_bytes(self, position):
+        return self.lib.ttlm_step_bytes(self.h, position)
 
 
 def load_library():
@@ -84,6 +216,23 @@ def load_library():
         "ttl_moe_gateup_swiglu": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp]),
         "ttl_moe_down": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp]),
         "ttl_moe_combine": (i32, [vp, vp, vp, u32, u32, vp]),
+        "ttl_moe_route_gateup": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp, vp]),
+        "ttl_synth_bf16": (i32, [vp, u64, u64, sz, sz, vp]),
+        "ttl_q8_upload": (i32, [vp, vp, u32, u32, vp, u32, C.POINTER(vp)]),
+        "ttl_q8_upload_dev": (i32, [vp, vp, u32, u32, vp, C.POINTER(vp)]),
+        "ttl_q8_download": (i32, [vp, vp, vp]),
+        "ttl_q8_free": (None, [vp, vp]),
+        "ttl_q8_bytes": (sz, [vp]),
+        "ttl_synth_q8_0_gguf": (i32, [vp, u64, u64, sz, sz, vp]),
+        "ttl_matvec_q8_0": (i32, [vp, vp, vp, C.POINTER(StageInput), vp, vp]),
+        "ttl_qkv_row_source": (i32, [vp]),
+        "ttl_attn_qkv": (i32, [vp, vp, vp, C.POINTER(StageInput), vp, vp, u32, vp, vp, vp]),
+        "ttl_attention_workspace_bytes": (sz, [u32]),
+        "ttl_attention_decode": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, vp, vp]),
+        "ttl_embedding_q8_0": (i32, [vp, vp, u32, vp, vp]),
+        "ttl_logits_workspace_bytes": (sz, [u32]),
+        "ttl_logits_bf16": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
+        "ttl_argmax": (i32, [vp, u32, vp, vp, vp, vp, u32]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
@@ -182,6 +331,23 @@ class Mxfp4:
     def free(self):
         if self.handle:
             self.dev.lib.ttl_mxfp4_free(self.dev.ctx, self.handle)
+            self.handle = None
+
+
+class Q8:
+    """Device Q8_0 tensor handle (ttl_q8)."""
+
+    def __init__(self, dev, handle, rows, cols):
+        self.dev, self.handle, self.rows, self.cols = dev, handle, rows, cols
+
+    def download_gguf(self):
+        out = np.empty(self.rows * self.cols // 32 * 34, np.uint8)
+        _check(self.dev.lib.ttl_q8_download(self.dev.ctx, self.handle, out.ctypes.data), "ttl_q8_download")
+        return out
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.ttl_q8_free(self.dev.ctx, self.handle)
             self.handle = None
 
 
@@ -295,6 +461,38 @@ class Device:
 
     def moe_combine(self, down, weights, k, n, out):
         _check(self.lib.ttl_moe_combine(self.ctx, down.ptr, weights.ptr, k, n, out.ptr), "ttl_moe_combine")
+
+    # ---- Q8_0 / attention / logits ----
+    def q8_upload(self, gguf_bytes, rows, cols, row_source=None, source_rows=None):
+        a = np.ascontiguousarray(gguf_bytes, np.uint8)
+        rs = None if row_source is None else np.ascontiguousarray(row_source, np.int32)
+        h = C.c_void_p()
+        _check(self.lib.ttl_q8_upload(self.ctx, a.ctypes.data, rows, cols, None if rs is None else rs.ctypes.data,
+                                      source_rows if source_rows is not None else rows, C.byref(h)), "ttl_q8_upload")
+        return Q8(self, h.value, rows, cols)
+
+    def matvec_q8_0(self, w, bias, stage, residual, y):
+        _check(self.lib.ttl_matvec_q8_0(self.ctx, w.handle, bias.ptr if bias else None, C.byref(stage),
+                                        residual.ptr if residual else None, y.ptr), "ttl_matvec_q8_0")
+
+    def attn_qkv(self, qkv, bias, stage, rope, position, capacity, q, kc, vc):
+        _check(self.lib.ttl_attn_qkv(self.ctx, qkv.handle, bias.ptr, C.byref(stage), rope.ptr, position.ptr, capacity,
+                                     q.ptr, kc.ptr, vc.ptr), "ttl_attn_qkv")
+
+    def attention_decode(self, q, kc, vc, sinks, position, capacity, layer_index, workspace, out):
+        _check(self.lib.ttl_attention_decode(self.ctx, q.ptr, kc.ptr, vc.ptr, sinks.ptr, position.ptr, capacity,
+                                             layer_index, workspace.ptr, out.ptr), "ttl_attention_decode")
+
+    def embedding_q8_0(self, table, vocab, token, out):
+        _check(self.lib.ttl_embedding_q8_0(self.ctx, table.ptr, vocab, token.ptr, out.ptr), "ttl_embedding_q8_0")
+
+    def logits_bf16(self, weight, vocab, stage, logits, workspace):
+        _check(self.lib.ttl_logits_bf16(self.ctx, weight.ptr, vocab, C.byref(stage), logits.ptr, workspace.ptr),
+               "ttl_logits_bf16")
+
+    def argmax(self, vocab, workspace, token, position=None, history=None, history_len=0):
+        _check(self.lib.ttl_argmax(self.ctx, vocab, workspace.ptr, token.ptr, position.ptr if position else None,
+                                   history.ptr if history else None, history_len), "ttl_argmax")
 
     # ---- graphs ----
     def capture(self, fn):
