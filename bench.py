@@ -1,20 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X backend for tt-lab's quantized decode path.
 
-Prints ONE JSON line (see the fields below).  One GPU only: --gpus N with N > 1
-exits with a message.
+Prints ONE JSON line.  One GPU only: --gpus N with N > 1 exits with a message.
 
-Workload: one gpt-oss-20b MoE layer at decode batch 1 --
-router 32x2880 (bf16 values in f32), top-4 + softmax, per selected expert MXFP4
-gate/up 2x2880x2880 with the clamped SwiGLU, MXFP4 down 2880x2880, weighted
-combine.  24 distinct synthetic layers (10.2 GB of experts) are resident and a step
-runs one token through all 24 in a HIP graph, so weights stream from HBM rather
-than the 256 MB Infinity Cache.
+Default workload: full synthetic gpt-oss-20b decode at
+batch 1 -- 24 layers, 64 q / 8 kv heads of 64, sinks, sliding window 128 on even
+layers, 32 experts top-4 MXFP4, vocab 201088 bf16 unembedding, greedy.  The KV
+caches are first filled to 2048 positions by running the decode itself; then a
+step is one token through the whole model (one HIP graph replay, the token fed
+back on the device) and value = tokens/s.
 
-roofline: the fused gate/up+SwiGLU kernel (the largest of the layer), timed live
-with HIP events around a graph of back-to-back launches over the 24 layers.
-cpu_baseline: the CPU oracle's restatement of the reference's v4 (AVX-512) body,
-one thread, on a bounded sample of the same workload.
+roofline: the MXFP4 gate/up + SwiGLU expert kernel (the path's dominant kernel),
+timed live with HIP events around a graph of the 24 layers' launches; bytes per
+launch are the 4 selected experts' gate and up rows, their biases, x and the
+SwiGLU output.
+
+cpu_baseline: the CPU oracle's restatement of the reference's forward
+(model.cpp:557-602) on one host core, over a bounded sample: one sliding-window
+layer and one full-context layer at position 2048 plus the unembedding; a token
+is 12 of each plus the unembedding.
+
+--workload moe runs BASELINE config 1 instead: one MoE layer per step over 24
+distinct resident layers, value = token-layers/s.
 """
 import argparse
 import json
@@ -27,21 +34,64 @@ sys.path.insert(0, os.path.join(ROOT, "tt-lab_amd"))
 
 METRIC = "decode tok/s at gpt-oss-20b shape; MXFP4 matvec GB/s and % of HBM peak"
 N = 2880
-EXPERTS, USED, LAYERS = 32, 4, 24
+EXPERTS, USED, LAYERS, VOCAB, CONTEXT = 32, 4, 24, 201088, 2048
 HBM_PEAK_GBS = 8000.0
+SEED = 0x77000003
 # Algorithmic bytes of one gate/up+SwiGLU launch: 4 experts x (gate + up) x 2880 rows x
 # 1530 B, their f32 biases, x (f32 2880) read, hidden (f32 4x2880) written.
 GATEUP_BYTES = USED * 2 * N * 1530 + USED * 2 * N * 4 + N * 4 + USED * N * 4
-# Algorithmic bytes of one token-layer (config 1): bf16 router, 4 x (gate+up+down) MXFP4,
-# x in, out, routing.
-LAYER_BYTES = EXPERTS * N * 2 + USED * 3 * N * 1530 + N * 4 + N * 4 + 128
 
 
 def log(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
-def build_layers(dev, ttlab_amd):
+def gpu_decode(args):
+    import ttlab_amd
+
+    context = args.context
+    capacity = context + args.warmup + args.steps + 8
+    t0 = time.time()
+    model = ttlab_amd.Model(args.layers, EXPERTS, VOCAB, capacity, SEED)
+    if args.eager:
+        model.set_graph_replay(False)
+    log(f"model resident: {model.device_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
+    t0 = time.time()
+    filled = model.generate(1, 0, context)
+    log(f"KV caches filled to {context} positions by decoding ({time.time() - t0:.1f} s)")
+    token = int(filled[-1])
+    ms = model.time_decode(token, context, args.warmup, args.steps)
+    tok_s = 1000.0 / ms
+    mid = context + args.warmup + args.steps // 2
+    step_bytes = model.step_bytes(mid)
+    log(f"{ms:.4f} ms per token, {tok_s:.1f} tok/s, step {step_bytes / 1e9:.3f} GB -> "
+        f"{step_bytes / (ms * 1e-3) / 1e9:.0f} GB/s algorithmic")
+    us = model.time_expert_kernel(max(20, args.steps // 5))
+    achieved = GATEUP_BYTES / (us * 1e-6) / 1e9
+    log(f"gateup_swiglu_kernel: {us:.2f} us per launch, {achieved:.0f} GB/s")
+    model.close()
+    return {
+        "value": tok_s,
+        "unit": "tok/s",
+        "ms_per_step": ms,
+        "config": {"workload": f"config 3: full synthetic gpt-oss-20b decode, batch 1, greedy, KV context {context} "
+                               "(filled by decoding), step = one token (one HIP graph replay)",
+                   "layers": args.layers, "experts": EXPERTS, "experts_used": USED, "vocab": VOCAB,
+                   "context": context, "unembedding": "bf16", "attention_weights": "Q8_0",
+                   "step_algorithmic_bytes": int(step_bytes),
+                   "step_algorithmic_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                   "step_frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
+                     "launch_us": round(us, 3)},
+    }
+
+
+def gpu_moe(args):
+    import ttlab_amd
+
+    dev = ttlab_amd.Device(0)
     layers = []
     for l in range(LAYERS):
         seed = 0x77000100 + l
@@ -58,21 +108,9 @@ def build_layers(dev, ttlab_amd):
         d.hidden, d.expert_hidden, d.experts, d.used = N, N, EXPERTS, USED
         d.router_weight, d.router_bias = rw.ptr, rb.ptr
         d.gate, d.up, d.down = gate.handle, up.handle, down.handle
-        d.gate_bias = d.up_bias = d.down_bias = None
         layers.append({"desc": d, "x": x, "out": dev.alloc(N * 4), "idx": dev.alloc(64), "w": dev.alloc(64),
                        "hidden": dev.alloc(USED * N * 4), "keep": (gate, up, down, rw, rb)})
     dev.sync()
-    return layers
-
-
-def gpu_run(args):
-    import ttlab_amd
-
-    dev = ttlab_amd.Device(0)
-    info = dev.info()
-    log(f"device {info}")
-    layers = build_layers(dev, ttlab_amd)
-    log(f"{LAYERS} layers resident")
 
     def step():
         for L in layers:
@@ -85,12 +123,8 @@ def gpu_run(args):
     dev.timer_start()
     for _ in range(args.steps):
         graph.launch()
-    ms = dev.timer_stop()
-    ms_per_step = ms / args.steps
-    token_layers_per_s = LAYERS / (ms_per_step * 1e-3)
-    log(f"{ms_per_step:.4f} ms per step ({LAYERS} token-layers), {token_layers_per_s:.0f} token-layers/s")
+    ms = dev.timer_stop() / args.steps
 
-    # Dominant kernel: gate/up + SwiGLU over the 24 layers, indices from the routing above.
     def gateup():
         for L in layers:
             dev.moe_gateup_swiglu(L["desc"], L["x"], L["idx"], L["hidden"])
@@ -103,54 +137,92 @@ def gpu_run(args):
     dev.timer_start()
     for _ in range(reps):
         g2.launch()
-    ms2 = dev.timer_stop()
-    launch_us = ms2 * 1e3 / (reps * LAYERS)
-    achieved = GATEUP_BYTES / (launch_us * 1e-6) / 1e9
-    log(f"gateup_swiglu_kernel: {launch_us:.2f} us per launch, {achieved:.0f} GB/s")
-    layer_gbs = LAYER_BYTES * token_layers_per_s / 1e9
+    us = dev.timer_stop() * 1e3 / (reps * LAYERS)
+    achieved = GATEUP_BYTES / (us * 1e-6) / 1e9
     graph.free()
     g2.free()
     dev.close()
+    layer_bytes = EXPERTS * N * 2 + USED * 3 * N * 1530 + N * 4 + N * 4 + 128
     return {
-        "ms_per_step": ms_per_step,
-        "value": token_layers_per_s,
-        "layer_gbs": layer_gbs,
+        "value": LAYERS / (ms * 1e-3),
+        "unit": "token-layers/s",
+        "ms_per_step": ms,
+        "config": {"workload": "config 1: gpt-oss-20b MoE layer, decode batch 1; step = one token through 24 "
+                               "distinct resident layers (HIP graph)",
+                   "experts": EXPERTS, "used": USED, "hidden": N, "layers_per_step": LAYERS,
+                   "layer_algorithmic_GBps": round(layer_bytes * LAYERS / (ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
-                     "launch_us": round(launch_us, 3)},
-        "device": info,
+                     "launch_us": round(us, 3)},
     }
 
 
-def cpu_baseline(seconds):
-    """Oracle (restated reference v4 body) on one host core, bounded sample of config 1."""
+def cpu_baseline(seconds, workload):
+    """The oracle (restated reference CPU path) on one host core, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import ctypes as C
 
     import numpy as np
 
     import oracle_lib as O
-    from moe_fixtures import HostLayer
 
     try:
         os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
     except OSError:
         pass
-    host = HostLayer(EXPERTS, USED, biases=False, seed=0x77000100)
     body = O.BODY_V4_SIMD if O.has_avx512() else O.BODY_V4
-    out = np.empty(N, np.float32)
-    s = host.oracle_struct()
-    xs = [O.synth_normal(0x78000200, t, N) for t in range(16)]
-    count, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        O.lib.orc_moe(C.byref(s), xs[count % 16], out, body, None, None, None)
-        count += 1
-    elapsed = time.perf_counter() - t0
     isa = "AVX-512 (x86-64-v4 body)" if body == O.BODY_V4_SIMD else "x86-64-v3 (v4 body restated with fmaf)"
-    return {"value": round(count / elapsed, 3), "unit": "token-layers/s", "cores": 1, "kind": "port",
-            "sample": f"{count} token-layers of config 1 (one 32-expert layer, 16 distinct x) in {elapsed:.1f} s; "
-                      f"oracle restatement of tensor.cpp v4 matvec + model.cpp moe; {isa}"}
+    if workload == "moe":
+        from moe_fixtures import HostLayer
+
+        host = HostLayer(EXPERTS, USED, biases=False, seed=0x77000100)
+        out = np.empty(N, np.float32)
+        s = host.oracle_struct()
+        xs = [O.synth_normal(0x78000200, t, N) for t in range(16)]
+        count, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            O.lib.orc_moe(C.byref(s), xs[count % 16], out, body, None, None, None)
+            count += 1
+        elapsed = time.perf_counter() - t0
+        return {"value": round(count / elapsed, 3), "unit": "token-layers/s", "cores": 1, "kind": "port",
+                "sample": f"{count} token-layers of config 1 in {elapsed:.1f} s; oracle restatement of tensor.cpp "
+                          f"matvecs + model.cpp moe; {isa}"}
+
+    from model_fixtures import HostModelLayer
+
+    # Layers with 4 experts (all selected): the same per-token work as 4 of 32.
+    layers = [HostModelLayer(SEED, l, 4) for l in (0, 1)]
+    freqs = np.empty(32, np.float32)
+    O.lib.orc_rope_frequencies(freqs)
+    cap = CONTEXT + 1
+    kc = O.synth_normal(0x78000300, 1, cap * 512)
+    vc = O.synth_normal(0x78000300, 2, cap * 512)
+    x = O.synth_normal(0x78000300, 3, N, sigma=30.0)
+    outs = {k: np.empty(n, np.float32) for k, n in (("x", N), ("q", 4096), ("a", 4096), ("r", N), ("ro", 4))}
+    idx, w = np.empty(4, np.int64), np.empty(4, np.float32)
+    times = {0: [], 1: []}
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds * 0.6 or not times[1]:
+        for l in (0, 1):
+            s = layers[l].struct()
+            t = time.perf_counter()
+            O.lib.orc_layer_forward(C.byref(s), l, CONTEXT, x, freqs, kc, vc, body, outs["x"], outs["q"], outs["a"],
+                                    outs["r"], outs["ro"], idx, w)
+            times[l].append(time.perf_counter() - t)
+    unembed = O.synth_bf16(SEED, 3 * 1000, VOCAB * N)
+    logits = np.empty(VOCAB, np.float32)
+    t = time.perf_counter()
+    O.lib.orc_matvec_bf16(unembed, VOCAB, N, x, logits)
+    t_logits = time.perf_counter() - t
+    t_window, t_full = float(np.median(times[0])), float(np.median(times[1]))
+    t_token = 12 * t_window + 12 * t_full + t_logits
+    return {"value": round(1.0 / t_token, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"oracle restatement of model.cpp forward at position {CONTEXT}: median of {len(times[0])} "
+                      f"window-layer ({t_window * 1e3:.0f} ms) and {len(times[1])} full-context-layer "
+                      f"({t_full * 1e3:.0f} ms) runs plus one 201088-row bf16 unembedding ({t_logits * 1e3:.0f} ms); "
+                      f"token = 12 + 12 layers + unembedding; MXFP4 {isa}, other matvecs as the reference's C loops "
+                      f"(-O3 -ffp-contract=off -march=x86-64-v3)"}
 
 
 def main():
@@ -158,19 +230,46 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=["decode", "moe"], default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each step's kernels one by one instead of replaying the step graph "
+                         "(for kernel tracers that cannot follow graph launches)")
+    ap.add_argument("--context", type=int, default=CONTEXT,
+                    help="KV positions filled before timing (2048 is the headline workload)")
+    ap.add_argument("--layers", type=int, default=LAYERS,
+                    help="decoder layers (24 is the headline workload; fewer only for counter probes)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first copy this many MiB device-to-device once, a known-size reference "
+                         "dispatch for scaling hardware byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
-    res = gpu_run(args)
-    base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    if args.copy_probe_mib:
+        import ttlab_amd
+
+        dev = ttlab_amd.Device(0)
+        n = args.copy_probe_mib << 20
+        src, dst = dev.alloc(n), dev.alloc(n)
+        dev.fill(src, 1)
+        dev.sync()
+        dev.copy(dst, src, n)
+        dev.sync()
+        log(f"copy probe: {n} bytes device to device")
+        src.free()
+        dst.free()
+        dev.close()
+    res = gpu_decode(args) if args.workload == "decode" else gpu_moe(args)
+    base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.workload)
+    if base:
+        log(f"cpu baseline: {base['value']} {base['unit']}")
     line = {
         "metric": METRIC,
-        "value": round(res["value"], 1),
-        "unit": "token-layers/s",
+        "value": round(res["value"], 2),
+        "unit": res["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -178,12 +277,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (MXFP4 weights)",
+        "dtype": "f32 (MXFP4/Q8_0/bf16 weights)",
         "data": "synthetic",
-        "config": {"workload": "config 1: gpt-oss-20b MoE layer, decode batch 1; step = one token through "
-                               "24 distinct resident layers (HIP graph)",
-                   "experts": EXPERTS, "used": USED, "hidden": N, "layers_per_step": LAYERS,
-                   "layer_algorithmic_GBps": round(res["layer_gbs"], 1)},
+        "config": dict(res["config"], launch="eager" if args.eager else "hip graph"),
         "roofline": res["roofline"],
         "cpu_baseline": base,
     }

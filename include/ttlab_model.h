@@ -39,6 +39,15 @@ int ttlm_generate(ttlm_model *model, int32_t token, uint32_t position, uint32_t 
 int ttlm_time_decode(ttlm_model *model, int32_t token, uint32_t position, uint32_t warmup, uint32_t steps,
                      double *ms_per_step);
 
+/* Microseconds per launch of the MXFP4 gate/up + SwiGLU kernel: every layer's launch
+ * with the last step's routing, as one graph replayed `reps` times (HIP events). */
+int ttlm_time_expert_kernel(ttlm_model *model, uint32_t reps, double *us_per_launch);
+
+/* Decode steps (and the expert-kernel timer) replay captured HIP graphs when `enabled`
+ * is nonzero (the default), else launch the same kernels one by one on the model's
+ * stream -- for tools that cannot follow graph launches. */
+int ttlm_set_graph_replay(ttlm_model *model, int enabled);
+
 /* State of the last step, for layer-by-layer checks (host outputs, each may be NULL):
  * x_in f32 [2880] = input of `layer` (the embedding for layer 0), residual f32 [2880]
  * after attention, indices int32 [4] / weights f32 [4] its routing. */

@@ -46,6 +46,10 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 
+// LDS row stride of the staged K/V chunk: 68 floats, so the 64 lanes of a score
+// pass (one position each) read rows that start in different banks.
+constexpr int kRowStride = kHead + 4;
+
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__restrict__ q,
                                                                 const float *__restrict__ k_cache,
                                                                 const float *__restrict__ v_cache,
@@ -53,6 +57,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
                                                                 uint32_t capacity, uint32_t layer_index,
                                                                 uint32_t max_chunks, float *__restrict__ o_part,
                                                                 float2 *__restrict__ ml_part) {
+    __shared__ __attribute__((aligned(16))) float ks[kChunk * kRowStride];
+    __shared__ __attribute__((aligned(16))) float vs[kChunk * kRowStride];
     __shared__ __attribute__((aligned(16))) float qs[kGroup][kHead];
     __shared__ float e[kGroup][kChunk];
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
@@ -66,37 +72,52 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
         return;
     }
     const uint32_t n = min(uint32_t(kChunk), sp.count - chunk * kChunk);
-    for (uint32_t i = t; i < kGroup * kHead; i += kThreads) {
-        qs[i / kHead][i % kHead] = q[(kvh * kGroup) * kHead + i];
+
+    // One round trip: the 8 query heads, and the chunk's K and V rows of head kvh
+    // (16 float4 per row; positions past n re-read the last valid one).
+    constexpr int kPer = kChunk * (kHead / 4) / kThreads;  // 4 float4 of K and of V per thread
+    float4 kr[kPer], vr[kPer];
+    const float4 qv = t < uint32_t(kGroup * kHead / 4)
+                          ? reinterpret_cast<const float4 *>(q + size_t(kvh) * kGroup * kHead)[t]
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t f = t + uint32_t(k) * kThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
+        const size_t row = (size_t(start + (p < n ? p : n - 1)) * kKvHeads + kvh) * kHead;
+        kr[k] = reinterpret_cast<const float4 *>(k_cache + row)[d4];
+        vr[k] = reinterpret_cast<const float4 *>(v_cache + row)[d4];
+    }
+    if (t < uint32_t(kGroup * kHead / 4)) {
+        *reinterpret_cast<float4 *>(&qs[t / (kHead / 4)][4 * (t % (kHead / 4))]) = qv;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t f = t + uint32_t(k) * kThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
+        *reinterpret_cast<float4 *>(ks + p * kRowStride + 4 * d4) = kr[k];
+        *reinterpret_cast<float4 *>(vs + p * kRowStride + 4 * d4) = vr[k];
     }
     __syncthreads();
 
     // scores: thread (p = t % 64, heads 2*(t/64), 2*(t/64)+1)
     {
         const uint32_t p = t % kChunk, g0 = 2 * (t / kChunk);
-        float s0 = -INFINITY, s1 = -INFINITY;
-        if (p < n) {
-            const float4 *k4 = reinterpret_cast<const float4 *>(k_cache + (size_t(start + p) * kKvHeads + kvh) * kHead);
-            float a0 = 0.0f, a1 = 0.0f;
+        float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-            for (int d = 0; d < kHead / 4; ++d) {
-                const float4 kv = k4[d];
-                const float4 qa = *reinterpret_cast<const float4 *>(&qs[g0][4 * d]);
-                const float4 qb = *reinterpret_cast<const float4 *>(&qs[g0 + 1][4 * d]);
-                a0 = fmaf(qa.x, kv.x, a0);
-                a0 = fmaf(qa.y, kv.y, a0);
-                a0 = fmaf(qa.z, kv.z, a0);
-                a0 = fmaf(qa.w, kv.w, a0);
-                a1 = fmaf(qb.x, kv.x, a1);
-                a1 = fmaf(qb.y, kv.y, a1);
-                a1 = fmaf(qb.z, kv.z, a1);
-                a1 = fmaf(qb.w, kv.w, a1);
-            }
-            s0 = a0 * 0.125f;  // 1/sqrt(64), exact
-            s1 = a1 * 0.125f;
+        for (int d = 0; d < kHead / 4; ++d) {
+            const float4 kv = *reinterpret_cast<const float4 *>(ks + p * kRowStride + 4 * d);
+            const float4 qa = *reinterpret_cast<const float4 *>(&qs[g0][4 * d]);
+            const float4 qb = *reinterpret_cast<const float4 *>(&qs[g0 + 1][4 * d]);
+            a0 = fmaf(qa.x, kv.x, a0);
+            a0 = fmaf(qa.y, kv.y, a0);
+            a0 = fmaf(qa.z, kv.z, a0);
+            a0 = fmaf(qa.w, kv.w, a0);
+            a1 = fmaf(qb.x, kv.x, a1);
+            a1 = fmaf(qb.y, kv.y, a1);
+            a1 = fmaf(qb.z, kv.z, a1);
+            a1 = fmaf(qb.w, kv.w, a1);
         }
-        e[g0][p] = s0;
-        e[g0 + 1][p] = s1;
+        e[g0][p] = p < n ? a0 * 0.125f : -INFINITY;  // 1/sqrt(64), exact
+        e[g0 + 1][p] = p < n ? a1 * 0.125f : -INFINITY;
     }
     __syncthreads();
     // per head: chunk max and exp sums (wave w handles heads 2w, 2w+1; lane = position)
@@ -119,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
         const uint32_t g = t / 32, d = 2 * (t % 32);
         float o0 = 0.0f, o1 = 0.0f;
         for (uint32_t p = 0; p < n; ++p) {
-            const float2 v = *reinterpret_cast<const float2 *>(v_cache + (size_t(start + p) * kKvHeads + kvh) * kHead + d);
+            const float2 v = *reinterpret_cast<const float2 *>(vs + p * kRowStride + d);
             const float x = e[g][p];
             o0 = fmaf(x, v.x, o0);
             o1 = fmaf(x, v.y, o1);
@@ -130,12 +151,17 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
     }
 }
 
+// One workgroup per query head, one thread per dimension.  The chunk statistics
+// are read once (a thread per chunk), the rescale factors shared through LDS.
+constexpr int kMaxCombineChunks = 256;  // capacity up to 16384 positions
+
 __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__restrict__ o_part,
                                                              const float2 *__restrict__ ml_part,
                                                              const float *__restrict__ sinks,
                                                              const int32_t *__restrict__ position,
                                                              uint32_t capacity, uint32_t layer_index,
                                                              uint32_t max_chunks, float *__restrict__ out) {
+    __shared__ float fs[kMaxCombineChunks];
     const uint32_t head = blockIdx.x, d = threadIdx.x;
     const uint32_t pos = uint32_t(*position);
     if (pos >= capacity) {
@@ -144,16 +170,34 @@ __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__rest
     const Span sp = span_of(pos, layer_index);
     const uint32_t chunks = (sp.count + kChunk - 1) / kChunk;
     const float sink = sinks[head];
-    float m = sink;
-    for (uint32_t c = 0; c < chunks; ++c) {
-        m = fmaxf(m, ml_part[size_t(head) * max_chunks + c].x);
+    constexpr int kPer = kMaxCombineChunks / kHead;
+    float2 ml[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t c = d + uint32_t(k) * kHead;
+        ml[k] = c < chunks ? ml_part[size_t(head) * max_chunks + c] : make_float2(-INFINITY, 0.0f);
     }
-    float den = expf(sink - m), acc = 0.0f;
+    float m = sink;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        m = fmaxf(m, ml[k].x);
+    }
+    m = wave_max(m);
+    float den = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t c = d + uint32_t(k) * kHead;
+        const float f = c < chunks ? expf(ml[k].x - m) : 0.0f;
+        den += ml[k].y * f;
+        fs[c] = f;
+    }
+    den = wave_sum(den) + expf(sink - m);
+    __syncthreads();
+    float acc = 0.0f;
+    const float *op = o_part + size_t(head) * max_chunks * kHead + d;
+#pragma unroll 8
     for (uint32_t c = 0; c < chunks; ++c) {
-        const float2 ml = ml_part[size_t(head) * max_chunks + c];
-        const float f = expf(ml.x - m);
-        den += ml.y * f;
-        acc = fmaf(o_part[(size_t(head) * max_chunks + c) * kHead + d], f, acc);
+        acc = fmaf(op[size_t(c) * kHead], fs[c], acc);
     }
     out[head * kHead + d] = acc / den;
 }
@@ -179,9 +223,10 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
                          float *workspace_dev, float *out_dev) {
     TTL_REQUIRE(ctx && q_dev && k_cache_dev && v_cache_dev && sinks_dev && position_dev && workspace_dev && out_dev,
                 TTL_ERR_INVALID, "ttl_attention_decode: null argument");
-    TTL_REQUIRE(capacity > 0, TTL_ERR_SHAPE, "ttl_attention_decode: capacity must be positive");
-    TTL_REQUIRE(((uintptr_t)q_dev & 15) == 0 && ((uintptr_t)k_cache_dev & 15) == 0 && ((uintptr_t)v_cache_dev & 7) == 0,
-                TTL_ERR_INVALID, "ttl_attention_decode: q/k must be 16-byte and v 8-byte aligned");
+    TTL_REQUIRE(capacity > 0 && capacity <= uint32_t(kMaxCombineChunks * kChunk), TTL_ERR_SHAPE,
+                "ttl_attention_decode: capacity must be 1..%d", kMaxCombineChunks * kChunk);
+    TTL_REQUIRE(((uintptr_t)q_dev & 15) == 0 && ((uintptr_t)k_cache_dev & 15) == 0 && ((uintptr_t)v_cache_dev & 15) == 0,
+                TTL_ERR_INVALID, "ttl_attention_decode: q, k and v must be 16-byte aligned");
     const uint32_t max_chunks = (capacity + kChunk - 1) / kChunk;
     // even layers never need more than the window's chunks (plus one for misalignment)
     const uint32_t launch_chunks = layer_index % 2 == 0 ? min(max_chunks, uint32_t(kWindow / kChunk + 1)) : max_chunks;

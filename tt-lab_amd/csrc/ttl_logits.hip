@@ -18,6 +18,7 @@ constexpr int kCols = 2880;
 constexpr int kChunks = kCols / 8;                // 16-byte chunks of 8 bf16 per row
 constexpr int kIters = (kChunks + 15) / 16;       // 23
 constexpr int kXBlocks = kCols / 32;
+constexpr int kMaxPartials = 1024;  // logits workgroups (4 per CU)
 
 struct Best {
     float value;
@@ -38,67 +39,91 @@ __device__ inline bool better(float v, int32_t i, float bv, int32_t bi) {
     return v > bv || (v == bv && i < bi);
 }
 
+// One workgroup stages the input once (combine + output norm fused), then walks
+// row groups g = blockIdx.x, blockIdx.x + gridDim.x, ...; each wave takes 4 rows
+// of a group, 16 lanes per row.  The workgroup's best (value, index) goes to
+// partial[blockIdx.x].
+template <int MODE>
 __global__ __launch_bounds__(kThreads) void logits_kernel(const uint16_t *__restrict__ w, uint32_t rows,
                                                           stage::Input in, float *__restrict__ logits,
                                                           Best *__restrict__ partial) {
     __shared__ __attribute__((aligned(16))) float xs[kXBlocks * stage::x_stride];
     __shared__ float red[stage::red_floats(kXBlocks)];
-    __shared__ float vals[kRowsPerGroup];
+    __shared__ float bvals[kThreads / 16];
+    __shared__ int32_t bidx[kThreads / 16];
+    __shared__ int32_t row0_nan;
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const uint32_t row = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave + lane / 16;
     const uint32_t j = lane % 16;
-    const bool valid = row < rows;
-    uint4 q[kIters];
-    const uint4 *src = reinterpret_cast<const uint4 *>(w + size_t(valid ? row : 0) * kCols);
-#pragma unroll
-    for (int i = 0; i < kIters; ++i) {
-        const uint32_t c = j + 16 * i;
-        q[i] = (valid && c < uint32_t(kChunks)) ? src[c] : make_uint4(0, 0, 0, 0);
-    }
+    const uint32_t groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
     if (blockIdx.x != 0) {
         in.v_out = nullptr;
     }
-    stage::stage(in, kCols, kXBlocks, xs, red);
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kIters; ++i) {
-        const uint32_t c = j + 16 * i;
-        if (c < uint32_t(kChunks)) {
-            const float *xb = xs + (c / 4) * stage::x_stride + (c % 4) * 8;
-            const float4 x0 = *reinterpret_cast<const float4 *>(xb);
-            const float4 x1 = *reinterpret_cast<const float4 *>(xb + 4);
-            const uint32_t ww[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
-            acc = fmaf(__uint_as_float(ww[0] << 16), x0.x, acc);
-            acc = fmaf(__uint_as_float(ww[0] & 0xffff0000u), x0.y, acc);
-            acc = fmaf(__uint_as_float(ww[1] << 16), x0.z, acc);
-            acc = fmaf(__uint_as_float(ww[1] & 0xffff0000u), x0.w, acc);
-            acc = fmaf(__uint_as_float(ww[2] << 16), x1.x, acc);
-            acc = fmaf(__uint_as_float(ww[2] & 0xffff0000u), x1.y, acc);
-            acc = fmaf(__uint_as_float(ww[3] << 16), x1.z, acc);
-            acc = fmaf(__uint_as_float(ww[3] & 0xffff0000u), x1.w, acc);
-        }
+    stage::stage<kCols, kXBlocks, kThreads, MODE>(in, xs, red);
+    float bv = NAN;
+    int32_t bi = 0x7fffffff;
+    if (threadIdx.x == 0) {
+        row0_nan = 0;
     }
+    for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
+        const uint32_t row = g * kRowsPerGroup + wave * kRowsPerWave + lane / 16;
+        const bool valid = row < rows;
+        // unconditional loads (a row past the end re-reads the last row)
+        const uint4 *src = reinterpret_cast<const uint4 *>(w + size_t(valid ? row : rows - 1) * kCols);
+        uint4 q[kIters];
 #pragma unroll
-    for (int d = 8; d >= 1; d >>= 1) {
-        acc += __shfl_xor(acc, d);
+        for (int i = 0; i < kIters; ++i) {
+            const uint32_t c = j + 16 * i;
+            q[i] = src[c < uint32_t(kChunks) ? c : uint32_t(kChunks) - 1];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const uint32_t c = j + 16 * i;
+            if (c < uint32_t(kChunks)) {
+                const float *xb = xs + (c / 4) * stage::x_stride + (c % 4) * 8;
+                const float4 x0 = *reinterpret_cast<const float4 *>(xb);
+                const float4 x1 = *reinterpret_cast<const float4 *>(xb + 4);
+                const uint32_t ww[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+                acc = fmaf(__uint_as_float(ww[0] << 16), x0.x, acc);
+                acc = fmaf(__uint_as_float(ww[0] & 0xffff0000u), x0.y, acc);
+                acc = fmaf(__uint_as_float(ww[1] << 16), x0.z, acc);
+                acc = fmaf(__uint_as_float(ww[1] & 0xffff0000u), x0.w, acc);
+                acc = fmaf(__uint_as_float(ww[2] << 16), x1.x, acc);
+                acc = fmaf(__uint_as_float(ww[2] & 0xffff0000u), x1.y, acc);
+                acc = fmaf(__uint_as_float(ww[3] << 16), x1.z, acc);
+                acc = fmaf(__uint_as_float(ww[3] & 0xffff0000u), x1.w, acc);
+            }
+        }
+#pragma unroll
+        for (int d = 8; d >= 1; d >>= 1) {
+            acc += __shfl_xor(acc, d);
+        }
+        if (j == 0 && valid) {
+            logits[row] = acc;
+            // rows arrive in increasing order, so better() keeps the first maximum
+            if (better(acc, int32_t(row), bv, bi)) {
+                bv = acc;
+                bi = int32_t(row);
+            }
+            if (row == 0 && isnan(acc)) {
+                row0_nan = 1;
+            }
+        }
     }
     if (j == 0) {
-        vals[wave * kRowsPerWave + lane / 16] = acc;
-        if (valid) {
-            logits[row] = acc;
-        }
+        bvals[threadIdx.x / 16] = bv;
+        bidx[threadIdx.x / 16] = bi;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        Best b{NAN, 0x7fffffff, 0, 0};
-        for (int r = 0; r < kRowsPerGroup; ++r) {
-            const int32_t idx = int32_t(blockIdx.x * kRowsPerGroup + r);
-            if (uint32_t(idx) < rows && better(vals[r], idx, b.value, b.index)) {
-                b.value = vals[r];
-                b.index = idx;
+        Best b{NAN, 0x7fffffff, row0_nan, 0};
+        for (int r = 0; r < kThreads / 16; ++r) {
+            if (better(bvals[r], bidx[r], b.value, b.index)) {
+                b.value = bvals[r];
+                b.index = bidx[r];
             }
         }
-        b.first_is_nan = blockIdx.x == 0 && isnan(vals[0]);
         partial[blockIdx.x] = b;
     }
 }
@@ -112,11 +137,20 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const Best *__restrict
     __shared__ int32_t si[kThreads];
     float bv = NAN;
     int32_t bi = 0x7fffffff;
-    for (uint32_t g = threadIdx.x; g < groups; g += kThreads) {
-        const Best b = partial[g];
-        if (better(b.value, b.index, bv, bi)) {
-            bv = b.value;
-            bi = b.index;
+    // groups <= kMaxPartials: all of a thread's loads are issued before any compare
+    constexpr int kPer = (kMaxPartials + kThreads - 1) / kThreads;
+    Best b[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t g = threadIdx.x + uint32_t(k) * kThreads;
+        b[k] = partial[g < groups ? g : 0];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t g = threadIdx.x + uint32_t(k) * kThreads;
+        if (g < groups && better(b[k].value, b[k].index, bv, bi)) {
+            bv = b[k].value;
+            bi = b[k].index;
         }
     }
     sv[threadIdx.x] = bv;
@@ -161,8 +195,10 @@ __global__ __launch_bounds__(kThreads) void embedding_kernel(const uint8_t *__re
 }  // namespace
 
 namespace ttl {
+// Workgroups of the logits launch (each writes one partial best).
 size_t logits_partials(uint32_t rows) {
-    return (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    const size_t groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    return groups < size_t(kMaxPartials) ? groups : size_t(kMaxPartials);
 }
 }  // namespace ttl
 
@@ -174,22 +210,19 @@ size_t ttl_logits_workspace_bytes(uint32_t vocab) {
 
 int ttl_logits_bf16(ttl_ctx *ctx, const uint16_t *weight_dev, uint32_t vocab, const ttl_stage_input *in,
                     float *logits_dev, void *workspace_dev) {
-    TTL_REQUIRE(ctx && weight_dev && in && in->base && logits_dev && workspace_dev, TTL_ERR_INVALID,
-                "ttl_logits_bf16: null argument");
+    TTL_REQUIRE(ctx && weight_dev && logits_dev && workspace_dev, TTL_ERR_INVALID, "ttl_logits_bf16: null argument");
+    const int rc = stage::check(in, "ttl_logits_bf16");
+    if (rc != TTL_OK) {
+        return rc;
+    }
     TTL_REQUIRE(vocab > 0, TTL_ERR_SHAPE, "ttl_logits_bf16: vocab must be positive");
-    TTL_REQUIRE(((uintptr_t)weight_dev & 15) == 0 && ((uintptr_t)in->base & 15) == 0, TTL_ERR_INVALID,
-                "ttl_logits_bf16: weights and input must be 16-byte aligned");
-    stage::Input s;
-    s.base = in->base;
-    s.add = in->add;
-    s.add_w = in->add_weights;
-    s.add_k = in->add_count;
-    s.norm_w = in->norm_weight;
-    s.eps = in->epsilon;
-    s.v_out = in->sum_out;
+    TTL_REQUIRE(((uintptr_t)weight_dev & 15) == 0, TTL_ERR_INVALID, "ttl_logits_bf16: weights must be 16-byte aligned");
+    const stage::Input s = stage::from_abi(in);
     const uint32_t groups = uint32_t(ttl::logits_partials(vocab));
-    logits_kernel<<<groups, kThreads, 0, ctx->stream>>>(weight_dev, vocab, s, logits_dev,
-                                                        reinterpret_cast<Best *>(workspace_dev));
+    stage::with_mode(s, [&](auto mode) {
+        logits_kernel<decltype(mode)::value><<<groups, kThreads, 0, ctx->stream>>>(
+            weight_dev, vocab, s, logits_dev, reinterpret_cast<Best *>(workspace_dev));
+    });
     TTL_LAUNCHED("logits_kernel");
     return TTL_OK;
 }

@@ -85,6 +85,7 @@ struct RouterScratch {
 
 // One workgroup per router row: the exact value of the row (f64) and the bound
 // on the reference's sequential-sum error.  180 lanes hold 16 columns each.
+template <int MODE>
 __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float *__restrict__ weight,
                                                                      const float *__restrict__ bias,
                                                                      stage::Input in, RouterScratch *scratch) {
@@ -95,6 +96,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
     const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
     const bool active = t < kRouterCols / 16;
 
+    stage::Pending<kRouterCols, mxt::x_blocks, kRouterThreads, MODE> pending;
+    stage::stage_load(in, pending);
     float4 wv[4];
     if (active) {
         const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols) + 4 * t;
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
             wv[q] = w4[q];
         }
     }
-    stage::stage(in, kRouterCols, mxt::x_blocks, xs, red);
+    stage::stage_finish(in, pending, xs, red);
     double prod[16];
     double local = 0.0, abs_sum = 0.0;
     if (active) {
@@ -202,6 +205,7 @@ __device__ inline double wave_max(double v) {
 // (and bumps the exact-path counter) -- only one workgroup of a launch does that.
 // The exact path stages the router input into xs/red (the same values the router
 // rows saw); the certified path does not touch them.
+template <int MODE>
 __device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
@@ -273,7 +277,7 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     }
 
     // ---- exact path: the reference's sequential sums (tensor.cpp:186-200) ----
-    stage::stage(in, kRouterCols, mxt::x_blocks, xs, red);
+    stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
     if (t < experts) {
 #pragma clang fp contract(off)
         const float *w = weight + size_t(t) * kRouterCols;
@@ -346,6 +350,7 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
 }
 
 // Standalone routing (ttl_router_topk): one workgroup, publishes everything.
+template <int MODE>
 __global__ __launch_bounds__(256) void router_select_kernel(const float *__restrict__ weight,
                                                             const float *__restrict__ bias, uint32_t experts,
                                                             stage::Input in, uint32_t k, uint32_t force_exact,
@@ -355,7 +360,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
     __shared__ RouteLds lds;
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    route_workgroup(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
+    route_workgroup<MODE>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
     if (threadIdx.x < k) {
         indices[threadIdx.x] = lds.indices[threadIdx.x];
         weights_out[threadIdx.x] = lds.weights[threadIdx.x];
@@ -391,6 +396,10 @@ struct GateUpArgs {
     float *weights_out, *logits_out;
 };
 
+// ROUTED: the routing is derived in the prologue (a.expert_ids unused); otherwise
+// a.expert_ids gives it.  Separate instantiations keep the given-routing kernel
+// straight-line, so its weight loads overlap the staging and the compute.
+template <int MODE, bool ROUTED>
 __global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUpArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
@@ -402,12 +411,16 @@ __global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUp
     const uint32_t which = wave / 2;  // 0 gate, 1 up
     const uint32_t tile = (blockIdx.x % pairs) * 2 + wave % 2;
 
+    // input loads first (they depend on nothing), then the routing, then the
+    // expert's weight loads; the staging completes while those are in flight
+    stage::Pending<mx::cols, mxt::x_blocks, kGateUpWaves * 64, MODE> pending;
+    stage::stage_load(a.in, pending);
     int32_t e;
-    if (a.expert_ids) {
+    if constexpr (!ROUTED) {
         e = a.expert_ids[slot];
     } else {
         const bool publish = blockIdx.x == 0;
-        route_workgroup(a.router_weight, a.router_bias, a.in, a.experts, a.k, false, a.scratch, route,
+        route_workgroup<MODE>(a.router_weight, a.router_bias, a.in, a.experts, a.k, false, a.scratch, route,
                         publish ? a.logits_out : nullptr, xs, red);
         e = route.indices[slot];
         if (publish && threadIdx.x < a.k) {
@@ -415,21 +428,21 @@ __global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUp
             a.weights_out[threadIdx.x] = route.weights[threadIdx.x];
         }
     }
+    // All weight loads are unconditional (an invalid expert reads expert 0 and its
+    // output becomes NaN below): loads under a branch make the compiler wait for
+    // every load at the branch's end.
     const bool valid = e >= 0 && uint32_t(e) < a.experts;
+    const uint32_t e_safe = valid ? uint32_t(e) : 0u;
+    const uint32_t tile_safe = tile < a.tiles ? tile : a.tiles - 1;
+    const float *b = which == 0 ? a.gate_bias : a.up_bias;
+    const float bias = b ? b[size_t(e_safe) * a.rows + tile_safe * mx::tile_rows + lane % mx::tile_rows] : 0.0f;
     mxt::TileRegs regs;
-    const size_t tile_index = size_t(e) * a.tiles + tile;
-    if (valid && tile < a.tiles) {
-        mxt::tile_load(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales, tile_index,
-                       lane, regs);
-    }
-    stage::stage(a.in, mx::cols, mxt::x_blocks, xs, red);
-    if (valid && tile < a.tiles) {
-        const float acc = mxt::tile_compute(regs, xs, lane);
-        if (lane < mx::tile_rows) {
-            const uint32_t row = tile * mx::tile_rows + lane;
-            const float *b = which == 0 ? a.gate_bias : a.up_bias;
-            result[which][(wave % 2) * mx::tile_rows + lane] = b ? acc + b[size_t(e) * a.rows + row] : acc;
-        }
+    mxt::tile_load(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales,
+                   size_t(e_safe) * a.tiles + tile_safe, lane, regs);
+    stage::stage_finish(a.in, pending, xs, red);
+    const float acc = mxt::tile_compute(regs, xs, lane);
+    if (lane < mx::tile_rows && tile < a.tiles) {
+        result[which][(wave % 2) * mx::tile_rows + lane] = b ? acc + bias : acc;
     }
     __syncthreads();
     if (threadIdx.x < 2 * mx::tile_rows) {
@@ -450,31 +463,28 @@ __global__ __launch_bounds__(kDownWaves * 64) void down_kernel(
     uint32_t rows, uint32_t tiles, uint32_t experts, const float *__restrict__ hidden, uint32_t hidden_stride,
     const int32_t *__restrict__ expert_ids, float *__restrict__ down) {
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
+    __shared__ float red[stage::red_floats(mxt::x_blocks)];
     const uint32_t groups = (tiles + kDownWaves - 1) / kDownWaves;
     const uint32_t slot = blockIdx.x / groups;
     const uint32_t tile = (blockIdx.x % groups) * kDownWaves + threadIdx.x / 64;
     const uint32_t lane = threadIdx.x % 64;
+    // the slot's input first, then the (unconditional) weight loads
+    stage::Input in{};
+    in.base = hidden + size_t(slot) * hidden_stride;
+    stage::Pending<mx::cols, mxt::x_blocks, kDownWaves * 64, stage::kPlain> pending;
+    stage::stage_load(in, pending);
     const int32_t e = expert_ids[slot];
-    const bool valid = tile < tiles && e >= 0 && uint32_t(e) < experts;
+    const bool valid = e >= 0 && uint32_t(e) < experts;
+    const uint32_t e_safe = valid ? uint32_t(e) : 0u;
+    const uint32_t tile_safe = tile < tiles ? tile : tiles - 1;
+    const uint32_t row = tile_safe * mx::tile_rows + lane % mx::tile_rows;
+    const float b = bias ? bias[size_t(e_safe) * rows + row] : 0.0f;
     mxt::TileRegs regs;
-    if (valid) {
-        mxt::tile_load(codes, scales, size_t(e) * tiles + tile, lane, regs);
-    }
-    mxt::stage_x(hidden + size_t(slot) * hidden_stride, xs);
-    __syncthreads();
-    if (tile >= tiles) {
-        return;
-    }
-    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
-    if (!valid) {
-        if (lane < mx::tile_rows) {
-            down[size_t(slot) * rows + row] = __builtin_nanf("");
-        }
-        return;
-    }
+    mxt::tile_load(codes, scales, size_t(e_safe) * tiles + tile_safe, lane, regs);
+    stage::stage_finish(in, pending, xs, red);
     const float acc = mxt::tile_compute(regs, xs, lane);
-    if (lane < mx::tile_rows) {
-        down[size_t(slot) * rows + row] = bias ? acc + bias[size_t(e) * rows + row] : acc;
+    if (lane < mx::tile_rows && tile < tiles) {
+        down[size_t(slot) * rows + row] = !valid ? __builtin_nanf("") : (bias ? acc + b : acc);
     }
 }
 
@@ -561,6 +571,14 @@ stage::Input layer_input(const ttl_moe_layer &L, const float *x) {
     return in;
 }
 
+void launch_router_rows(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, RouterScratch *scratch) {
+    const stage::Input in = layer_input(L, x);
+    stage::with_mode(in, [&](auto mode) {
+        router_rows_kernel<decltype(mode)::value><<<L.experts, kRouterThreads, 0, ctx->stream>>>(
+            L.router_weight, L.router_bias, in, scratch);
+    });
+}
+
 int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden,
                   int32_t *indices_out, float *weights_out) {
     GateUpArgs a;
@@ -584,7 +602,14 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
     a.weights_out = weights_out;
     a.logits_out = workspace(ctx)->logits;
     const uint32_t pairs = (a.tiles + 1) / 2;
-    gateup_swiglu_kernel<<<pairs * L.used, kGateUpWaves * 64, 0, ctx->stream>>>(a);
+    stage::with_mode(a.in, [&](auto mode) {
+        constexpr int M = decltype(mode)::value;
+        if (expert_ids) {
+            gateup_swiglu_kernel<M, false><<<pairs * L.used, kGateUpWaves * 64, 0, ctx->stream>>>(a);
+        } else {
+            gateup_swiglu_kernel<M, true><<<pairs * L.used, kGateUpWaves * 64, 0, ctx->stream>>>(a);
+        }
+    });
     TTL_LAUNCHED("gateup_swiglu_kernel");
     return TTL_OK;
 }
@@ -604,10 +629,10 @@ int ttl_router_topk(ttl_ctx *ctx, const float *weight_dev, const float *bias_dev
     RouterScratch *scratch = &workspace(ctx)->router;
     ttl_moe_layer plain{};
     const stage::Input in = layer_input(plain, x_dev);
-    router_rows_kernel<<<experts, kRouterThreads, 0, ctx->stream>>>(weight_dev, bias_dev, in, scratch);
+    router_rows_kernel<stage::kPlain><<<experts, kRouterThreads, 0, ctx->stream>>>(weight_dev, bias_dev, in, scratch);
     TTL_LAUNCHED("router_rows_kernel");
-    router_select_kernel<<<1, 256, 0, ctx->stream>>>(weight_dev, bias_dev, experts, in, k, flags & 1u, scratch,
-                                                     logits_dev, indices_dev, weights_dev);
+    router_select_kernel<stage::kPlain><<<1, 256, 0, ctx->stream>>>(weight_dev, bias_dev, experts, in, k, flags & 1u,
+                                                                    scratch, logits_dev, indices_dev, weights_dev);
     TTL_LAUNCHED("router_select_kernel");
     return TTL_OK;
 }
@@ -662,8 +687,7 @@ int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
     if (rc != TTL_OK) {
         return rc;
     }
-    router_rows_kernel<<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias,
-                                                                      layer_input(L, x_dev), &workspace(ctx)->router);
+    launch_router_rows(ctx, L, x_dev, &workspace(ctx)->router);
     TTL_LAUNCHED("router_rows_kernel");
     return launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
 }
@@ -692,8 +716,7 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
     ttl::MoeWorkspace *ws = workspace(ctx);
     int32_t *indices = indices_dev ? indices_dev : ws->indices;
     float *weights = weights_dev ? weights_dev : ws->weights;
-    router_rows_kernel<<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias,
-                                                                      layer_input(L, x_dev), &ws->router);
+    launch_router_rows(ctx, L, x_dev, &ws->router);
     TTL_LAUNCHED("router_rows_kernel");
     rc = launch_gateup(ctx, L, x_dev, nullptr, ws->hidden, indices, weights);
     if (rc == TTL_OK) {

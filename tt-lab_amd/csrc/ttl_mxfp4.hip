@@ -172,7 +172,7 @@ int alloc_tensor(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, t
     const size_t tiles_total = size_t(t->tiles) * experts;
     t->code_bytes = tiles_total * mx::tile_code_bytes;
     t->scale_bytes = tiles_total * mx::tile_scale_bytes;
-    hipError_t err = hipMalloc(&t->codes, t->code_bytes);
+    hipError_t err = hipMalloc(&t->codes, t->code_bytes + mx::tail_pad_bytes);
     if (err == hipSuccess) {
         err = hipMalloc(&t->scales, t->scale_bytes);
     }
@@ -182,7 +182,10 @@ int alloc_tensor(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, t
         return ttl::hip_fail(err, who);
     }
     // Padding scale bytes must decode to a finite scale (their blocks are zero).
-    const int rc = ttl_fill_bytes(ctx, t->scales, mx::pad_scale, t->scale_bytes);
+    int rc = ttl_fill_bytes(ctx, t->scales, mx::pad_scale, t->scale_bytes);
+    if (rc == TTL_OK) {
+        rc = ttl_fill_bytes(ctx, t->codes + t->code_bytes, 0, mx::tail_pad_bytes);
+    }
     if (rc != TTL_OK) {
         ttl_mxfp4_free(ctx, t);
         return rc;

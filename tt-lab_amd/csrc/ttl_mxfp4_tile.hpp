@@ -70,8 +70,8 @@ struct TileRegs {
     uint32_t sw[6];
 };
 
-// Issues all of the lane's loads for one tile (they do not depend on x, so
-// callers issue them before staging x into LDS).
+// Issues all of the lane's loads for one tile.  Callers issue their x loads
+// first, so that finishing the staging waits for those alone.
 __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *__restrict__ codes,
                                                                 const uint8_t *__restrict__ scales,
                                                                 size_t tile_index, uint32_t lane, TileRegs &regs) {
@@ -87,10 +87,15 @@ __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *_
     regs.sw[3] = s23.y;
     regs.sw[4] = s45.x;
     regs.sw[5] = s45.y;
+    // Unconditional loads (no branch, so the compiler can wait for them one by one
+    // as the compute consumes them): the last iteration's lanes for blocks 90 and 91
+    // read the next tile or the tensor's zero tail; their x is zero.
+    // Issued in iteration order (the scheduler may not reorder them), so that the
+    // compute can wait for each chunk alone as it arrives.
 #pragma unroll
     for (int i = 0; i < mx::iters; ++i) {
-        const uint32_t kb = 4 * i + kl;
-        regs.q[i] = (i < mx::iters - 1 || kb < mx::blocks) ? tc[size_t(kb) * mx::tile_rows] : make_uint4(0, 0, 0, 0);
+        regs.q[i] = tc[size_t(4 * i + kl) * mx::tile_rows];
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

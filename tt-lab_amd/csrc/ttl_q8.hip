@@ -84,7 +84,7 @@ __global__ void q8_synth_kernel(uint64_t seed, uint64_t stream, size_t block_off
 
 // Common body: one workgroup = one 16-row tile; returns the row sum for row
 // threadIdx.x (valid for threadIdx.x < 16) after the wave-order reduction.
-template <int K>
+template <int K, int MODE>
 __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t *__restrict__ codes,
                                                                   const uint16_t *__restrict__ scales,
                                                                   size_t tile, const stage::Input &in,
@@ -92,9 +92,13 @@ __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t
                                                                   float (*part)[q8::tile_rows]) {
     using S = q8::Shape<K>;
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    // input loads first: the staging then waits for them alone while the weight
+    // loads are still in flight
+    stage::Pending<K, S::x_blocks, kThreads, MODE> pending;
+    stage::stage_load(in, pending);
     q8::TileRegs<K> regs;
     q8::tile_load<K>(codes, scales, tile, wave, lane, regs);
-    stage::stage(in, K, S::x_blocks, xs, red);
+    stage::stage_finish(in, pending, xs, red);
     q8::block_sums(xs, S::x_blocks, xsum);
     const float acc = q8::tile_compute<K>(regs, wave, lane, xs, xsum);
     if (lane < q8::tile_rows) {
@@ -111,7 +115,7 @@ __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t
     return sum;
 }
 
-template <int K>
+template <int K, int MODE>
 __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(const uint8_t *__restrict__ codes,
                                                              const uint16_t *__restrict__ scales, uint32_t rows,
                                                              stage::Input in, const float *__restrict__ bias,
@@ -125,12 +129,15 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(const uint8_t *__re
     if (blockIdx.x != 0) {
         in.v_out = nullptr;
     }
-    const float sum = tile_matvec<K>(codes, scales, tile, in, xs, xsum, red, part);
-    const uint32_t row = uint32_t(tile) * q8::tile_rows + threadIdx.x;
-    if (threadIdx.x < q8::tile_rows && row < rows) {
+    // epilogue operands first, so no load waits at the end (rows is a multiple of 16)
+    const uint32_t row = uint32_t(tile) * q8::tile_rows + threadIdx.x % q8::tile_rows;
+    const float bv = bias ? bias[row] : 0.0f;
+    const float rv = residual ? residual[row] : 0.0f;
+    const float sum = tile_matvec<K, MODE>(codes, scales, tile, in, xs, xsum, red, part);
+    if (threadIdx.x < q8::tile_rows) {
         // tensor.cpp:235: bias + sum; model.cpp:586-588: residual = x + projected
-        const float projected = bias ? bias[row] + sum : sum;
-        y[row] = residual ? residual[row] + projected : projected;
+        const float projected = bias ? bv + sum : sum;
+        y[row] = residual ? rv + projected : projected;
     }
 }
 
@@ -146,6 +153,7 @@ __host__ __device__ inline uint32_t qkv_dim(uint32_t tile, uint32_t r) {
     return r < 8 ? 8 * j + r : 32 + 8 * j + (r - 8);
 }
 
+template <int MODE>
 __global__ __launch_bounds__(kThreads) void qkv_kernel(const uint8_t *__restrict__ codes,
                                                        const uint16_t *__restrict__ scales, stage::Input in,
                                                        const float *__restrict__ bias,
@@ -163,29 +171,31 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(const uint8_t *__restrict
     if (blockIdx.x != 0) {
         in.v_out = nullptr;
     }
-    const float sum = tile_matvec<2880>(codes, scales, tile, in, xs, xsum, red, part);
-    const uint32_t r = threadIdx.x;
+    // epilogue operands first (bias, position, the RoPE pair), so no load waits at the end
+    const uint32_t r = threadIdx.x, r16 = r % q8::tile_rows;
     const uint32_t pos = uint32_t(*position);
     const bool is_q = tile < uint32_t(kQHeads) * 4, is_k = !is_q && tile < uint32_t(kQHeads + kKvHeads) * 4;
     const uint32_t head = is_q ? tile / 4 : (is_k ? (tile - kQHeads * 4) / 4 : (tile - (kQHeads + kKvHeads) * 4) / 4);
     const uint32_t base = is_q ? 0u : (is_k ? uint32_t(kQRows) : uint32_t(kQRows + kKvRows));
+    const uint32_t dim = qkv_dim(tile, r16);
+    const float bv = bias[base + head * kHead + dim];
+    const uint32_t pair = r16 < 8 ? dim : dim - 32;
+    const bool rotate = (is_q || is_k) && pos < capacity;
+    const float2 cs = rotate ? rope[size_t(pos) * (kHead / 2) + pair] : make_float2(0.f, 0.f);
+    const float sum = tile_matvec<2880, MODE>(codes, scales, tile, in, xs, xsum, red, part);
     if (r < q8::tile_rows) {
-        const uint32_t dim = qkv_dim(tile, r);
-        vals[r] = bias[base + head * kHead + dim] + sum;
+        vals[r] = bv + sum;
     }
     __syncthreads();
     if (r >= q8::tile_rows || pos >= capacity) {
         return;
     }
-    const uint32_t dim = qkv_dim(tile, r);
     float out = vals[r];
     if (!(is_q || is_k)) {
         v_cache[(size_t(pos) * kKvHeads + head) * kHead + dim] = out;
         return;
     }
     // model.cpp:236-242 with cos/sin precomputed by the host exactly as the reference does
-    const uint32_t pair = r < 8 ? dim : dim - 32;
-    const float2 cs = rope[size_t(pos) * (kHead / 2) + pair];
     const float x = vals[r < 8 ? r : r - 8];
     const float yv = vals[r < 8 ? r + 8 : r];
     out = r < 8 ? x * cs.x - yv * cs.y : x * cs.y + yv * cs.x;
@@ -198,32 +208,6 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(const uint8_t *__restrict
 
 int check_q8(const ttl_q8 *t, const char *who) {
     TTL_REQUIRE(t && t->codes && t->scales, TTL_ERR_INVALID, "%s: null tensor", who);
-    return TTL_OK;
-}
-
-stage::Input to_stage(const ttl_stage_input *in) {
-    stage::Input s;
-    s.base = in->base;
-    s.add = in->add;
-    s.add_w = in->add_weights;
-    s.add_k = in->add_count;
-    s.norm_w = in->norm_weight;
-    s.eps = in->epsilon;
-    s.v_out = in->sum_out;
-    return s;
-}
-
-int check_stage(const ttl_stage_input *in, uint32_t n, const char *who) {
-    TTL_REQUIRE(in && in->base, TTL_ERR_INVALID, "%s: null input", who);
-    TTL_REQUIRE(((uintptr_t)in->base & 15) == 0, TTL_ERR_INVALID, "%s: input must be 16-byte aligned", who);
-    TTL_REQUIRE(!in->add || (in->add_weights && in->add_count >= 1 && in->add_count <= 16 &&
-                             ((uintptr_t)in->add & 15) == 0),
-                TTL_ERR_INVALID, "%s: bad combine input", who);
-    TTL_REQUIRE(!in->norm_weight || ((uintptr_t)in->norm_weight & 15) == 0, TTL_ERR_INVALID,
-                "%s: norm weights must be 16-byte aligned", who);
-    TTL_REQUIRE(!in->sum_out || ((uintptr_t)in->sum_out & 15) == 0, TTL_ERR_INVALID,
-                "%s: sum_out must be 16-byte aligned", who);
-    (void)n;
     return TTL_OK;
 }
 
@@ -244,12 +228,16 @@ int ttl_q8_upload_dev(ttl_ctx *ctx, const void *gguf_dev, uint32_t rows, uint32_
     t->code_bytes = size_t(t->tiles) * q8::blocks_of(int(cols)) * q8::tile_rows * 32;
     t->scale_bytes = size_t(t->tiles) * q8::lanes_k * q8::tile_rows * q8::scale_pad_of(int(cols)) * 2;
     int32_t *perm = nullptr;
-    hipError_t err = hipMalloc(&t->codes, t->code_bytes);
+    const size_t tail = q8::tail_pad_bytes(int(cols));
+    hipError_t err = hipMalloc(&t->codes, t->code_bytes + tail);
     if (err == hipSuccess) {
         err = hipMalloc(&t->scales, t->scale_bytes);
     }
     if (err == hipSuccess) {
         err = hipMemsetAsync(t->scales, 0, t->scale_bytes, ctx->stream);
+    }
+    if (err == hipSuccess && tail) {
+        err = hipMemsetAsync(t->codes + t->code_bytes, 0, tail, ctx->stream);
     }
     if (err == hipSuccess && row_source) {
         err = hipMalloc(&perm, sizeof(int32_t) * rows);
@@ -360,19 +348,22 @@ int ttl_matvec_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
     TTL_REQUIRE(ctx && y_dev, TTL_ERR_INVALID, "ttl_matvec_q8_0: null argument");
     int rc = check_q8(w, "ttl_matvec_q8_0");
     if (rc == TTL_OK) {
-        rc = check_stage(in, w->cols, "ttl_matvec_q8_0");
+        rc = stage::check(in, "ttl_matvec_q8_0");
     }
     if (rc != TTL_OK) {
         return rc;
     }
-    const stage::Input s = to_stage(in);
-    if (w->cols == 2880) {
-        q8_matvec_kernel<2880><<<w->tiles, kThreads, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s, bias_dev,
-                                                                      residual_dev, y_dev);
-    } else {
-        q8_matvec_kernel<4096><<<w->tiles, kThreads, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s, bias_dev,
-                                                                      residual_dev, y_dev);
-    }
+    const stage::Input s = stage::from_abi(in);
+    stage::with_mode(s, [&](auto mode) {
+        constexpr int M = decltype(mode)::value;
+        if (w->cols == 2880) {
+            q8_matvec_kernel<2880, M><<<w->tiles, kThreads, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s,
+                                                                             bias_dev, residual_dev, y_dev);
+        } else {
+            q8_matvec_kernel<4096, M><<<w->tiles, kThreads, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s,
+                                                                             bias_dev, residual_dev, y_dev);
+        }
+    });
     TTL_LAUNCHED("q8_matvec_kernel");
     return TTL_OK;
 }
@@ -384,16 +375,19 @@ int ttl_attn_qkv(ttl_ctx *ctx, const ttl_q8 *qkv, const float *bias_dev, const t
                 "ttl_attn_qkv: null argument");
     int rc = check_q8(qkv, "ttl_attn_qkv");
     if (rc == TTL_OK) {
-        rc = check_stage(in, 2880, "ttl_attn_qkv");
+        rc = stage::check(in, "ttl_attn_qkv");
     }
     if (rc != TTL_OK) {
         return rc;
     }
     TTL_REQUIRE(qkv->rows == uint32_t(kQkvRows) && qkv->cols == 2880, TTL_ERR_SHAPE,
                 "ttl_attn_qkv: the QKV tensor must be 5120 x 2880 (q|k|v rows in ttl_qkv_row_source order)");
-    qkv_kernel<<<qkv->tiles, kThreads, 0, ctx->stream>>>(qkv->codes, qkv->scales, to_stage(in), bias_dev,
-                                                         reinterpret_cast<const float2 *>(rope_dev), position_dev,
-                                                         capacity, q_dev, k_cache_dev, v_cache_dev);
+    const stage::Input s = stage::from_abi(in);
+    stage::with_mode(s, [&](auto mode) {
+        qkv_kernel<decltype(mode)::value><<<qkv->tiles, kThreads, 0, ctx->stream>>>(
+            qkv->codes, qkv->scales, s, bias_dev, reinterpret_cast<const float2 *>(rope_dev), position_dev, capacity,
+            q_dev, k_cache_dev, v_cache_dev);
+    });
     TTL_LAUNCHED("qkv_kernel");
     return TTL_OK;
 }

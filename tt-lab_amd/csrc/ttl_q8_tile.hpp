@@ -30,7 +30,9 @@ struct Shape {
     static constexpr int iters = (blocks + lanes_k - 1) / lanes_k;
     static constexpr int per_wave = (iters + waves - 1) / waves;
     static constexpr int scale_pad = per_wave * waves;  // fp16 scales per lane
-    static constexpr int x_blocks = iters * lanes_k;
+    // x blocks staged: every block any wave's iterations touch; blocks past the row
+    // end are zero, so padding iterations add exactly zero (their scale is zero too)
+    static constexpr int x_blocks = scale_pad * lanes_k;
     static constexpr size_t tile_code_bytes = size_t(blocks) * tile_rows * 32;
     static constexpr size_t tile_scales = size_t(lanes_k) * tile_rows * scale_pad;
 };
@@ -42,6 +44,13 @@ __host__ __device__ inline int scale_pad_of(int cols) {
     const int iters = (cols / 32 + lanes_k - 1) / lanes_k;
     return ((iters + waves - 1) / waves) * waves;
 }
+// Zero bytes after the last tile: lanes of iterations past the last block read there
+// unconditionally (their scale is zero).
+__host__ __device__ inline size_t tail_pad_bytes(int cols) {
+    const int iters = (cols / 32 + lanes_k - 1) / lanes_k;
+    const int covered = ((iters + waves - 1) / waves) * waves * lanes_k;
+    return size_t(covered - cols / 32) * tile_rows * 32;
+}
 __host__ __device__ inline size_t code_offset(size_t tile, uint32_t block, uint32_t row, int cols) {
     return ((tile * blocks_of(cols) + block) * tile_rows + row) * 32;
 }
@@ -52,8 +61,9 @@ __host__ __device__ inline size_t scale_index(size_t tile, uint32_t block, uint3
 
 template <int K>
 struct TileRegs {
+    static_assert(Shape<K>::per_wave % 2 == 0, "scales are loaded in fp16 pairs");
     uint4 c[Shape<K>::per_wave][2];
-    float d[Shape<K>::per_wave];
+    uint32_t s[Shape<K>::per_wave / 2];  // fp16 scales, two per word
 };
 
 // Issues the loads of wave `wave`'s share of one tile.
@@ -65,15 +75,23 @@ __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *_
     const uint32_t r = lane % tile_rows, kl = lane / tile_rows;
     const uint16_t *sp = scales + tile * S::tile_scales + (size_t(kl) * tile_rows + r) * S::scale_pad +
                          wave * S::per_wave;
+    // the lane's per_wave fp16 scales are contiguous; loaded first, since every
+    // iteration needs them
+    const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sp);
+#pragma unroll
+    for (int j = 0; j < S::per_wave / 2; ++j) {
+        regs.s[j] = s32[j];
+    }
+    // Unconditional loads (see tail_pad_bytes): blocks past the row end have a zero
+    // scale in the padded scale layout, so their codes contribute nothing.
 #pragma unroll
     for (int j = 0; j < S::per_wave; ++j) {
         const int i = int(wave) * S::per_wave + j;
         const uint32_t kb = 4 * i + kl;
-        const bool ok = i < S::iters && kb < uint32_t(S::blocks);
         const uint4 *p = reinterpret_cast<const uint4 *>(codes + ((tile * S::blocks + kb) * tile_rows + r) * 32);
-        regs.c[j][0] = ok ? p[0] : make_uint4(0, 0, 0, 0);
-        regs.c[j][1] = ok ? p[1] : make_uint4(0, 0, 0, 0);
-        regs.d[j] = ok ? __half2float(__ushort_as_half(sp[j])) : 0.0f;
+        regs.c[j][0] = p[0];
+        regs.c[j][1] = p[1];
+        __builtin_amdgcn_sched_barrier(0);  // keep the issue order (see the compute)
     }
 }
 
@@ -102,11 +120,12 @@ __device__ __attribute__((always_inline)) inline float tile_compute(const TileRe
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < S::per_wave; ++j) {
+        // no bounds test: padding iterations have zero x and a zero scale
         const int i = int(wave) * S::per_wave + j;
-        if (i < S::iters) {
-            const uint32_t kb = 4 * i + kl;
-            acc = fmaf(regs.d[j], block_dot(regs.c[j][0], regs.c[j][1], xs + kb * stage::x_stride, xsum[kb]), acc);
-        }
+        const uint32_t kb = 4 * i + kl;
+        const uint16_t bits = uint16_t(regs.s[j / 2] >> (16 * (j % 2)));
+        const float d = __half2float(__ushort_as_half(bits));
+        acc = fmaf(d, block_dot(regs.c[j][0], regs.c[j][1], xs + kb * stage::x_stride, xsum[kb]), acc);
     }
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);

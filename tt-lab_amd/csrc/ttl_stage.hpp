@@ -14,6 +14,8 @@
 
 #include "ttl_internal.hpp"
 
+#include <type_traits>
+
 namespace stage {
 
 constexpr int x_stride = 36;  // padded LDS floats per 32-value block (bank-conflict-free b128 reads)
@@ -33,73 +35,195 @@ __host__ __device__ constexpr int red_floats(int x_blocks) {
     return x_blocks * 8 + 1;
 }
 
-// Writes blocks [0, x_blocks) of the padded layout; blocks >= n/32 are zero.
-// blockDim.x must be a multiple of 64.
-__device__ inline void stage(const Input &in, uint32_t n, uint32_t x_blocks, float *xs, float *red) {
-#pragma clang fp contract(off)
-    const uint32_t blocks = n / 32, groups = blocks * 8;
+// Host side: the C ABI's ttl_stage_input as the kernels take it, and its checks.
+inline Input from_abi(const ttl_stage_input *in) {
+    Input s;
+    s.base = in->base;
+    s.add = in->add;
+    s.add_w = in->add_weights;
+    s.add_k = in->add_count;
+    s.norm_w = in->norm_weight;
+    s.eps = in->epsilon;
+    s.v_out = in->sum_out;
+    return s;
+}
+
+inline int check(const ttl_stage_input *in, const char *who) {
+    TTL_REQUIRE(in && in->base, TTL_ERR_INVALID, "%s: null input", who);
+    TTL_REQUIRE(((uintptr_t)in->base & 15) == 0, TTL_ERR_INVALID, "%s: input must be 16-byte aligned", who);
+    TTL_REQUIRE(!in->add || (in->add_weights && in->add_count >= 1 && in->add_count <= 4 &&
+                             ((uintptr_t)in->add & 15) == 0),
+                TTL_ERR_INVALID, "%s: the combine needs 1..4 terms, 16-byte aligned", who);
+    TTL_REQUIRE(!in->norm_weight || ((uintptr_t)in->norm_weight & 15) == 0, TTL_ERR_INVALID,
+                "%s: norm weights must be 16-byte aligned", who);
+    TTL_REQUIRE(!in->sum_out || ((uintptr_t)in->sum_out & 15) == 0, TTL_ERR_INVALID,
+                "%s: sum_out must be 16-byte aligned", who);
+    return TTL_OK;
+}
+
+// Which optional steps a staging runs (a template parameter of the kernels, so
+// the staging is straight-line code: no branch between issuing the loads and
+// using them, which lets the compiler wait for each load only where it is used).
+enum Mode : int { kPlain = 0, kNorm = 1, kAdd = 2, kAddNorm = 3 };
+constexpr uint32_t kMaxAdd = 4;  // combine terms a staging holds in registers
+
+inline int mode_of(const Input &in) {
+    return (in.norm_w ? kNorm : 0) | (in.add ? kAdd : 0);
+}
+
+// Calls f(std::integral_constant<int, MODE>{}) for the staging's mode.
+template <class F>
+inline void with_mode(const Input &in, F &&f) {
+    switch (mode_of(in)) {
+    case kPlain:
+        f(std::integral_constant<int, kPlain>{});
+        break;
+    case kNorm:
+        f(std::integral_constant<int, kNorm>{});
+        break;
+    case kAdd:
+        f(std::integral_constant<int, kAdd>{});
+        break;
+    default:
+        f(std::integral_constant<int, kAddNorm>{});
+        break;
+    }
+}
+
+// Per-thread registers of a staging in flight: the loads of stage_load() land
+// here, so a kernel can issue them before its weight loads and finish the
+// staging while those are still in flight.
+template <int N, int XB, int NT, int MODE>
+struct Pending {
+    static_assert(N % 32 == 0 && N / 32 <= XB, "vector does not fit the layout");
+    static constexpr int groups = (N / 32) * 8;        // float4 groups of the vector
+    static constexpr int per = (XB * 8 + NT - 1) / NT;  // layout groups per thread
+    static constexpr bool add = (MODE & kAdd) != 0, norm = (MODE & kNorm) != 0;
+    float4 v[per];
+    float4 a[per][add ? kMaxAdd : 1];
+    float4 w[per];
+    float aw[kMaxAdd];
+};
+
+// Issues every global load of the staging, unconditionally: base, the combine
+// terms and their weights, the norm weights.  Threads past the vector's end
+// re-read its last group (discarded in stage_finish).
+template <int N, int XB, int NT, int MODE>
+__device__ __attribute__((always_inline)) inline void stage_load(const Input &in, Pending<N, XB, NT, MODE> &p) {
+    using P = Pending<N, XB, NT, MODE>;
     const float4 *b4 = reinterpret_cast<const float4 *>(in.base);
-    for (uint32_t i = threadIdx.x; i < x_blocks * 8; i += blockDim.x) {
-        const uint32_t block = i / 8, part = i % 8;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (block < blocks) {
-            v = b4[i];
-            if (in.add) {
-                float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
-                for (uint32_t r = 0; r < in.add_k; ++r) {
-                    const float w = in.add_w[r];
-                    const float4 a = reinterpret_cast<const float4 *>(in.add + size_t(r) * n)[i];
+    if constexpr (P::add) {
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxAdd; ++r) {
+            p.aw[r] = in.add_w[r < in.add_k ? r : 0];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < P::per; ++j) {
+        const uint32_t i = threadIdx.x + uint32_t(j) * NT;
+        const uint32_t c = i < uint32_t(P::groups) ? i : uint32_t(P::groups) - 1;
+        p.v[j] = b4[c];
+        if constexpr (P::norm) {
+            p.w[j] = reinterpret_cast<const float4 *>(in.norm_w)[c];
+        }
+        if constexpr (P::add) {
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxAdd; ++r) {
+                const uint32_t rr = r < in.add_k ? r : 0;
+                p.a[j][r] = reinterpret_cast<const float4 *>(in.add + size_t(rr) * N)[c];
+            }
+        }
+    }
+}
+
+// Completes a staging begun by stage_load(): writes blocks [0, XB) of the padded
+// layout (blocks >= N/32 are zero) and v_out, then applies the norm.
+// blockDim.x == NT.
+template <int N, int XB, int NT, int MODE>
+__device__ __attribute__((always_inline)) inline void stage_finish(const Input &in, const Pending<N, XB, NT, MODE> &p,
+                                                                   float *xs, float *red) {
+#pragma clang fp contract(off)
+    using P = Pending<N, XB, NT, MODE>;
+#pragma unroll
+    for (int j = 0; j < P::per; ++j) {
+        const uint32_t i = threadIdx.x + uint32_t(j) * NT;
+        if (i >= uint32_t(XB) * 8) {
+            continue;
+        }
+        const bool inside = i < uint32_t(P::groups);
+        float4 v = inside ? p.v[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (P::add) {
+            // model.cpp:323-337: out = 0; out += w_r * down_r (rank order); then x + out
+            float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxAdd; ++r) {
+                if (r < in.add_k) {
+                    const float w = p.aw[r];
+                    const float4 a = p.a[j][r];
                     m.x = m.x + w * a.x;
                     m.y = m.y + w * a.y;
                     m.z = m.z + w * a.z;
                     m.w = m.w + w * a.w;
                 }
+            }
+            if (inside) {
                 v.x = v.x + m.x;
                 v.y = v.y + m.y;
                 v.z = v.z + m.z;
                 v.w = v.w + m.w;
             }
+        }
+        if (inside) {
             if (in.v_out) {
                 reinterpret_cast<float4 *>(in.v_out)[i] = v;
             }
-            if (in.norm_w) {
+            if constexpr (P::norm) {
                 red[i] = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
         }
-        *reinterpret_cast<float4 *>(xs + block * x_stride + part * 4) = v;
+        *reinterpret_cast<float4 *>(xs + (i / 8) * x_stride + (i % 8) * 4) = v;
     }
     __syncthreads();
-    if (!in.norm_w) {
-        return;
-    }
-    if (threadIdx.x < 64) {
-        float s = 0.0f;
-        for (uint32_t i = threadIdx.x; i < groups; i += 64) {
-            s = s + red[i];
-        }
+    if constexpr (P::norm) {
+        if (threadIdx.x < 64) {
+            float s = 0.0f;
+            for (uint32_t i = threadIdx.x; i < uint32_t(P::groups); i += 64) {
+                s = s + red[i];
+            }
 #pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-            s = s + __shfl_xor(s, d);
+            for (int d = 32; d >= 1; d >>= 1) {
+                s = s + __shfl_xor(s, d);
+            }
+            if (threadIdx.x == 0) {
+                red[XB * 8] = 1.0f / sqrtf(s / float(N) + in.eps);
+            }
         }
-        if (threadIdx.x == 0) {
-            red[x_blocks * 8] = 1.0f / sqrtf(s / float(n) + in.eps);
+        __syncthreads();
+        const float scale = red[XB * 8];
+#pragma unroll
+        for (int j = 0; j < P::per; ++j) {
+            const uint32_t i = threadIdx.x + uint32_t(j) * NT;
+            if (i < uint32_t(P::groups)) {
+                float4 *q = reinterpret_cast<float4 *>(xs + (i / 8) * x_stride + (i % 8) * 4);
+                float4 v = *q;
+                const float4 w = p.w[j];
+                v.x = v.x * scale * w.x;
+                v.y = v.y * scale * w.y;
+                v.z = v.z * scale * w.z;
+                v.w = v.w * scale * w.w;
+                *q = v;
+            }
         }
+        __syncthreads();
     }
-    __syncthreads();
-    const float scale = red[x_blocks * 8];
-    const float4 *w4 = reinterpret_cast<const float4 *>(in.norm_w);
-    for (uint32_t i = threadIdx.x; i < groups; i += blockDim.x) {
-        const uint32_t block = i / 8, part = i % 8;
-        float4 *p = reinterpret_cast<float4 *>(xs + block * x_stride + part * 4);
-        float4 v = *p;
-        const float4 w = w4[i];
-        v.x = v.x * scale * w.x;
-        v.y = v.y * scale * w.y;
-        v.z = v.z * scale * w.z;
-        v.w = v.w * scale * w.w;
-        *p = v;
-    }
-    __syncthreads();
+}
+
+// Both halves at once, for kernels with nothing else to load first.
+template <int N, int XB, int NT, int MODE>
+__device__ __attribute__((always_inline)) inline void stage(const Input &in, float *xs, float *red) {
+    Pending<N, XB, NT, MODE> p;
+    stage_load(in, p);
+    stage_finish(in, p, xs, red);
 }
 
 }  // namespace stage

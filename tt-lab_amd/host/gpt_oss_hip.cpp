@@ -240,9 +240,8 @@ void HipGptOssModel::generate_weights() {
 //   RoPE, KV store), attention, output projection + residual, router + gate/up +
 //   SwiGLU (+ post-attention norm), down; final combine + output norm + logits;
 //   greedy argmax (writes the next token, advances the position).
-void HipGptOssModel::record_step() {
+int HipGptOssModel::enqueue_step() {
     const size_t L = spec_.layers;
-    check(ttl_capture_begin(ctx_), "ttl_capture_begin");
     int status = ttl_embedding_q8_0(ctx_, embedding_, spec_.vocab, token_, x_);
     for (size_t l = 0; l < L && status == TTL_OK; ++l) {
         Layer &layer = layers_[l];
@@ -292,6 +291,12 @@ void HipGptOssModel::record_step() {
     if (status == TTL_OK) {
         status = ttl_argmax(ctx_, spec_.vocab, logits_workspace_, token_, position_, history_, spec_.capacity);
     }
+    return status;
+}
+
+void HipGptOssModel::record_step() {
+    check(ttl_capture_begin(ctx_), "ttl_capture_begin");
+    const int status = enqueue_step();
     std::string error = status == TTL_OK ? "" : ttl_last_error();
     const int end = ttl_capture_end(ctx_, &step_);
     if (status != TTL_OK) {
@@ -319,10 +324,18 @@ void HipGptOssModel::set_position(int32_t token, size_t position) {
     check(ttl_memcpy_h2d(ctx_, position_, &state[1], sizeof(int32_t)), "ttl_memcpy_h2d");
 }
 
+void HipGptOssModel::run_step() {
+    if (use_graph_) {
+        check(ttl_graph_launch(ctx_, step_), "ttl_graph_launch");
+    } else {
+        check(enqueue_step(), "decode step");
+    }
+}
+
 const float *HipGptOssModel::forward(int32_t token, size_t position) {
     validate(token, position);
     set_position(token, position);
-    check(ttl_graph_launch(ctx_, step_), "ttl_graph_launch");
+    run_step();
     check(ttl_memcpy_d2h(ctx_, host_logits_.data(), logits_, sizeof(float) * spec_.vocab), "ttl_memcpy_d2h");
     return host_logits_.data();
 }
@@ -343,7 +356,7 @@ const float *HipGptOssModel::prefill(const int32_t *tokens, size_t count) {
     }
     for (size_t p = 0; p < count; ++p) {
         set_position(tokens[p], p);
-        check(ttl_graph_launch(ctx_, step_), "ttl_graph_launch");
+        run_step();
     }
     check(ttl_memcpy_d2h(ctx_, host_logits_.data(), logits_, sizeof(float) * spec_.vocab), "ttl_memcpy_d2h");
     return host_logits_.data();
@@ -367,7 +380,7 @@ std::vector<int32_t> HipGptOssModel::generate(int32_t token, size_t position, si
     }
     set_position(token, position);
     for (size_t s = 0; s < steps; ++s) {
-        check(ttl_graph_launch(ctx_, step_), "ttl_graph_launch");
+        run_step();
     }
     std::vector<int32_t> out(steps);
     if (steps) {
@@ -383,16 +396,60 @@ double HipGptOssModel::time_decode(int32_t token, size_t position, size_t warmup
     }
     set_position(token, position);
     for (size_t s = 0; s < warmup; ++s) {
-        check(ttl_graph_launch(ctx_, step_), "ttl_graph_launch");
+        run_step();
     }
     check(ttl_sync(ctx_), "ttl_sync");
     check(ttl_timer_start(ctx_), "ttl_timer_start");
     for (size_t s = 0; s < steps; ++s) {
-        check(ttl_graph_launch(ctx_, step_), "ttl_graph_launch");
+        run_step();
     }
     float ms = 0.0f;
     check(ttl_timer_stop(ctx_, &ms), "ttl_timer_stop");
     return double(ms) / double(steps);
+}
+
+double HipGptOssModel::time_expert_kernel(size_t reps) {
+    // The gate/up + SwiGLU launch of every layer, with the routing of the last step,
+    // replayed back to back: microseconds per launch.
+    const auto enqueue = [this]() {
+        int status = TTL_OK;
+        for (size_t l = 0; l < spec_.layers && status == TTL_OK; ++l) {
+            status = ttl_moe_gateup_swiglu(ctx_, &layers_[l].moe, residual_ + l * kHidden, indices_ + l * kUsed,
+                                           hidden_);
+        }
+        return status;
+    };
+    ttl_graph *graph = nullptr;
+    if (use_graph_) {
+        check(ttl_capture_begin(ctx_), "ttl_capture_begin");
+        const int status = enqueue();
+        const std::string error = status == TTL_OK ? "" : ttl_last_error();
+        check(ttl_capture_end(ctx_, &graph), "ttl_capture_end");
+        if (status != TTL_OK) {
+            ttl_graph_free(graph);
+            throw std::runtime_error("recording the expert kernels: " + error);
+        }
+    }
+    const auto run = [&]() {
+        check(graph ? ttl_graph_launch(ctx_, graph) : enqueue(), "expert kernels");
+    };
+    float ms = 0.0f;
+    try {
+        for (int w = 0; w < 3; ++w) {
+            run();
+        }
+        check(ttl_sync(ctx_), "ttl_sync");
+        check(ttl_timer_start(ctx_), "ttl_timer_start");
+        for (size_t r = 0; r < reps; ++r) {
+            run();
+        }
+        check(ttl_timer_stop(ctx_, &ms), "ttl_timer_stop");
+    } catch (...) {
+        ttl_graph_free(graph);
+        throw;
+    }
+    ttl_graph_free(graph);
+    return double(ms) * 1000.0 / double(reps * spec_.layers);
 }
 
 void HipGptOssModel::layer_state(size_t layer, float *x_in, float *residual, int32_t *indices, float *weights) const {

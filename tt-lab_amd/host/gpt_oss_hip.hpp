@@ -82,6 +82,15 @@ class HipGptOssModel {
     std::vector<int32_t> generate(int32_t token, size_t position, size_t steps);
     // Milliseconds per device-resident decode step (HIP events around graph replays).
     double time_decode(int32_t token, size_t position, size_t warmup, size_t steps);
+    // Microseconds per launch of the MXFP4 gate/up + SwiGLU kernel (all layers, the
+    // last step's routing, replayed `reps` times; HIP events on the model's stream).
+    double time_expert_kernel(size_t reps);
+
+    // Decode steps replay the captured step graph (default) or launch its kernels
+    // one by one on the model's stream (same kernels, same order).
+    void set_graph_replay(bool enabled) {
+        use_graph_ = enabled;
+    }
 
     // Last step's state, for layer-by-layer checks.
     void layer_state(size_t layer, float *x_in, float *residual, int32_t *indices, float *weights) const;
@@ -113,7 +122,9 @@ class HipGptOssModel {
     void *alloc(size_t bytes);
     void release();
     void generate_weights();
+    int enqueue_step();
     void record_step();
+    void run_step();
     void set_position(int32_t token, size_t position);
     void validate(int32_t token, size_t position) const;
 
@@ -137,6 +148,7 @@ class HipGptOssModel {
     float *logits_ = nullptr;
     void *logits_workspace_ = nullptr;
     ttl_graph *step_ = nullptr;
+    bool use_graph_ = true;
     std::vector<float> host_logits_;
 };
 

@@ -93,6 +93,14 @@ int ttlm_time_decode(ttlm_model *model, int32_t token, uint32_t position, uint32
     return guarded([&] { *ms_per_step = model->model->time_decode(token, position, warmup, steps); });
 }
 
+int ttlm_time_expert_kernel(ttlm_model *model, uint32_t reps, double *us_per_launch) {
+    return guarded([&] { *us_per_launch = model->model->time_expert_kernel(reps); });
+}
+
+int ttlm_set_graph_replay(ttlm_model *model, int enabled) {
+    return guarded([&] { model->model->set_graph_replay(enabled != 0); });
+}
+
 int ttlm_layer_state(ttlm_model *model, uint32_t layer, float *x_in, float *residual, int32_t *indices,
                      float *weights) {
     return guarded([&] { model->model->layer_state(layer, x_in, residual, indices, weights); });

@@ -89,6 +89,8 @@ def load_model_library():
         "ttlm_prefill": (i32, [vp, vp, u32, vp]),
         "ttlm_generate": (i32, [vp, C.c_int32, u32, u32, vp]),
         "ttlm_time_decode": (i32, [vp, C.c_int32, u32, u32, u32, C.POINTER(C.c_double)]),
+        "ttlm_time_expert_kernel": (i32, [vp, u32, C.POINTER(C.c_double)]),
+        "ttlm_set_graph_replay": (i32, [vp, i32]),
         "ttlm_layer_state": (i32, [vp, u32, vp, vp, vp, vp]),
         "ttlm_final_state": (i32, [vp, vp]),
         "ttlm_kv_cache": (i32, [vp, u32, u32, vp, vp]),
@@ -145,6 +147,14 @@ class Model:
         ms = C.c_double()
         _mcheck(self.lib.ttlm_time_decode(self.h, token, position, warmup, steps, C.byref(ms)), "ttlm_time_decode")
         return ms.value
+
+    def time_expert_kernel(self, reps):
+        us = C.c_double()
+        _mcheck(self.lib.ttlm_time_expert_kernel(self.h, reps, C.byref(us)), "ttlm_time_expert_kernel")
+        return us.value
+
+    def set_graph_replay(self, enabled):
+        _mcheck(self.lib.ttlm_set_graph_replay(self.h, 1 if enabled else 0), "ttlm_set_graph_replay")
 
     def layer_state(self, layer):
         x = np.empty(2880, np.float32)
@@ -400,6 +410,12 @@ class Device:
     def fill(self, buf, value, nbytes=None):
         _check(self.lib.ttl_fill_bytes(self.ctx, buf.ptr, value, buf.nbytes if nbytes is None else nbytes),
                "ttl_fill_bytes")
+
+    def copy(self, dst, src, nbytes):
+        """Device-to-device copy; dst/src are Buffers or device pointers (Buffer.offset)."""
+        d = dst.ptr if isinstance(dst, Buffer) else dst
+        s = src.ptr if isinstance(src, Buffer) else src
+        _check(self.lib.ttl_memcpy_d2d(self.ctx, d, s, nbytes), "ttl_memcpy_d2d")
 
     def timer_start(self):
         _check(self.lib.ttl_timer_start(self.ctx), "ttl_timer_start")
