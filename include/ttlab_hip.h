@@ -180,15 +180,23 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
  * combine: out = sum_r weights[r] * down_r, unfused, r = 0..k-1 (model.cpp:323,334-336). */
 int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
                           const int32_t *indices_dev, float *hidden_dev);
-/* Router + top-k + gate/up + SwiGLU in two launches (the routing is derived inside the
- * gate/up kernel); writes hidden f32 [used][expert_hidden], indices int32 [used] and
- * weights f32 [used] (model.cpp:293-332). */
+/* Router + top-k + gate/up + SwiGLU (three launches: router rows, the certified
+ * selection, gate/up); writes hidden f32 [used][expert_hidden], indices int32 [used]
+ * and weights f32 [used] (model.cpp:293-332). */
 int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
                          int32_t *indices_dev, float *weights_dev);
 int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
                  float *down_dev);
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
                     float *out_dev);
+/* down + combine + residual add in one launch (for used == 4; other counts run the
+ * down and combine kernels): out = residual + (0 + w_0 d_0 + ... + w_{k-1} d_{k-1})
+ * with d_r = down_e hidden_r + bd, in the reference's order (model.cpp:323-337,
+ * 592-594).  residual_dev may be NULL (out = the MoE output); down_dev, if not NULL,
+ * receives d (f32 [used][hidden]). */
+int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev,
+                         const int32_t *indices_dev, const float *weights_dev, const float *residual_dev,
+                         float *out_dev, float *down_dev);
 
 /* ---- matvec inputs ----------------------------------------------------------------- *
  * The vector a matvec reads, with the elementwise steps GptOssModel::forward runs

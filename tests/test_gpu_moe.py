@@ -169,3 +169,39 @@ def test_graph_replays_match_eager_bitwise(dev, layer32):
     graph.free()
     for b in (x, eager_out, graph_out, ib, wb):
         b.free()
+
+
+@pytest.mark.parametrize("used", [4, 2])
+def test_down_combine_adds_residual_in_reference_order(dev, used):
+    """ttl_moe_down_combine (the fused kernel for 4 experts, down + combine otherwise)
+    against its parts: the down outputs equal ttl_moe_down's bitwise, and
+    out = residual + (0 + w_0 d_0 + w_1 d_1 + ...) evaluated in f32 in that order
+    (model.cpp:323-337, 592-594) is bitwise what the kernel writes."""
+    host = HostLayer(32, used, biases=True, seed=0x77000003)
+    device = DeviceLayer(dev, host)
+    x = O.synth_normal(X_SEED, 300 + used, N)
+    residual = O.synth_normal(X_SEED, 400 + used, N, sigma=4.0)
+    xb, rb = dev.upload(x), dev.upload(residual)
+    ib, wb = dev.alloc(4 * used), dev.alloc(4 * used)
+    hidden = dev.alloc(used * N * 4)
+    ref_down, got_down, out = dev.alloc(used * N * 4), dev.alloc(used * N * 4), dev.alloc(N * 4)
+    dev.moe_decode(device.desc, xb, out, ib, wb)             # routing of x
+    dev.moe_gateup_swiglu(device.desc, xb, ib, hidden)
+    dev.moe_down(device.desc, hidden, ib, ref_down)
+    dev.moe_down_combine(device.desc, hidden, ib, wb, rb, out, got_down)
+    d = got_down.download(np.float32).reshape(used, N)
+    assert np.array_equal(d.view(np.uint32), ref_down.download(np.float32).reshape(used, N).view(np.uint32))
+    w = wb.download(np.float32)
+    m = np.zeros(N, np.float32)
+    for r in range(used):
+        m = (m + (w[r] * d[r]).astype(np.float32)).astype(np.float32)
+    expect = (residual + m).astype(np.float32)
+    assert np.array_equal(out.download(np.float32).view(np.uint32), expect.view(np.uint32))
+    # without a residual the output is the MoE layer itself, against the oracle
+    dev.moe_down_combine(device.desc, hidden, ib, wb, None, out)
+    ref, _, ref_idx, _ = host.oracle_moe(x, O.BODY_V4)
+    assert list(ib.download(np.int32)) == list(ref_idx)
+    assert O.rel_l2(out.download(np.float32), ref) <= TOL
+    for b in (xb, rb, ib, wb, hidden, ref_down, got_down, out):
+        b.free()
+    device.free()

@@ -103,9 +103,9 @@ constexpr int scale_pad = 24;                                 // per-lane scale 
 constexpr size_t tile_code_bytes = size_t(blocks) * tile_rows * 16;          // 23040
 constexpr size_t tile_scale_bytes = size_t(lanes_k) * tile_rows * scale_pad; // 1536
 constexpr uint8_t pad_scale = 127;                            // scale of padding blocks
-// Zero bytes after the last tile: the final iteration's lanes for blocks 90 and 91
-// read there unconditionally (their x is zero, and E2M1 codes are all finite).
-constexpr size_t tail_pad_bytes = size_t(iters * lanes_k - blocks) * tile_rows * 16;  // 512
+// Zero bytes after the last tile: iterations past the row end (blocks 90..95) read
+// there unconditionally (their x is zero, and E2M1 codes are all finite).
+constexpr size_t tail_pad_bytes = size_t(24 * lanes_k - blocks) * tile_rows * 16;  // 1536: up to block 95
 
 __host__ __device__ inline size_t code_chunk(size_t tile_index, uint32_t block, uint32_t row) {
     return (tile_index * blocks + block) * tile_rows + row;

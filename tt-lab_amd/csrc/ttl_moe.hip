@@ -16,9 +16,8 @@
 // recomputes every logit in the reference's sequential order and replays the
 // reference's selection sort (model.cpp:296-309) on them.
 //
-// route_workgroup() runs in the prologue of every gate/up workgroup (each one
-// derives its expert from the same data, deterministically), so routing costs
-// no kernel of its own; workgroup 0 publishes indices, weights and logits.
+// route_workgroup() runs in one workgroup after the rows are known and publishes
+// indices, weights and logits; the gate/up kernel then reads the indices.
 #include "ttl_mxfp4_tile.hpp"
 #include "ttl_stage.hpp"
 
@@ -175,22 +174,11 @@ struct RouteLds {
     float selected[kMaxUsed];
     float ref_logits[kMaxExperts];
     int32_t order[kMaxExperts];
+    double value[kMaxExperts];  // exact logits
+    double bound[kMaxExperts];
+    uint32_t rank[kMaxExperts];
     int certified;
 };
-
-// Wave-wide (value, bound, index) maximum: larger value, then lower index.
-__device__ inline void wave_argmax(double &v, double &b, int32_t &i) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const double ov = __shfl_xor(v, d), ob = __shfl_xor(b, d);
-        const int32_t oi = __shfl_xor(i, d);
-        if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            b = ob;
-            i = oi;
-        }
-    }
-}
 
 __device__ inline double wave_max(double v) {
 #pragma unroll
@@ -205,70 +193,67 @@ __device__ inline double wave_max(double v) {
 // (and bumps the exact-path counter) -- only one workgroup of a launch does that.
 // The exact path stages the router input into xs/red (the same values the router
 // rows saw); the certified path does not touch them.
-template <int MODE>
+template <int MODE, int NT>
 __device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
                                 float *red) {
     const uint32_t t = threadIdx.x, lane = t % 64;
-    if (t < 64) {
-        // ---- certified path: wave 0 ranks the exact values -------------------
-        double v[kPerLane], b[kPerLane];
-        bool finite = true;
-#pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
-            const uint32_t c = lane + 64 * j;
-            v[j] = c < experts ? scratch->exact[c] : -INFINITY;
-            b[j] = c < experts ? scratch->bound[c] : 0.0;
-            if (c < experts) {
-                finite = finite && isfinite(v[j]) && isfinite(b[j]);
-            }
+    // ---- certified path ------------------------------------------------------
+    // Thread c < experts ranks expert c by (exact value descending, index
+    // ascending) -- the order the reference's selection sort produces when no two
+    // values are within their error bounds -- and checks that separation for the
+    // top k: value - bound of rank r must exceed value + bound of every expert
+    // ranked below r.  Only LDS broadcast reads, no cross-lane chains.
+    if (t == 0) {
+        lds.certified = force_exact ? 0 : 1;
+    }
+    if (t < experts) {
+        const double v = scratch->exact[t], b = scratch->bound[t];
+        lds.value[t] = v;
+        lds.bound[t] = b;
+        if (!isfinite(v) || !isfinite(b)) {
+            lds.certified = 0;
         }
-        bool ok = !force_exact && __all(finite);
-        uint32_t taken = 0;
-        for (uint32_t r = 0; r < k && ok; ++r) {
-            double bv = -INFINITY, bb = 0.0;
-            int32_t bi = 0x7fffffff;
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                const int32_t c = int32_t(lane + 64 * j);
-                if (uint32_t(c) < experts && !(taken >> j & 1u) && (v[j] > bv || (v[j] == bv && c < bi))) {
-                    bv = v[j];
-                    bb = b[j];
-                    bi = c;
-                }
-            }
-            wave_argmax(bv, bb, bi);
-            if (uint32_t(bi) % 64 == lane) {
-                taken |= 1u << (uint32_t(bi) / 64);
-            }
-            double up = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                if (lane + 64 * j < experts && !(taken >> j & 1u)) {
-                    up = fmax(up, v[j] + b[j]);
-                }
-            }
-            up = wave_max(up);
-            ok = bv - bb > up;
-            if (lane == 0) {
-                lds.indices[r] = bi;
-                lds.selected[r] = float(bv);
-            }
+    }
+    __syncthreads();
+    if (t < experts) {
+        const double v = lds.value[t];
+        uint32_t rank = 0;
+#pragma unroll 16
+        for (uint32_t j = 0; j < experts; ++j) {
+            const double vj = lds.value[j];
+            rank += (vj > v || (vj == v && j < t)) ? 1u : 0u;
         }
-        if (lane == 0) {
-            lds.certified = ok;
-            if (ok) {
-                softmax_selected(lds.selected, k, lds.weights);
-            }
+        lds.rank[t] = rank;
+        if (rank < k) {
+            lds.indices[rank] = int32_t(t);
+            lds.selected[rank] = float(v);
         }
-        if (logits && ok) {
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                if (lane + 64 * j < experts) {
-                    logits[lane + 64 * j] = float(v[j]);
-                }
-            }
+    }
+    __syncthreads();
+    if (t < experts && lds.rank[t] < k) {
+        const uint32_t rank = lds.rank[t];
+        const double low = lds.value[t] - lds.bound[t];
+        double up = -INFINITY;
+#pragma unroll 16
+        for (uint32_t j = 0; j < experts; ++j) {
+            // arithmetic masking (finite values here), so no branch holds back the
+            // LDS reads of the unrolled iterations
+            const double mask = lds.rank[j] > rank ? 0.0 : -INFINITY;
+            up = fmax(up, (lds.value[j] + lds.bound[j]) + mask);
+        }
+        if (!(low > up)) {
+            lds.certified = 0;
+        }
+    }
+    __syncthreads();
+    if (lds.certified) {
+        if (t == 0) {
+            softmax_selected(lds.selected, k, lds.weights);
+        }
+        if (logits && t < experts) {
+            logits[t] = float(lds.value[t]);
         }
     }
     __syncthreads();
@@ -277,7 +262,7 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     }
 
     // ---- exact path: the reference's sequential sums (tensor.cpp:186-200) ----
-    stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
+    stage::stage<kRouterCols, mxt::x_blocks, NT, MODE>(in, xs, red);
     if (t < experts) {
 #pragma clang fp contract(off)
         const float *w = weight + size_t(t) * kRouterCols;
@@ -360,7 +345,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
     __shared__ RouteLds lds;
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    route_workgroup<MODE>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
+    route_workgroup<MODE, 256>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
     if (threadIdx.x < k) {
         indices[threadIdx.x] = lds.indices[threadIdx.x];
         weights_out[threadIdx.x] = lds.weights[threadIdx.x];
@@ -369,7 +354,22 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
 
 // ---- gate/up + SwiGLU -------------------------------------------------------
 
-constexpr int kGateUpWaves = 4;  // waves 0,1: gate tiles 2g, 2g+1; waves 2,3: the same up tiles
+// gate/up: one workgroup per (slot, 16-row tile); waves 0..3 split the gate
+// tile's K range, waves 4..7 the up tile's, then the SwiGLU of the 16 rows.
+constexpr int kSplit = 4;
+constexpr int kGateUpThreads = 2 * kSplit * 64;
+using GateUpSplit = mxt::Split<kSplit>;
+
+// Row `row` of a split-K tile: the waves' partial sums in wave order.
+template <int W>
+__device__ inline float sum_parts(const float (*part)[mx::tile_rows], uint32_t row) {
+    float sum = part[0][row];
+#pragma unroll
+    for (int k = 1; k < W; ++k) {
+        sum += part[k][row];
+    }
+    return sum;
+}
 
 // model.cpp:328-332
 __device__ inline float clamped_swiglu(float gate, float up) {
@@ -386,111 +386,167 @@ struct GateUpArgs {
     const float *up_bias;
     uint32_t rows, tiles, experts, k;
     stage::Input in;  // the layer input (optionally the residual stream + norm)
-    // routing: either given (expert_ids) or derived in the prologue from the router
     const int32_t *expert_ids;
-    const float *router_weight, *router_bias;
-    RouterScratch *scratch;
-    // outputs
     float *hidden;
-    int32_t *indices_out;
-    float *weights_out, *logits_out;
 };
 
-// ROUTED: the routing is derived in the prologue (a.expert_ids unused); otherwise
-// a.expert_ids gives it.  Separate instantiations keep the given-routing kernel
-// straight-line, so its weight loads overlap the staging and the compute.
-template <int MODE, bool ROUTED>
-__global__ __launch_bounds__(kGateUpWaves * 64) void gateup_swiglu_kernel(GateUpArgs a) {
-    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
-    __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    __shared__ float result[2][2 * mx::tile_rows];
-    __shared__ RouteLds route;
-    const uint32_t pairs = (a.tiles + 1) / 2;
-    const uint32_t slot = blockIdx.x / pairs;
+template <int MODE>
+__global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[GateUpSplit::x_floats];
+    __shared__ float red[stage::red_floats(GateUpSplit::x_blocks)];
+    __shared__ float part[2][kSplit][mx::tile_rows];
+    const uint32_t slot = blockIdx.x / a.tiles, tile = blockIdx.x % a.tiles;
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const uint32_t which = wave / 2;  // 0 gate, 1 up
-    const uint32_t tile = (blockIdx.x % pairs) * 2 + wave % 2;
+    const uint32_t which = wave / kSplit, w = wave % kSplit;  // which: 0 gate, 1 up
 
-    // input loads first (they depend on nothing), then the routing, then the
-    // expert's weight loads; the staging completes while those are in flight
-    stage::Pending<mx::cols, mxt::x_blocks, kGateUpWaves * 64, MODE> pending;
+    // input loads first (they depend on nothing), then the expert's weight loads;
+    // the staging completes while those are in flight
+    stage::Pending<mx::cols, GateUpSplit::x_blocks, kGateUpThreads, MODE> pending;
     stage::stage_load(a.in, pending);
-    int32_t e;
-    if constexpr (!ROUTED) {
-        e = a.expert_ids[slot];
-    } else {
-        const bool publish = blockIdx.x == 0;
-        route_workgroup<MODE>(a.router_weight, a.router_bias, a.in, a.experts, a.k, false, a.scratch, route,
-                        publish ? a.logits_out : nullptr, xs, red);
-        e = route.indices[slot];
-        if (publish && threadIdx.x < a.k) {
-            a.indices_out[threadIdx.x] = route.indices[threadIdx.x];
-            a.weights_out[threadIdx.x] = route.weights[threadIdx.x];
-        }
-    }
+    const int32_t e = a.expert_ids[slot];
     // All weight loads are unconditional (an invalid expert reads expert 0 and its
     // output becomes NaN below): loads under a branch make the compiler wait for
     // every load at the branch's end.
     const bool valid = e >= 0 && uint32_t(e) < a.experts;
     const uint32_t e_safe = valid ? uint32_t(e) : 0u;
-    const uint32_t tile_safe = tile < a.tiles ? tile : a.tiles - 1;
-    const float *b = which == 0 ? a.gate_bias : a.up_bias;
-    const float bias = b ? b[size_t(e_safe) * a.rows + tile_safe * mx::tile_rows + lane % mx::tile_rows] : 0.0f;
-    mxt::TileRegs regs;
-    mxt::tile_load(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales,
-                   size_t(e_safe) * a.tiles + tile_safe, lane, regs);
+    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
+    const size_t brow = size_t(e_safe) * a.rows + row;
+    const float gb = a.gate_bias ? a.gate_bias[brow] : 0.0f;
+    const float ub = a.up_bias ? a.up_bias[brow] : 0.0f;
+    mxt::SplitRegs<kSplit> regs;
+    mxt::split_load<kSplit>(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales,
+                            size_t(e_safe) * a.tiles + tile, w, lane, regs);
     stage::stage_finish(a.in, pending, xs, red);
-    const float acc = mxt::tile_compute(regs, xs, lane);
-    if (lane < mx::tile_rows && tile < a.tiles) {
-        result[which][(wave % 2) * mx::tile_rows + lane] = b ? acc + bias : acc;
+    const float acc = mxt::split_compute<kSplit>(regs, xs, w, lane);
+    if (lane < mx::tile_rows) {
+        part[which][w][lane] = acc;
     }
     __syncthreads();
-    if (threadIdx.x < 2 * mx::tile_rows) {
-        const uint32_t row = (blockIdx.x % pairs) * 2 * mx::tile_rows + threadIdx.x;
-        if (row < a.rows) {
-            a.hidden[size_t(slot) * a.rows + row] =
-                valid ? clamped_swiglu(result[0][threadIdx.x], result[1][threadIdx.x]) : __builtin_nanf("");
-        }
+    if (threadIdx.x < mx::tile_rows) {
+        const float g = sum_parts<kSplit>(part[0], threadIdx.x), u = sum_parts<kSplit>(part[1], threadIdx.x);
+        a.hidden[size_t(slot) * a.rows + row] =
+            valid ? clamped_swiglu(a.gate_bias ? g + gb : g, a.up_bias ? u + ub : u) : __builtin_nanf("");
     }
 }
 
 // ---- down matvec (per-slot input) -------------------------------------------
 
-constexpr int kDownWaves = 4;
-
-__global__ __launch_bounds__(kDownWaves * 64) void down_kernel(
+// one workgroup per (slot, 16-row tile), its four waves splitting K
+__global__ __launch_bounds__(kSplit * 64) void down_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const float *__restrict__ bias,
     uint32_t rows, uint32_t tiles, uint32_t experts, const float *__restrict__ hidden, uint32_t hidden_stride,
     const int32_t *__restrict__ expert_ids, float *__restrict__ down) {
-    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
-    __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    const uint32_t groups = (tiles + kDownWaves - 1) / kDownWaves;
-    const uint32_t slot = blockIdx.x / groups;
-    const uint32_t tile = (blockIdx.x % groups) * kDownWaves + threadIdx.x / 64;
-    const uint32_t lane = threadIdx.x % 64;
+    __shared__ __attribute__((aligned(16))) float xs[GateUpSplit::x_floats];
+    __shared__ float red[stage::red_floats(GateUpSplit::x_blocks)];
+    __shared__ float part[kSplit][mx::tile_rows];
+    const uint32_t slot = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+    const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
     // the slot's input first, then the (unconditional) weight loads
     stage::Input in{};
     in.base = hidden + size_t(slot) * hidden_stride;
-    stage::Pending<mx::cols, mxt::x_blocks, kDownWaves * 64, stage::kPlain> pending;
+    stage::Pending<mx::cols, GateUpSplit::x_blocks, kSplit * 64, stage::kPlain> pending;
     stage::stage_load(in, pending);
     const int32_t e = expert_ids[slot];
     const bool valid = e >= 0 && uint32_t(e) < experts;
     const uint32_t e_safe = valid ? uint32_t(e) : 0u;
-    const uint32_t tile_safe = tile < tiles ? tile : tiles - 1;
-    const uint32_t row = tile_safe * mx::tile_rows + lane % mx::tile_rows;
+    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
     const float b = bias ? bias[size_t(e_safe) * rows + row] : 0.0f;
-    mxt::TileRegs regs;
-    mxt::tile_load(codes, scales, size_t(e_safe) * tiles + tile_safe, lane, regs);
+    mxt::SplitRegs<kSplit> regs;
+    mxt::split_load<kSplit>(codes, scales, size_t(e_safe) * tiles + tile, w, lane, regs);
     stage::stage_finish(in, pending, xs, red);
-    const float acc = mxt::tile_compute(regs, xs, lane);
-    if (lane < mx::tile_rows && tile < tiles) {
-        down[size_t(slot) * rows + row] = !valid ? __builtin_nanf("") : (bias ? acc + b : acc);
+    const float acc = mxt::split_compute<kSplit>(regs, xs, w, lane);
+    if (lane < mx::tile_rows) {
+        part[w][lane] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < mx::tile_rows) {
+        const float sum = sum_parts<kSplit>(part, threadIdx.x);
+        down[size_t(slot) * rows + row] = !valid ? __builtin_nanf("") : (bias ? sum + b : sum);
+    }
+}
+
+// down + combine + residual for used == 4: one workgroup per 16-row tile holds all
+// four slots (16 waves: slot = wave / 4, K split over wave % 4), so it can finish
+// the rows: out = residual + (0 + w_0 d_0 + w_1 d_1 + w_2 d_2 + w_3 d_3), the
+// reference's combine order (model.cpp:323-337) and residual add (model.cpp:592-594).
+constexpr int kDcSlots = 4;
+constexpr int kDcThreads = kDcSlots * kSplit * 64;
+
+__global__ __launch_bounds__(kDcThreads) void down_combine_kernel(
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const float *__restrict__ bias,
+    uint32_t rows, uint32_t tiles, uint32_t experts, const float *__restrict__ hidden, uint32_t hidden_stride,
+    const int32_t *__restrict__ expert_ids, const float *__restrict__ weights, const float *__restrict__ residual,
+    float *__restrict__ out, float *__restrict__ down_out) {
+#pragma clang fp contract(off)
+    constexpr int kGroups = GateUpSplit::x_blocks * 8;                       // float4 groups per slot (padded)
+    constexpr int kPer = (kDcSlots * kGroups + kDcThreads - 1) / kDcThreads;  // 3
+    __shared__ __attribute__((aligned(16))) float xs[kDcSlots][GateUpSplit::x_floats];
+    __shared__ float part[kDcSlots][kSplit][mx::tile_rows];
+    const uint32_t tile = blockIdx.x;
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t slot = wave / kSplit, w = wave % kSplit;
+    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
+
+    // the four slots' inputs first (groups past the row end re-read group 0)
+    float4 hv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t f = threadIdx.x + uint32_t(k) * kDcThreads;
+        const uint32_t sl = f / kGroups, g = f % kGroups;
+        const bool inside = f < uint32_t(kDcSlots * kGroups) && g < uint32_t(mx::blocks * 8);
+        hv[k] = reinterpret_cast<const float4 *>(hidden + size_t(inside ? sl : 0) * hidden_stride)[inside ? g : 0];
+    }
+    // epilogue operands (threads < 16 finish the rows), then the weight loads
+    int32_t e[kDcSlots];
+    float b[kDcSlots], wr[kDcSlots];
+#pragma unroll
+    for (int r = 0; r < kDcSlots; ++r) {
+        e[r] = expert_ids[r];
+        wr[r] = weights[r];
+        const uint32_t er = (e[r] >= 0 && uint32_t(e[r]) < experts) ? uint32_t(e[r]) : 0u;
+        b[r] = bias ? bias[size_t(er) * rows + row] : 0.0f;
+    }
+    const float res = residual ? residual[row] : 0.0f;
+    const int32_t my_e = e[0] * (slot == 0) + e[1] * (slot == 1) + e[2] * (slot == 2) + e[3] * (slot == 3);
+    const uint32_t e_safe = (my_e >= 0 && uint32_t(my_e) < experts) ? uint32_t(my_e) : 0u;
+    mxt::SplitRegs<kSplit> regs;
+    mxt::split_load<kSplit>(codes, scales, size_t(e_safe) * tiles + tile, w, lane, regs);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t f = threadIdx.x + uint32_t(k) * kDcThreads;
+        const uint32_t sl = f / kGroups, g = f % kGroups;
+        if (f < uint32_t(kDcSlots * kGroups)) {
+            const float4 v = g < uint32_t(mx::blocks * 8) ? hv[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4 *>(&xs[sl][(g / 8) * mxt::x_stride + (g % 8) * 4]) = v;
+        }
+    }
+    __syncthreads();
+    const float acc = mxt::split_compute<kSplit>(regs, xs[slot], w, lane);
+    if (lane < mx::tile_rows) {
+        part[slot][w][lane] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < mx::tile_rows) {
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kDcSlots; ++r) {
+            float d = sum_parts<kSplit>(part[r], threadIdx.x);
+            d = bias ? d + b[r] : d;
+            if (!(e[r] >= 0 && uint32_t(e[r]) < experts)) {
+                d = __builtin_nanf("");
+            }
+            if (down_out) {
+                down_out[size_t(r) * rows + row] = d;
+            }
+            m = m + wr[r] * d;
+        }
+        out[row] = residual ? res + m : m;
     }
 }
 
 // model.cpp:323-337: out = 0; out += w_r * down_r for r = 0..k-1 (unfused).
 __global__ void combine_kernel(const float *__restrict__ down, const float *__restrict__ weights, uint32_t k,
-                               uint32_t n, float *__restrict__ out) {
+                               uint32_t n, const float *__restrict__ residual, float *__restrict__ out) {
 #pragma clang fp contract(off)
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) {
@@ -500,7 +556,7 @@ __global__ void combine_kernel(const float *__restrict__ down, const float *__re
     for (uint32_t r = 0; r < k; ++r) {
         acc = acc + weights[r] * down[size_t(r) * n + i];
     }
-    out[i] = acc;
+    out[i] = residual ? residual[i] + acc : acc;
 }
 
 }  // namespace
@@ -571,16 +627,21 @@ stage::Input layer_input(const ttl_moe_layer &L, const float *x) {
     return in;
 }
 
-void launch_router_rows(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, RouterScratch *scratch) {
-    const stage::Input in = layer_input(L, x);
+// Router + top-k + softmax: the exact rows and their bounds (one workgroup per
+// expert), then the certified selection (one workgroup), which publishes indices,
+// weights and logits.
+void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_t experts, uint32_t k,
+                   const stage::Input &in, bool force_exact, float *logits, int32_t *indices, float *weights) {
+    RouterScratch *scratch = &workspace(ctx)->router;
     stage::with_mode(in, [&](auto mode) {
-        router_rows_kernel<decltype(mode)::value><<<L.experts, kRouterThreads, 0, ctx->stream>>>(
-            L.router_weight, L.router_bias, in, scratch);
+        constexpr int M = decltype(mode)::value;
+        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch);
+        router_select_kernel<M><<<1, 256, 0, ctx->stream>>>(weight, bias, experts, in, k, force_exact ? 1u : 0u,
+                                                            scratch, logits, indices, weights);
     });
 }
 
-int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden,
-                  int32_t *indices_out, float *weights_out) {
+int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden) {
     GateUpArgs a;
     a.gate_codes = L.gate->codes;
     a.gate_scales = L.gate->scales;
@@ -594,21 +655,9 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
     a.k = L.used;
     a.in = layer_input(L, x);
     a.expert_ids = expert_ids;
-    a.router_weight = L.router_weight;
-    a.router_bias = L.router_bias;
-    a.scratch = &workspace(ctx)->router;
     a.hidden = hidden;
-    a.indices_out = indices_out;
-    a.weights_out = weights_out;
-    a.logits_out = workspace(ctx)->logits;
-    const uint32_t pairs = (a.tiles + 1) / 2;
     stage::with_mode(a.in, [&](auto mode) {
-        constexpr int M = decltype(mode)::value;
-        if (expert_ids) {
-            gateup_swiglu_kernel<M, false><<<pairs * L.used, kGateUpWaves * 64, 0, ctx->stream>>>(a);
-        } else {
-            gateup_swiglu_kernel<M, true><<<pairs * L.used, kGateUpWaves * 64, 0, ctx->stream>>>(a);
-        }
+        gateup_swiglu_kernel<decltype(mode)::value><<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
     });
     TTL_LAUNCHED("gateup_swiglu_kernel");
     return TTL_OK;
@@ -626,14 +675,10 @@ int ttl_router_topk(ttl_ctx *ctx, const float *weight_dev, const float *bias_dev
     if (rc != TTL_OK) {
         return rc;
     }
-    RouterScratch *scratch = &workspace(ctx)->router;
     ttl_moe_layer plain{};
-    const stage::Input in = layer_input(plain, x_dev);
-    router_rows_kernel<stage::kPlain><<<experts, kRouterThreads, 0, ctx->stream>>>(weight_dev, bias_dev, in, scratch);
-    TTL_LAUNCHED("router_rows_kernel");
-    router_select_kernel<stage::kPlain><<<1, 256, 0, ctx->stream>>>(weight_dev, bias_dev, experts, in, k, flags & 1u,
-                                                                    scratch, logits_dev, indices_dev, weights_dev);
-    TTL_LAUNCHED("router_select_kernel");
+    launch_router(ctx, weight_dev, bias_dev, experts, k, layer_input(plain, x_dev), (flags & 1u) != 0, logits_dev,
+                  indices_dev, weights_dev);
+    TTL_LAUNCHED("router kernels");
     return TTL_OK;
 }
 
@@ -654,7 +699,7 @@ int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float 
     if (rc != TTL_OK) {
         return rc;
     }
-    return launch_gateup(ctx, *layer, x_dev, indices_dev, hidden_dev, nullptr, nullptr);
+    return launch_gateup(ctx, *layer, x_dev, indices_dev, hidden_dev);
 }
 
 int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
@@ -666,8 +711,7 @@ int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_d
     }
     const ttl_moe_layer &L = *layer;
     const uint32_t down_tiles = L.hidden / mx::tile_rows;
-    const uint32_t groups = (down_tiles + kDownWaves - 1) / kDownWaves;
-    down_kernel<<<groups * L.used, kDownWaves * 64, 0, ctx->stream>>>(L.down->codes, L.down->scales, L.down_bias,
+    down_kernel<<<down_tiles * L.used, kSplit * 64, 0, ctx->stream>>>(L.down->codes, L.down->scales, L.down_bias,
                                                                        L.hidden, down_tiles, L.experts, hidden_dev,
                                                                        L.expert_hidden, indices_dev, down_dev);
     TTL_LAUNCHED("down_kernel");
@@ -687,16 +731,47 @@ int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
     if (rc != TTL_OK) {
         return rc;
     }
-    launch_router_rows(ctx, L, x_dev, &workspace(ctx)->router);
-    TTL_LAUNCHED("router_rows_kernel");
-    return launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
+    launch_router(ctx, L.router_weight, L.router_bias, L.experts, L.used, layer_input(L, x_dev), false,
+                  workspace(ctx)->logits, indices_dev, weights_dev);
+    TTL_LAUNCHED("router kernels");
+    return launch_gateup(ctx, L, x_dev, indices_dev, hidden_dev);
 }
 
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
                     float *out_dev) {
     TTL_REQUIRE(ctx && down_dev && weights_dev && out_dev, TTL_ERR_INVALID, "ttl_moe_combine: null argument");
     TTL_REQUIRE(k >= 1 && k <= kMaxUsed && n > 0, TTL_ERR_SHAPE, "ttl_moe_combine: bad k or n");
-    combine_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>(down_dev, weights_dev, k, n, out_dev);
+    combine_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>(down_dev, weights_dev, k, n, nullptr, out_dev);
+    TTL_LAUNCHED("combine_kernel");
+    return TTL_OK;
+}
+
+int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev,
+                         const int32_t *indices_dev, const float *weights_dev, const float *residual_dev,
+                         float *out_dev, float *down_dev) {
+    TTL_REQUIRE(ctx && hidden_dev && indices_dev && weights_dev && out_dev, TTL_ERR_INVALID,
+                "ttl_moe_down_combine: null argument");
+    int rc = check_layer(layer, "ttl_moe_down_combine");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const ttl_moe_layer &L = *layer;
+    const uint32_t tiles = L.hidden / mx::tile_rows;
+    if (L.used == uint32_t(kDcSlots)) {
+        down_combine_kernel<<<tiles, kDcThreads, 0, ctx->stream>>>(
+            L.down->codes, L.down->scales, L.down_bias, L.hidden, tiles, L.experts, hidden_dev, L.expert_hidden,
+            indices_dev, weights_dev, residual_dev, out_dev, down_dev);
+        TTL_LAUNCHED("down_combine_kernel");
+        return TTL_OK;
+    }
+    // other expert counts: the down matvecs, then the combine
+    float *down = down_dev ? down_dev : workspace(ctx)->down;
+    rc = ttl_moe_down(ctx, layer, hidden_dev, indices_dev, down);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    combine_kernel<<<ttl::blocks_for(L.hidden, 256), 256, 0, ctx->stream>>>(down, weights_dev, L.used, L.hidden,
+                                                                           residual_dev, out_dev);
     TTL_LAUNCHED("combine_kernel");
     return TTL_OK;
 }
@@ -716,14 +791,12 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
     ttl::MoeWorkspace *ws = workspace(ctx);
     int32_t *indices = indices_dev ? indices_dev : ws->indices;
     float *weights = weights_dev ? weights_dev : ws->weights;
-    launch_router_rows(ctx, L, x_dev, &ws->router);
-    TTL_LAUNCHED("router_rows_kernel");
-    rc = launch_gateup(ctx, L, x_dev, nullptr, ws->hidden, indices, weights);
+    launch_router(ctx, L.router_weight, L.router_bias, L.experts, L.used, layer_input(L, x_dev), false, ws->logits,
+                  indices, weights);
+    TTL_LAUNCHED("router kernels");
+    rc = launch_gateup(ctx, L, x_dev, indices, ws->hidden);
     if (rc == TTL_OK) {
-        rc = ttl_moe_down(ctx, layer, ws->hidden, indices, ws->down);
-    }
-    if (rc == TTL_OK) {
-        rc = ttl_moe_combine(ctx, ws->down, weights, L.used, L.hidden, out_dev);
+        rc = ttl_moe_down_combine(ctx, layer, ws->hidden, indices, weights, nullptr, out_dev, nullptr);
     }
     return rc;
 }

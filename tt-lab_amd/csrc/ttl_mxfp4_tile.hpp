@@ -116,4 +116,67 @@ __device__ __attribute__((always_inline)) inline float tile_compute(const TileRe
     return acc;
 }
 
+// ---- split-K: W waves share one tile ----------------------------------------
+//
+// Wave w of a tile takes iterations [w*P, w*P + P), P = ceil(23 / W), so the
+// per-wave dependency chain (and the time the last wave of a SIMD computes after
+// its data arrived) shrinks W-fold.  Iterations past 22 read blocks 92.. of the
+// padded layout: zero x in LDS, scale byte 127, codes from the next tile or the
+// tensor's zero tail, so they add exactly zero.
+template <int W>
+struct Split {
+    static constexpr int per = (mx::iters + W - 1) / W;   // iterations per wave
+    static constexpr int x_blocks = per * W * mx::lanes_k;  // staged x blocks (zero padded)
+    static constexpr int x_floats = x_blocks * x_stride;
+    static_assert(per % 2 == 0 && per * W <= mx::scale_pad, "scale bytes are read in pairs from the lane record");
+};
+
+template <int W>
+struct SplitRegs {
+    uint4 q[Split<W>::per];
+    uint32_t s[Split<W>::per / 2];  // the wave's scale bytes, two per word (low halves)
+};
+
+// Issues wave w's loads for one tile: its scale bytes first (every iteration
+// needs them), then its code chunks in iteration order.
+template <int W>
+__device__ __attribute__((always_inline)) inline void split_load(const uint8_t *__restrict__ codes,
+                                                                 const uint8_t *__restrict__ scales,
+                                                                 size_t tile_index, uint32_t w, uint32_t lane,
+                                                                 SplitRegs<W> &regs) {
+    constexpr int P = Split<W>::per;
+    const uint32_t r = lane % mx::tile_rows;
+    const uint32_t kl = lane / mx::tile_rows;
+    const uint16_t *ts = reinterpret_cast<const uint16_t *>(scales + tile_index * mx::tile_scale_bytes +
+                                                            size_t(lane) * mx::scale_pad + w * P);
+#pragma unroll
+    for (int j = 0; j < P / 2; ++j) {
+        regs.s[j] = ts[j];
+    }
+    const uint4 *tc = reinterpret_cast<const uint4 *>(codes) + tile_index * mx::blocks * mx::tile_rows + r;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        regs.q[j] = tc[size_t(4 * (w * P + j) + kl) * mx::tile_rows];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Wave w's partial dot products for the tile's 16 rows (row lane%16 in every lane).
+template <int W>
+__device__ __attribute__((always_inline)) inline float split_compute(const SplitRegs<W> &regs, const float *xs,
+                                                                    uint32_t w, uint32_t lane) {
+    constexpr int P = Split<W>::per;
+    const uint32_t kl = lane / mx::tile_rows;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        const uint32_t kb = 4 * (w * P + j) + kl;
+        const int e8 = int((regs.s[j / 2] >> (8 * (j % 2))) & 0xffu);
+        acc += __builtin_amdgcn_ldexpf(block_dot(regs.q[j], xs + kb * x_stride), e8 - 127);
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    return acc;
+}
+
 }  // namespace mxt

@@ -187,8 +187,12 @@ __device__ __attribute__((always_inline)) inline void stage_finish(const Input &
     if constexpr (P::norm) {
         if (threadIdx.x < 64) {
             float s = 0.0f;
-            for (uint32_t i = threadIdx.x; i < uint32_t(P::groups); i += 64) {
-                s = s + red[i];
+#pragma unroll
+            for (int k = 0; k < (P::groups + 63) / 64; ++k) {
+                const uint32_t i = threadIdx.x + 64u * uint32_t(k);
+                if (i < uint32_t(P::groups)) {
+                    s = s + red[i];
+                }
             }
 #pragma unroll
             for (int d = 32; d >= 1; d >>= 1) {

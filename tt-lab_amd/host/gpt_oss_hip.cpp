@@ -75,7 +75,6 @@ HipGptOssModel::HipGptOssModel(const SyntheticSpec &spec, int device) : spec_(sp
         history_ = static_cast<int32_t *>(alloc(sizeof(int32_t) * spec_.capacity));
         x_ = static_cast<float *>(alloc(sizeof(float) * (L + 1) * kHidden));
         residual_ = static_cast<float *>(alloc(sizeof(float) * L * kHidden));
-        down_ = static_cast<float *>(alloc(sizeof(float) * L * kUsed * kHidden));
         indices_ = static_cast<int32_t *>(alloc(sizeof(int32_t) * L * kUsed));
         weights_ = static_cast<float *>(alloc(sizeof(float) * L * kUsed));
         hidden_ = static_cast<float *>(alloc(sizeof(float) * kUsed * kHidden));
@@ -236,25 +235,17 @@ void HipGptOssModel::generate_weights() {
 }
 
 // One decode step (model.cpp:567-602) as launches on the context's stream:
-//   embedding; per layer: Q/K/V (+ previous MoE combine, residual, attention norm,
-//   RoPE, KV store), attention, output projection + residual, router + gate/up +
-//   SwiGLU (+ post-attention norm), down; final combine + output norm + logits;
-//   greedy argmax (writes the next token, advances the position).
+//   embedding; per layer: Q/K/V (+ attention norm, RoPE, KV store), attention,
+//   output projection + residual, router (+ post-attention norm), gate/up +
+//   SwiGLU, down + combine + residual; output norm + logits; greedy argmax
+//   (writes the next token, advances the position).
 int HipGptOssModel::enqueue_step() {
     const size_t L = spec_.layers;
     int status = ttl_embedding_q8_0(ctx_, embedding_, spec_.vocab, token_, x_);
     for (size_t l = 0; l < L && status == TTL_OK; ++l) {
         Layer &layer = layers_[l];
         ttl_stage_input in{};
-        if (l == 0) {
-            in.base = x_;
-        } else {
-            in.base = residual_ + (l - 1) * kHidden;
-            in.add = down_ + (l - 1) * kUsed * kHidden;
-            in.add_weights = weights_ + (l - 1) * kUsed;
-            in.add_count = uint32_t(kUsed);
-            in.sum_out = x_ + l * kHidden;
-        }
+        in.base = x_ + l * kHidden;
         in.norm_weight = layer.attn_norm;
         in.epsilon = norm_epsilon;
         status = ttl_attn_qkv(ctx_, layer.qkv, layer.qkv_bias, &in, rope_, position_, spec_.capacity, query_,
@@ -274,18 +265,17 @@ int HipGptOssModel::enqueue_step() {
                                           weights_ + l * kUsed);
         }
         if (status == TTL_OK) {
-            status = ttl_moe_down(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, down_ + l * kUsed * kHidden);
+            // the MoE output's combine and the residual add (model.cpp:592-594) are fused
+            // into the down projection; its output is the next layer's input
+            status = ttl_moe_down_combine(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, weights_ + l * kUsed,
+                                          residual_ + l * kHidden, x_ + (l + 1) * kHidden, nullptr);
         }
     }
     if (status == TTL_OK) {
         ttl_stage_input f{};
-        f.base = residual_ + (L - 1) * kHidden;
-        f.add = down_ + (L - 1) * kUsed * kHidden;
-        f.add_weights = weights_ + (L - 1) * kUsed;
-        f.add_count = uint32_t(kUsed);
+        f.base = x_ + L * kHidden;
         f.norm_weight = output_norm_;
         f.epsilon = norm_epsilon;
-        f.sum_out = x_ + L * kHidden;
         status = ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits_, logits_workspace_);
     }
     if (status == TTL_OK) {

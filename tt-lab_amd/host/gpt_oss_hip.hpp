@@ -141,7 +141,6 @@ class HipGptOssModel {
     int32_t *token_ = nullptr, *position_ = nullptr, *history_ = nullptr;
     float *x_ = nullptr;             // [layers + 1][2880]: layer inputs, then the final stream
     float *residual_ = nullptr;      // [layers][2880]
-    float *down_ = nullptr;          // [layers][4][2880]
     int32_t *indices_ = nullptr;     // [layers][4]
     float *weights_ = nullptr;       // [layers][4]
     float *hidden_ = nullptr, *query_ = nullptr, *attended_ = nullptr, *attn_workspace_ = nullptr;

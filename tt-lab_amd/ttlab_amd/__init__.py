@@ -226,6 +226,7 @@ def load_library():
         "ttl_moe_gateup_swiglu": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp]),
         "ttl_moe_down": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp]),
         "ttl_moe_combine": (i32, [vp, vp, vp, u32, u32, vp]),
+        "ttl_moe_down_combine": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
         "ttl_moe_route_gateup": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp, vp]),
         "ttl_synth_bf16": (i32, [vp, u64, u64, sz, sz, vp]),
         "ttl_q8_upload": (i32, [vp, vp, u32, u32, vp, u32, C.POINTER(vp)]),
@@ -474,6 +475,11 @@ class Device:
 
     def moe_down(self, layer, hidden, indices, down):
         _check(self.lib.ttl_moe_down(self.ctx, C.byref(layer), hidden.ptr, indices.ptr, down.ptr), "ttl_moe_down")
+
+    def moe_down_combine(self, layer, hidden, indices, weights, residual, out, down=None):
+        _check(self.lib.ttl_moe_down_combine(self.ctx, C.byref(layer), hidden.p, indices.p, weights.p,
+                                             residual.p if residual is not None else None, out.p,
+                                             down.p if down is not None else None), "ttl_moe_down_combine")
 
     def moe_combine(self, down, weights, k, n, out):
         _check(self.lib.ttl_moe_combine(self.ctx, down.ptr, weights.ptr, k, n, out.ptr), "ttl_moe_combine")
