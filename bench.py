@@ -40,6 +40,9 @@ SEED = 0x77000003
 # Algorithmic bytes of one gate/up+SwiGLU launch: 4 experts x (gate + up) x 2880 rows x
 # 1530 B, their f32 biases, x (f32 2880) read, hidden (f32 4x2880) written.
 GATEUP_BYTES = USED * 2 * N * 1530 + USED * 2 * N * 4 + N * 4 + USED * N * 4
+# HBM bytes one gate/up launch moves, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE
+# (scaled on a 256 MiB copy): profiles/decode_cfg3_hbm_bytes.txt.
+GATEUP_TRAFFIC_BYTES = 35_889_000
 
 
 def log(msg):
@@ -82,7 +85,7 @@ def gpu_decode(args):
                    "step_algorithmic_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
                    "step_frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
                      "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
                      "launch_us": round(us, 3)},
     }
@@ -152,7 +155,7 @@ def gpu_moe(args):
                    "experts": EXPERTS, "used": USED, "hidden": N, "layers_per_step": LAYERS,
                    "layer_algorithmic_GBps": round(layer_bytes * LAYERS / (ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
                      "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
                      "launch_us": round(us, 3)},
     }

@@ -28,7 +28,7 @@
  * "parity unpinned" for the bit level.
  *
  * The synthetic-input generators at the end are the shared specification that
- * the device generators in tt-lab_amd/csrc/synth.hip also implement; the tests
+ * the device generators in tt-lab_amd/csrc/ttl_synth.hip also implement; the tests
  * compare the two bit for bit.
  */
 #ifndef TTLAB_ORACLE_H
@@ -172,7 +172,7 @@ void orc_layer_forward(const orc_layer *layer, size_t layer_index, size_t positi
                        float *query, float *attended, float *residual, float *router, int64_t *indices,
                        float *weights);
 
-/* ---- synthetic inputs (shared specification with tt-lab_amd/csrc/synth.hip) */
+/* ---- synthetic inputs (shared specification with tt-lab_amd/csrc/ttl_synth.hip) */
 uint64_t orc_hash(uint64_t seed, uint64_t stream, uint64_t index);
 /* N(0,1) drawn as an Irwin-Hall sum of 12 24-bit uniforms in exact integer arithmetic,
  * times sigma, plus mean. */

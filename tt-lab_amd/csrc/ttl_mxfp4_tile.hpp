@@ -91,10 +91,11 @@ __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *_
     // as the compute consumes them): the last iteration's lanes for blocks 90 and 91
     // read the next tile or the tensor's zero tail; their x is zero.
     // Issued in iteration order (the scheduler may not reorder them), so that the
-    // compute can wait for each chunk alone as it arrives.
+    // compute can wait for each chunk alone as it arrives.  Blocks 90 and 91 of the
+    // last iteration re-read block 89 (zero x there).
 #pragma unroll
     for (int i = 0; i < mx::iters; ++i) {
-        regs.q[i] = tc[size_t(4 * i + kl) * mx::tile_rows];
+        regs.q[i] = tc[size_t(min(uint32_t(4 * i) + kl, uint32_t(mx::blocks - 1))) * mx::tile_rows];
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -156,7 +157,10 @@ __device__ __attribute__((always_inline)) inline void split_load(const uint8_t *
     const uint4 *tc = reinterpret_cast<const uint4 *>(codes) + tile_index * mx::blocks * mx::tile_rows + r;
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-        regs.q[j] = tc[size_t(4 * (w * P + j) + kl) * mx::tile_rows];
+        // blocks past the row end re-read block 89 (same address as another lane of
+        // the load: no extra memory traffic); their x is zero
+        const uint32_t kb = min(uint32_t(4 * (w * P + j)) + kl, uint32_t(mx::blocks - 1));
+        regs.q[j] = tc[size_t(kb) * mx::tile_rows];
         __builtin_amdgcn_sched_barrier(0);
     }
 }

@@ -86,8 +86,10 @@ __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *_
     // scale in the padded scale layout, so their codes contribute nothing.
 #pragma unroll
     for (int j = 0; j < S::per_wave; ++j) {
+        // blocks past the row end re-read the last block (a duplicate address within the
+        // load, so no extra memory traffic); their scale is zero
         const int i = int(wave) * S::per_wave + j;
-        const uint32_t kb = 4 * i + kl;
+        const uint32_t kb = min(uint32_t(4 * i) + kl, uint32_t(S::blocks - 1));
         const uint4 *p = reinterpret_cast<const uint4 *>(codes + ((tile * S::blocks + kb) * tile_rows + r) * 32);
         regs.c[j][0] = p[0];
         regs.c[j][1] = p[1];
