@@ -109,7 +109,9 @@ size_t ttl_mxfp4_bytes(const ttl_mxfp4 *tensor);
 /* Decodes expert `expert` to f32 [rows][cols] on the device (out_dev).
  * mode 0: the reference's table, weight = 2^(e-128) * int(code) (tensor.cpp:34-74).
  * mode 1: the decode the matvec kernels perform: the gfx950 fp4 conversion
- *         instruction, then the block scale 2^(e-127) applied by ldexp. */
+ *         instruction, then the block scale 2^(e-127) applied by ldexp.
+ * mode 2: the decode the batched (MFMA) kernels perform: the gfx950 conversion to
+ *         bf16 with the E8M0 scale folded in, widened to f32. */
 int ttl_mxfp4_dequantize(ttl_ctx *ctx, const ttl_mxfp4 *tensor, uint32_t expert, int mode, float *out_dev);
 
 /* y = W[expert] x + bias[expert].  Replaces matvec_add_mxfp4_2880
@@ -197,6 +199,47 @@ int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_de
 int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev,
                          const int32_t *indices_dev, const float *weights_dev, const float *residual_dev,
                          float *out_dev, float *down_dev);
+
+/* ---- batched prefill on MFMA ------------------------------------- *
+ * bf16 MFMA with f32 accumulation.  Every product is exact: the weights E2M1 x
+ * 2^(e-127) are bf16 values for E8M0 e in 1..254, and f32 activations are split
+ * into three bf16 planes that sum to them exactly.  Results therefore agree with
+ * the reference's f32 sums to rounding (relative L2 <= 1e-5), not bit for bit.
+ * workspace_dev is caller-owned device memory, 256-byte aligned, of at least the
+ * size the matching *_workspace_bytes function returns (workspace_bytes says how
+ * much the caller holds; a smaller workspace is an error); calls sharing a
+ * workspace must not overlap. */
+
+#define TTL_DTYPE_F32 0
+#define TTL_DTYPE_BF16 1
+
+/* out[tokens[s]][r] = bias[expert][r] + sum_k W[expert][r][k] x[tokens[s]][k] for
+ * s < count; other rows of out are untouched.  Replaces transpose_selected +
+ * matmul_add_mxfp4_selected_transposed (tensor.h:38-51, tensor.cpp:306-495): the
+ * reference transposes the selected rows of x on the host; here x_dev is the
+ * untransposed f32 [x_rows][x_stride] and tokens_dev int32 [count] in device memory
+ * (a token >= x_rows is skipped).  out_dev is f32 [x_rows][rows].  w->rows must be
+ * a multiple of 192 (the reference's only shape is 2880). */
+size_t ttl_matmul_mxfp4_selected_workspace_bytes(uint32_t count);
+int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
+                              uint32_t x_stride, uint32_t x_rows, const int32_t *tokens_dev, uint32_t count,
+                              float *out_dev, uint32_t expert, void *workspace_dev, size_t workspace_bytes);
+
+/* The expert half of GptOssModel::moe_batch (model.cpp:378-460) for `count` tokens
+ * with given routing: indices_dev int32 [count][used] and weights_dev f32
+ * [count][used] (rank order, as the router writes them).  Pairs are bucketed by
+ * expert in the reference's order (expert, then token, then rank); per expert the
+ * gate and up GEMMs with the clamped SwiGLU, then the down GEMM; then
+ * out[p] = sum over p's experts in ascending expert index of w * down (unfused,
+ * from 0; model.cpp:450-459).  x_dev is [count][2880] of x_dtype (TTL_DTYPE_F32 or
+ * TTL_DTYPE_BF16); out_dev f32 [count][2880].  A token with an expert index out of
+ * range gets NaN outputs.  Unlike the reference, buckets of at most 4 tokens also
+ * take the GEMM (the reference switches to per-token matvecs there,
+ * model.cpp:22,404; the two differ only in f32 rounding). */
+size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used, int x_dtype);
+int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
+                            uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
+                            void *workspace_dev, size_t workspace_bytes);
 
 /* ---- matvec inputs ----------------------------------------------------------------- *
  * The vector a matvec reads, with the elementwise steps GptOssModel::forward runs

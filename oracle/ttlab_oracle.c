@@ -457,18 +457,16 @@ void orc_moe(const orc_moe_layer *layer, const float *input, float *output, int 
     }
 }
 
-/* model.cpp:340-461.  Router via the F32 matmul, per-token top-k, buckets per
- * expert in token order, then per expert (ascending index): per-token matvecs
- * when at most 4 tokens chose it (model.cpp:22,404), the selected-token matmul
- * otherwise; SwiGLU; down; out[token] += w * down in expert-index order. */
-void orc_moe_batch(const orc_moe_layer *layer, const float *input, size_t count, float *output, int body) {
+/* model.cpp:378-460 with the routing given: buckets per expert in token order,
+ * then per expert (ascending index): per-token matvecs when at most 4 tokens
+ * chose it (model.cpp:22,404), the selected-token matmul otherwise; SwiGLU; down;
+ * out[token] += w * down in expert-index order, from 0. */
+void orc_moe_batch_experts(const orc_moe_layer *layer, const float *input, size_t count, const int64_t *indices,
+                           const float *weights, float *output, int body) {
     const size_t H = layer->hidden, F = layer->expert_hidden, E = layer->experts, K = layer->used;
     const size_t width = H > F ? H : F;
-    float *router = malloc(sizeof(float) * count * E);
     float *workspace = malloc(sizeof(float) * count * 4 + sizeof(float) * count);
     float *transposed = malloc(sizeof(float) * count * width);
-    int64_t *indices = malloc(sizeof(int64_t) * count * K);
-    float *weights = malloc(sizeof(float) * count * K);
     size_t *bucket_tokens = malloc(sizeof(size_t) * count * E);
     float *bucket_weights = malloc(sizeof(float) * count * E);
     size_t *bucket_counts = calloc(E, sizeof(size_t));
@@ -477,11 +475,6 @@ void orc_moe_batch(const orc_moe_layer *layer, const float *input, size_t count,
     float *hidden = malloc(sizeof(float) * count * F);
     float *down = malloc(sizeof(float) * count * H);
 
-    orc_matmul_add_f32(layer->router_weight, layer->router_bias, E, H, input, count, router, workspace,
-                       transposed);
-    for (size_t p = 0; p < count; ++p) {
-        orc_router_topk(router + p * E, E, K, indices + p * K, weights + p * K);
-    }
     for (size_t i = 0; i < count * H; ++i) {
         output[i] = 0.0f;
     }
@@ -537,11 +530,8 @@ void orc_moe_batch(const orc_moe_layer *layer, const float *input, size_t count,
             }
         }
     }
-    free(router);
     free(workspace);
     free(transposed);
-    free(indices);
-    free(weights);
     free(bucket_tokens);
     free(bucket_weights);
     free(bucket_counts);
@@ -549,6 +539,29 @@ void orc_moe_batch(const orc_moe_layer *layer, const float *input, size_t count,
     free(up);
     free(hidden);
     free(down);
+}
+
+/* model.cpp:340-461.  Router via the F32 matmul, per-token top-k (model.cpp:347-377),
+ * then the experts as orc_moe_batch_experts. */
+void orc_moe_batch(const orc_moe_layer *layer, const float *input, size_t count, float *output, int body) {
+    const size_t H = layer->hidden, E = layer->experts, K = layer->used;
+    float *router = malloc(sizeof(float) * count * E);
+    float *workspace = malloc(sizeof(float) * count * 4 + sizeof(float) * count);
+    float *transposed = malloc(sizeof(float) * count * H);
+    int64_t *indices = malloc(sizeof(int64_t) * count * K);
+    float *weights = malloc(sizeof(float) * count * K);
+
+    orc_matmul_add_f32(layer->router_weight, layer->router_bias, E, H, input, count, router, workspace,
+                       transposed);
+    for (size_t p = 0; p < count; ++p) {
+        orc_router_topk(router + p * E, E, K, indices + p * K, weights + p * K);
+    }
+    orc_moe_batch_experts(layer, input, count, indices, weights, output, body);
+    free(router);
+    free(workspace);
+    free(transposed);
+    free(indices);
+    free(weights);
 }
 
 /* ------------------------------------------------------------------------- */

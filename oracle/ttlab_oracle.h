@@ -117,6 +117,10 @@ void orc_moe(const orc_moe_layer *layer, const float *input, float *output, int 
 
 /* model.cpp:340-461: prefill MoE over `count` tokens (layer-major, expert-order combine). */
 void orc_moe_batch(const orc_moe_layer *layer, const float *input, size_t count, float *output, int body);
+/* model.cpp:378-460, the experts of orc_moe_batch with the routing given: indices
+ * int64 [count][used] (each in 0..experts-1), weights f32 [count][used]. */
+void orc_moe_batch_experts(const orc_moe_layer *layer, const float *input, size_t count, const int64_t *indices,
+                           const float *weights, float *output, int body);
 
 /* ---- a10: RoPE and attention with sinks (model.cpp:124-139,230-290) ------ */
 void orc_rope_frequencies(float *frequencies /* [32] */);

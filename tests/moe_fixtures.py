@@ -17,7 +17,11 @@ ROUTER_STREAM, BIAS_STREAM = 20, 30
 
 
 class HostLayer:
-    def __init__(self, experts=32, used=4, biases=False, seed=W_SEED):
+    """Host copy of a synthetic MoE layer.  fill_experts (optional) limits the expert
+    matrices generated to those experts; the others stay zero (for oracle runs that
+    only read the listed experts)."""
+
+    def __init__(self, experts=32, used=4, biases=False, seed=W_SEED, fill_experts=None):
         self.experts, self.used, self.seed = experts, used, seed
         self.router_w = O.synth_normal_bf16(seed, ROUTER_STREAM, experts * N, 0.02)
         if biases:
@@ -30,9 +34,13 @@ class HostLayer:
             self.gate_b = np.zeros(experts * N, np.float32)
             self.up_b = np.zeros(experts * N, np.float32)
             self.down_b = np.zeros(experts * N, np.float32)
-        self.gate = np.concatenate([O.synth_mxfp4(seed, GATE_STREAM + e, N * 90) for e in range(experts)])
-        self.up = np.concatenate([O.synth_mxfp4(seed, UP_STREAM + e, N * 90) for e in range(experts)])
-        self.down = np.concatenate([O.synth_mxfp4(seed, DOWN_STREAM + e, N * 90) for e in range(experts)])
+        per = N * 90 * 17
+        fill = range(experts) if fill_experts is None else sorted(set(int(e) for e in fill_experts))
+        for name, stream in (("gate", GATE_STREAM), ("up", UP_STREAM), ("down", DOWN_STREAM)):
+            arr = np.zeros(experts * per, np.uint8)
+            for e in fill:
+                arr[e * per:(e + 1) * per] = O.synth_mxfp4(seed, stream + e, N * 90)
+            setattr(self, name, arr)
 
     def oracle_struct(self):
         s = O.MoeLayer()

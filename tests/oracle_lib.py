@@ -80,6 +80,7 @@ def _load():
         "orc_swiglu": (None, [_f32p, _f32p, _sz, _f32p]),
         "orc_moe": (None, [C.POINTER(MoeLayer), _f32p, _f32p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
         "orc_moe_batch": (None, [C.POINTER(MoeLayer), _f32p, _sz, _f32p, C.c_int]),
+        "orc_moe_batch_experts": (None, [C.POINTER(MoeLayer), _f32p, _sz, _i64p, _f32p, _f32p, C.c_int]),
         "orc_rope_frequencies": (None, [_f32p]),
         "orc_apply_rope": (None, [_f32p, _sz, _sz, _f32p]),
         "orc_attention": (None, [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _f32p, _f32p]),

@@ -92,6 +92,24 @@ def test_matvec_decode_instruction_lane_layout(dev):
     t.free()
 
 
+def test_prefill_decode_to_bf16_is_exact(dev):
+    """The bf16 conversion with the E8M0 scale folded in (the MFMA kernels' weights)
+    gives the reference's values for every code and every scale the MFMA path
+    supports (E8M0 1..254), code 8 again as -0.0."""
+    blocks = exhaustive_decode_blocks()
+    t = dev.mxfp4_upload(blocks, 16, N, 1)
+    got = t.dequantize(0, mode=2).reshape(-1)
+    expected = O.dequant_mxfp4(blocks)
+    b = blocks.reshape(-1, 17)
+    codes = np.concatenate([b[:, 1:] & 15, b[:, 1:] >> 4], axis=1).ravel()
+    scales = np.repeat(b[:, 0], 32)
+    same = (got.view(np.uint32) == expected.view(np.uint32)) | ((codes == 8) & (got == 0) & (expected == 0))
+    bad_scales = sorted(set(scales[~same].tolist()))
+    print("E8M0 values whose bf16 decode differs from the reference:", bad_scales)
+    assert all(e in (0, 255) for e in bad_scales), bad_scales
+    t.free()
+
+
 def test_matvec_reference_kat_1080_25(dev):
     # tests/host_dispatch.cpp:92-107
     expert_bytes = N * 90 * 17

@@ -1,0 +1,220 @@
+"""GPU parity of the batched prefill path (MFMA) against the oracle.
+
+ttl_matmul_mxfp4_selected vs orc_matmul_add_mxfp4_selected_transposed
+(tensor.cpp:306-495) and ttl_moe_prefill_experts vs orc_moe_batch_experts
+(model.cpp:378-460).  Exact: the reference's selected-matmul known answer
+(tests/host_dispatch.cpp:108-126) and the rows it must leave untouched.
+Tolerance: relative L2 <= 1e-5 per token and overall (the MFMA sums exact
+products in f32 in another order than the reference).  At the full config-2
+shape: the oracle on a sample of tokens (a token's result depends on no other
+token), and bitwise invariance under token and rank permutations.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import ttlab_amd
+from moe_fixtures import N, DeviceLayer, HostLayer
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = ttlab_amd.Device(0)
+    yield d
+    d.close()
+
+
+def balanced_routing(count, experts, used, seed):
+    """Config-2 routing: every expert chosen equally often, `used` distinct experts per
+    token, weights = softmax of N(0,1) logits (rank order)."""
+    assert (count * used) % experts == 0 and experts % used == 0
+    rng = np.random.RandomState(seed)
+    step = experts // used
+    base = np.arange(count) % experts
+    idx = np.stack([(base + step * r) % experts for r in range(used)], axis=1)
+    labels = rng.permutation(experts)
+    idx = labels[idx][rng.permutation(count)]
+    for p in range(count):
+        idx[p] = idx[p][rng.permutation(used)]
+    logits = rng.randn(count, used)
+    w = np.exp(logits - logits.max(1, keepdims=True))
+    return idx.astype(np.int32), (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def kat_matrix():
+    expert_bytes = N * 90 * 17
+    data = np.zeros(2 * expert_bytes, np.uint8)
+    blocks = data[expert_bytes:].reshape(-1, 17)
+    blocks[:, 0] = 127
+    blocks[:, 1:] = 0x21
+    return data
+
+
+@pytest.mark.parametrize("count", [3, 16, 17, 64, 65])
+def test_selected_matmul_reference_kat(dev, count):
+    # tests/host_dispatch.cpp:108-126: expert 1, scale 127, bytes 0x21, bias 0.25,
+    # tokens[s] = count - s with input (s+1)/2 -> 1080 (s+1) + 0.25; token 0 untouched
+    w = dev.mxfp4_upload(kat_matrix(), N, N, 2)
+    bias = dev.upload(np.full(2 * N, 0.25, np.float32))
+    x = np.zeros((count + 1, N), np.float32)
+    tokens = np.array([count - s for s in range(count)], np.int32)
+    for s in range(count):
+        x[count - s] = (s + 1) * 0.5
+    xb, tb = dev.upload(x), dev.upload(tokens)
+    out = dev.upload(np.full((count + 1) * N, -1.0, np.float32))
+    dev.matmul_mxfp4_selected(w, bias, xb, N, count + 1, tb, count, out, 1)
+    got = out.download(np.float32).reshape(count + 1, N)
+    assert np.all(got[0] == -1.0)
+    for s in range(count):
+        assert np.all(got[count - s] == np.float32(1080.0 * (s + 1) + 0.25)), s
+    for b in (bias, xb, tb, out):
+        b.free()
+    w.free()
+
+
+@pytest.mark.parametrize("count", [1, 5, 64, 70])
+def test_selected_matmul_matches_oracle(dev, count):
+    rows_x = 80
+    blocks = O.synth_mxfp4(0x77000002, 7, 2 * N * 90)
+    bias = O.synth_normal(0x77000002, 8, 2 * N, sigma=0.5)
+    x = O.synth_normal(0x78000002, 9, rows_x * N).reshape(rows_x, N)
+    tokens = np.random.RandomState(count).permutation(rows_x)[:count].astype(np.int32)
+    w = dev.mxfp4_upload(blocks, N, N, 2)
+    bb, xb, tb = dev.upload(bias), dev.upload(x), dev.upload(tokens)
+    out = dev.upload(np.full(rows_x * N, np.nan, np.float32))
+    dev.matmul_mxfp4_selected(w, bb, xb, N, rows_x, tb, count, out, 1)
+    got = out.download(np.float32).reshape(rows_x, N)
+    tr = np.empty(N * count, np.float32)
+    O.lib.orc_transpose_selected(N, np.ascontiguousarray(x).ravel(), tokens.astype(np.uintp), count, tr)
+    ref = np.full(rows_x * N, np.nan, np.float32)
+    ws = np.empty(5 * count, np.float32)
+    O.lib.orc_matmul_add_mxfp4_selected_transposed(blocks, bias, N, N, tr, tokens.astype(np.uintp), count, ref, ws,
+                                                   1, O.BODY_V4)
+    ref = ref.reshape(rows_x, N)
+    for t in tokens:
+        err = O.rel_l2(got[t], ref[t])
+        assert err <= TOL, (t, err)
+    untouched = np.setdiff1d(np.arange(rows_x), tokens)
+    assert np.all(np.isnan(got[untouched]))
+    for b in (bb, xb, tb, out):
+        b.free()
+    w.free()
+
+
+def run_prefill(dev, layer, x, idx, w, dtype):
+    count, used = idx.shape
+    if dtype == ttlab_amd.TTL_DTYPE_BF16:
+        bits = (np.ascontiguousarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        xb = dev.upload(bits)
+    else:
+        xb = dev.upload(np.ascontiguousarray(x, np.float32))
+    ib, wb = dev.upload(idx.astype(np.int32)), dev.upload(w.astype(np.float32))
+    out = dev.alloc(count * N * 4)
+    ws = dev.alloc(dev.moe_prefill_workspace_bytes(count, layer.desc.experts, used, dtype))
+    dev.moe_prefill_experts(layer.desc, xb, dtype, count, ib, wb, out, ws)
+    got = out.download(np.float32).reshape(count, N)
+    for b in (xb, ib, wb, out, ws):
+        b.free()
+    return got
+
+
+def oracle_prefill(host, x, idx, w):
+    count = x.shape[0]
+    s = host.oracle_struct()
+    out = np.empty(count * N, np.float32)
+    O.lib.orc_moe_batch_experts(s, np.ascontiguousarray(x, np.float32).ravel(), count,
+                                np.ascontiguousarray(idx, np.int64).ravel(), np.ascontiguousarray(w, np.float32).ravel(),
+                                out, O.BODY_V4)
+    return out.reshape(count, N)
+
+
+@pytest.fixture(scope="module")
+def layer8(dev):
+    host = HostLayer(8, 4, biases=True, seed=0x77000012)
+    device = DeviceLayer(dev, host)
+    yield host, device
+    device.free()
+
+
+@pytest.mark.parametrize("dtype", [ttlab_amd.TTL_DTYPE_BF16, ttlab_amd.TTL_DTYPE_F32])
+def test_moe_prefill_experts_matches_oracle(dev, layer8, dtype):
+    host, device = layer8
+    count = 32
+    if dtype == ttlab_amd.TTL_DTYPE_BF16:
+        x = O.synth_normal_bf16(0x78000002, 1, count * N, 1.0).reshape(count, N)
+    else:
+        x = O.synth_normal(0x78000002, 2, count * N).reshape(count, N)
+    idx, w = balanced_routing(count, 8, 4, 3)
+    got = run_prefill(dev, device, x, idx, w, dtype)
+    ref = oracle_prefill(host, x, idx, w)
+    assert O.rel_l2(got, ref) <= TOL
+    for p in range(count):
+        assert O.rel_l2(got[p], ref[p]) <= TOL, p
+
+
+def test_moe_prefill_uneven_buckets_and_invalid_index(dev, layer8):
+    # experts with 0, 1, 2 and 70 (two tiles) tokens; one pair with an index out of range
+    host, device = layer8
+    count = 72
+    x = O.synth_normal(0x78000002, 4, count * N).reshape(count, N)
+    rng = np.random.RandomState(5)
+    idx = np.zeros((count, 4), np.int32)
+    for p in range(count):
+        idx[p] = [7, 3, 6, 5] if p % 36 == 0 else ([7, 3, 2, 5] if p == 1 else [7, 3, 4, 5])
+    idx[:, :] = idx[:, rng.permutation(4)]
+    w = rng.rand(count, 4).astype(np.float32)
+    bad = idx.copy()
+    bad[10, 2] = 8
+    got = run_prefill(dev, device, x, bad, w, ttlab_amd.TTL_DTYPE_F32)
+    assert np.all(np.isnan(got[10]))
+    keep = np.setdiff1d(np.arange(count), [10])
+    ref = oracle_prefill(host, x[keep], idx[keep], w[keep])
+    for j, p in enumerate(keep):
+        assert O.rel_l2(got[p], ref[j]) <= TOL, p
+    one = run_prefill(dev, device, x[:1], idx[:1], w[:1], ttlab_amd.TTL_DTYPE_F32)
+    assert O.rel_l2(one[0], oracle_prefill(host, x[:1], idx[:1], w[:1])[0]) <= TOL
+
+
+def test_moe_prefill_config2_shape(dev):
+    # 512 bf16 tokens, 32 experts, top-4 balanced (64 tokens each)
+    count = 512
+    idx, w = balanced_routing(count, 32, 4, 11)
+    sample = np.random.RandomState(12).choice(count, 6, replace=False)
+    # host matrices only for the sampled tokens' experts (the device generates all 32)
+    host = HostLayer(32, 4, biases=False, seed=0x77000102, fill_experts=idx[sample].ravel())
+    device = DeviceLayer(dev, host)
+    try:
+        x = O.synth_normal_bf16(0x78000102, 0, count * N, 1.0).reshape(count, N)
+        got = run_prefill(dev, device, x, idx, w, ttlab_amd.TTL_DTYPE_BF16)
+        assert np.all(np.isfinite(got))
+        # the oracle on a sample of tokens: each token's result depends on no other token
+        ref = oracle_prefill(host, x[sample], idx[sample], w[sample])
+        for j, p in enumerate(sample):
+            assert O.rel_l2(got[p], ref[j]) <= TOL, p
+        # token order and rank order change the buckets, not any per-token sum
+        perm = np.random.RandomState(13).permutation(count)
+        shuffled = run_prefill(dev, device, x[perm], idx[perm], w[perm], ttlab_amd.TTL_DTYPE_BF16)
+        assert np.array_equal(shuffled.view(np.uint32), got[perm].view(np.uint32))
+        flipped = run_prefill(dev, device, x, idx[:, ::-1].copy(), w[:, ::-1].copy(), ttlab_amd.TTL_DTYPE_BF16)
+        assert np.array_equal(flipped.view(np.uint32), got.view(np.uint32))
+    finally:
+        device.free()
+
+
+def test_prefill_rejects_small_workspace(dev, layer8):
+    host, device = layer8
+    count = 8
+    x = dev.alloc(count * N * 4)
+    idx, w = balanced_routing(count, 8, 4, 3)
+    ib, wb = dev.upload(idx), dev.upload(w)
+    out = dev.alloc(count * N * 4)
+    need = dev.moe_prefill_workspace_bytes(count, 8, 4, ttlab_amd.TTL_DTYPE_F32)
+    assert need > dev.moe_prefill_workspace_bytes(count, 8, 4, ttlab_amd.TTL_DTYPE_BF16)
+    small = dev.alloc(dev.moe_prefill_workspace_bytes(count, 8, 4, ttlab_amd.TTL_DTYPE_BF16))
+    with pytest.raises(ttlab_amd.TtlError, match="workspace"):
+        dev.moe_prefill_experts(device.desc, x, ttlab_amd.TTL_DTYPE_F32, count, ib, wb, out, small)
+    for b in (x, ib, wb, out, small):
+        b.free()

@@ -5,6 +5,8 @@ src/tests.cpp:194-234).  Beyond those: brute force in float64 (numpy), exact
 cross-body relations of the reference's two multiversioned bodies, and
 hand-derived answers for the selection sort's tie and NaN rules (model.cpp:296-309).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -313,3 +315,104 @@ def test_attention_against_float64(layer_index, position):
         e = np.exp(s - m)
         ref[h] = (e / (e.sum() + np.exp(sinks[h] - m))) @ V[:, h // 8]
     assert O.rel_l2(out, ref.ravel()) < 1e-5
+
+
+# ---- a9 prefill: GptOssModel::moe_batch's experts (model.cpp:378-460) ----------------
+
+def _small_moe(hidden=64, experts=6, used=2, seed=51):
+    """A gpt-oss-shaped MoE layer at a small width, host arrays kept alive on the struct."""
+    keep = {}
+    keep["router_w"] = O.synth_normal(seed, 1, experts * hidden, sigma=0.1)
+    keep["router_b"] = O.synth_normal(seed, 2, experts, sigma=0.1)
+    for i, name in enumerate(("gate", "up", "down")):
+        keep[name] = O.synth_mxfp4(seed, 10 + i, experts * hidden * hidden // 32)
+        keep[name + "_b"] = O.synth_normal(seed, 20 + i, experts * hidden, sigma=0.5)
+    s = O.MoeLayer()
+    s.hidden, s.expert_hidden, s.experts, s.used = hidden, hidden, experts, used
+    s.router_weight, s.router_bias = keep["router_w"].ctypes.data, keep["router_b"].ctypes.data
+    s.gate_weight, s.gate_bias = keep["gate"].ctypes.data, keep["gate_b"].ctypes.data
+    s.up_weight, s.up_bias = keep["up"].ctypes.data, keep["up_b"].ctypes.data
+    s.down_weight, s.down_bias = keep["down"].ctypes.data, keep["down_b"].ctypes.data
+    s._keep = keep
+    return s
+
+
+def _routing(count, experts, used, seed):
+    rng = np.random.RandomState(seed)
+    idx = np.stack([rng.choice(experts, used, replace=False) for _ in range(count)]).astype(np.int64)
+    logits = rng.randn(count, used)
+    w = np.exp(logits - logits.max(1, keepdims=True))
+    return idx, (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def _moe_batch_experts(s, x, idx, w, body=O.BODY_V4):
+    count = x.shape[0]
+    out = np.empty(count * s.hidden, np.float32)
+    lib.orc_moe_batch_experts(C.byref(s), np.ascontiguousarray(x, np.float32).ravel(), count,
+                              np.ascontiguousarray(idx, np.int64).ravel(), np.ascontiguousarray(w, np.float32).ravel(),
+                              out, body)
+    return out.reshape(count, s.hidden)
+
+
+def _brute_force_moe(s, x, idx, w):
+    H = s.hidden
+    k = s._keep
+    dense = {n: decode_f64(k[n], s.experts * H, H).reshape(s.experts, H, H) for n in ("gate", "up", "down")}
+    bias = {n: k[n + "_b"].astype(np.float64).reshape(s.experts, H) for n in ("gate", "up", "down")}
+    out = np.zeros((x.shape[0], H))
+    for p in range(x.shape[0]):
+        for r in range(idx.shape[1]):
+            e = idx[p, r]
+            g = dense["gate"][e] @ x[p] + bias["gate"][e]
+            u = dense["up"][e] @ x[p] + bias["up"][e]
+            xg = np.minimum(g, 7.0)
+            h = xg / (1.0 + np.exp(-1.702 * xg)) * (np.clip(u, -7.0, 7.0) + 1.0)
+            out[p] += w[p, r] * (dense["down"][e] @ h + bias["down"][e])
+    return out
+
+
+
+@pytest.mark.parametrize("count", [3, 40])  # 40 tokens: buckets above 4 take the selected matmul
+def test_moe_batch_experts_brute_force(count):
+    s = _small_moe()
+    x = O.synth_normal(52, 0, count * s.hidden).reshape(count, s.hidden)
+    idx, w = _routing(count, s.experts, s.used, 53)
+    got = _moe_batch_experts(s, x, idx, w)
+    exact = _brute_force_moe(s, x.astype(np.float64), idx, w.astype(np.float64))
+    assert O.rel_l2(got, exact) < 1e-5
+    for p in range(count):
+        assert O.rel_l2(got[p], exact[p]) < 1e-5
+
+
+def test_moe_batch_experts_combines_in_expert_order():
+    # model.cpp:450-459 adds each token's expert outputs in ascending expert index, so
+    # permuting a token's ranks (with their weights) leaves the result bit-identical,
+    # and permuting the tokens permutes the rows bit for bit (every per-(row, token)
+    # sum is independent of the other tokens).
+    s = _small_moe()
+    count = 40
+    x = O.synth_normal(54, 0, count * s.hidden).reshape(count, s.hidden)
+    idx, w = _routing(count, s.experts, s.used, 55)
+    base = _moe_batch_experts(s, x, idx, w)
+    flip = idx[:, ::-1].copy(), w[:, ::-1].copy()
+    assert np.array_equal(base.view(np.uint32), _moe_batch_experts(s, x, *flip).view(np.uint32))
+    perm = np.random.RandomState(56).permutation(count)
+    shuffled = _moe_batch_experts(s, x[perm], idx[perm], w[perm])
+    assert np.array_equal(base[perm].view(np.uint32), shuffled.view(np.uint32))
+
+
+def test_moe_batch_routes_then_runs_experts():
+    # orc_moe_batch = F32 router matmul + per-token top-k, then orc_moe_batch_experts
+    s = _small_moe()
+    count = 12
+    x = O.synth_normal(57, 0, count * s.hidden).reshape(count, s.hidden)
+    out = np.empty(count * s.hidden, np.float32)
+    lib.orc_moe_batch(C.byref(s), np.ascontiguousarray(x).ravel(), count, out, O.BODY_V4)
+    k = s._keep
+    idx = np.empty((count, s.used), np.int64)
+    w = np.empty((count, s.used), np.float32)
+    for p in range(count):
+        logits = np.empty(s.experts, np.float32)
+        lib.orc_matvec_add_f32(k["router_w"], k["router_b"], s.experts, s.hidden, np.ascontiguousarray(x[p]), logits)
+        idx[p], w[p] = O.router_topk(logits, s.used)
+    assert np.array_equal(out.reshape(count, s.hidden), _moe_batch_experts(s, x, idx, w))

@@ -18,6 +18,7 @@
 //
 // route_workgroup() runs in one workgroup after the rows are known and publishes
 // indices, weights and logits; the gate/up kernel then reads the indices.
+#include "ttl_moe_math.hpp"
 #include "ttl_mxfp4_tile.hpp"
 #include "ttl_stage.hpp"
 
@@ -31,13 +32,9 @@ constexpr uint32_t kMaxExperts = 192;
 constexpr uint32_t kMaxUsed = 16;
 constexpr int kPerLane = kMaxExperts / 64;  // candidates per lane in the wave-wide selection
 
-// std::max / std::min as the reference's libstdc++ defines them.
-__device__ inline float std_max(float a, float b) {
-    return (a < b) ? b : a;
-}
-__device__ inline float std_min(float a, float b) {
-    return (b < a) ? b : a;
-}
+using moe_math::clamped_swiglu;
+using moe_math::std_max;
+using moe_math::std_min;
 
 __device__ inline double wave_inclusive_scan(double v, uint32_t lane) {
 #pragma unroll
@@ -369,14 +366,6 @@ __device__ inline float sum_parts(const float (*part)[mx::tile_rows], uint32_t r
         sum += part[k][row];
     }
     return sum;
-}
-
-// model.cpp:328-332
-__device__ inline float clamped_swiglu(float gate, float up) {
-#pragma clang fp contract(off)
-    const float x = std_min(gate, 7.0f);
-    const float y = (up < -7.0f) ? -7.0f : ((7.0f < up) ? 7.0f : up);
-    return (x / (1.0f + expf(-1.702f * x))) * (y + 1.0f);
 }
 
 struct GateUpArgs {

@@ -1,5 +1,6 @@
 // MXFP4 tensors (GGUF block layout in, repacked planes on the device) and the
 // expert-indexed MXFP4 matvec.  The per-tile inner loop is in ttl_mxfp4_tile.hpp.
+#include "ttl_mfma.hpp"
 #include "ttl_mxfp4_tile.hpp"
 
 #include <cmath>
@@ -94,6 +95,19 @@ __global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *_
             const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
             dst[j] = scale * float(mxfp4_int(byte & 15u));
             dst[j + 16] = scale * float(mxfp4_int(byte >> 4));
+        }
+    } else if (mode == 2) {
+        // the prefill kernels' decode: bf16 = E2M1 x 2^(e-127) straight from the
+        // gfx950 conversion with the E8M0 scale (ttl_mfma.hpp), widened to f32
+        const float scale = mf::e8m0_scale(e);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const mf::bf16x8 v = mf::decode_step(w[q], scale);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                dst[4 * q + b] = float(v[2 * b]);
+                dst[4 * q + b + 16] = float(v[2 * b + 1]);
+            }
         }
     } else {
 #pragma unroll
@@ -293,7 +307,7 @@ int ttl_mxfp4_dequantize(ttl_ctx *ctx, const ttl_mxfp4 *t, uint32_t expert, int 
         return rc;
     }
     TTL_REQUIRE(expert < t->experts, TTL_ERR_INVALID, "ttl_mxfp4_dequantize: expert %u out of range", expert);
-    TTL_REQUIRE(mode == 0 || mode == 1, TTL_ERR_INVALID, "ttl_mxfp4_dequantize: mode must be 0 or 1");
+    TTL_REQUIRE(mode >= 0 && mode <= 2, TTL_ERR_INVALID, "ttl_mxfp4_dequantize: mode must be 0, 1 or 2");
     const size_t n = size_t(t->rows) * mx::blocks;
     dequant_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>((const uint4 *)t->codes, t->scales, t->rows,
                                                                       expert, mode, out_dev);

@@ -1,0 +1,954 @@
+// Batched (prefill) MXFP4 expert GEMMs on MFMA.
+//
+// Two entry points share the kernels:
+//  - ttl_matmul_mxfp4_selected: the selected-token matmul of one expert,
+//    matmul_add_mxfp4_selected_transposed (tensor.cpp:306-495);
+//  - ttl_moe_prefill_experts: the expert half of GptOssModel::moe_batch
+//    (model.cpp:378-460) for a batch of tokens whose routing is given.
+//
+// Numerics.  v_mfma_f32_16x16x32_bf16 accumulates in f32, and every product it
+// forms is exact:
+//  - a weight E2M1 x 2^(e-127) has at most two significant bits, so it is a bf16
+//    exactly for E8M0 e in 1..254; v_cvt_scalef32_pk_bf16_fp4 decodes it in registers;
+//  - an f32 activation is split into three bf16 planes whose sum is the value
+//    exactly (mf::split_planes); a bf16 activation is one plane.
+// The MFMA therefore sums the reference's exact products in f32, starting from the
+// bias as the reference does (tensor.cpp:455-462), in a different order: results
+// agree to f32 rounding, not bit for bit.
+//
+// Data flow of ttl_moe_prefill_experts (S = count * used (token, rank) pairs):
+//  1. plan_kernel (one workgroup): buckets the pairs by expert in the reference's
+//     order (model.cpp:380-394: expert-major, then token, then rank); a pair's
+//     position in that order is its slot.  Each expert's bucket is cut into tiles
+//     of 64 slots.
+//  2. gather_kernel: the tokens of every tile as MFMA B fragments (bf16 planes).
+//  3. gateup_kernel: per (tile, 192 rows) the gate and up GEMMs, the clamped SwiGLU
+//     in registers, and the hidden written straight into the down GEMM's B
+//     fragments (a lane's D rows 4g..4g+3 of the two 16-row tiles of one 32-row
+//     block are exactly the 8 values of the down fragment for K step g).
+//  4. matmul_kernel: the down GEMM per (tile, 192 rows), f32 output per slot.
+//  5. combine_kernel: out[token] = sum over the token's slots in expert order of
+//     weight * down, unfused, from 0 (model.cpp:380,450-459).
+#include "ttl_mfma.hpp"
+#include "ttl_moe_math.hpp"
+
+#include <cmath>
+
+namespace {
+
+using mf::bf16x8;
+using mf::f32x4;
+
+constexpr uint32_t kMaxExperts = 256;
+constexpr uint32_t kMaxUsed = 16;
+constexpr uint32_t kPlanThreads = 1024;
+constexpr uint32_t kMaxEntries = 1u << 22;  // count * used
+
+// gate/up: 6 waves x 32 rows (two 16-row tiles of gate and of up per wave)
+constexpr int kGuWaves = 6;
+constexpr int kGuRows = kGuWaves * 32;
+// matmul (down): 4 waves x 48 rows (three 16-row tiles per wave)
+constexpr int kMmWaves = 4;
+constexpr int kMmTiles = 3;
+constexpr int kMmRows = kMmWaves * kMmTiles * 16;
+
+// Hidden planes between gate/up and down: three, exact (the hidden is f32).
+constexpr int kHiddenPlanes = 3;
+
+// ---- the plan ------------------------------------------------------------------
+
+struct PlanHeader {
+    uint32_t tiles;    // token tiles in use
+    uint32_t invalid;  // pairs whose expert index was out of range
+    uint32_t pad[62];
+};
+
+// Device pointers into the caller's workspace.
+struct Plan {
+    PlanHeader *header;
+    uint32_t *tile_expert;  // [tmax]
+    uint32_t *tile_first;   // [tmax] first slot
+    uint32_t *tile_count;   // [tmax] slots in the tile (1..64)
+    uint32_t *slot_token;   // [S]
+    float *slot_weight;     // [S]
+    int32_t *pair_slot;     // [S] slot of pair (token, rank) = token*used + rank, -1 if invalid
+    uint8_t *xb;            // [tmax][x planes][plane_bytes]
+    uint8_t *hb;            // [tmax][hidden planes][plane_bytes]
+    float *down;            // [S][rows]
+};
+
+struct Layout {
+    size_t header, tile_expert, tile_first, tile_count, slot_token, slot_weight, pair_slot, xb, hb, down, total;
+    uint32_t tmax;
+};
+
+size_t align256(size_t v) {
+    return (v + 255) & ~size_t(255);
+}
+
+// Upper bound on the tiles: sum_e ceil(c_e / 64) <= (S + 63 * nonempty) / 64.
+uint32_t max_tiles(uint32_t pairs, uint32_t experts) {
+    const uint32_t nonempty = pairs < experts ? pairs : experts;
+    return uint32_t((uint64_t(pairs) + 63ull * nonempty) / mf::tile_slots) + 1;
+}
+
+Layout make_layout(uint32_t pairs, uint32_t experts, int x_planes, bool with_hidden, uint32_t rows) {
+    Layout L{};
+    L.tmax = max_tiles(pairs, experts);
+    size_t o = 0;
+    L.header = o;
+    o = align256(o + sizeof(PlanHeader));
+    L.tile_expert = o;
+    o = align256(o + 4ull * L.tmax);
+    L.tile_first = o;
+    o = align256(o + 4ull * L.tmax);
+    L.tile_count = o;
+    o = align256(o + 4ull * L.tmax);
+    L.slot_token = o;
+    o = align256(o + 4ull * pairs);
+    L.slot_weight = o;
+    o = align256(o + 4ull * pairs);
+    L.pair_slot = o;
+    o = align256(o + 4ull * pairs);
+    L.xb = o;
+    o = align256(o + size_t(L.tmax) * x_planes * mf::plane_bytes);
+    L.hb = o;
+    if (with_hidden) {
+        o = align256(o + size_t(L.tmax) * kHiddenPlanes * mf::plane_bytes);
+    }
+    L.down = o;
+    if (with_hidden) {
+        o = align256(o + 4ull * pairs * rows);
+    }
+    L.total = o;
+    return L;
+}
+
+Plan plan_at(void *workspace, const Layout &L) {
+    uint8_t *w = static_cast<uint8_t *>(workspace);
+    Plan p;
+    p.header = reinterpret_cast<PlanHeader *>(w + L.header);
+    p.tile_expert = reinterpret_cast<uint32_t *>(w + L.tile_expert);
+    p.tile_first = reinterpret_cast<uint32_t *>(w + L.tile_first);
+    p.tile_count = reinterpret_cast<uint32_t *>(w + L.tile_count);
+    p.slot_token = reinterpret_cast<uint32_t *>(w + L.slot_token);
+    p.slot_weight = reinterpret_cast<float *>(w + L.slot_weight);
+    p.pair_slot = reinterpret_cast<int32_t *>(w + L.pair_slot);
+    p.xb = w + L.xb;
+    p.hb = w + L.hb;
+    p.down = reinterpret_cast<float *>(w + L.down);
+    return p;
+}
+
+// Buckets the (token, rank) pairs by expert in the reference's order and cuts the
+// buckets into 64-slot tiles.  One workgroup of 1024 threads; pairs are taken in
+// rounds of 1024 in pair order, and a pair's slot is its expert's base plus the
+// number of earlier pairs with the same expert.
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__restrict__ indices,
+                                                            const float *__restrict__ weights, uint32_t pairs,
+                                                            uint32_t used, uint32_t experts, Plan plan) {
+    __shared__ uint32_t count[kMaxExperts], base[kMaxExperts], running[kMaxExperts];
+    __shared__ uint32_t wave_count[kPlanThreads / 64][kMaxExperts];
+    __shared__ uint32_t invalid;
+    const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
+    for (uint32_t e = t; e < kMaxExperts; e += kPlanThreads) {
+        count[e] = 0;
+        running[e] = 0;
+    }
+    if (t == 0) {
+        invalid = 0;
+    }
+    __syncthreads();
+    for (uint32_t j = t; j < pairs; j += kPlanThreads) {
+        const int32_t e = indices[j];
+        if (e >= 0 && uint32_t(e) < experts) {
+            atomicAdd(&count[e], 1u);
+        } else {
+            atomicAdd(&invalid, 1u);
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        uint32_t slots = 0, tiles = 0;
+        for (uint32_t e = 0; e < experts; ++e) {
+            base[e] = slots;
+            slots += count[e];
+            running[e] = tiles;  // first tile of expert e (reset below)
+            tiles += (count[e] + mf::tile_slots - 1) / mf::tile_slots;
+        }
+        plan.header->tiles = tiles;
+        plan.header->invalid = invalid;
+    }
+    __syncthreads();
+    for (uint32_t e = t; e < experts; e += kPlanThreads) {
+        const uint32_t first_tile = running[e], n = count[e];
+        for (uint32_t j = 0; j * mf::tile_slots < n; ++j) {
+            plan.tile_expert[first_tile + j] = e;
+            plan.tile_first[first_tile + j] = base[e] + j * mf::tile_slots;
+            plan.tile_count[first_tile + j] = min(uint32_t(mf::tile_slots), n - j * mf::tile_slots);
+        }
+    }
+    __syncthreads();
+    for (uint32_t e = t; e < kMaxExperts; e += kPlanThreads) {
+        running[e] = 0;
+    }
+    for (uint32_t round = 0; round < pairs; round += kPlanThreads) {
+        for (uint32_t e = t; e < (kPlanThreads / 64) * kMaxExperts; e += kPlanThreads) {
+            (&wave_count[0][0])[e] = 0;
+        }
+        __syncthreads();
+        const uint32_t j = round + t;
+        const int32_t ej = j < pairs ? indices[j] : -1;
+        const bool valid = ej >= 0 && uint32_t(ej) < experts;
+        // rank among the earlier lanes of this wave with the same expert
+        uint32_t rank = 0;
+        uint64_t remaining = __ballot(valid);
+        while (remaining) {
+            const uint32_t leader = uint32_t(__ffsll((long long)remaining) - 1);
+            const int32_t key = __shfl(ej, int(leader));
+            const uint64_t same = __ballot(valid && ej == key);
+            if (valid && ej == key) {
+                rank = uint32_t(__popcll(same & ((1ull << lane) - 1ull)));
+            }
+            if (lane == leader) {
+                wave_count[wave][key] = uint32_t(__popcll(same));
+            }
+            remaining &= ~same;
+        }
+        __syncthreads();
+        if (j < pairs) {
+            if (valid) {
+                uint32_t slot = base[ej] + running[ej] + rank;
+                for (uint32_t w = 0; w < wave; ++w) {
+                    slot += wave_count[w][ej];
+                }
+                plan.slot_token[slot] = j / used;
+                plan.slot_weight[slot] = weights[j];
+                plan.pair_slot[j] = int32_t(slot);
+            } else {
+                plan.pair_slot[j] = -1;
+            }
+        }
+        __syncthreads();
+        for (uint32_t e = t; e < experts; e += kPlanThreads) {
+            uint32_t add = 0;
+            for (uint32_t w = 0; w < kPlanThreads / 64; ++w) {
+                add += wave_count[w][e];
+            }
+            running[e] += add;
+        }
+        __syncthreads();
+    }
+}
+
+// The plan of one selected-token matmul: one expert, slot s = token tokens[s].
+__global__ void plan_selected_kernel(const int32_t *__restrict__ tokens, uint32_t count, uint32_t expert,
+                                     Plan plan) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t tiles = (count + mf::tile_slots - 1) / mf::tile_slots;
+    if (i == 0) {
+        plan.header->tiles = tiles;
+        plan.header->invalid = 0;
+    }
+    if (i < tiles) {
+        plan.tile_expert[i] = expert;
+        plan.tile_first[i] = i * mf::tile_slots;
+        plan.tile_count[i] = min(uint32_t(mf::tile_slots), count - i * mf::tile_slots);
+    }
+    if (i < count) {
+        plan.slot_token[i] = uint32_t(tokens[i]);  // range-checked where it is used
+        plan.slot_weight[i] = 1.0f;
+        plan.pair_slot[i] = int32_t(i);
+    }
+}
+
+// ---- activation fragments ------------------------------------------------------------
+
+// One thread per (tile, step, column tile, lane): the 8 activations of that B
+// fragment lane, as P bf16 planes.  Slots past the tile's count, tokens out of
+// range (NaN), and blocks 90/91 (zero) are filled so that every fragment is defined.
+template <bool BF16_IN, int P>
+__global__ __launch_bounds__(256) void gather_kernel(const void *__restrict__ x, uint32_t x_stride,
+                                                     uint32_t x_rows, Plan plan) {
+    const uint32_t tile = blockIdx.y;
+    if (tile >= plan.header->tiles) {
+        return;
+    }
+    const uint32_t step = blockIdx.x;  // 0..91
+    const uint32_t ct = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t n = ct * 16 + lane % 16;
+    const uint32_t block = (step / 4) * 4 + lane / 16, s = step % 4;
+    float v[8];
+    const uint32_t cnt = plan.tile_count[tile];
+    const bool live = n < cnt && block < uint32_t(mx::blocks);
+    uint32_t token = 0;
+    bool token_ok = false;
+    if (live) {
+        token = plan.slot_token[plan.tile_first[tile] + n];
+        token_ok = token < x_rows;
+    }
+    if (live && token_ok) {
+        const size_t base = size_t(token) * x_stride + size_t(block) * 32 + 4 * s;
+        if (BF16_IN) {
+            const uint2 lo = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + base);
+            const uint2 hi = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + base + 16);
+            v[0] = __uint_as_float(lo.x << 16);
+            v[1] = __uint_as_float(hi.x << 16);
+            v[2] = __uint_as_float(lo.x & 0xffff0000u);
+            v[3] = __uint_as_float(hi.x & 0xffff0000u);
+            v[4] = __uint_as_float(lo.y << 16);
+            v[5] = __uint_as_float(hi.y << 16);
+            v[6] = __uint_as_float(lo.y & 0xffff0000u);
+            v[7] = __uint_as_float(hi.y & 0xffff0000u);
+        } else {
+            const float4 lo = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+            const float4 hi = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base + 16);
+            v[0] = lo.x;
+            v[1] = hi.x;
+            v[2] = lo.y;
+            v[3] = hi.y;
+            v[4] = lo.z;
+            v[5] = hi.z;
+            v[6] = lo.w;
+            v[7] = hi.w;
+        }
+    } else {
+        const float fill = (live && !token_ok) ? __builtin_nanf("") : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = fill;
+        }
+    }
+    uint4 out[P];
+    mf::split_planes<P>(v, out);
+    uint8_t *dst = plan.xb + size_t(tile) * P * mf::plane_bytes +
+                   (size_t(step) * mf::col_tiles + ct) * mf::frag_bytes + lane * 16;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        *reinterpret_cast<uint4 *>(dst + size_t(p) * mf::plane_bytes) = out[p];
+    }
+}
+
+// ---- the MFMA main loop ----------------------------------------------------------------
+
+// K steps per LDS stage for P activation planes: a stage holds P * steps * 4
+// fragments (16 KiB for one plane, 12 KiB for three).
+template <int P>
+struct StageShape {
+    static constexpr int steps = P == 1 ? 4 : (P == 2 ? 2 : 1);
+    static constexpr int count = mf::steps / steps;
+    static constexpr int frags = P * steps * mf::col_tiles;
+    static constexpr int chunks = frags * 64;  // 16-byte pieces
+    static_assert(mf::steps % steps == 0, "stages must divide the K steps");
+};
+
+// Copies stage `j` of a token tile's fragments (P planes) between global memory
+// and LDS through registers; LDS order is [plane][step][column tile][lane].  Every
+// thread moves `per` pieces with no condition (a branch around a load makes the
+// compiler wait for it at once): pieces past the stage re-read its last piece and
+// land in the LDS buffer's padding.
+template <int P, int THREADS>
+struct Stager {
+    using SS = StageShape<P>;
+    static constexpr int per = (SS::chunks + THREADS - 1) / THREADS;
+    static constexpr int lds_chunks = per * THREADS;  // LDS buffer size in pieces
+    mf::u32x4 r[per];
+
+    __device__ inline void load(const uint8_t *__restrict__ tile_frags, int j, uint32_t t) {
+#pragma unroll
+        for (int k = 0; k < per; ++k) {
+            const uint32_t c = min(t + uint32_t(k) * THREADS, uint32_t(SS::chunks - 1));
+            const uint32_t plane = c / (SS::steps * mf::col_tiles * 64);
+            const uint32_t within = c % (SS::steps * mf::col_tiles * 64);
+            r[k] = *reinterpret_cast<const mf::u32x4 *>(tile_frags + size_t(plane) * mf::plane_bytes +
+                                                    size_t(j) * SS::steps * mf::col_tiles * mf::frag_bytes +
+                                                    size_t(within) * 16);
+        }
+    }
+    __device__ inline void store(mf::u32x4 *lds, uint32_t t) const {
+#pragma unroll
+        for (int k = 0; k < per; ++k) {
+            lds[t + uint32_t(k) * THREADS] = r[k];
+        }
+    }
+};
+
+// One wave's A operand: NT 16-row tiles of repacked MXFP4 (ttl_internal.hpp), the
+// codes of one quad (4 K steps) per tile and the lane's 24 scale bytes per tile.
+template <int NT>
+struct AOperand {
+    const uint4 *codes[NT];  // tile base + lane row
+    uint32_t sw[NT][6];
+
+    __device__ inline void init(const uint8_t *__restrict__ codes_base, const uint8_t *__restrict__ scales_base,
+                                const size_t (&tile_index)[NT], uint32_t lane) {
+#pragma unroll
+        for (int a = 0; a < NT; ++a) {
+            codes[a] = reinterpret_cast<const uint4 *>(codes_base) + tile_index[a] * mx::blocks * mx::tile_rows +
+                       lane % mx::tile_rows;
+            const uint2 *rec = reinterpret_cast<const uint2 *>(scales_base + tile_index[a] * mx::tile_scale_bytes +
+                                                               size_t(lane) * mx::scale_pad);
+            const uint2 s01 = rec[0], s23 = rec[1], s45 = rec[2];
+            sw[a][0] = s01.x;
+            sw[a][1] = s01.y;
+            sw[a][2] = s23.x;
+            sw[a][3] = s23.y;
+            sw[a][4] = s45.x;
+            sw[a][5] = s45.y;
+        }
+    }
+    // Codes of quad i (blocks 4i..4i+3; past block 89 the lane re-reads block 89,
+    // whose activations there are zero and whose scale byte is the padding 127).
+    __device__ inline void load(int i, uint32_t lane, uint4 (&q)[NT]) const {
+        const uint32_t block = min(uint32_t(4 * i) + lane / mx::tile_rows, uint32_t(mx::blocks - 1));
+#pragma unroll
+        for (int a = 0; a < NT; ++a) {
+            q[a] = codes[a][size_t(block) * mx::tile_rows];
+        }
+    }
+    // Scale of tile a for the current quad; next_quad() moves every record on by
+    // one byte, so the indices stay static.
+    __device__ inline float scale(int a) const {
+        return mf::e8m0_scale(sw[a][0] & 0xffu);
+    }
+    __device__ inline void next_quad() {
+#pragma unroll
+        for (int a = 0; a < NT; ++a) {
+#pragma unroll
+            for (int k = 0; k < 5; ++k) {
+                sw[a][k] = (sw[a][k] >> 8) | (sw[a][k + 1] << 24);
+            }
+            sw[a][5] >>= 8;
+        }
+    }
+};
+
+// ---- gate/up + SwiGLU -------------------------------------------------------------------
+
+struct GateUpArgs {
+    const uint8_t *gate_codes, *gate_scales, *up_codes, *up_scales;
+    const float *gate_bias, *up_bias;  // [experts][rows] or null
+    uint32_t rows, tiles_per_expert;
+    Plan plan;
+};
+
+// Accumulators: [matrix (gate 0/1, up 2/3)][column tile]
+template <int PX>
+__global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
+    using SS = StageShape<PX>;
+    constexpr int kThreads = kGuWaves * 64;
+    __shared__ mf::u32x4 lds[2][Stager<PX, kThreads>::lds_chunks];
+    const uint32_t tile = blockIdx.y;
+    if (tile >= a.plan.header->tiles) {
+        return;
+    }
+    const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const uint32_t expert = a.plan.tile_expert[tile];
+    const uint32_t row0 = blockIdx.x * kGuRows + wave * 32;  // this wave's 32 rows (one down K block)
+    const size_t tile0 = size_t(expert) * a.tiles_per_expert + row0 / 16;
+    const uint8_t *frags = a.plan.xb + size_t(tile) * PX * mf::plane_bytes;
+
+    AOperand<2> ga, ua;
+    const size_t ti[2] = {tile0, tile0 + 1};
+    ga.init(a.gate_codes, a.gate_scales, ti, lane);
+    ua.init(a.up_codes, a.up_scales, ti, lane);
+
+    f32x4 acc[4][mf::col_tiles];
+    {
+        const uint32_t g = lane / 16;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float *bias = m < 2 ? a.gate_bias : a.up_bias;
+            f32x4 b = {0.f, 0.f, 0.f, 0.f};
+            if (bias) {
+                const float4 v = *reinterpret_cast<const float4 *>(bias + size_t(expert) * a.rows + row0 +
+                                                                   16 * (m % 2) + 4 * g);
+                b = f32x4{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+            for (int c = 0; c < mf::col_tiles; ++c) {
+                acc[m][c] = b;
+            }
+        }
+    }
+
+    Stager<PX, kThreads> st;
+    st.load(frags, 0, t);
+    uint4 qa[3][4];  // codes of three quads in flight: [buffer][gate0, gate1, up0, up1]
+    auto load_quad = [&](int i, uint4(&q)[4]) __attribute__((always_inline)) {
+        uint4 g2[2], u2[2];
+        ga.load(i, lane, g2);
+        ua.load(i, lane, u2);
+        q[0] = g2[0];
+        q[1] = g2[1];
+        q[2] = u2[0];
+        q[3] = u2[1];
+    };
+    load_quad(0, qa[0]);
+    load_quad(1, qa[1]);
+    st.store(lds[0], t);
+    __syncthreads();
+    if (SS::count > 1) {
+        st.load(frags, 1, t);
+    }
+
+    auto compute_quad = [&](int i, const uint4(&q)[4]) __attribute__((always_inline)) {
+        float sc[4];
+        sc[0] = ga.scale(0);
+        sc[1] = ga.scale(1);
+        sc[2] = ua.scale(0);
+        sc[3] = ua.scale(1);
+        ga.next_quad();
+        ua.next_quad();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int step = 4 * i + s;
+            const int stage = step / SS::steps, ls = step % SS::steps;
+            const mf::u32x4 *buf = lds[stage % 2];
+            bf16x8 w[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t word = s == 0 ? q[m].x : (s == 1 ? q[m].y : (s == 2 ? q[m].z : q[m].w));
+                w[m] = mf::decode_step(word, sc[m]);
+            }
+#pragma unroll
+            for (int c = 0; c < mf::col_tiles; ++c) {
+#pragma unroll
+                for (int p = 0; p < PX; ++p) {
+                    const bf16x8 b = mf::as_bf16x8v(buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        acc[m][c] = mf::mfma(w[m], b, acc[m][c]);
+                    }
+                }
+            }
+            if (ls == SS::steps - 1) {
+                // end of stage: publish the next stage, fetch the one after
+                if (stage + 1 < SS::count) {
+                    st.store(lds[(stage + 1) % 2], t);
+                }
+                __syncthreads();
+                if (stage + 2 < SS::count) {
+                    st.load(frags, stage + 2, t);
+                }
+            }
+        }
+    };
+
+    // quads 0..22, three code buffers rotating with static indices: each quad's
+    // codes are requested two quads before they are used (loads past quad 22
+    // repeat quad 22)
+    for (int i = 0; i < mf::quads; i += 3) {
+        load_quad(min(i + 2, mf::quads - 1), qa[2]);
+        compute_quad(i, qa[0]);
+        load_quad(min(i + 3, mf::quads - 1), qa[0]);
+        if (i + 1 < mf::quads) {
+            compute_quad(i + 1, qa[1]);
+            load_quad(min(i + 4, mf::quads - 1), qa[1]);
+        }
+        if (i + 2 < mf::quads) {
+            compute_quad(i + 2, qa[2]);
+        }
+    }
+
+    // SwiGLU and the hidden as down-GEMM B fragments: this wave's 32 rows are down K
+    // block beta; lane (n, g) holds rows 4g..4g+3 of both 16-row halves, i.e. the
+    // 8 values of K step g of that block for token n.
+    const uint32_t beta = row0 / 32, quad = beta / 4, gb = beta % 4;
+    const uint32_t g = lane / 16, n16 = lane % 16;
+    uint8_t *hb = a.plan.hb + size_t(tile) * kHiddenPlanes * mf::plane_bytes;
+#pragma unroll
+    for (int c = 0; c < mf::col_tiles; ++c) {
+        float h[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[2 * i] = moe_math::clamped_swiglu(acc[0][c][i], acc[2][c][i]);
+            h[2 * i + 1] = moe_math::clamped_swiglu(acc[1][c][i], acc[3][c][i]);
+        }
+        uint4 planes[kHiddenPlanes];
+        mf::split_planes<kHiddenPlanes>(h, planes);
+        const size_t off = ((size_t(quad) * 4 + g) * mf::col_tiles + c) * mf::frag_bytes + (gb * 16 + n16) * 16;
+#pragma unroll
+        for (int p = 0; p < kHiddenPlanes; ++p) {
+            *reinterpret_cast<uint4 *>(hb + size_t(p) * mf::plane_bytes + off) = planes[p];
+        }
+        // blocks 90 and 91 (quad 22, lane groups 2 and 3) hold no rows: zero
+        if (beta + 2 >= uint32_t(mx::blocks) && beta < uint32_t(mx::blocks)) {
+            const size_t zoff = off + 2 * 16 * 16;
+#pragma unroll
+            for (int p = 0; p < kHiddenPlanes; ++p) {
+                *reinterpret_cast<uint4 *>(hb + size_t(p) * mf::plane_bytes + zoff) = make_uint4(0, 0, 0, 0);
+            }
+        }
+    }
+}
+
+// ---- plain GEMM (down projection, selected matmul) -----------------------------------------
+
+struct MatmulArgs {
+    const uint8_t *codes, *scales;
+    const float *bias;  // [experts][rows] or null
+    uint32_t rows, tiles_per_expert;
+    const uint8_t *frags;  // [tile][P][plane_bytes]
+    Plan plan;
+    float *out;          // SCATTER: [x_rows][rows] by token; else [slots][rows] by slot
+    uint32_t out_rows;   // SCATTER: rows of out (tokens beyond are skipped)
+};
+
+template <int P, bool SCATTER>
+__global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
+    using SS = StageShape<P>;
+    constexpr int kThreads = kMmWaves * 64;
+    __shared__ mf::u32x4 lds[2][Stager<P, kThreads>::lds_chunks];
+    const uint32_t tile = blockIdx.y;
+    if (tile >= a.plan.header->tiles) {
+        return;
+    }
+    const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const uint32_t expert = a.plan.tile_expert[tile];
+    const uint32_t row0 = blockIdx.x * kMmRows + wave * (kMmTiles * 16);
+    const bool rows_ok = row0 < a.rows;  // waves past the last row only help stage
+    const uint32_t row_base = rows_ok ? row0 : 0;
+    const size_t tile0 = size_t(expert) * a.tiles_per_expert + row_base / 16;
+    const uint8_t *frags = a.frags + size_t(tile) * P * mf::plane_bytes;
+
+    AOperand<kMmTiles> wa;
+    size_t ti[kMmTiles];
+#pragma unroll
+    for (int m = 0; m < kMmTiles; ++m) {
+        ti[m] = tile0 + m;
+    }
+    wa.init(a.codes, a.scales, ti, lane);
+
+    f32x4 acc[kMmTiles][mf::col_tiles];
+    {
+        const uint32_t g = lane / 16;
+#pragma unroll
+        for (int m = 0; m < kMmTiles; ++m) {
+            f32x4 b = {0.f, 0.f, 0.f, 0.f};
+            if (a.bias) {
+                const float4 v =
+                    *reinterpret_cast<const float4 *>(a.bias + size_t(expert) * a.rows + row_base + 16 * m + 4 * g);
+                b = f32x4{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+            for (int c = 0; c < mf::col_tiles; ++c) {
+                acc[m][c] = b;
+            }
+        }
+    }
+
+    Stager<P, kThreads> st;
+    st.load(frags, 0, t);
+    uint4 qa[3][kMmTiles];
+    wa.load(0, lane, qa[0]);
+    wa.load(1, lane, qa[1]);
+    st.store(lds[0], t);
+    __syncthreads();
+    if (SS::count > 1) {
+        st.load(frags, 1, t);
+    }
+
+    auto compute_quad = [&](int i, const uint4(&q)[kMmTiles]) __attribute__((always_inline)) {
+        float sc[kMmTiles];
+#pragma unroll
+        for (int m = 0; m < kMmTiles; ++m) {
+            sc[m] = wa.scale(m);
+        }
+        wa.next_quad();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int step = 4 * i + s;
+            const int stage = step / SS::steps, ls = step % SS::steps;
+            const mf::u32x4 *buf = lds[stage % 2];
+            bf16x8 w[kMmTiles];
+#pragma unroll
+            for (int m = 0; m < kMmTiles; ++m) {
+                const uint32_t word = s == 0 ? q[m].x : (s == 1 ? q[m].y : (s == 2 ? q[m].z : q[m].w));
+                w[m] = mf::decode_step(word, sc[m]);
+            }
+#pragma unroll
+            for (int c = 0; c < mf::col_tiles; ++c) {
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const bf16x8 b = mf::as_bf16x8v(buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
+#pragma unroll
+                    for (int m = 0; m < kMmTiles; ++m) {
+                        acc[m][c] = mf::mfma(w[m], b, acc[m][c]);
+                    }
+                }
+            }
+            if (ls == SS::steps - 1) {
+                if (stage + 1 < SS::count) {
+                    st.store(lds[(stage + 1) % 2], t);
+                }
+                __syncthreads();
+                if (stage + 2 < SS::count) {
+                    st.load(frags, stage + 2, t);
+                }
+            }
+        }
+    };
+
+    for (int i = 0; i < mf::quads; i += 3) {
+        wa.load(min(i + 2, mf::quads - 1), lane, qa[2]);
+        compute_quad(i, qa[0]);
+        wa.load(min(i + 3, mf::quads - 1), lane, qa[0]);
+        if (i + 1 < mf::quads) {
+            compute_quad(i + 1, qa[1]);
+            wa.load(min(i + 4, mf::quads - 1), lane, qa[1]);
+        }
+        if (i + 2 < mf::quads) {
+            compute_quad(i + 2, qa[2]);
+        }
+    }
+
+    if (!rows_ok) {
+        return;
+    }
+    const uint32_t cnt = a.plan.tile_count[tile], first = a.plan.tile_first[tile];
+    const uint32_t g = lane / 16, n16 = lane % 16;
+#pragma unroll
+    for (int c = 0; c < mf::col_tiles; ++c) {
+        const uint32_t n = c * 16 + n16;
+        if (n >= cnt) {
+            continue;
+        }
+        size_t out_row;
+        if (SCATTER) {
+            const uint32_t token = a.plan.slot_token[first + n];
+            if (token >= a.out_rows) {
+                continue;
+            }
+            out_row = token;
+        } else {
+            out_row = first + n;
+        }
+        float *dst = a.out + out_row * a.rows + row0 + 4 * g;
+#pragma unroll
+        for (int m = 0; m < kMmTiles; ++m) {
+            *reinterpret_cast<float4 *>(dst + 16 * m) = make_float4(acc[m][c][0], acc[m][c][1], acc[m][c][2],
+                                                                    acc[m][c][3]);
+        }
+    }
+}
+
+// ---- combine ----------------------------------------------------------------------------
+
+// out[p][i] = sum over token p's slots in slot order (= expert order) of
+// weight * down[slot][i]: products rounded, then added to a running sum from +0
+// (model.cpp:380, 450-459).  A pair with an invalid expert index makes the token NaN.
+// USED is the pairs per token (the sort is a fixed network over USED registers).
+template <int USED>
+__global__ __launch_bounds__(256) void combine_kernel(Plan plan, uint32_t count, uint32_t rows,
+                                                      float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const uint32_t quads_per_row = rows / 4;
+    const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= size_t(count) * quads_per_row) {
+        return;
+    }
+    const uint32_t p = uint32_t(gid / quads_per_row), q = uint32_t(gid % quads_per_row);
+    int32_t slots[USED];
+    bool bad = false;
+#pragma unroll
+    for (int r = 0; r < USED; ++r) {
+        slots[r] = plan.pair_slot[size_t(p) * USED + r];
+        bad |= slots[r] < 0;
+    }
+    // ascending slot order: odd-even transposition sort over the registers
+#pragma unroll
+    for (int pass = 0; pass < USED; ++pass) {
+#pragma unroll
+        for (int i = pass % 2; i + 1 < USED; i += 2) {
+            const int32_t lo = min(slots[i], slots[i + 1]), hi = max(slots[i], slots[i + 1]);
+            slots[i] = lo;
+            slots[i + 1] = hi;
+        }
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bad) {
+        const float nan = __builtin_nanf("");
+        acc = make_float4(nan, nan, nan, nan);
+    } else {
+#pragma unroll
+        for (int r = 0; r < USED; ++r) {
+            const uint32_t s = uint32_t(slots[r]);
+            const float w = plan.slot_weight[s];
+            const float4 d = reinterpret_cast<const float4 *>(plan.down + size_t(s) * rows)[q];
+            acc.x = acc.x + w * d.x;
+            acc.y = acc.y + w * d.y;
+            acc.z = acc.z + w * d.z;
+            acc.w = acc.w + w * d.w;
+        }
+    }
+    reinterpret_cast<float4 *>(out + size_t(p) * rows)[q] = acc;
+}
+
+template <int USED>
+void launch_combine(const Plan &plan, uint32_t count, uint32_t rows, float *out, hipStream_t stream) {
+    const size_t threads = size_t(count) * (rows / 4);
+    combine_kernel<USED><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(plan, count, rows, out);
+}
+
+// Dispatches the combine on the number of pairs per token (1..16).
+template <int U = 1>
+void combine_for(uint32_t used, const Plan &plan, uint32_t count, uint32_t rows, float *out, hipStream_t stream) {
+    if constexpr (U <= int(kMaxUsed)) {
+        if (used == uint32_t(U)) {
+            launch_combine<U>(plan, count, rows, out, stream);
+        } else {
+            combine_for<U + 1>(used, plan, count, rows, out, stream);
+        }
+    }
+}
+
+int check_mxfp4(const ttl_mxfp4 *w, const char *who) {
+    TTL_REQUIRE(w && w->codes && w->scales, TTL_ERR_INVALID, "%s: null tensor", who);
+    TTL_REQUIRE(w->cols == uint32_t(mx::cols), TTL_ERR_SHAPE, "%s: cols must be %d", who, mx::cols);
+    return TTL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ttl_matmul_mxfp4_selected_workspace_bytes(uint32_t count) {
+    return make_layout(count, 1, 3, false, 0).total;
+}
+
+int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
+                              uint32_t x_stride, uint32_t x_rows, const int32_t *tokens_dev, uint32_t count,
+                              float *out_dev, uint32_t expert, void *workspace_dev, size_t workspace_bytes) {
+    TTL_REQUIRE(ctx && x_dev && tokens_dev && out_dev && workspace_dev, TTL_ERR_INVALID,
+                "ttl_matmul_mxfp4_selected: null argument");
+    int rc = check_mxfp4(w, "ttl_matmul_mxfp4_selected");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(w->rows % kMmRows == 0, TTL_ERR_SHAPE, "ttl_matmul_mxfp4_selected: rows must be a multiple of %d",
+                kMmRows);
+    TTL_REQUIRE(expert < w->experts, TTL_ERR_INVALID, "ttl_matmul_mxfp4_selected: expert %u out of range", expert);
+    TTL_REQUIRE(x_stride >= uint32_t(mx::cols) && x_stride % 4 == 0, TTL_ERR_SHAPE,
+                "ttl_matmul_mxfp4_selected: x_stride must be >= %d and a multiple of 4", mx::cols);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && (reinterpret_cast<uintptr_t>(out_dev) & 15) == 0,
+                TTL_ERR_INVALID, "ttl_matmul_mxfp4_selected: x and out must be 16-byte aligned");
+    TTL_REQUIRE(count <= kMaxEntries, TTL_ERR_SHAPE, "ttl_matmul_mxfp4_selected: count above %u", kMaxEntries);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 255) == 0, TTL_ERR_INVALID,
+                "ttl_matmul_mxfp4_selected: workspace must be 256-byte aligned");
+    if (count == 0) {
+        return TTL_OK;
+    }
+    const Layout L = make_layout(count, 1, 3, false, 0);
+    TTL_REQUIRE(workspace_bytes >= L.total, TTL_ERR_SHAPE,
+                "ttl_matmul_mxfp4_selected: workspace of %zu bytes, %zu needed", workspace_bytes, L.total);
+    const Plan plan = plan_at(workspace_dev, L);
+    const uint32_t tiles = (count + mf::tile_slots - 1) / mf::tile_slots;
+    plan_selected_kernel<<<ttl::blocks_for(count > tiles ? count : tiles, 256), 256, 0, ctx->stream>>>(
+        tokens_dev, count, expert, plan);
+    TTL_LAUNCHED("plan_selected_kernel");
+    gather_kernel<false, 3><<<dim3(mf::steps, tiles), 256, 0, ctx->stream>>>(x_dev, x_stride, x_rows, plan);
+    TTL_LAUNCHED("gather_kernel");
+    MatmulArgs m;
+    m.codes = w->codes;
+    m.scales = w->scales;
+    m.bias = bias_dev;
+    m.rows = w->rows;
+    m.tiles_per_expert = w->tiles;
+    m.frags = plan.xb;
+    m.plan = plan;
+    m.out = out_dev;
+    m.out_rows = x_rows;
+    matmul_kernel<3, true><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
+    TTL_LAUNCHED("matmul_kernel");
+    return TTL_OK;
+}
+
+size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used, int x_dtype) {
+    const int planes = x_dtype == TTL_DTYPE_BF16 ? 1 : 3;
+    return make_layout(count * used, experts, planes, true, uint32_t(mx::cols)).total;
+}
+
+int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
+                            uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
+                            void *workspace_dev, size_t workspace_bytes) {
+    TTL_REQUIRE(ctx && layer && x_dev && indices_dev && weights_dev && out_dev && workspace_dev, TTL_ERR_INVALID,
+                "ttl_moe_prefill_experts: null argument");
+    const ttl_moe_layer &L = *layer;
+    TTL_REQUIRE(L.gate && L.up && L.down, TTL_ERR_INVALID, "ttl_moe_prefill_experts: null expert tensor");
+    TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16, TTL_ERR_INVALID,
+                "ttl_moe_prefill_experts: x_dtype must be TTL_DTYPE_F32 or TTL_DTYPE_BF16");
+    TTL_REQUIRE(L.hidden == uint32_t(mx::cols) && L.expert_hidden == uint32_t(mx::cols), TTL_ERR_SHAPE,
+                "ttl_moe_prefill_experts: hidden and expert_hidden must be %d", mx::cols);
+    TTL_REQUIRE(L.gate->rows == L.expert_hidden && L.up->rows == L.expert_hidden && L.down->rows == L.hidden &&
+                    L.gate->cols == L.hidden && L.up->cols == L.hidden && L.down->cols == L.expert_hidden,
+                TTL_ERR_SHAPE, "ttl_moe_prefill_experts: expert tensor shapes do not match the layer");
+    TTL_REQUIRE(L.gate->experts == L.experts && L.up->experts == L.experts && L.down->experts == L.experts,
+                TTL_ERR_SHAPE, "ttl_moe_prefill_experts: expert tensors must hold %u experts", L.experts);
+    TTL_REQUIRE(L.experts >= 1 && L.experts <= kMaxExperts, TTL_ERR_SHAPE,
+                "ttl_moe_prefill_experts: experts must be 1..%u", kMaxExperts);
+    TTL_REQUIRE(L.used >= 1 && L.used <= kMaxUsed, TTL_ERR_SHAPE, "ttl_moe_prefill_experts: used must be 1..%u",
+                kMaxUsed);
+    TTL_REQUIRE(uint64_t(count) * L.used <= kMaxEntries, TTL_ERR_SHAPE,
+                "ttl_moe_prefill_experts: count * used above %u", kMaxEntries);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && (reinterpret_cast<uintptr_t>(out_dev) & 15) == 0,
+                TTL_ERR_INVALID, "ttl_moe_prefill_experts: x and out must be 16-byte aligned");
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 255) == 0, TTL_ERR_INVALID,
+                "ttl_moe_prefill_experts: workspace must be 256-byte aligned");
+    if (count == 0) {
+        return TTL_OK;
+    }
+    const uint32_t pairs = count * L.used;
+    const bool bf16 = x_dtype == TTL_DTYPE_BF16;
+    const Layout lay = make_layout(pairs, L.experts, bf16 ? 1 : 3, true, L.hidden);
+    TTL_REQUIRE(workspace_bytes >= lay.total, TTL_ERR_SHAPE,
+                "ttl_moe_prefill_experts: workspace of %zu bytes, %zu needed for this count and x_dtype",
+                workspace_bytes, lay.total);
+    const Plan plan = plan_at(workspace_dev, lay);
+
+    plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(indices_dev, weights_dev, pairs, L.used, L.experts, plan);
+    TTL_LAUNCHED("plan_kernel");
+    if (bf16) {
+        gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+    } else {
+        gather_kernel<false, 3><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+    }
+    TTL_LAUNCHED("gather_kernel");
+
+    GateUpArgs g;
+    g.gate_codes = L.gate->codes;
+    g.gate_scales = L.gate->scales;
+    g.up_codes = L.up->codes;
+    g.up_scales = L.up->scales;
+    g.gate_bias = L.gate_bias;
+    g.up_bias = L.up_bias;
+    g.rows = L.expert_hidden;
+    g.tiles_per_expert = L.gate->tiles;
+    g.plan = plan;
+    const dim3 gu_grid(L.expert_hidden / kGuRows, lay.tmax);
+    if (bf16) {
+        gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+    } else {
+        gateup_kernel<3><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+    }
+    TTL_LAUNCHED("gateup_kernel");
+
+    MatmulArgs m;
+    m.codes = L.down->codes;
+    m.scales = L.down->scales;
+    m.bias = L.down_bias;
+    m.rows = L.hidden;
+    m.tiles_per_expert = L.down->tiles;
+    m.frags = plan.hb;
+    m.plan = plan;
+    m.out = plan.down;
+    m.out_rows = 0;
+    matmul_kernel<kHiddenPlanes, false><<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
+    TTL_LAUNCHED("matmul_kernel");
+
+    combine_for(L.used, plan, count, L.hidden, out_dev, ctx->stream);
+    TTL_LAUNCHED("combine_kernel");
+    return TTL_OK;
+}
+
+}  // extern "C"

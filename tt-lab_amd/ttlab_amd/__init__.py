@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(PKG_DIR, "build", "libttlab_hip.so")
 HEADER_PATH = os.path.join(REPO_DIR, "include", "ttlab_hip.h")
 
 TTL_OK = 0
+TTL_DTYPE_F32 = 0
+TTL_DTYPE_BF16 = 1
 
 
 class TtlError(RuntimeError):
@@ -244,6 +246,10 @@ def load_library():
         "ttl_logits_workspace_bytes": (sz, [u32]),
         "ttl_logits_bf16": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
         "ttl_argmax": (i32, [vp, u32, vp, vp, vp, vp, u32]),
+        "ttl_matmul_mxfp4_selected_workspace_bytes": (sz, [u32]),
+        "ttl_matmul_mxfp4_selected": (i32, [vp, vp, vp, vp, u32, u32, vp, u32, vp, u32, vp, sz]),
+        "ttl_moe_prefill_workspace_bytes": (sz, [u32, u32, u32, i32]),
+        "ttl_moe_prefill_experts": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
@@ -527,6 +533,30 @@ class Device:
             rc = self.lib.ttl_capture_end(self.ctx, C.byref(g))
         _check(rc, "ttl_capture_end")
         return Graph(self, g.value)
+
+    # ---- batched prefill (MFMA) ----
+    def matmul_mxfp4_selected(self, w, bias, x, x_stride, x_rows, tokens, count, out, expert, workspace=None):
+        """out[tokens[s]] = W[expert] x[tokens[s]] + bias[expert]; allocates a workspace if none is given."""
+        ws = workspace
+        if ws is None:
+            ws = self.alloc(max(self.lib.ttl_matmul_mxfp4_selected_workspace_bytes(count), 256))
+        try:
+            _check(self.lib.ttl_matmul_mxfp4_selected(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
+                                                      x_rows, tokens.ptr, count, out.ptr, expert, ws.ptr, ws.nbytes),
+                   "ttl_matmul_mxfp4_selected")
+            if workspace is None:
+                self.sync()
+        finally:
+            if workspace is None:
+                ws.free()
+
+    def moe_prefill_workspace_bytes(self, count, experts, used, x_dtype):
+        return self.lib.ttl_moe_prefill_workspace_bytes(count, experts, used, x_dtype)
+
+    def moe_prefill_experts(self, layer, x, x_dtype, count, indices, weights, out, workspace):
+        _check(self.lib.ttl_moe_prefill_experts(self.ctx, C.byref(layer), x.ptr, x_dtype, count, indices.ptr,
+                                                weights.ptr, out.ptr, workspace.ptr, workspace.nbytes),
+               "ttl_moe_prefill_experts")
 
     def matvec_mxfp4_experts(self, w, bias, x, x_stride, experts, n, y):
         _check(self.lib.ttl_matvec_mxfp4_experts(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
