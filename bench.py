@@ -22,6 +22,10 @@ is 12 of each plus the unembedding.
 
 --workload moe runs BASELINE config 1 instead: one MoE layer per step over 24
 distinct resident layers, value = token-layers/s.
+
+--workload prefill runs BASELINE config 2: the batched prefill experts of one MoE
+layer for 512 bf16 tokens with balanced given routing (bf16 MFMA), value =
+token-layers/s; roofline on the larger of the gate/up and down GEMM launches.
 """
 import argparse
 import json
@@ -161,6 +165,104 @@ def gpu_moe(args):
     }
 
 
+PREFILL_TOKENS = 512
+PREFILL_LAYERS = 3  # distinct resident layers (1.27 GB of experts, beyond every cache)
+PREFILL_PAIRS = PREFILL_TOKENS * USED
+# Algorithmic bytes and flops of the two GEMM launches of one config-2 layer:
+# gate/up reads all 32 experts' gate and up rows, the bf16 activations of the 512
+# tokens, and writes the f32 hidden of the 2048 (token, expert) pairs; down reads
+# the down rows and that hidden and writes the f32 down outputs.
+PF_GATEUP_BYTES = EXPERTS * 2 * N * 1530 + PREFILL_TOKENS * N * 2 + PREFILL_PAIRS * N * 4
+PF_DOWN_BYTES = EXPERTS * N * 1530 + 2 * PREFILL_PAIRS * N * 4
+PF_GATEUP_FLOP = 2 * 2 * PREFILL_PAIRS * N * N
+PF_DOWN_FLOP = 2 * PREFILL_PAIRS * N * N
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def gpu_prefill(args):
+    import numpy as np
+
+    import ttlab_amd
+
+    dev = ttlab_amd.Device(0)
+    keep, descs = [], []
+    for l in range(PREFILL_LAYERS):
+        seed = 0x77000300 + l
+        gate = dev.mxfp4_synthetic(N, N, EXPERTS, seed, 1000)
+        up = dev.mxfp4_synthetic(N, N, EXPERTS, seed, 2000)
+        down = dev.mxfp4_synthetic(N, N, EXPERTS, seed, 3000)
+        d = ttlab_amd.MoeLayerDesc()
+        d.hidden, d.expert_hidden, d.experts, d.used = N, N, EXPERTS, USED
+        d.gate, d.up, d.down = gate.handle, up.handle, down.handle
+        keep += [gate, up, down]
+        descs.append(d)
+    xs = np.random.RandomState(0x78000002).randn(PREFILL_TOKENS * N).astype(np.float32)
+    x = dev.upload(ttlab_amd.bf16_bits(xs))
+    idx, w = ttlab_amd.balanced_routing(PREFILL_TOKENS, EXPERTS, USED, 0x79000002)
+    ib, wb = dev.upload(idx), dev.upload(w)
+    out = dev.alloc(PREFILL_TOKENS * N * 4)
+    dt = ttlab_amd.TTL_DTYPE_BF16
+    ws = dev.alloc(dev.moe_prefill_workspace_bytes(PREFILL_TOKENS, EXPERTS, USED, dt))
+
+    def run(stages, layers):
+        def fn():
+            for d in layers:
+                dev.moe_prefill_experts(d, x, dt, PREFILL_TOKENS, ib, wb, out, ws, stages)
+        return fn
+
+    def time_graph(fn, launches, reps):
+        g = dev.capture(fn)
+        for _ in range(3):
+            g.launch()
+        dev.sync()
+        dev.timer_start()
+        for _ in range(reps):
+            g.launch()
+        ms = dev.timer_stop() / (reps * launches)
+        g.free()
+        return ms
+
+    ms = time_graph(run(ttlab_amd.TTL_PREFILL_ALL, descs), PREFILL_LAYERS, max(1, args.steps // PREFILL_LAYERS))
+    # the two GEMM launches alone (the plan and fragments stay in the workspace)
+    reps = max(10, args.steps // (2 * PREFILL_LAYERS))
+    us_gu = 1e3 * time_graph(run(ttlab_amd.TTL_PREFILL_GATEUP, descs * 2), 2 * PREFILL_LAYERS, reps)
+    us_dn = 1e3 * time_graph(run(ttlab_amd.TTL_PREFILL_DOWN, descs * 2), 2 * PREFILL_LAYERS, reps)
+    dev.sync()
+    for b in (x, ib, wb, out, ws):
+        b.free()
+    for t in keep:
+        t.free()
+    dev.close()
+    log(f"prefill layer: {ms * 1e3:.1f} us ({PREFILL_TOKENS / ms * 1e3:.0f} token-layers/s); gate/up "
+        f"{us_gu:.1f} us, down {us_dn:.1f} us")
+    kernels = {
+        "gateup_kernel": (us_gu, PF_GATEUP_BYTES, PF_GATEUP_FLOP),
+        "matmul_kernel (down)": (us_dn, PF_DOWN_BYTES, PF_DOWN_FLOP),
+    }
+    name = max(kernels, key=lambda k: kernels[k][0])
+    us, nbytes, flop = kernels[name]
+    achieved = nbytes / (us * 1e-6) / 1e9
+    per_kernel = {k: {"us": round(v[0], 2), "algorithmic_GBps": round(v[1] / (v[0] * 1e-6) / 1e9, 1),
+                      "algorithmic_TFLOPs": round(v[2] / (v[0] * 1e-6) / 1e12, 1)} for k, v in kernels.items()}
+    return {
+        "value": PREFILL_TOKENS / (ms * 1e-3),
+        "unit": "token-layers/s",
+        "ms_per_step": ms,
+        "dtype": "bf16 activations x MXFP4 weights, f32 accumulate (bf16 MFMA)",
+        "config": {"workload": "config 2: batched prefill experts of one gpt-oss-20b MoE layer, 512 bf16 tokens, "
+                               "top-4 of 32 experts, balanced given routing (64 tokens per expert); step = one layer "
+                               f"(plan, gather, gate/up+SwiGLU, down, combine) over {PREFILL_LAYERS} distinct "
+                               "resident layers (HIP graph)",
+                   "tokens": PREFILL_TOKENS, "experts": EXPERTS, "used": USED, "hidden": N,
+                   "kernels": per_kernel},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+                     "bytes_per_launch": nbytes, "launch_us": round(us, 3),
+                     "mfma_algorithmic_TFLOPs": round(flop / (us * 1e-6) / 1e12, 1),
+                     "mfma_peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS},
+    }
+
+
 def cpu_baseline(seconds, workload):
     """The oracle (restated reference CPU path) on one host core, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -176,6 +278,29 @@ def cpu_baseline(seconds, workload):
         pass
     body = O.BODY_V4_SIMD if O.has_avx512() else O.BODY_V4
     isa = "AVX-512 (x86-64-v4 body)" if body == O.BODY_V4_SIMD else "x86-64-v3 (v4 body restated with fmaf)"
+    if workload == "prefill":
+        from moe_fixtures import HostLayer
+
+        # one expert's share of a config-2 layer: 64 tokens through its gate, up and down
+        # (selected-token matmuls, model.cpp:404-447), times the 32 experts
+        host = HostLayer(1, 1, biases=False, seed=0x77000300)
+        s = host.oracle_struct()
+        tokens = 64
+        x = O.synth_normal_bf16(0x78000002, 0, tokens * N, 1.0)
+        idx = np.zeros(tokens, np.int64)
+        w = np.ones(tokens, np.float32)
+        out = np.empty(tokens * N, np.float32)
+        count, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds or count == 0:
+            O.lib.orc_moe_batch_experts(C.byref(s), x, tokens, idx, w, out, body)
+            count += 1
+        per_expert = (time.perf_counter() - t0) / count
+        layer_s = per_expert * EXPERTS
+        return {"value": round(PREFILL_TOKENS / layer_s, 2), "unit": "token-layers/s", "cores": 1, "kind": "port",
+                "sample": f"{count} runs of one expert's 64-token share (gate, up, SwiGLU, down selected-token "
+                          f"matmuls) in {per_expert * 1e3:.0f} ms each, times 32 experts = one 512-token layer; "
+                          f"oracle restatement of tensor.cpp:319-495 / model.cpp:378-460 (the matmul's token loop "
+                          f"auto-vectorized, -O3 -ffp-contract=off -march=x86-64-v3)"}
     if workload == "moe":
         from moe_fixtures import HostLayer
 
@@ -233,7 +358,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "moe"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "moe", "prefill"], default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -265,7 +390,8 @@ def main():
         src.free()
         dst.free()
         dev.close()
-    res = gpu_decode(args) if args.workload == "decode" else gpu_moe(args)
+    runner = {"decode": gpu_decode, "moe": gpu_moe, "prefill": gpu_prefill}[args.workload]
+    res = runner(args)
     base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.workload)
     if base:
         log(f"cpu baseline: {base['value']} {base['unit']}")
@@ -280,7 +406,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (MXFP4/Q8_0/bf16 weights)",
+        "dtype": res.get("dtype", "f32 (MXFP4/Q8_0/bf16 weights)"),
         "data": "synthetic",
         "config": dict(res["config"], launch="eager" if args.eager else "hip graph"),
         "roofline": res["roofline"],

@@ -240,6 +240,19 @@ size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_
 int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
                             uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
                             void *workspace_dev, size_t workspace_bytes);
+/* ttl_moe_prefill_experts split into its launches, for callers that time or
+ * reorder them: the stages in `stages` run in this order, each reading what the
+ * earlier stages left in the workspace (so a stage may be re-run alone after one
+ * full call with the same arguments).  No reference counterpart. */
+#define TTL_PREFILL_PLAN 1u     /* bucket the pairs by expert, cut 64-slot tiles      */
+#define TTL_PREFILL_GATHER 2u   /* the tiles' activations as MFMA operand fragments   */
+#define TTL_PREFILL_GATEUP 4u   /* gate and up GEMMs + clamped SwiGLU                  */
+#define TTL_PREFILL_DOWN 8u     /* down GEMM, per slot                                 */
+#define TTL_PREFILL_COMBINE 16u /* weighted sum per token in expert order              */
+#define TTL_PREFILL_ALL 31u
+int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
+                           uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
+                           void *workspace_dev, size_t workspace_bytes, uint32_t stages);
 
 /* ---- matvec inputs ----------------------------------------------------------------- *
  * The vector a matvec reads, with the elementwise steps GptOssModel::forward runs

@@ -27,21 +27,7 @@ def dev():
     d.close()
 
 
-def balanced_routing(count, experts, used, seed):
-    """Config-2 routing: every expert chosen equally often, `used` distinct experts per
-    token, weights = softmax of N(0,1) logits (rank order)."""
-    assert (count * used) % experts == 0 and experts % used == 0
-    rng = np.random.RandomState(seed)
-    step = experts // used
-    base = np.arange(count) % experts
-    idx = np.stack([(base + step * r) % experts for r in range(used)], axis=1)
-    labels = rng.permutation(experts)
-    idx = labels[idx][rng.permutation(count)]
-    for p in range(count):
-        idx[p] = idx[p][rng.permutation(used)]
-    logits = rng.randn(count, used)
-    w = np.exp(logits - logits.max(1, keepdims=True))
-    return idx.astype(np.int32), (w / w.sum(1, keepdims=True)).astype(np.float32)
+balanced_routing = ttlab_amd.balanced_routing
 
 
 def kat_matrix():

@@ -332,10 +332,10 @@ __global__ __launch_bounds__(256) void gather_kernel(const void *__restrict__ x,
 // ---- the MFMA main loop ----------------------------------------------------------------
 
 // K steps per LDS stage for P activation planes: a stage holds P * steps * 4
-// fragments (16 KiB for one plane, 12 KiB for three).
+// fragments (16 KiB for one plane, 24 KiB for three).
 template <int P>
 struct StageShape {
-    static constexpr int steps = P == 1 ? 4 : (P == 2 ? 2 : 1);
+    static constexpr int steps = P == 1 ? 4 : 2;
     static constexpr int count = mf::steps / steps;
     static constexpr int frags = P * steps * mf::col_tiles;
     static constexpr int chunks = frags * 64;  // 16-byte pieces
@@ -432,19 +432,36 @@ struct GateUpArgs {
     Plan plan;
 };
 
+// Workgroup -> (token tile, row group).  Workgroups are dispatched round-robin
+// over the chip's 8 XCDs (each with its own L2), so consecutive logical indices
+// are taken from the same XCD: all row groups of one token tile then read its
+// activation fragments through one L2.  Workgroups past the tiles in use return.
+__device__ inline bool tile_of_workgroup(uint32_t tiles, uint32_t &tile, uint32_t &row_group) {
+    const uint32_t groups = gridDim.x;
+    const uint32_t id = blockIdx.y * groups + blockIdx.x;
+    const uint32_t active = tiles * groups;
+    if (id >= active) {
+        return false;
+    }
+    const uint32_t logical = active % 8 == 0 ? (id % 8) * (active / 8) + id / 8 : id;
+    tile = logical / groups;
+    row_group = logical % groups;
+    return true;
+}
+
 // Accumulators: [matrix (gate 0/1, up 2/3)][column tile]
 template <int PX>
 __global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
     using SS = StageShape<PX>;
     constexpr int kThreads = kGuWaves * 64;
     __shared__ mf::u32x4 lds[2][Stager<PX, kThreads>::lds_chunks];
-    const uint32_t tile = blockIdx.y;
-    if (tile >= a.plan.header->tiles) {
+    uint32_t tile, row_group;
+    if (!tile_of_workgroup(a.plan.header->tiles, tile, row_group)) {
         return;
     }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
-    const uint32_t row0 = blockIdx.x * kGuRows + wave * 32;  // this wave's 32 rows (one down K block)
+    const uint32_t row0 = row_group * kGuRows + wave * 32;  // this wave's 32 rows (one down K block)
     const size_t tile0 = size_t(expert) * a.tiles_per_expert + row0 / 16;
     const uint8_t *frags = a.plan.xb + size_t(tile) * PX * mf::plane_bytes;
 
@@ -600,13 +617,13 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
     using SS = StageShape<P>;
     constexpr int kThreads = kMmWaves * 64;
     __shared__ mf::u32x4 lds[2][Stager<P, kThreads>::lds_chunks];
-    const uint32_t tile = blockIdx.y;
-    if (tile >= a.plan.header->tiles) {
+    uint32_t tile, row_group;
+    if (!tile_of_workgroup(a.plan.header->tiles, tile, row_group)) {
         return;
     }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
-    const uint32_t row0 = blockIdx.x * kMmRows + wave * (kMmTiles * 16);
+    const uint32_t row0 = row_group * kMmRows + wave * (kMmTiles * 16);
     const bool rows_ok = row0 < a.rows;  // waves past the last row only help stage
     const uint32_t row_base = rows_ok ? row0 : 0;
     const size_t tile0 = size_t(expert) * a.tiles_per_expert + row_base / 16;
@@ -869,11 +886,13 @@ size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_
     return make_layout(count * used, experts, planes, true, uint32_t(mx::cols)).total;
 }
 
-int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
-                            uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
-                            void *workspace_dev, size_t workspace_bytes) {
+int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
+                           uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
+                           void *workspace_dev, size_t workspace_bytes, uint32_t stages) {
     TTL_REQUIRE(ctx && layer && x_dev && indices_dev && weights_dev && out_dev && workspace_dev, TTL_ERR_INVALID,
                 "ttl_moe_prefill_experts: null argument");
+    TTL_REQUIRE((stages & ~uint32_t(TTL_PREFILL_ALL)) == 0, TTL_ERR_INVALID,
+                "ttl_moe_prefill_stages: unknown stage bits 0x%x", stages);
     const ttl_moe_layer &L = *layer;
     TTL_REQUIRE(L.gate && L.up && L.down, TTL_ERR_INVALID, "ttl_moe_prefill_experts: null expert tensor");
     TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16, TTL_ERR_INVALID,
@@ -906,14 +925,21 @@ int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void
                 workspace_bytes, lay.total);
     const Plan plan = plan_at(workspace_dev, lay);
 
-    plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(indices_dev, weights_dev, pairs, L.used, L.experts, plan);
-    TTL_LAUNCHED("plan_kernel");
-    if (bf16) {
-        gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
-    } else {
-        gather_kernel<false, 3><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+    if (stages & TTL_PREFILL_PLAN) {
+        plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(indices_dev, weights_dev, pairs, L.used, L.experts, plan);
+        TTL_LAUNCHED("plan_kernel");
     }
-    TTL_LAUNCHED("gather_kernel");
+    if (stages & TTL_PREFILL_GATHER) {
+        if (bf16) {
+            gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+        } else {
+            gather_kernel<false, 3><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+        }
+        TTL_LAUNCHED("gather_kernel");
+    }
+    if ((stages & (TTL_PREFILL_GATEUP | TTL_PREFILL_DOWN | TTL_PREFILL_COMBINE)) == 0) {
+        return TTL_OK;
+    }
 
     GateUpArgs g;
     g.gate_codes = L.gate->codes;
@@ -926,12 +952,14 @@ int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void
     g.tiles_per_expert = L.gate->tiles;
     g.plan = plan;
     const dim3 gu_grid(L.expert_hidden / kGuRows, lay.tmax);
-    if (bf16) {
-        gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
-    } else {
-        gateup_kernel<3><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+    if (stages & TTL_PREFILL_GATEUP) {
+        if (bf16) {
+            gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        } else {
+            gateup_kernel<3><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        }
+        TTL_LAUNCHED("gateup_kernel");
     }
-    TTL_LAUNCHED("gateup_kernel");
 
     MatmulArgs m;
     m.codes = L.down->codes;
@@ -943,12 +971,23 @@ int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void
     m.plan = plan;
     m.out = plan.down;
     m.out_rows = 0;
-    matmul_kernel<kHiddenPlanes, false><<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
-    TTL_LAUNCHED("matmul_kernel");
-
-    combine_for(L.used, plan, count, L.hidden, out_dev, ctx->stream);
-    TTL_LAUNCHED("combine_kernel");
+    if (stages & TTL_PREFILL_DOWN) {
+        matmul_kernel<kHiddenPlanes, false>
+            <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
+        TTL_LAUNCHED("matmul_kernel");
+    }
+    if (stages & TTL_PREFILL_COMBINE) {
+        combine_for(L.used, plan, count, L.hidden, out_dev, ctx->stream);
+        TTL_LAUNCHED("combine_kernel");
+    }
     return TTL_OK;
+}
+
+int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
+                            uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
+                            void *workspace_dev, size_t workspace_bytes) {
+    return ttl_moe_prefill_stages(ctx, layer, x_dev, x_dtype, count, indices_dev, weights_dev, out_dev,
+                                  workspace_dev, workspace_bytes, TTL_PREFILL_ALL);
 }
 
 }  // extern "C"

@@ -17,6 +17,8 @@ HEADER_PATH = os.path.join(REPO_DIR, "include", "ttlab_hip.h")
 TTL_OK = 0
 TTL_DTYPE_F32 = 0
 TTL_DTYPE_BF16 = 1
+TTL_PREFILL_PLAN, TTL_PREFILL_GATHER, TTL_PREFILL_GATEUP, TTL_PREFILL_DOWN, TTL_PREFILL_COMBINE = 1, 2, 4, 8, 16
+TTL_PREFILL_ALL = 31
 
 
 class TtlError(RuntimeError):
@@ -250,6 +252,7 @@ def load_library():
         "ttl_matmul_mxfp4_selected": (i32, [vp, vp, vp, vp, u32, u32, vp, u32, vp, u32, vp, sz]),
         "ttl_moe_prefill_workspace_bytes": (sz, [u32, u32, u32, i32]),
         "ttl_moe_prefill_experts": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz]),
+        "ttl_moe_prefill_stages": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz, u32]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
@@ -263,6 +266,31 @@ def load_library():
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+def balanced_routing(count, experts, used, seed):
+    """Synthetic routing of BASELINE config 2: every expert is chosen equally often,
+    each token has `used` distinct experts (rank order shuffled), and the weights are
+    the softmax of N(0,1) logits.  Returns int32 [count][used], f32 [count][used]."""
+    if (count * used) % experts or experts % used:
+        raise ValueError("balanced routing needs experts | count*used and used | experts")
+    rng = np.random.RandomState(seed)
+    step = experts // used
+    base = np.arange(count) % experts
+    idx = np.stack([(base + step * r) % experts for r in range(used)], axis=1)
+    labels = rng.permutation(experts)
+    idx = labels[idx][rng.permutation(count)]
+    for p in range(count):
+        idx[p] = idx[p][rng.permutation(used)]
+    logits = rng.randn(count, used)
+    w = np.exp(logits - logits.max(1, keepdims=True))
+    return idx.astype(np.int32), (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def bf16_bits(values):
+    """f32 -> bf16 bit patterns, round to nearest even (requant.cpp:311-316 for finite values)."""
+    u = np.ascontiguousarray(values, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
 def header_symbols():
@@ -553,10 +581,15 @@ class Device:
     def moe_prefill_workspace_bytes(self, count, experts, used, x_dtype):
         return self.lib.ttl_moe_prefill_workspace_bytes(count, experts, used, x_dtype)
 
-    def moe_prefill_experts(self, layer, x, x_dtype, count, indices, weights, out, workspace):
-        _check(self.lib.ttl_moe_prefill_experts(self.ctx, C.byref(layer), x.ptr, x_dtype, count, indices.ptr,
-                                                weights.ptr, out.ptr, workspace.ptr, workspace.nbytes),
-               "ttl_moe_prefill_experts")
+    def moe_prefill_experts(self, layer, x, x_dtype, count, indices, weights, out, workspace, stages=None):
+        if stages is None:
+            _check(self.lib.ttl_moe_prefill_experts(self.ctx, C.byref(layer), x.ptr, x_dtype, count, indices.ptr,
+                                                    weights.ptr, out.ptr, workspace.ptr, workspace.nbytes),
+                   "ttl_moe_prefill_experts")
+        else:
+            _check(self.lib.ttl_moe_prefill_stages(self.ctx, C.byref(layer), x.ptr, x_dtype, count, indices.ptr,
+                                                   weights.ptr, out.ptr, workspace.ptr, workspace.nbytes, stages),
+                   "ttl_moe_prefill_stages")
 
     def matvec_mxfp4_experts(self, w, bias, x, x_stride, experts, n, y):
         _check(self.lib.ttl_matvec_mxfp4_experts(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
