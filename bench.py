@@ -56,13 +56,14 @@ def log(msg):
 def gpu_decode(args):
     import ttlab_amd
 
-    context = args.context
+    context, experts = args.context, args.experts
     capacity = context + args.warmup + args.steps + 8
     t0 = time.time()
-    model = ttlab_amd.Model(args.layers, EXPERTS, VOCAB, capacity, SEED)
+    model = ttlab_amd.Model(args.layers, experts, VOCAB, capacity, SEED)
     if args.eager:
         model.set_graph_replay(False)
-    log(f"model resident: {model.device_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
+    model_bytes = model.device_bytes
+    log(f"model resident: {model_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
     t0 = time.time()
     filled = model.generate(1, 0, context)
     log(f"KV caches filled to {context} positions by decoding ({time.time() - t0:.1f} s)")
@@ -81,9 +82,11 @@ def gpu_decode(args):
         "value": tok_s,
         "unit": "tok/s",
         "ms_per_step": ms,
-        "config": {"workload": f"config 3: full synthetic gpt-oss-20b decode, batch 1, greedy, KV context {context} "
-                               "(filled by decoding), step = one token (one HIP graph replay)",
-                   "layers": args.layers, "experts": EXPERTS, "experts_used": USED, "vocab": VOCAB,
+        "config": {"workload": f"config {args.config}: full synthetic gpt-oss-{'20b' if args.config == 3 else '120b'} "
+                               f"decode, batch 1, greedy, KV context {context} (filled by decoding), step = one token "
+                               "(one HIP graph replay)",
+                   "layers": args.layers, "experts": experts, "experts_used": USED, "vocab": VOCAB,
+                   "device_GB": round(model_bytes / 1e9, 2),
                    "context": context, "unembedding": "bf16", "attention_weights": "Q8_0",
                    "step_algorithmic_bytes": int(step_bytes),
                    "step_algorithmic_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
@@ -263,7 +266,7 @@ def gpu_prefill(args):
     }
 
 
-def cpu_baseline(seconds, workload):
+def cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
     """The oracle (restated reference CPU path) on one host core, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import ctypes as C
@@ -320,10 +323,10 @@ def cpu_baseline(seconds, workload):
     from model_fixtures import HostModelLayer
 
     # Layers with 4 experts (all selected): the same per-token work as 4 of 32.
-    layers = [HostModelLayer(SEED, l, 4) for l in (0, 1)]
+    host_layers = [HostModelLayer(SEED, l, 4) for l in (0, 1)]
     freqs = np.empty(32, np.float32)
     O.lib.orc_rope_frequencies(freqs)
-    cap = CONTEXT + 1
+    cap = context + 1
     kc = O.synth_normal(0x78000300, 1, cap * 512)
     vc = O.synth_normal(0x78000300, 2, cap * 512)
     x = O.synth_normal(0x78000300, 3, N, sigma=30.0)
@@ -333,9 +336,9 @@ def cpu_baseline(seconds, workload):
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds * 0.6 or not times[1]:
         for l in (0, 1):
-            s = layers[l].struct()
+            s = host_layers[l].struct()
             t = time.perf_counter()
-            O.lib.orc_layer_forward(C.byref(s), l, CONTEXT, x, freqs, kc, vc, body, outs["x"], outs["q"], outs["a"],
+            O.lib.orc_layer_forward(C.byref(s), l, context, x, freqs, kc, vc, body, outs["x"], outs["q"], outs["a"],
                                     outs["r"], outs["ro"], idx, w)
             times[l].append(time.perf_counter() - t)
     unembed = O.synth_bf16(SEED, 3 * 1000, VOCAB * N)
@@ -344,12 +347,13 @@ def cpu_baseline(seconds, workload):
     O.lib.orc_matvec_bf16(unembed, VOCAB, N, x, logits)
     t_logits = time.perf_counter() - t
     t_window, t_full = float(np.median(times[0])), float(np.median(times[1]))
-    t_token = 12 * t_window + 12 * t_full + t_logits
+    t_token = (layers // 2) * t_window + (layers - layers // 2) * t_full + t_logits
     return {"value": round(1.0 / t_token, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"oracle restatement of model.cpp forward at position {CONTEXT}: median of {len(times[0])} "
+            "sample": f"oracle restatement of model.cpp forward at position {context}: median of {len(times[0])} "
                       f"window-layer ({t_window * 1e3:.0f} ms) and {len(times[1])} full-context-layer "
                       f"({t_full * 1e3:.0f} ms) runs plus one 201088-row bf16 unembedding ({t_logits * 1e3:.0f} ms); "
-                      f"token = 12 + 12 layers + unembedding; MXFP4 {isa}, other matvecs as the reference's C loops "
+                      f"token = {layers // 2} + {layers - layers // 2} layers + unembedding; MXFP4 {isa}, other matvecs "
+                      f"as the reference's C loops "
                       f"(-O3 -ffp-contract=off -march=x86-64-v3)"}
 
 
@@ -364,14 +368,22 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch each step's kernels one by one instead of replaying the step graph "
                          "(for kernel tracers that cannot follow graph launches)")
-    ap.add_argument("--context", type=int, default=CONTEXT,
-                    help="KV positions filled before timing (2048 is the headline workload)")
-    ap.add_argument("--layers", type=int, default=LAYERS,
-                    help="decoder layers (24 is the headline workload; fewer only for counter probes)")
+    ap.add_argument("--config", type=int, choices=[3, 4], default=3,
+                    help="decode workload: 3 = gpt-oss-20b shape (24 layers, 32 experts, KV 2048; the headline), "
+                         "4 = gpt-oss-120b shape (36 layers, 128 experts, KV 4096)")
+    ap.add_argument("--context", type=int, default=None,
+                    help="KV positions filled before timing (default: 2048 for config 3, 4096 for config 4)")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="decoder layers (default 24 / 36; fewer only for counter probes)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device once, a known-size reference "
                          "dispatch for scaling hardware byte counters")
     args = ap.parse_args()
+    args.experts = EXPERTS if args.config == 3 else 128
+    if args.layers is None:
+        args.layers = LAYERS if args.config == 3 else 36
+    if args.context is None:
+        args.context = CONTEXT if args.config == 3 else 4096
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
@@ -392,7 +404,7 @@ def main():
         dev.close()
     runner = {"decode": gpu_decode, "moe": gpu_moe, "prefill": gpu_prefill}[args.workload]
     res = runner(args)
-    base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.workload)
+    base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.workload, args.layers, args.context)
     if base:
         log(f"cpu baseline: {base['value']} {base['unit']}")
     line = {

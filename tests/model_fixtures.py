@@ -19,7 +19,11 @@ def stream(layer, kind):
 
 
 class HostModelLayer:
-    def __init__(self, seed, l, experts):
+    """One layer's tensors.  lazy=True leaves the expert matrices zero until
+    ensure_experts() generates the ones an oracle run reads (120b-shaped layers hold
+    128 experts x 3 x 4.4 MB)."""
+
+    def __init__(self, seed, l, experts, lazy=False):
         n = lambda kind, count, sigma, mean=0.0: O.synth_normal(seed, stream(l, kind), count, sigma=sigma, mean=mean)
         self.attn_norm = n(ATTN_NORM, N, 0.05, 1.0)
         self.post_norm = n(POST_NORM, N, 0.05, 1.0)
@@ -33,12 +37,22 @@ class HostModelLayer:
         self.sinks = n(SINKS, 64, 1.0)
         self.router = O.synth_normal_bf16(seed, stream(l, ROUTER), experts * N, 0.02)
         self.router_b = n(ROUTER_BIAS, experts, 0.02)
-        mx = lambda kind: np.concatenate([O.synth_mxfp4(seed, stream(l, kind) + e, N * 90) for e in range(experts)])
-        self.gate, self.up, self.down = mx(GATE), mx(UP), mx(DOWN)
+        self.seed, self.l = seed, l
+        per = N * 90 * 17
+        self.gate, self.up, self.down = (np.zeros(experts * per, np.uint8) for _ in range(3))
+        self.filled = set()
+        self.ensure_experts(range(experts) if not lazy else [])
         self.gate_b = n(GATE_BIAS, experts * N, 0.05)
         self.up_b = n(UP_BIAS, experts * N, 0.05)
         self.down_b = n(DOWN_BIAS, experts * N, 0.05)
         self.experts = experts
+
+    def ensure_experts(self, ids):
+        per = N * 90 * 17
+        for e in sorted(set(int(i) for i in ids) - self.filled):
+            for arr, kind in ((self.gate, GATE), (self.up, UP), (self.down, DOWN)):
+                arr[e * per:(e + 1) * per] = O.synth_mxfp4(self.seed, stream(self.l, kind) + e, N * 90)
+            self.filled.add(e)
 
     def struct(self):
         s = O.OrcLayer()
@@ -60,9 +74,9 @@ class HostModelLayer:
 
 
 class HostModel:
-    def __init__(self, seed, layers, experts, vocab):
+    def __init__(self, seed, layers, experts, vocab, lazy=False):
         self.seed, self.vocab = seed, vocab
-        self.layers = [HostModelLayer(seed, l, experts) for l in range(layers)]
+        self.layers = [HostModelLayer(seed, l, experts, lazy) for l in range(layers)]
         self.output_norm = O.synth_normal(seed, stream(-1, OUTPUT_NORM), N, sigma=0.05, mean=1.0)
         self.unembedding = O.synth_bf16(seed, stream(-1, UNEMBEDDING), vocab * N)
         self.freqs = np.empty(32, np.float32)
@@ -83,9 +97,17 @@ class HostModel:
         router = np.empty(self.layers[l].experts, np.float32)
         idx = np.empty(4, np.int64)
         w = np.empty(4, np.float32)
-        s = self.layers[l].struct()
-        O.lib.orc_layer_forward(C.byref(s), l, position, np.ascontiguousarray(x_in, np.float32), self.freqs,
-                                key_cache, value_cache, body, x_out, q, att, res, router, idx, w)
+        layer = self.layers[l]
+        kc0, vc0 = key_cache.copy(), value_cache.copy()
+        while True:
+            s = layer.struct()
+            O.lib.orc_layer_forward(C.byref(s), l, position, np.ascontiguousarray(x_in, np.float32), self.freqs,
+                                    key_cache, value_cache, body, x_out, q, att, res, router, idx, w)
+            if set(int(i) for i in idx) <= layer.filled:
+                break
+            # a lazy layer had not generated the experts this token routes to: fill, rerun
+            layer.ensure_experts(idx)
+            key_cache[:], value_cache[:] = kc0, vc0
         return {"x_out": x_out, "query": q, "attended": att, "residual": res, "router": router, "indices": idx,
                 "weights": w}
 

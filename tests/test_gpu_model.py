@@ -19,10 +19,13 @@ TOL = 1e-5
 SEED, LAYERS, EXPERTS, VOCAB, CAPACITY = 0x77000003, 2, 32, 4096, 160
 
 
-@pytest.fixture(scope="module")
-def models():
-    gpu = ttlab_amd.Model(LAYERS, EXPERTS, VOCAB, CAPACITY, SEED)
-    host = HostModel(SEED, LAYERS, EXPERTS, VOCAB)
+# 32 experts: the 20b shape; 128: the 120b routing width (config 4),
+# whose host copy generates only the experts the oracle routes to.
+@pytest.fixture(scope="module", params=[EXPERTS, 128], ids=["20b", "120b"])
+def models(request):
+    experts = request.param
+    gpu = ttlab_amd.Model(LAYERS, experts, VOCAB, CAPACITY, SEED)
+    host = HostModel(SEED, LAYERS, experts, VOCAB, lazy=experts > 32)
     yield gpu, host
     gpu.close()
 
