@@ -334,6 +334,11 @@ size_t ttl_logits_workspace_bytes(uint32_t vocab);
  * partials in workspace_dev for ttl_argmax. */
 int ttl_logits_bf16(ttl_ctx *ctx, const uint16_t *weight_dev, uint32_t vocab, const ttl_stage_input *in,
                     float *logits_dev, void *workspace_dev);
+/* The same for a Q8_0 unembedding (a GGUF model's output.weight, vocab x 2880;
+ * matvec_q8_0 at model.cpp:598-599).  The partials feed ttl_argmax as those of
+ * ttl_logits_bf16 do. */
+int ttl_logits_q8_0(ttl_ctx *ctx, const ttl_q8 *weight, uint32_t vocab, const ttl_stage_input *in, float *logits_dev,
+                    void *workspace_dev);
 /* greedy (model.cpp:604-612) from ttl_logits_bf16's partials: writes the token to
  * token_dev and, if position_dev is non-NULL, also history_dev[position] (when
  * history_dev is non-NULL and position < history_len) and increments the position. */

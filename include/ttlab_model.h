@@ -4,10 +4,10 @@
  *
  * The model mirrors the reference's GptOssModel (model.h:15-31): construction
  * allocates everything, forward(token, position) advances one token and returns
- * logits, greedy() picks the first maximum.  Weights here are synthetic (the
- * BASELINE configurations 3 and 4), generated on the device from the stream
- * layout of ttlab::synth_stream().  Every call returns 0 or a negative code;
- * ttlm_last_error() has the message.
+ * logits, greedy() picks the first maximum.  Weights come from a gpt-oss GGUF
+ * file (ttlm_create_from_gguf) or are synthetic (the BASELINE configurations 3 and
+ * 4), generated on the device from the stream layout of ttlab::synth_stream().
+ * Every call returns 0 or a negative code; ttlm_last_error() has the message.
  */
 #ifndef TTLAB_MODEL_H
 #define TTLAB_MODEL_H
@@ -24,6 +24,22 @@ typedef struct ttlm_model ttlm_model;
 /* layers >= 1, experts 32 or 128, vocab >= 1, capacity = KV positions (token capacity). */
 int ttlm_create_synthetic(int device, uint32_t layers, uint32_t experts, uint32_t vocab, uint32_t capacity,
                           uint64_t seed, ttlm_model **out);
+/* A gpt-oss GGUF file (version 3, as the reference's GgufFile reads it, gguf.cpp:145-239):
+ * the metadata and tensors GptOssModel's constructor checks (model.cpp:64-206), with
+ * its error messages.  strict != 0 applies the reference's limits exactly (24 or 36
+ * layers, 32 or 128 experts, vocabulary 201088, Q8_0 output.weight); strict == 0
+ * also accepts 1..36 layers, 4..128 experts, a vocabulary that is a multiple of 16
+ * and a BF16 output.weight (small test models, bf16-unembedding configurations). */
+typedef struct {
+    uint32_t layers, experts, vocab;
+    uint32_t output_type; /* GGML type of output.weight: 8 (Q8_0) or 30 (BF16) */
+    uint32_t tensors;
+} ttlm_gguf_info;
+/* Checks a file without a device. */
+int ttlm_gguf_inspect(const char *path, int strict, ttlm_gguf_info *info);
+/* The model with a GGUF file's weights (uploaded to the device, MXFP4 and Q8_0
+ * repacked there); capacity = token capacity of the KV caches (model.cpp:64). */
+int ttlm_create_from_gguf(const char *path, int device, uint32_t capacity, int strict, ttlm_model **out);
 void ttlm_destroy(ttlm_model *model);
 const char *ttlm_last_error(void);
 

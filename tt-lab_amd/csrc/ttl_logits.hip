@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 
 #include "ttl_internal.hpp"
+#include "ttl_q8_tile.hpp"
 #include "ttl_stage.hpp"
 
 #include <cmath>
@@ -128,6 +129,93 @@ __global__ __launch_bounds__(kThreads) void logits_kernel(const uint16_t *__rest
     }
 }
 
+// The Q8_0 unembedding of a GGUF model (output.weight, model.cpp:598-599 through
+// matvec_q8_0, tensor.cpp:202-218), with the same per-workgroup argmax as
+// logits_kernel.  Rows are repacked Q8_0 tiles of 16 (ttl_q8_tile.hpp); one
+// workgroup stages the input once and walks tiles blockIdx.x, blockIdx.x + gridDim.x,
+// ..., the next tile's codes in flight while the current one is reduced.
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void logits_q8_kernel(const uint8_t *__restrict__ codes,
+                                                             const uint16_t *__restrict__ scales, uint32_t rows,
+                                                             stage::Input in, float *__restrict__ logits,
+                                                             Best *__restrict__ partial) {
+    using S = q8::Shape<kCols>;
+    __shared__ __attribute__((aligned(16))) float xs[S::x_blocks * stage::x_stride];
+    __shared__ float xsum[S::x_blocks];
+    __shared__ float red[stage::red_floats(S::x_blocks)];
+    __shared__ float part[q8::waves][q8::tile_rows];
+    __shared__ float bvals[q8::tile_rows];
+    __shared__ int32_t bidx[q8::tile_rows];
+    __shared__ int32_t row0_nan;
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t tiles = rows / q8::tile_rows, stride = gridDim.x;
+    if (blockIdx.x != 0) {
+        in.v_out = nullptr;
+    }
+    stage::Pending<kCols, S::x_blocks, kThreads, MODE> pending;
+    stage::stage_load(in, pending);
+    q8::TileRegs<kCols> regs[2];
+    q8::tile_load<kCols>(codes, scales, blockIdx.x, wave, lane, regs[0]);
+    stage::stage_finish(in, pending, xs, red);
+    q8::block_sums(xs, S::x_blocks, xsum);
+    if (threadIdx.x == 0) {
+        row0_nan = 0;
+    }
+    float bv = NAN;
+    int32_t bi = 0x7fffffff;
+    auto finish = [&](uint32_t t, const q8::TileRegs<kCols> &r) __attribute__((always_inline)) {
+        const float acc = q8::tile_compute<kCols>(r, wave, lane, xs, xsum);
+        if (lane < q8::tile_rows) {
+            part[wave][lane] = acc;
+        }
+        __syncthreads();
+        if (threadIdx.x < q8::tile_rows) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < q8::waves; ++w) {
+                sum += part[w][threadIdx.x];
+            }
+            const uint32_t row = t * q8::tile_rows + threadIdx.x;
+            logits[row] = sum;
+            // a thread's rows arrive in increasing order, so better() keeps the first maximum
+            if (better(sum, int32_t(row), bv, bi)) {
+                bv = sum;
+                bi = int32_t(row);
+            }
+            if (row == 0 && isnan(sum)) {
+                row0_nan = 1;
+            }
+        }
+        __syncthreads();
+    };
+    // two register sets with static indices: tile t computes while t + stride loads
+    for (uint32_t t = blockIdx.x; t < tiles; t += 2 * stride) {
+        const uint32_t t1 = t + stride;
+        q8::tile_load<kCols>(codes, scales, min(t1, tiles - 1), wave, lane, regs[1]);
+        finish(t, regs[0]);
+        if (t1 >= tiles) {
+            break;
+        }
+        q8::tile_load<kCols>(codes, scales, min(t1 + stride, tiles - 1), wave, lane, regs[0]);
+        finish(t1, regs[1]);
+    }
+    if (threadIdx.x < q8::tile_rows) {
+        bvals[threadIdx.x] = bv;
+        bidx[threadIdx.x] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Best b{NAN, 0x7fffffff, row0_nan, 0};
+        for (int r = 0; r < q8::tile_rows; ++r) {
+            if (better(bvals[r], bidx[r], b.value, b.index)) {
+                b.value = bvals[r];
+                b.index = bidx[r];
+            }
+        }
+        partial[blockIdx.x] = b;
+    }
+}
+
 // Reduces the per-group bests, writes the greedy token and advances the position.
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const Best *__restrict__ partial, uint32_t groups,
                                                           int32_t *__restrict__ token, int32_t *__restrict__ position,
@@ -224,6 +312,27 @@ int ttl_logits_bf16(ttl_ctx *ctx, const uint16_t *weight_dev, uint32_t vocab, co
             weight_dev, vocab, s, logits_dev, reinterpret_cast<Best *>(workspace_dev));
     });
     TTL_LAUNCHED("logits_kernel");
+    return TTL_OK;
+}
+
+int ttl_logits_q8_0(ttl_ctx *ctx, const ttl_q8 *weight, uint32_t vocab, const ttl_stage_input *in, float *logits_dev,
+                    void *workspace_dev) {
+    TTL_REQUIRE(ctx && weight && weight->codes && weight->scales && logits_dev && workspace_dev, TTL_ERR_INVALID,
+                "ttl_logits_q8_0: null argument");
+    const int rc = stage::check(in, "ttl_logits_q8_0");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(weight->cols == uint32_t(kCols) && weight->rows == vocab && vocab > 0, TTL_ERR_SHAPE,
+                "ttl_logits_q8_0: the tensor must be vocab x %d (got %u x %u, vocab %u)", kCols, weight->rows,
+                weight->cols, vocab);
+    const stage::Input s = stage::from_abi(in);
+    const uint32_t groups = uint32_t(ttl::logits_partials(vocab));  // vocab / 16 tiles, at most 1024 workgroups
+    stage::with_mode(s, [&](auto mode) {
+        logits_q8_kernel<decltype(mode)::value><<<groups, kThreads, 0, ctx->stream>>>(
+            weight->codes, weight->scales, vocab, s, logits_dev, reinterpret_cast<Best *>(workspace_dev));
+    });
+    TTL_LAUNCHED("logits_q8_kernel");
     return TTL_OK;
 }
 

@@ -68,6 +68,52 @@ HipGptOssModel::HipGptOssModel(const SyntheticSpec &spec, int device) : spec_(sp
     check(ttl_create(device, &ctx_), "ttl_create");
     try {
         generate_weights();
+        finish_construction();
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+HipGptOssModel::HipGptOssModel(const GgufFile &file, size_t token_capacity, int device, bool strict) {
+    const GgufModelShape shape = check_gguf_model(file, strict);
+    if (token_capacity < 1 || token_capacity > context_length) {
+        throw std::runtime_error("token capacity exceeds model context");  // model.cpp:99-101
+    }
+    spec_.layers = shape.layers;
+    spec_.experts = shape.experts;
+    spec_.vocab = shape.vocab;
+    spec_.capacity = uint32_t(token_capacity);
+    spec_.seed = 0;
+    check(ttl_create(device, &ctx_), "ttl_create");
+    try {
+        upload_gguf(file);
+        finish_construction();
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+// RoPE table, activations and the captured step: the part of construction that does
+// not depend on where the weights came from.
+void HipGptOssModel::finish_construction() {
+    {
+        // RoPE coefficients per position and pair, as apply_rope computes them (model.cpp:230-245).
+        const std::array<float, 32> f = rope_frequencies();
+        const float magnitude = 1.0f + 0.1f * std::log(1.0f / (1.0f / 32.0f));
+        std::vector<float> table(size_t(spec_.capacity) * 64);
+        for (size_t pos = 0; pos < spec_.capacity; ++pos) {
+            for (size_t pair = 0; pair < 32; ++pair) {
+                const float theta = float(pos) * f[pair];
+                table[pos * 64 + pair * 2] = std::cos(theta) * magnitude;
+                table[pos * 64 + pair * 2 + 1] = std::sin(theta) * magnitude;
+            }
+        }
+        rope_ = static_cast<float *>(alloc(sizeof(float) * table.size()));
+        check(ttl_memcpy_h2d(ctx_, rope_, table.data(), sizeof(float) * table.size()), "ttl_memcpy_h2d");
+    }
+    {
         // activations (all sizes fixed at construction; nothing is allocated per token)
         const size_t L = spec_.layers;
         token_ = static_cast<int32_t *>(alloc(sizeof(int32_t)));
@@ -86,9 +132,6 @@ HipGptOssModel::HipGptOssModel(const SyntheticSpec &spec, int device) : spec_(sp
         host_logits_.resize(spec_.vocab);
         check(ttl_sync(ctx_), "ttl_sync");
         record_step();
-    } catch (...) {
-        release();
-        throw;
     }
 }
 
@@ -105,6 +148,8 @@ void HipGptOssModel::release() {
         ttl_graph_free(step_);
         step_ = nullptr;
     }
+    ttl_q8_free(ctx_, unembedding_q8_);
+    unembedding_q8_ = nullptr;
     for (Layer &layer : layers_) {
         ttl_q8_free(ctx_, layer.qkv);
         ttl_q8_free(ctx_, layer.attn_output);
@@ -218,20 +263,6 @@ void HipGptOssModel::generate_weights() {
     unembedding_ = static_cast<uint16_t *>(alloc(sizeof(uint16_t) * size_t(spec_.vocab) * kHidden));
     check(ttl_synth_bf16(ctx_, seed, synth_stream(-1, kUnembedding), 0, size_t(spec_.vocab) * kHidden, unembedding_),
           "ttl_synth_bf16");
-
-    // RoPE coefficients per position and pair, as apply_rope computes them (model.cpp:230-245).
-    const std::array<float, 32> f = rope_frequencies();
-    const float magnitude = 1.0f + 0.1f * std::log(1.0f / (1.0f / 32.0f));
-    std::vector<float> table(size_t(spec_.capacity) * 64);
-    for (size_t pos = 0; pos < spec_.capacity; ++pos) {
-        for (size_t pair = 0; pair < 32; ++pair) {
-            const float theta = float(pos) * f[pair];
-            table[pos * 64 + pair * 2] = std::cos(theta) * magnitude;
-            table[pos * 64 + pair * 2 + 1] = std::sin(theta) * magnitude;
-        }
-    }
-    rope_ = static_cast<float *>(alloc(sizeof(float) * table.size()));
-    check(ttl_memcpy_h2d(ctx_, rope_, table.data(), sizeof(float) * table.size()), "ttl_memcpy_h2d");
 }
 
 // One decode step (model.cpp:567-602) as launches on the context's stream:
@@ -276,7 +307,8 @@ int HipGptOssModel::enqueue_step() {
         f.base = x_ + L * kHidden;
         f.norm_weight = output_norm_;
         f.epsilon = norm_epsilon;
-        status = ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits_, logits_workspace_);
+        status = unembedding_q8_ ? ttl_logits_q8_0(ctx_, unembedding_q8_, spec_.vocab, &f, logits_, logits_workspace_)
+                                 : ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits_, logits_workspace_);
     }
     if (status == TTL_OK) {
         status = ttl_argmax(ctx_, spec_.vocab, logits_workspace_, token_, position_, history_, spec_.capacity);
@@ -481,7 +513,8 @@ double HipGptOssModel::step_bytes(size_t position) const {
                              4.0 * (kQkvRows + kHidden + 64 + 2 * kHidden);
     const double router = double(spec_.experts) * kHidden * 4 + double(spec_.experts) * 4;
     const double experts = double(kUsed) * (3.0 * kHidden * kMxfp4RowBytes + 3.0 * kHidden * 4);
-    double total = double(kQ8RowBytes2880) + double(spec_.vocab) * kHidden * 2 + kHidden * 4;
+    const double unembedding = unembedding_q8_ ? double(spec_.vocab) * kQ8RowBytes2880 : double(spec_.vocab) * kHidden * 2;
+    double total = double(kQ8RowBytes2880) + unembedding + kHidden * 4;
     for (size_t l = 0; l < spec_.layers; ++l) {
         const size_t first = (l % 2 == 0 && position + 1 > kSlidingWindow) ? position + 1 - kSlidingWindow : 0;
         const double span = double(position + 1 - first);

@@ -60,6 +60,20 @@ struct SyntheticSpec {
 // YaRN RoPE frequencies exactly as model.cpp:124-139 computes them.
 std::array<float, 32> rope_frequencies();
 
+class GgufFile;
+
+// What a gpt-oss GGUF file holds, after the reference's metadata and tensor checks
+// (GptOssModel's constructor, model.cpp:64-206, with its error messages).  strict
+// applies the reference's limits exactly (24 or 36 layers, 32 or 128 experts, the
+// 201088-token vocabulary, a Q8_0 output.weight); without it, any 1..36 layers,
+// 1..128 experts, a vocabulary that is a multiple of 16 and a BF16 output.weight are
+// also accepted (small test models and the bf16-unembedding configurations).
+struct GgufModelShape {
+    uint32_t layers = 0, experts = 0, vocab = 0;
+    uint32_t output_type = 0;  // GGML type id of output.weight: 8 (Q8_0) or 30 (BF16)
+};
+GgufModelShape check_gguf_model(const GgufFile &file, bool strict);
+
 class HipGptOssModel {
   public:
     static constexpr size_t context_length = 131072;      // model.h:17
@@ -69,6 +83,10 @@ class HipGptOssModel {
     static constexpr float norm_epsilon = 1.0e-5f;
 
     explicit HipGptOssModel(const SyntheticSpec &spec, int device = 0);
+    // The weights of a gpt-oss GGUF file (check_gguf_model), uploaded and repacked on
+    // the device; the file may be closed afterwards.  token_capacity as the reference's
+    // constructor (model.cpp:64, 99-101).
+    HipGptOssModel(const GgufFile &file, size_t token_capacity, int device = 0, bool strict = true);
     ~HipGptOssModel();
     HipGptOssModel(const HipGptOssModel &) = delete;
     HipGptOssModel &operator=(const HipGptOssModel &) = delete;
@@ -122,6 +140,8 @@ class HipGptOssModel {
     void *alloc(size_t bytes);
     void release();
     void generate_weights();
+    void upload_gguf(const GgufFile &file);
+    void finish_construction();
     int enqueue_step();
     void record_step();
     void run_step();
@@ -135,7 +155,8 @@ class HipGptOssModel {
     size_t device_bytes_ = 0;
     uint8_t *embedding_ = nullptr;   // Q8_0, GGUF rows
     float *output_norm_ = nullptr;
-    uint16_t *unembedding_ = nullptr;
+    uint16_t *unembedding_ = nullptr;     // bf16 [vocab][2880] (synthetic configurations)
+    ttl_q8 *unembedding_q8_ = nullptr;    // Q8_0 output.weight (GGUF models)
     float *rope_ = nullptr;          // [capacity][32][2]
     // activations
     int32_t *token_ = nullptr, *position_ = nullptr, *history_ = nullptr;

@@ -1,4 +1,5 @@
 // C API of ttlab::HipGptOssModel (include/ttlab_model.h): exceptions become status codes.
+#include "gguf.hpp"
 #include "gpt_oss_hip.hpp"
 #include "ttlab_model.h"
 
@@ -50,6 +51,37 @@ int ttlm_create_synthetic(int device, uint32_t layers, uint32_t experts, uint32_
         spec.capacity = capacity;
         spec.seed = seed;
         auto *m = new ttlab::HipGptOssModel(spec, device);
+        *out = new ttlm_model{m};
+    });
+}
+
+int ttlm_gguf_inspect(const char *path, int strict, ttlm_gguf_info *info) {
+    return guarded([&] {
+        if (!path || !info) {
+            throw std::runtime_error("ttlm_gguf_inspect: null argument");
+        }
+        const ttlab::GgufFile file(path);
+        const ttlab::GgufModelShape shape = ttlab::check_gguf_model(file, strict != 0);
+        info->layers = shape.layers;
+        info->experts = shape.experts;
+        info->vocab = shape.vocab;
+        info->output_type = shape.output_type;
+        info->tensors = uint32_t(file.tensors().size());
+    });
+}
+
+int ttlm_create_from_gguf(const char *path, int device, uint32_t capacity, int strict, ttlm_model **out) {
+    if (!out) {
+        last_error = "ttlm_create_from_gguf: null output pointer";
+        return -1;
+    }
+    *out = nullptr;
+    return guarded([&] {
+        if (!path) {
+            throw std::runtime_error("ttlm_create_from_gguf: null path");
+        }
+        const ttlab::GgufFile file(path);
+        auto *m = new ttlab::HipGptOssModel(file, capacity, device, strict != 0);
         *out = new ttlm_model{m};
     });
 }

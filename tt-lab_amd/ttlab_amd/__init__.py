@@ -100,6 +100,8 @@ def load_model_library():
         "ttlm_kv_cache": (i32, [vp, u32, u32, vp, vp]),
         "ttlm_device_bytes": (C.c_size_t, [vp]),
         "ttlm_step_bytes": (C.c_double, [vp, u32]),
+        "ttlm_gguf_inspect": (i32, [C.c_char_p, i32, C.POINTER(GgufInfo)]),
+        "ttlm_create_from_gguf": (i32, [C.c_char_p, i32, u32, i32, C.POINTER(vp)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -115,16 +117,42 @@ def _mcheck(rc, what):
         raise TtlError(f"{what} failed: {msg.decode() if msg else ''}")
 
 
-class Model:
-    """ttlab::HipGptOssModel with synthetic weights (BASELINE configurations 3/4)."""
+class GgufInfo(C.Structure):
+    """Mirror of ttlm_gguf_info."""
+    _fields_ = [("layers", C.c_uint32), ("experts", C.c_uint32), ("vocab", C.c_uint32), ("output_type", C.c_uint32),
+                ("tensors", C.c_uint32)]
 
-    def __init__(self, layers=24, experts=32, vocab=201088, capacity=2112, seed=0x77000003, device=0):
+
+def gguf_inspect(path, strict=True):
+    """The reference's checks of a gpt-oss GGUF file (no device needed); raises TtlError."""
+    lib = load_model_library()
+    info = GgufInfo()
+    _mcheck(lib.ttlm_gguf_inspect(os.fsencode(path), 1 if strict else 0, C.byref(info)), "ttlm_gguf_inspect")
+    return {k: getattr(info, k) for k, _ in GgufInfo._fields_}
+
+
+class Model:
+    """ttlab::HipGptOssModel with synthetic weights (BASELINE configurations 3/4), or
+    with a GGUF file's weights (Model.from_gguf)."""
+
+    def __init__(self, layers=24, experts=32, vocab=201088, capacity=2112, seed=0x77000003, device=0, _handle=None):
         self.lib = load_model_library()
-        p = C.c_void_p()
-        _mcheck(self.lib.ttlm_create_synthetic(device, layers, experts, vocab, capacity, seed, C.byref(p)),
-                "ttlm_create_synthetic")
-        self.h = p.value
+        if _handle is None:
+            p = C.c_void_p()
+            _mcheck(self.lib.ttlm_create_synthetic(device, layers, experts, vocab, capacity, seed, C.byref(p)),
+                    "ttlm_create_synthetic")
+            _handle = p.value
+        self.h = _handle
         self.layers, self.experts, self.vocab, self.capacity, self.seed = layers, experts, vocab, capacity, seed
+
+    @classmethod
+    def from_gguf(cls, path, capacity, strict=True, device=0):
+        lib = load_model_library()
+        info = gguf_inspect(path, strict)
+        p = C.c_void_p()
+        _mcheck(lib.ttlm_create_from_gguf(os.fsencode(path), device, capacity, 1 if strict else 0, C.byref(p)),
+                "ttlm_create_from_gguf")
+        return cls(info["layers"], info["experts"], info["vocab"], capacity, 0, device, _handle=p.value)
 
     def close(self):
         if self.h:
