@@ -240,6 +240,17 @@ size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_
 int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
                             uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
                             void *workspace_dev, size_t workspace_bytes);
+/* The whole of GptOssModel::moe_batch (model.cpp:340-461) for `count` tokens: the F32
+ * router per token (matmul_add_f32, model.cpp:341) with the exact top-k and softmax
+ * of the decode router (the certified selection, else the reference's sequential
+ * sums and selection sort), then ttl_moe_prefill_experts on f32 input.  x_dev is the
+ * normalized MoE input f32 [count][2880] as moe_batch receives it (model.cpp:549-551),
+ * so layer->input_norm must be NULL; indices_dev / weights_dev (int32 / f32
+ * [count][used]) may be NULL, else they receive the routing. */
+size_t ttl_moe_prefill_batch_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used);
+int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, uint32_t count, float *out_dev,
+                    int32_t *indices_dev, float *weights_dev, void *workspace_dev, size_t workspace_bytes);
+
 /* ttl_moe_prefill_experts split into its launches, for callers that time or
  * reorder them: the stages in `stages` run in this order, each reading what the
  * earlier stages left in the workspace (so a stage may be re-run alone after one

@@ -2,13 +2,16 @@
 
 ttl_matmul_mxfp4_selected vs orc_matmul_add_mxfp4_selected_transposed
 (tensor.cpp:306-495) and ttl_moe_prefill_experts vs orc_moe_batch_experts
-(model.cpp:378-460).  Exact: the reference's selected-matmul known answer
+(model.cpp:378-460), and ttl_moe_prefill (router + experts, model.cpp:340-461)
+vs orc_moe_batch.  Exact: the reference's selected-matmul known answer
 (tests/host_dispatch.cpp:108-126) and the rows it must leave untouched.
 Tolerance: relative L2 <= 1e-5 per token and overall (the MFMA sums exact
 products in f32 in another order than the reference).  At the full config-2
 shape: the oracle on a sample of tokens (a token's result depends on no other
 token), and bitwise invariance under token and rank permutations.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -203,4 +206,101 @@ def test_prefill_rejects_small_workspace(dev, layer8):
     with pytest.raises(ttlab_amd.TtlError, match="workspace"):
         dev.moe_prefill_experts(device.desc, x, ttlab_amd.TTL_DTYPE_F32, count, ib, wb, out, small)
     for b in (x, ib, wb, out, small):
+        b.free()
+
+
+def run_moe_prefill(dev, layer, x):
+    count = x.shape[0]
+    used = layer.desc.used
+    xb = dev.upload(np.ascontiguousarray(x, np.float32))
+    out = dev.alloc(count * N * 4)
+    ib, wb = dev.alloc(count * used * 4), dev.alloc(count * used * 4)
+    dev.moe_prefill(layer.desc, xb, count, out, ib, wb)
+    got = (out.download(np.float32).reshape(count, N), ib.download(np.int32).reshape(count, used),
+           wb.download(np.float32).reshape(count, used))
+    for b in (xb, out, ib, wb):
+        b.free()
+    return got
+
+
+def oracle_routing(host, x):
+    """The router of orc_moe_batch: batched F32 matmul (tensor.cpp:497-527), then top-4
+    and softmax per token (model.cpp:296-321)."""
+    count, E = x.shape[0], host.experts
+    logits = np.empty(count * E, np.float32)
+    ws, tr = np.empty(count * 5, np.float32), np.empty(count * N, np.float32)
+    O.lib.orc_matmul_add_f32(host.router_w, host.router_b, E, N, np.ascontiguousarray(x, np.float32).ravel(), count,
+                             logits, ws, tr)
+    idx, w = np.empty((count, 4), np.int64), np.empty((count, 4), np.float32)
+    for p in range(count):
+        O.lib.orc_router_topk(logits[p * E:(p + 1) * E], E, 4, idx[p], w[p])
+    return logits.reshape(count, E), idx, w
+
+
+def near_tie(logits, k=4, eps=1e-4):
+    s = np.sort(logits.astype(np.float64))[::-1]
+    return bool(np.any(np.abs(np.diff(s[:k + 1])) < eps))
+
+
+def test_moe_prefill_router_and_experts_match_oracle(dev, layer8):
+    # GptOssModel::moe_batch (model.cpp:340-461): router + top-4 + softmax per token, then experts
+    host, device = layer8
+    count = 40
+    x = O.synth_normal(0x78000002, 6, count * N).reshape(count, N)
+    got, idx, w = run_moe_prefill(dev, device, x)
+    logits, ref_idx, ref_w = oracle_routing(host, x)
+    ref = np.empty(count * N, np.float32)
+    O.lib.orc_moe_batch(host.oracle_struct(), x.ravel(), count, ref, O.BODY_V4)
+    ref = ref.reshape(count, N)
+    checked = 0
+    for p in range(count):
+        if list(idx[p]) != list(ref_idx[p]):
+            assert near_tie(logits[p]), (p, idx[p], ref_idx[p])
+            continue
+        assert np.allclose(w[p], ref_w[p], rtol=1e-5, atol=1e-7), p
+        assert O.rel_l2(got[p], ref[p]) <= TOL, p
+        checked += 1
+    assert checked >= count - 2
+    # the routing it chose, given back to the experts entry point, gives the same bits
+    again = run_prefill(dev, device, x, idx, w, ttlab_amd.TTL_DTYPE_F32)
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+
+
+def test_moe_prefill_config2_router(dev):
+    # 32 experts, 256 f32 tokens: the oracle on a sample of tokens, routing for all
+    count = 256
+    x = O.synth_normal(0x78000103, 0, count * N).reshape(count, N)
+    sample = np.random.RandomState(14).choice(count, 5, replace=False)
+    router_only = HostLayer(32, 4, biases=True, seed=0x77000103, fill_experts=[])
+    logits, ref_idx, ref_w = oracle_routing(router_only, x)
+    host = HostLayer(32, 4, biases=True, seed=0x77000103, fill_experts=ref_idx[sample].ravel())
+    device = DeviceLayer(dev, host)
+    try:
+        got, idx, w = run_moe_prefill(dev, device, x)
+        assert np.all(np.isfinite(got))
+        ties = [p for p in range(count) if list(idx[p]) != list(ref_idx[p])]
+        assert all(near_tie(logits[p]) for p in ties), ties
+        same = np.setdiff1d(np.arange(count), ties)
+        assert np.allclose(w[same], ref_w[same], rtol=1e-5, atol=1e-7)
+        for p in sample:
+            if p in ties:
+                continue
+            ref = np.empty(N, np.float32)
+            O.lib.orc_moe_batch(host.oracle_struct(), np.ascontiguousarray(x[p]), 1, ref, O.BODY_V4)
+            assert O.rel_l2(got[p], ref) <= TOL, p
+    finally:
+        device.free()
+
+
+def test_moe_prefill_zero_tokens_and_input_norm(dev, layer8):
+    host, device = layer8
+    out, xb = dev.alloc(256), dev.alloc(256)
+    ws = dev.alloc(dev.lib.ttl_moe_prefill_batch_workspace_bytes(0, 8, 4))
+    assert dev.lib.ttl_moe_prefill(dev.ctx, C.byref(device.desc), xb.ptr, 0, out.ptr, None, None, ws.ptr,
+                                   ws.nbytes) == 0
+    desc = ttlab_amd.MoeLayerDesc.from_buffer_copy(device.desc)
+    desc.input_norm = xb.ptr
+    with pytest.raises(ttlab_amd.TtlError, match="input_norm"):
+        dev.moe_prefill(desc, xb, 1, out)
+    for b in (out, ws, xb):
         b.free()

@@ -54,6 +54,11 @@ namespace ttl {
 constexpr int iota_size = 1024;
 
 size_t moe_workspace_bytes();
+// Batched router of moe_batch (ttl_moe.hip): per-token exact rows in `scratch`
+// (router_scratch_bytes() each), indices/weights [count][used].
+size_t router_scratch_bytes();
+int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, uint32_t count, void *scratch,
+                        int32_t *indices, float *weights);
 
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t err, const char *what);

@@ -81,10 +81,15 @@ struct RouterScratch {
 
 // One workgroup per router row: the exact value of the row (f64) and the bound
 // on the reference's sequential-sum error.  180 lanes hold 16 columns each.
+// Grid y indexes tokens of a batch: token t reads in.base + t * x_stride and uses
+// scratch[t] (one token: grid y = 1).
 template <int MODE>
 __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float *__restrict__ weight,
                                                                      const float *__restrict__ bias,
-                                                                     stage::Input in, RouterScratch *scratch) {
+                                                                     stage::Input in, RouterScratch *scratch,
+                                                                     uint32_t x_stride) {
+    in.base += size_t(blockIdx.y) * x_stride;
+    scratch += blockIdx.y;
     __shared__ double wave_part[3][3];
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
@@ -331,15 +336,21 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     __syncthreads();
 }
 
-// Standalone routing (ttl_router_topk): one workgroup, publishes everything.
+// Standalone routing (ttl_router_topk): one workgroup per token, publishes
+// everything.  Workgroup t of a batch routes token t: input in.base + t * x_stride,
+// scratch[t], outputs indices/weights_out + t * k (logits only for one token).
 template <int MODE>
 __global__ __launch_bounds__(256) void router_select_kernel(const float *__restrict__ weight,
                                                             const float *__restrict__ bias, uint32_t experts,
                                                             stage::Input in, uint32_t k, uint32_t force_exact,
                                                             RouterScratch *scratch, float *__restrict__ logits,
                                                             int32_t *__restrict__ indices,
-                                                            float *__restrict__ weights_out) {
+                                                            float *__restrict__ weights_out, uint32_t x_stride) {
     __shared__ RouteLds lds;
+    in.base += size_t(blockIdx.x) * x_stride;
+    scratch += blockIdx.x;
+    indices += size_t(blockIdx.x) * k;
+    weights_out += size_t(blockIdx.x) * k;
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
     route_workgroup<MODE, 256>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
@@ -624,11 +635,48 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
     RouterScratch *scratch = &workspace(ctx)->router;
     stage::with_mode(in, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
-        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch);
+        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch, 0u);
         router_select_kernel<M><<<1, 256, 0, ctx->stream>>>(weight, bias, experts, in, k, force_exact ? 1u : 0u,
-                                                            scratch, logits, indices, weights);
+                                                            scratch, logits, indices, weights, 0u);
     });
 }
+
+}  // namespace
+
+namespace ttl {
+
+size_t router_scratch_bytes() {
+    return sizeof(RouterScratch);
+}
+
+// Routing of `count` tokens at once (GptOssModel::moe_batch's router and top-k,
+// model.cpp:341-377): token t's input is x + t * hidden (normalized by the layer's
+// input norm if it has one), its exact rows go to scratch[t], its indices and
+// weights to indices/weights + t * used.
+int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, uint32_t count, void *scratch,
+                        int32_t *indices, float *weights) {
+    const int rc = check_router(L.router_weight, L.router_bias, L.experts, L.hidden, x, L.used);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(count < 65536, TTL_ERR_SHAPE, "moe_batch router: at most 65535 tokens per call");
+    RouterScratch *s = static_cast<RouterScratch *>(scratch);
+    const stage::Input in = layer_input(L, x);
+    stage::with_mode(in, [&](auto mode) {
+        constexpr int M = decltype(mode)::value;
+        router_rows_kernel<M><<<dim3(L.experts, count), kRouterThreads, 0, ctx->stream>>>(L.router_weight,
+                                                                                          L.router_bias, in, s,
+                                                                                          L.hidden);
+        router_select_kernel<M><<<count, 256, 0, ctx->stream>>>(L.router_weight, L.router_bias, L.experts, in,
+                                                                L.used, 0u, s, nullptr, indices, weights, L.hidden);
+    });
+    TTL_LAUNCHED("moe_batch router kernels");
+    return TTL_OK;
+}
+
+}  // namespace ttl
+
+namespace {
 
 int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden) {
     GateUpArgs a;

@@ -990,4 +990,41 @@ int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void
                                   workspace_dev, workspace_bytes, TTL_PREFILL_ALL);
 }
 
+size_t ttl_moe_prefill_batch_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used) {
+    const size_t routing = align256(ttl::router_scratch_bytes() * count) + 2 * align256(4ull * count * used);
+    return routing + ttl_moe_prefill_workspace_bytes(count, experts, used, TTL_DTYPE_F32);
+}
+
+int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, uint32_t count, float *out_dev,
+                    int32_t *indices_dev, float *weights_dev, void *workspace_dev, size_t workspace_bytes) {
+    TTL_REQUIRE(ctx && layer && x_dev && out_dev && workspace_dev, TTL_ERR_INVALID, "ttl_moe_prefill: null argument");
+    TTL_REQUIRE(!layer->input_norm, TTL_ERR_INVALID,
+                "ttl_moe_prefill: x is the normalized MoE input (model.cpp:549-551); the layer's input_norm must be NULL");
+    TTL_REQUIRE(layer->used >= 1 && layer->used <= kMaxUsed, TTL_ERR_SHAPE, "ttl_moe_prefill: used must be 1..%u",
+                kMaxUsed);
+    TTL_REQUIRE(workspace_bytes >= ttl_moe_prefill_batch_workspace_bytes(count, layer->experts, layer->used),
+                TTL_ERR_SHAPE, "ttl_moe_prefill: workspace of %zu bytes, %zu needed", workspace_bytes,
+                ttl_moe_prefill_batch_workspace_bytes(count, layer->experts, layer->used));
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 255) == 0, TTL_ERR_INVALID,
+                "ttl_moe_prefill: workspace must be 256-byte aligned");
+    if (count == 0) {
+        return TTL_OK;
+    }
+    uint8_t *w = static_cast<uint8_t *>(workspace_dev);
+    void *scratch = w;
+    w += align256(ttl::router_scratch_bytes() * count);
+    int32_t *indices = reinterpret_cast<int32_t *>(w);
+    w += align256(4ull * count * layer->used);
+    float *weights = reinterpret_cast<float *>(w);
+    w += align256(4ull * count * layer->used);
+    const size_t rest = workspace_bytes - size_t(w - static_cast<uint8_t *>(workspace_dev));
+    int rc = ttl::launch_router_batch(ctx, *layer, x_dev, count, scratch, indices_dev ? indices_dev : indices,
+                                      weights_dev ? weights_dev : weights);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    return ttl_moe_prefill_experts(ctx, layer, x_dev, TTL_DTYPE_F32, count, indices_dev ? indices_dev : indices,
+                                   weights_dev ? weights_dev : weights, out_dev, w, rest);
+}
+
 }  // extern "C"

@@ -281,6 +281,9 @@ def load_library():
         "ttl_moe_prefill_workspace_bytes": (sz, [u32, u32, u32, i32]),
         "ttl_moe_prefill_experts": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz]),
         "ttl_moe_prefill_stages": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz, u32]),
+        "ttl_moe_prefill_batch_workspace_bytes": (sz, [u32, u32, u32]),
+        "ttl_moe_prefill": (i32, [vp, C.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp, vp, sz]),
+        "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
@@ -618,6 +621,17 @@ class Device:
             _check(self.lib.ttl_moe_prefill_stages(self.ctx, C.byref(layer), x.ptr, x_dtype, count, indices.ptr,
                                                    weights.ptr, out.ptr, workspace.ptr, workspace.nbytes, stages),
                    "ttl_moe_prefill_stages")
+
+    def moe_prefill(self, layer, x, count, out, indices=None, weights=None):
+        """GptOssModel::moe_batch on the device (router + experts); allocates its workspace."""
+        ws = self.alloc(self.lib.ttl_moe_prefill_batch_workspace_bytes(count, layer.experts, layer.used))
+        try:
+            _check(self.lib.ttl_moe_prefill(self.ctx, C.byref(layer), x.ptr, count, out.ptr,
+                                            indices.ptr if indices else None, weights.ptr if weights else None,
+                                            ws.ptr, ws.nbytes), "ttl_moe_prefill")
+            self.sync()
+        finally:
+            ws.free()
 
     def matvec_mxfp4_experts(self, w, bias, x, x_stride, experts, n, y):
         _check(self.lib.ttl_matvec_mxfp4_experts(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
