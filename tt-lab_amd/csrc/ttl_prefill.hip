@@ -22,7 +22,7 @@
 //     position in that order is its slot.  Each expert's bucket is cut into tiles
 //     of 64 slots.
 //  2. gather_kernel: the tokens of every tile as MFMA B fragments (bf16 planes).
-//  3. gateup_kernel: per (tile, 192 rows) the gate and up GEMMs, the clamped SwiGLU
+//  3. gateup_kernel: per (tile, 128 rows) the gate and up GEMMs, the clamped SwiGLU
 //     in registers, and the hidden written straight into the down GEMM's B
 //     fragments (a lane's D rows 4g..4g+3 of the two 16-row tiles of one 32-row
 //     block are exactly the 8 values of the down fragment for K step g).
@@ -44,9 +44,11 @@ constexpr uint32_t kMaxUsed = 16;
 constexpr uint32_t kPlanThreads = 1024;
 constexpr uint32_t kMaxEntries = 1u << 22;  // count * used
 
-// gate/up: 6 waves x 32 rows (two 16-row tiles of gate and of up per wave)
-constexpr int kGuWaves = 6;
+// gate/up: 4 waves x 32 rows (two 16-row tiles of gate and of up per wave); two
+// workgroups share a CU, one wave of each per SIMD
+constexpr int kGuWaves = 4;
 constexpr int kGuRows = kGuWaves * 32;
+constexpr int kGuCodeBuffers = 4;  // weight codes are requested this many quads minus one ahead
 // matmul (down): 4 waves x 48 rows (three 16-row tiles per wave)
 constexpr int kMmWaves = 4;
 constexpr int kMmTiles = 3;
@@ -423,6 +425,72 @@ struct AOperand {
     }
 };
 
+// The MFMAs of quad i (K steps 4i..4i+3) for M 16-row A tiles and P activation
+// planes: acc[m][c] += A_m * B(p, c) in the order c, then p, per step.  B
+// fragments are read LOOK fragments before their MFMAs, within a stage (the
+// next stage is readable only after the barrier that ends this one), so the wave
+// waits for LDS about once per stage rather than once per fragment.
+// decode(s, w) fills the M A fragments of step s of the quad; stage_end(stage)
+// runs after the last MFMA of each stage (publishes the next one).
+template <int P, int M, int LOOK, class Decode, class StageEnd>
+__device__ __attribute__((always_inline)) inline void quad_mfma(const mf::u32x4 *buf0, const mf::u32x4 *buf1,
+                                                                int i, uint32_t lane, Decode &&decode,
+                                                                StageEnd &&stage_end,
+                                                                f32x4 (&acc)[M][mf::col_tiles]) {
+    using SS = StageShape<P>;
+    constexpr int FPS = P * mf::col_tiles;  // fragments per K step
+    constexpr int SF = SS::steps * FPS;     // fragments per stage
+    constexpr int D = LOOK < SF ? LOOK : SF;
+#pragma unroll
+    for (int q = 0; q < 4 / SS::steps; ++q) {
+        const int stage = (4 * i) / SS::steps + q;
+        const mf::u32x4 *buf = (stage % 2) ? buf1 : buf0;
+        auto frag = [&](int f) __attribute__((always_inline)) {
+            const int ls = f / FPS, c = (f % FPS) / P, p = f % P;
+            return mf::as_bf16x8v(buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
+        };
+        bf16x8 ring[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            ring[d] = frag(d);
+        }
+        bf16x8 w[M];
+#pragma unroll
+        for (int f = 0; f < SF; ++f) {
+            const bf16x8 b = ring[f % D];
+            if (f + D < SF) {
+                ring[f % D] = frag(f + D);
+            }
+            if (f % FPS == 0) {
+                decode(q * SS::steps + f / FPS, w);
+            }
+            const int c = (f % FPS) / P;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                acc[m][c] = mf::mfma(w[m], b, acc[m][c]);
+            }
+        }
+        stage_end(stage);
+    }
+}
+
+// Quads 0..22 with NB code buffers rotating under static indices: quad i's codes
+// are requested NB - 1 quads before they are used (requests past quad 22 repeat
+// it).  The caller has requested quads 0..NB-2 into buffers 0..NB-2.
+template <int NB, int M, class Load, class Compute>
+__device__ __attribute__((always_inline)) inline void rotate_quads(uint4 (&qa)[NB][M], Load &&load,
+                                                                   Compute &&compute) {
+    for (int i = 0; i < mf::quads; i += NB) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (i + b < mf::quads) {
+                load(min(i + b + NB - 1, mf::quads - 1), qa[(b + NB - 1) % NB]);
+                compute(i + b, qa[b]);
+            }
+        }
+    }
+}
+
 // ---- gate/up + SwiGLU -------------------------------------------------------------------
 
 struct GateUpArgs {
@@ -451,7 +519,7 @@ __device__ inline bool tile_of_workgroup(uint32_t tiles, uint32_t &tile, uint32_
 
 // Accumulators: [matrix (gate 0/1, up 2/3)][column tile]
 template <int PX>
-__global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void gateup_kernel(GateUpArgs a) {
     using SS = StageShape<PX>;
     constexpr int kThreads = kGuWaves * 64;
     __shared__ mf::u32x4 lds[2][Stager<PX, kThreads>::lds_chunks];
@@ -462,7 +530,11 @@ __global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
     const uint32_t row0 = row_group * kGuRows + wave * 32;  // this wave's 32 rows (one down K block)
-    const size_t tile0 = size_t(expert) * a.tiles_per_expert + row0 / 16;
+    // waves past the last row only help stage; they read the first wave's rows
+    // (L2 hits) so that every wave runs the same code
+    const bool rows_ok = row0 < a.rows;
+    const uint32_t row_base = rows_ok ? row0 : row_group * kGuRows;
+    const size_t tile0 = size_t(expert) * a.tiles_per_expert + row_base / 16;
     const uint8_t *frags = a.plan.xb + size_t(tile) * PX * mf::plane_bytes;
 
     AOperand<2> ga, ua;
@@ -478,7 +550,7 @@ __global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
             const float *bias = m < 2 ? a.gate_bias : a.up_bias;
             f32x4 b = {0.f, 0.f, 0.f, 0.f};
             if (bias) {
-                const float4 v = *reinterpret_cast<const float4 *>(bias + size_t(expert) * a.rows + row0 +
+                const float4 v = *reinterpret_cast<const float4 *>(bias + size_t(expert) * a.rows + row_base +
                                                                    16 * (m % 2) + 4 * g);
                 b = f32x4{v.x, v.y, v.z, v.w};
             }
@@ -491,7 +563,7 @@ __global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
 
     Stager<PX, kThreads> st;
     st.load(frags, 0, t);
-    uint4 qa[3][4];  // codes of three quads in flight: [buffer][gate0, gate1, up0, up1]
+    uint4 qa[kGuCodeBuffers][4];  // codes of the quads in flight: [buffer][gate0, gate1, up0, up1]
     auto load_quad = [&](int i, uint4(&q)[4]) __attribute__((always_inline)) {
         uint4 g2[2], u2[2];
         ga.load(i, lane, g2);
@@ -501,14 +573,26 @@ __global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
         q[2] = u2[0];
         q[3] = u2[1];
     };
-    load_quad(0, qa[0]);
-    load_quad(1, qa[1]);
+#pragma unroll
+    for (int b = 0; b < kGuCodeBuffers - 1; ++b) {
+        load_quad(b, qa[b]);
+    }
     st.store(lds[0], t);
     __syncthreads();
     if (SS::count > 1) {
         st.load(frags, 1, t);
     }
 
+    auto stage_end = [&](int stage) __attribute__((always_inline)) {
+        // end of stage: publish the next stage, fetch the one after
+        if (stage + 1 < SS::count) {
+            st.store(lds[(stage + 1) % 2], t);
+        }
+        __syncthreads();
+        if (stage + 2 < SS::count) {
+            st.load(frags, stage + 2, t);
+        }
+    };
     auto compute_quad = [&](int i, const uint4(&q)[4]) __attribute__((always_inline)) {
         float sc[4];
         sc[0] = ga.scale(0);
@@ -517,55 +601,20 @@ __global__ __launch_bounds__(kGuWaves * 64) void gateup_kernel(GateUpArgs a) {
         sc[3] = ua.scale(1);
         ga.next_quad();
         ua.next_quad();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int step = 4 * i + s;
-            const int stage = step / SS::steps, ls = step % SS::steps;
-            const mf::u32x4 *buf = lds[stage % 2];
-            bf16x8 w[4];
+        auto decode = [&](int s, bf16x8(&w)[4]) __attribute__((always_inline)) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const uint32_t word = s == 0 ? q[m].x : (s == 1 ? q[m].y : (s == 2 ? q[m].z : q[m].w));
                 w[m] = mf::decode_step(word, sc[m]);
             }
-#pragma unroll
-            for (int c = 0; c < mf::col_tiles; ++c) {
-#pragma unroll
-                for (int p = 0; p < PX; ++p) {
-                    const bf16x8 b = mf::as_bf16x8v(buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        acc[m][c] = mf::mfma(w[m], b, acc[m][c]);
-                    }
-                }
-            }
-            if (ls == SS::steps - 1) {
-                // end of stage: publish the next stage, fetch the one after
-                if (stage + 1 < SS::count) {
-                    st.store(lds[(stage + 1) % 2], t);
-                }
-                __syncthreads();
-                if (stage + 2 < SS::count) {
-                    st.load(frags, stage + 2, t);
-                }
-            }
-        }
+        };
+        // three activation planes leave registers for a shorter lookahead only
+        quad_mfma<PX, 4, PX == 1 ? 4 : 2>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
-    // quads 0..22, three code buffers rotating with static indices: each quad's
-    // codes are requested two quads before they are used (loads past quad 22
-    // repeat quad 22)
-    for (int i = 0; i < mf::quads; i += 3) {
-        load_quad(min(i + 2, mf::quads - 1), qa[2]);
-        compute_quad(i, qa[0]);
-        load_quad(min(i + 3, mf::quads - 1), qa[0]);
-        if (i + 1 < mf::quads) {
-            compute_quad(i + 1, qa[1]);
-            load_quad(min(i + 4, mf::quads - 1), qa[1]);
-        }
-        if (i + 2 < mf::quads) {
-            compute_quad(i + 2, qa[2]);
-        }
+    rotate_quads(qa, load_quad, compute_quad);
+    if (!rows_ok) {
+        return;
     }
 
     // SwiGLU and the hidden as down-GEMM B fragments: this wave's 32 rows are down K
@@ -666,6 +715,15 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
         st.load(frags, 1, t);
     }
 
+    auto stage_end = [&](int stage) __attribute__((always_inline)) {
+        if (stage + 1 < SS::count) {
+            st.store(lds[(stage + 1) % 2], t);
+        }
+        __syncthreads();
+        if (stage + 2 < SS::count) {
+            st.load(frags, stage + 2, t);
+        }
+    };
     auto compute_quad = [&](int i, const uint4(&q)[kMmTiles]) __attribute__((always_inline)) {
         float sc[kMmTiles];
 #pragma unroll
@@ -673,38 +731,14 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
             sc[m] = wa.scale(m);
         }
         wa.next_quad();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int step = 4 * i + s;
-            const int stage = step / SS::steps, ls = step % SS::steps;
-            const mf::u32x4 *buf = lds[stage % 2];
-            bf16x8 w[kMmTiles];
+        auto decode = [&](int s, bf16x8(&w)[kMmTiles]) __attribute__((always_inline)) {
 #pragma unroll
             for (int m = 0; m < kMmTiles; ++m) {
                 const uint32_t word = s == 0 ? q[m].x : (s == 1 ? q[m].y : (s == 2 ? q[m].z : q[m].w));
                 w[m] = mf::decode_step(word, sc[m]);
             }
-#pragma unroll
-            for (int c = 0; c < mf::col_tiles; ++c) {
-#pragma unroll
-                for (int p = 0; p < P; ++p) {
-                    const bf16x8 b = mf::as_bf16x8v(buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
-#pragma unroll
-                    for (int m = 0; m < kMmTiles; ++m) {
-                        acc[m][c] = mf::mfma(w[m], b, acc[m][c]);
-                    }
-                }
-            }
-            if (ls == SS::steps - 1) {
-                if (stage + 1 < SS::count) {
-                    st.store(lds[(stage + 1) % 2], t);
-                }
-                __syncthreads();
-                if (stage + 2 < SS::count) {
-                    st.load(frags, stage + 2, t);
-                }
-            }
-        }
+        };
+        quad_mfma<P, kMmTiles, 4>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
     for (int i = 0; i < mf::quads; i += 3) {
@@ -951,7 +985,7 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     g.rows = L.expert_hidden;
     g.tiles_per_expert = L.gate->tiles;
     g.plan = plan;
-    const dim3 gu_grid(L.expert_hidden / kGuRows, lay.tmax);
+    const dim3 gu_grid((L.expert_hidden + kGuRows - 1) / kGuRows, lay.tmax);
     if (stages & TTL_PREFILL_GATEUP) {
         if (bf16) {
             gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
