@@ -20,10 +20,10 @@ cpu_baseline: the CPU oracle's restatement of the reference's forward
 layer and one full-context layer at position 2048 plus the unembedding; a token
 is 12 of each plus the unembedding.
 
---workload moe runs BASELINE config 1 instead: one MoE layer per step over 24
+--workload moe runs benchmark config 1 instead: one MoE layer per step over 24
 distinct resident layers, value = token-layers/s.
 
---workload prefill runs BASELINE config 2: the batched prefill experts of one MoE
+--workload prefill runs benchmark config 2: the batched prefill experts of one MoE
 layer for 512 bf16 tokens with balanced given routing (bf16 MFMA), value =
 token-layers/s; roofline on the larger of the gate/up and down GEMM launches.
 """

@@ -200,7 +200,7 @@ int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
                          const int32_t *indices_dev, const float *weights_dev, const float *residual_dev,
                          float *out_dev, float *down_dev);
 
-/* ---- batched prefill on MFMA ------------------------------------- *
+/* ---- batched prefill on MFMA (benchmark config 2) ------------------------------------ *
  * bf16 MFMA with f32 accumulation.  Every product is exact: the weights E2M1 x
  * 2^(e-127) are bf16 values for E8M0 e in 1..254, and f32 activations are split
  * into three bf16 planes that sum to them exactly.  Results therefore agree with

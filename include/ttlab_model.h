@@ -5,7 +5,7 @@
  * The model mirrors the reference's GptOssModel (model.h:15-31): construction
  * allocates everything, forward(token, position) advances one token and returns
  * logits, greedy() picks the first maximum.  Weights come from a gpt-oss GGUF
- * file (ttlm_create_from_gguf) or are synthetic (the BASELINE configurations 3 and
+ * file (ttlm_create_from_gguf) or are synthetic (the benchmark configurations 3 and
  * 4), generated on the device from the stream layout of ttlab::synth_stream().
  * Every call returns 0 or a negative code; ttlm_last_error() has the message.
  */

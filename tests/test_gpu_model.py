@@ -19,7 +19,7 @@ TOL = 1e-5
 SEED, LAYERS, EXPERTS, VOCAB, CAPACITY = 0x77000003, 2, 32, 4096, 160
 
 
-# 32 experts: the 20b shape; 128: the 120b routing width (config 4),
+# 32 experts: the 20b shape (benchmark config 3); 128: the 120b routing width (config 4),
 # whose host copy generates only the experts the oracle routes to.
 @pytest.fixture(scope="module", params=[EXPERTS, 128], ids=["20b", "120b"])
 def models(request):

@@ -168,7 +168,7 @@ def test_moe_prefill_uneven_buckets_and_invalid_index(dev, layer8):
 
 
 def test_moe_prefill_config2_shape(dev):
-    # 512 bf16 tokens, 32 experts, top-4 balanced (64 tokens each)
+    # benchmark config 2: 512 bf16 tokens, 32 experts, top-4 balanced (64 tokens each)
     count = 512
     idx, w = balanced_routing(count, 32, 4, 11)
     sample = np.random.RandomState(12).choice(count, 6, replace=False)

@@ -132,7 +132,7 @@ def gguf_inspect(path, strict=True):
 
 
 class Model:
-    """ttlab::HipGptOssModel with synthetic weights (BASELINE configurations 3/4), or
+    """ttlab::HipGptOssModel with synthetic weights (benchmark configurations 3/4), or
     with a GGUF file's weights (Model.from_gguf)."""
 
     def __init__(self, layers=24, experts=32, vocab=201088, capacity=2112, seed=0x77000003, device=0, _handle=None):
@@ -300,7 +300,7 @@ def load_library():
 
 
 def balanced_routing(count, experts, used, seed):
-    """Synthetic routing of BASELINE config 2: every expert is chosen equally often,
+    """Synthetic routing of benchmark config 2: every expert is chosen equally often,
     each token has `used` distinct experts (rank order shuffled), and the weights are
     the softmax of N(0,1) logits.  Returns int32 [count][used], f32 [count][used]."""
     if (count * used) % experts or experts % used:
