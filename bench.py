@@ -53,6 +53,47 @@ def log(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
+def read_ceiling(nbytes, buffers, reps=20):
+    """Microseconds per launch of a plain streaming read (ttl_stream_read) of nbytes,
+    over `buffers` distinct buffers replayed as one graph: the fixed launch cost and
+    the streaming rate this chip gives a kernel that only reads, at the same bytes
+    per launch as the measured kernel."""
+    import ctypes as C
+
+    import ttlab_amd
+
+    dev = ttlab_amd.Device(0)
+    bufs = [dev.alloc(nbytes) for _ in range(buffers)]
+    for b in bufs:
+        dev.fill(b, 0x5a)
+    sink = dev.alloc(256)
+
+    def launches():
+        for b in bufs:
+            ttlab_amd._check(dev.lib.ttl_stream_read(dev.ctx, b.ptr, nbytes, sink.ptr), "ttl_stream_read")
+
+    g = dev.capture(launches)
+    for _ in range(3):
+        g.launch()
+    dev.sync()
+    dev.timer_start()
+    for _ in range(reps):
+        g.launch()
+    us = 1e3 * dev.timer_stop() / (reps * buffers)
+    g.free()
+    for b in bufs + [sink]:
+        b.free()
+    dev.close()
+    return us
+
+
+def ceiling_entry(achieved_gbs, nbytes, us_read):
+    gbs = nbytes / (us_read * 1e-6) / 1e9
+    return {"kernel": "stream_read_kernel (plain 16-byte loads, no arithmetic)", "bytes_per_launch": nbytes,
+            "launch_us": round(us_read, 3), "GBps": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel_frac_of_ceiling": round(achieved_gbs / gbs, 4)}
+
+
 def gpu_decode(args):
     import ttlab_amd
 
@@ -78,6 +119,9 @@ def gpu_decode(args):
     achieved = GATEUP_BYTES / (us * 1e-6) / 1e9
     log(f"gateup_swiglu_kernel: {us:.2f} us per launch, {achieved:.0f} GB/s")
     model.close()
+    us_read = read_ceiling(GATEUP_BYTES, args.layers)
+    log(f"plain read of the same {GATEUP_BYTES / 1e6:.1f} MB per launch: {us_read:.2f} us, "
+        f"{GATEUP_BYTES / (us_read * 1e-6) / 1e9:.0f} GB/s")
     return {
         "value": tok_s,
         "unit": "tok/s",
@@ -94,7 +138,7 @@ def gpu_decode(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
                      "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
-                     "launch_us": round(us, 3)},
+                     "launch_us": round(us, 3), "read_ceiling": ceiling_entry(achieved, GATEUP_BYTES, us_read)},
     }
 
 
@@ -245,6 +289,9 @@ def gpu_prefill(args):
     name = max(kernels, key=lambda k: kernels[k][0])
     us, nbytes, flop = kernels[name]
     achieved = nbytes / (us * 1e-6) / 1e9
+    us_read = read_ceiling(nbytes, 2 * PREFILL_LAYERS)
+    log(f"plain read of the same {nbytes / 1e6:.1f} MB per launch: {us_read:.2f} us, "
+        f"{nbytes / (us_read * 1e-6) / 1e9:.0f} GB/s")
     per_kernel = {k: {"us": round(v[0], 2), "algorithmic_GBps": round(v[1] / (v[0] * 1e-6) / 1e9, 1),
                       "algorithmic_TFLOPs": round(v[2] / (v[0] * 1e-6) / 1e12, 1)} for k, v in kernels.items()}
     return {
@@ -262,7 +309,8 @@ def gpu_prefill(args):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
                      "bytes_per_launch": nbytes, "launch_us": round(us, 3),
                      "mfma_algorithmic_TFLOPs": round(flop / (us * 1e-6) / 1e12, 1),
-                     "mfma_peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS},
+                     "mfma_peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS,
+                     "read_ceiling": ceiling_entry(achieved, nbytes, us_read)},
     }
 
 

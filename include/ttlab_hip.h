@@ -63,6 +63,13 @@ int ttl_memcpy_d2d(ttl_ctx *ctx, void *dst_dev, const void *src_dev, size_t byte
 /* Fills with a byte value using a kernel (safe inside HIP graph capture). */
 int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes);
 
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) once with plain 16-byte loads
+ * and no arithmetic: the streaming-read reference the matvec kernels are measured
+ * against at the same bytes per launch.  Measurement only, with no counterpart in
+ * the reference.  sink_dev (4 bytes) is written only if the XOR of one thread's
+ * words equals a fixed constant. */
+int ttl_stream_read(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *sink_dev);
+
 /* ---- timing (HIP events on the context's stream) -------------------------------- */
 
 int ttl_timer_start(ttl_ctx *ctx);

@@ -25,6 +25,30 @@ __global__ void copy16_kernel(const uint4 *__restrict__ src, uint4 *__restrict__
         dst[k] = src[k];
     }
 }
+
+// Plain streaming read, the bandwidth reference for the matvec kernels: thread t of
+// block b reads the 16-byte words b * 1024 + t + 256 k (k < 4) once, with all four
+// loads in flight.  The XOR of the words is stored only when it equals a fixed
+// constant, so the loads stay live and nothing is written in practice.
+constexpr int kReadThreads = 256, kReadPerThread = 4;
+__global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4 *__restrict__ src, size_t n,
+                                                                   uint32_t *__restrict__ sink) {
+    const size_t base = size_t(blockIdx.x) * kReadThreads * kReadPerThread + threadIdx.x;
+    uint4 v[kReadPerThread];
+#pragma unroll
+    for (int k = 0; k < kReadPerThread; ++k) {
+        const size_t i = base + size_t(k) * kReadThreads;
+        v[k] = src[i < n ? i : n - 1];
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kReadPerThread; ++k) {
+        acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    if (acc == 0x9e3779b9u) {
+        *sink = acc;
+    }
+}
 }  // namespace
 
 namespace ttl {
@@ -203,6 +227,21 @@ int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes) {
     const unsigned blocks = unsigned(std::min<size_t>(ttl::blocks_for(bytes, threads), 4096));
     fill_bytes_kernel<<<blocks, threads, 0, ctx->stream>>>((uint8_t *)dst_dev, value, bytes);
     TTL_LAUNCHED("fill_bytes_kernel");
+    return TTL_OK;
+}
+
+int ttl_stream_read(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *sink_dev) {
+    TTL_REQUIRE(ctx && src_dev && sink_dev, TTL_ERR_INVALID, "ttl_stream_read: null argument");
+    TTL_REQUIRE(bytes >= 16 && bytes % 16 == 0, TTL_ERR_SHAPE, "ttl_stream_read: bytes must be a positive multiple of 16");
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(src_dev) & 15) == 0, TTL_ERR_INVALID,
+                "ttl_stream_read: source must be 16-byte aligned");
+    const size_t words = bytes / 16;
+    const size_t per_block = size_t(kReadThreads) * kReadPerThread;
+    const size_t blocks = (words + per_block - 1) / per_block;
+    TTL_REQUIRE(blocks <= 0x7fffffffu, TTL_ERR_SHAPE, "ttl_stream_read: too many bytes for one launch");
+    stream_read_kernel<<<unsigned(blocks), kReadThreads, 0, ctx->stream>>>(static_cast<const uint4 *>(src_dev), words,
+                                                                       sink_dev);
+    TTL_LAUNCHED("stream_read_kernel");
     return TTL_OK;
 }
 

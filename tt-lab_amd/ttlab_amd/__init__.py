@@ -284,6 +284,7 @@ def load_library():
         "ttl_moe_prefill_batch_workspace_bytes": (sz, [u32, u32, u32]),
         "ttl_moe_prefill": (i32, [vp, C.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp, vp, sz]),
         "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
+        "ttl_stream_read": (i32, [vp, vp, sz, vp]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
