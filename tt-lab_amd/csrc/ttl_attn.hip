@@ -8,8 +8,8 @@
 //           den = exp(sink - M) + sum_c l_c exp(m_c - M),
 //           out = sum_c o_c exp(m_c - M) / den -- the reference's softmax with the
 //           sink in the max and the denominator only, regrouped by chunk.
-// Even layers see the last 128 positions (the sliding window), odd layers all
-// (model.cpp:260).  The position is read from device memory, so one captured
+// Even layers see the last 128 positions (the sliding window, one launch of
+// attn_window_kernel), odd layers all (model.cpp:260).  The position is read from device memory, so one captured
 // launch serves every decode step; chunks past the current length do nothing.
 #include "ttl_internal.hpp"
 
@@ -202,6 +202,106 @@ __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__rest
     out[head * kHead + d] = acc / den;
 }
 
+// Sliding-window layers in one launch: workgroup = query head; the window (at most
+// 128 positions of its kv head) sits in LDS, and the softmax with the sink is done
+// in place -- no partials and no second kernel.
+constexpr int kWinThreads = 256;
+
+__global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *__restrict__ q,
+                                                                  const float *__restrict__ k_cache,
+                                                                  const float *__restrict__ v_cache,
+                                                                  const float *__restrict__ sinks,
+                                                                  const int32_t *__restrict__ position,
+                                                                  uint32_t capacity, uint32_t layer_index,
+                                                                  float *__restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float ks[kWindow * kRowStride];
+    __shared__ __attribute__((aligned(16))) float vs[kWindow * kRowStride];
+    __shared__ __attribute__((aligned(16))) float qs[kHead];
+    __shared__ float e[kWindow];
+    __shared__ float stat[4];
+    __shared__ float part[kWinThreads / kHead][kHead];
+    const uint32_t head = blockIdx.x, kvh = head / kGroup, t = threadIdx.x;
+    const uint32_t pos = uint32_t(*position);
+    if (pos >= capacity) {
+        return;
+    }
+    const Span sp = span_of(pos, layer_index);
+    const uint32_t n = sp.count;  // 1..128
+
+    // one round trip: q and the window's K and V rows (positions past n re-read the last)
+    constexpr int kPer = kWindow * (kHead / 4) / kWinThreads;  // 8 float4 of K and of V per thread
+    float4 kr[kPer], vr[kPer];
+    const float4 qv = t < uint32_t(kHead / 4) ? reinterpret_cast<const float4 *>(q + size_t(head) * kHead)[t]
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t f = t + uint32_t(k) * kWinThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
+        const size_t row = (size_t(sp.first + (p < n ? p : n - 1)) * kKvHeads + kvh) * kHead;
+        kr[k] = reinterpret_cast<const float4 *>(k_cache + row)[d4];
+        vr[k] = reinterpret_cast<const float4 *>(v_cache + row)[d4];
+    }
+    if (t < uint32_t(kHead / 4)) {
+        *reinterpret_cast<float4 *>(&qs[4 * t]) = qv;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t f = t + uint32_t(k) * kWinThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
+        *reinterpret_cast<float4 *>(ks + p * kRowStride + 4 * d4) = kr[k];
+        *reinterpret_cast<float4 *>(vs + p * kRowStride + 4 * d4) = vr[k];
+    }
+    __syncthreads();
+
+    // scores and their max (waves 0 and 1: one position per thread)
+    const uint32_t w = t / 64, lane = t % 64;
+    if (t < uint32_t(kWindow)) {
+        float a = 0.0f;
+#pragma unroll
+        for (int d = 0; d < kHead / 4; ++d) {
+            const float4 kv = *reinterpret_cast<const float4 *>(ks + t * kRowStride + 4 * d);
+            const float4 qq = *reinterpret_cast<const float4 *>(&qs[4 * d]);
+            a = fmaf(qq.x, kv.x, a);
+            a = fmaf(qq.y, kv.y, a);
+            a = fmaf(qq.z, kv.z, a);
+            a = fmaf(qq.w, kv.w, a);
+        }
+        const float s = t < n ? a * 0.125f : -INFINITY;  // 1/sqrt(64), exact
+        e[t] = s;
+        const float m = wave_max(s);
+        if (lane == 0) {
+            stat[w] = m;
+        }
+    }
+    __syncthreads();
+    // model.cpp:270-281: the sink enters the max and the denominator only
+    const float sink = sinks[head];
+    const float m = fmaxf(sink, fmaxf(stat[0], stat[1]));
+    if (t < uint32_t(kWindow)) {
+        const float x = t < n ? expf(e[t] - m) : 0.0f;
+        e[t] = x;
+        const float l = wave_sum(x);
+        if (lane == 0) {
+            stat[2 + w] = l;
+        }
+    }
+    __syncthreads();
+    const float den = expf(sink - m) + (stat[2] + stat[3]);
+    // o[d] = sum_p e[p] v[p][d]: thread (quarter g = t / 64 of the positions, dim d)
+    {
+        const uint32_t g = t / kHead, d = t % kHead;
+        float o = 0.0f;
+        const uint32_t p0 = g * (kWindow / 4), p1 = min(p0 + kWindow / 4, n);
+        for (uint32_t p = p0; p < p1; ++p) {
+            o = fmaf(e[p], vs[p * kRowStride + d], o);
+        }
+        part[g][d] = o;
+    }
+    __syncthreads();
+    if (t < uint32_t(kHead)) {
+        const float o = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+        out[head * kHead + t] = o / den;
+    }
+}
+
 }  // namespace
 
 namespace ttl {
@@ -227,9 +327,15 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
                 "ttl_attention_decode: capacity must be 1..%d", kMaxCombineChunks * kChunk);
     TTL_REQUIRE(((uintptr_t)q_dev & 15) == 0 && ((uintptr_t)k_cache_dev & 15) == 0 && ((uintptr_t)v_cache_dev & 15) == 0,
                 TTL_ERR_INVALID, "ttl_attention_decode: q, k and v must be 16-byte aligned");
+    if (layer_index % 2 == 0) {
+        // the sliding window fits one workgroup per query head
+        attn_window_kernel<<<kQHeads, kWinThreads, 0, ctx->stream>>>(q_dev, k_cache_dev, v_cache_dev, sinks_dev,
+                                                                     position_dev, capacity, layer_index, out_dev);
+        TTL_LAUNCHED("attn_window_kernel");
+        return TTL_OK;
+    }
     const uint32_t max_chunks = (capacity + kChunk - 1) / kChunk;
-    // even layers never need more than the window's chunks (plus one for misalignment)
-    const uint32_t launch_chunks = layer_index % 2 == 0 ? min(max_chunks, uint32_t(kWindow / kChunk + 1)) : max_chunks;
+    const uint32_t launch_chunks = max_chunks;
     float *o_part = workspace_dev;
     float2 *ml_part = reinterpret_cast<float2 *>(workspace_dev + size_t(kQHeads) * max_chunks * kHead);
     attn_partial_kernel<<<dim3(launch_chunks, kKvHeads), kThreads, 0, ctx->stream>>>(
