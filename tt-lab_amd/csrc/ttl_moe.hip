@@ -178,6 +178,7 @@ struct RouteLds {
     int32_t order[kMaxExperts];
     double value[kMaxExperts];  // exact logits
     double bound[kMaxExperts];
+    double up[kMaxExperts];  // value + bound
     uint32_t rank[kMaxExperts];
     int certified;
 };
@@ -190,23 +191,25 @@ __device__ inline double wave_max(double v) {
     return v;
 }
 
-// Routing for one token, computed by the whole workgroup (blockDim.x >= experts).
-// Leaves indices/weights in lds; when `logits` is non-null also writes the logits
-// (and bumps the exact-path counter) -- only one workgroup of a launch does that.
-// The exact path stages the router input into xs/red (the same values the router
-// rows saw); the certified path does not touch them.
-template <int MODE, int NT>
-__device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
-                                const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
-                                RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
-                                float *red) {
-    const uint32_t t = threadIdx.x, lane = t % 64;
+// Routing for one token, computed by the whole workgroup (blockDim.x >= experts),
+// in two parts.  route_certified() ranks the exact rows; when the ranking is
+// certified it leaves indices/weights in lds (and writes the logits when `logits`
+// is non-null -- only one workgroup of a launch does that) and lds.certified = 1.
+// Otherwise route_exact() recomputes the logits in the reference's order from the
+// staged router input xs (the same values the router rows saw) and replays the
+// reference's selection sort (it also bumps the exact-path counter when `logits`
+// is non-null).  Both end with a barrier, so lds.certified is uniform.
+__device__ void route_certified(uint32_t experts, uint32_t k, bool force_exact, const RouterScratch *scratch,
+                                RouteLds &lds, float *__restrict__ logits, bool publish) {
+    const uint32_t t = threadIdx.x;
     // ---- certified path ------------------------------------------------------
     // Thread c < experts ranks expert c by (exact value descending, index
     // ascending) -- the order the reference's selection sort produces when no two
     // values are within their error bounds -- and checks that separation for the
     // top k: value - bound of rank r must exceed value + bound of every expert
-    // ranked below r.  Only LDS broadcast reads, no cross-lane chains.
+    // ranked below r.  Only LDS broadcast reads, no cross-lane chains.  The
+    // softmax weights (and logits) are computed only when `publish` is set, which
+    // must be the same for the whole workgroup; indices are always left in lds.
     if (t == 0) {
         lds.certified = force_exact ? 0 : 1;
     }
@@ -214,6 +217,7 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
         const double v = scratch->exact[t], b = scratch->bound[t];
         lds.value[t] = v;
         lds.bound[t] = b;
+        lds.up[t] = v + b;
         if (!isfinite(v) || !isfinite(b)) {
             lds.certified = 0;
         }
@@ -222,7 +226,7 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     if (t < experts) {
         const double v = lds.value[t];
         uint32_t rank = 0;
-#pragma unroll 16
+#pragma unroll 8
         for (uint32_t j = 0; j < experts; ++j) {
             const double vj = lds.value[j];
             rank += (vj > v || (vj == v && j < t)) ? 1u : 0u;
@@ -238,33 +242,35 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
         const uint32_t rank = lds.rank[t];
         const double low = lds.value[t] - lds.bound[t];
         double up = -INFINITY;
-#pragma unroll 16
+#pragma unroll 8
         for (uint32_t j = 0; j < experts; ++j) {
             // arithmetic masking (finite values here), so no branch holds back the
             // LDS reads of the unrolled iterations
             const double mask = lds.rank[j] > rank ? 0.0 : -INFINITY;
-            up = fmax(up, (lds.value[j] + lds.bound[j]) + mask);
+            up = fmax(up, lds.up[j] + mask);
         }
         if (!(low > up)) {
             lds.certified = 0;
         }
     }
     __syncthreads();
-    if (lds.certified) {
-        if (t == 0) {
-            softmax_selected(lds.selected, k, lds.weights);
+    if (publish) {
+        if (lds.certified) {
+            if (t == 0) {
+                softmax_selected(lds.selected, k, lds.weights);
+            }
+            if (logits && t < experts) {
+                logits[t] = float(lds.value[t]);
+            }
         }
-        if (logits && t < experts) {
-            logits[t] = float(lds.value[t]);
-        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (lds.certified) {
-        return;
-    }
+}
 
-    // ---- exact path: the reference's sequential sums (tensor.cpp:186-200) ----
-    stage::stage<kRouterCols, mxt::x_blocks, NT, MODE>(in, xs, red);
+__device__ void route_exact(const float *__restrict__ weight, const float *__restrict__ bias, uint32_t experts,
+                            uint32_t k, const float *xs, RouterScratch *scratch, RouteLds &lds,
+                            float *__restrict__ logits) {
+    const uint32_t t = threadIdx.x, lane = t % 64;
     if (t < experts) {
 #pragma clang fp contract(off)
         const float *w = weight + size_t(t) * kRouterCols;
@@ -336,6 +342,18 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     __syncthreads();
 }
 
+template <int MODE, int NT>
+__device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
+                                const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
+                                RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
+                                float *red) {
+    route_certified(experts, k, force_exact, scratch, lds, logits, true);
+    if (!lds.certified) {
+        stage::stage<kRouterCols, mxt::x_blocks, NT, MODE>(in, xs, red);
+        route_exact(weight, bias, experts, k, xs, scratch, lds, logits);
+    }
+}
+
 // Standalone routing (ttl_router_topk): one workgroup per token, publishes
 // everything.  Workgroup t of a batch routes token t: input in.base + t * x_stride,
 // scratch[t], outputs indices/weights_out + t * k (logits only for one token).
@@ -388,9 +406,18 @@ struct GateUpArgs {
     stage::Input in;  // the layer input (optionally the residual stream + norm)
     const int32_t *expert_ids;
     float *hidden;
+    // ROUTE: the selection from the router rows (expert_ids unused); workgroup 0
+    // publishes indices, weights and logits
+    const float *router_weight, *router_bias;
+    RouterScratch *scratch;
+    int32_t *indices_out;
+    float *weights_out, *logits_out;
 };
 
-template <int MODE>
+// ROUTE: every workgroup ranks the router rows itself (route_workgroup, the
+// certified selection or the exact fallback) instead of reading a separate
+// selection kernel's indices; the input loads are in flight meanwhile.
+template <int MODE, bool ROUTE>
 __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[GateUpSplit::x_floats];
     __shared__ float red[stage::red_floats(GateUpSplit::x_blocks)];
@@ -403,7 +430,28 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
     // the staging completes while those are in flight
     stage::Pending<mx::cols, GateUpSplit::x_blocks, kGateUpThreads, MODE> pending;
     stage::stage_load(a.in, pending);
-    const int32_t e = a.expert_ids[slot];
+    int32_t e;
+    bool staged = false;
+    if constexpr (ROUTE) {
+        __shared__ RouteLds rl;
+        // workgroup 0 publishes the routing; the others only need the indices
+        const bool first = blockIdx.x == 0;
+        float *logits = first ? a.logits_out : nullptr;
+        route_certified(a.experts, a.k, false, a.scratch, rl, logits, first);
+        if (!rl.certified) {
+            // rare: the exact path needs the staged input first
+            stage::stage_finish(a.in, pending, xs, red);
+            route_exact(a.router_weight, a.router_bias, a.experts, a.k, xs, a.scratch, rl, logits);
+            staged = true;
+        }
+        e = rl.indices[slot];
+        if (first && threadIdx.x < a.k) {
+            a.indices_out[threadIdx.x] = rl.indices[threadIdx.x];
+            a.weights_out[threadIdx.x] = rl.weights[threadIdx.x];
+        }
+    } else {
+        e = a.expert_ids[slot];
+    }
     // All weight loads are unconditional (an invalid expert reads expert 0 and its
     // output becomes NaN below): loads under a branch make the compiler wait for
     // every load at the branch's end.
@@ -416,7 +464,9 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
     mxt::SplitRegs<kSplit> regs;
     mxt::split_load<kSplit>(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales,
                             size_t(e_safe) * a.tiles + tile, w, lane, regs);
-    stage::stage_finish(a.in, pending, xs, red);
+    if (!staged) {
+        stage::stage_finish(a.in, pending, xs, red);
+    }
     const float acc = mxt::split_compute<kSplit>(regs, xs, w, lane);
     if (lane < mx::tile_rows) {
         part[which][w][lane] = acc;
@@ -641,6 +691,16 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
     });
 }
 
+// The router rows alone (one workgroup per expert): the routed gate/up kernel
+// does the selection.
+void launch_router_rows(ttl_ctx *ctx, const ttl_moe_layer &L, const stage::Input &in) {
+    RouterScratch *scratch = &workspace(ctx)->router;
+    stage::with_mode(in, [&](auto mode) {
+        router_rows_kernel<decltype(mode)::value>
+            <<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias, in, scratch, 0u);
+    });
+}
+
 }  // namespace
 
 namespace ttl {
@@ -678,8 +738,12 @@ int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, ui
 
 namespace {
 
-int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden) {
-    GateUpArgs a;
+// gate/up of the experts in expert_ids, or (expert_ids == nullptr) of the experts
+// the kernel selects itself from the router rows in the context's scratch, which
+// it publishes to indices/weights.
+int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const int32_t *expert_ids, float *hidden,
+                  int32_t *indices = nullptr, float *weights = nullptr) {
+    GateUpArgs a{};
     a.gate_codes = L.gate->codes;
     a.gate_scales = L.gate->scales;
     a.gate_bias = L.gate_bias;
@@ -693,8 +757,19 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
     a.in = layer_input(L, x);
     a.expert_ids = expert_ids;
     a.hidden = hidden;
+    a.router_weight = L.router_weight;
+    a.router_bias = L.router_bias;
+    a.scratch = &workspace(ctx)->router;
+    a.indices_out = indices;
+    a.weights_out = weights;
+    a.logits_out = workspace(ctx)->logits;
     stage::with_mode(a.in, [&](auto mode) {
-        gateup_swiglu_kernel<decltype(mode)::value><<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
+        if (expert_ids) {
+            gateup_swiglu_kernel<decltype(mode)::value, false>
+                <<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
+        } else {
+            gateup_swiglu_kernel<decltype(mode)::value, true><<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
+        }
     });
     TTL_LAUNCHED("gateup_swiglu_kernel");
     return TTL_OK;
@@ -768,10 +843,9 @@ int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
     if (rc != TTL_OK) {
         return rc;
     }
-    launch_router(ctx, L.router_weight, L.router_bias, L.experts, L.used, layer_input(L, x_dev), false,
-                  workspace(ctx)->logits, indices_dev, weights_dev);
-    TTL_LAUNCHED("router kernels");
-    return launch_gateup(ctx, L, x_dev, indices_dev, hidden_dev);
+    launch_router_rows(ctx, L, layer_input(L, x_dev));
+    TTL_LAUNCHED("router_rows_kernel");
+    return launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
 }
 
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
@@ -828,10 +902,9 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
     ttl::MoeWorkspace *ws = workspace(ctx);
     int32_t *indices = indices_dev ? indices_dev : ws->indices;
     float *weights = weights_dev ? weights_dev : ws->weights;
-    launch_router(ctx, L.router_weight, L.router_bias, L.experts, L.used, layer_input(L, x_dev), false, ws->logits,
-                  indices, weights);
-    TTL_LAUNCHED("router kernels");
-    rc = launch_gateup(ctx, L, x_dev, indices, ws->hidden);
+    launch_router_rows(ctx, L, layer_input(L, x_dev));
+    TTL_LAUNCHED("router_rows_kernel");
+    rc = launch_gateup(ctx, L, x_dev, nullptr, ws->hidden, indices, weights);
     if (rc == TTL_OK) {
         rc = ttl_moe_down_combine(ctx, layer, ws->hidden, indices, weights, nullptr, out_dev, nullptr);
     }
