@@ -100,6 +100,39 @@ def test_router_exact_ties_follow_reference_selection_sort(dev):
     bb.free()
 
 
+def test_moe_decode_exact_routing_inside_gateup(dev):
+    """The MoE decode selects its experts inside the gate/up kernel.  With router rows
+    3, 5 and 9 identical their logits tie exactly, so no workgroup can certify the
+    ranking: every one recomputes the logits in the reference's order and replays its
+    selection sort.  The routing must be the reference's and the layer match the oracle."""
+    x = O.synth_normal(X_SEED, 7, N)
+    lead = np.sign(x).astype(np.float32) * np.float32(0.05)
+    router_only = HostLayer(32, 4, biases=False, seed=0x7700000B, fill_experts=[])
+    w = router_only.router_w.reshape(32, N).copy()
+    for r in (3, 5, 9):
+        w[r] = lead
+    w = np.ascontiguousarray(w.ravel())
+    logits = np.empty(32, np.float32)
+    O.lib.orc_matvec_add_f32(w, router_only.router_b, 32, N, x, logits)
+    ref_idx, ref_w = O.router_topk(logits, 4)
+    assert logits[3] == logits[5] == logits[9] and list(ref_idx[:3]) == [3, 5, 9]
+    host = HostLayer(32, 4, biases=False, seed=0x7700000B, fill_experts=ref_idx)
+    host.router_w = w
+    device = DeviceLayer(dev, host)
+    xb, out = dev.upload(x), dev.alloc(N * 4)
+    ib, wb = dev.alloc(16), dev.alloc(16)
+    before = dev.router_exact_count()
+    dev.moe_decode(device.desc, xb, out, ib, wb)
+    assert dev.router_exact_count() == before + 1
+    assert list(ib.download(np.int32)) == list(ref_idx)
+    assert np.allclose(wb.download(np.float32), ref_w, rtol=5e-7, atol=0)
+    ref, _, _, _ = host.oracle_moe(x, O.BODY_V4)
+    assert O.rel_l2(out.download(np.float32), ref) <= TOL
+    for b in (xb, out, ib, wb):
+        b.free()
+    device.free()
+
+
 @pytest.mark.parametrize("body", [O.BODY_V4, O.BODY_DEFAULT])
 def test_moe_layer_config1_matches_oracle(dev, layer32, body):
     host, device = layer32
