@@ -10,7 +10,6 @@
 
 namespace {
 
-constexpr int kThreads = q8::waves * 64;
 constexpr int kHead = 64, kQHeads = 64, kKvHeads = 8;
 constexpr int kQRows = kQHeads * kHead, kKvRows = kKvHeads * kHead, kQkvRows = kQRows + 2 * kKvRows;
 
@@ -84,7 +83,7 @@ __global__ void q8_synth_kernel(uint64_t seed, uint64_t stream, size_t block_off
 
 // Common body: one workgroup = one 16-row tile; returns the row sum for row
 // threadIdx.x (valid for threadIdx.x < 16) after the wave-order reduction.
-template <int K, int MODE>
+template <int K, int W, int MODE>
 __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t *__restrict__ codes,
                                                                   const uint16_t *__restrict__ scales,
                                                                   size_t tile, const stage::Input &in,
@@ -94,13 +93,13 @@ __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     // input loads first: the staging then waits for them alone while the weight
     // loads are still in flight
-    stage::Pending<K, S::x_blocks, kThreads, MODE> pending;
+    stage::Pending<K, S::x_blocks, W * 64, MODE> pending;
     stage::stage_load(in, pending);
-    q8::TileRegs<K> regs;
-    q8::tile_load<K>(codes, scales, tile, wave, lane, regs);
+    q8::TileRegs<K, W> regs;
+    q8::tile_load<K, W>(codes, scales, tile, wave, lane, regs);
     stage::stage_finish(in, pending, xs, red);
     q8::block_sums(xs, S::x_blocks, xsum);
-    const float acc = q8::tile_compute<K>(regs, wave, lane, xs, xsum);
+    const float acc = q8::tile_compute<K, W>(regs, wave, lane, xs, xsum);
     if (lane < q8::tile_rows) {
         part[wave][lane] = acc;
     }
@@ -108,23 +107,33 @@ __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t
     float sum = 0.0f;
     if (threadIdx.x < q8::tile_rows) {
 #pragma unroll
-        for (int w = 0; w < q8::waves; ++w) {
+        for (int w = 0; w < W; ++w) {
             sum += part[w][threadIdx.x];
         }
     }
     return sum;
 }
 
+// Waves per tile (each divides its K's padded iterations, 24 and 32): measured on
+// the decode step, 12 and 8 beat 4 (the layout's own split), 6 and 16.  More waves
+// shorten each wave's decode chain after its loads arrive.
+template <int K>
+constexpr int waves_for() {
+    return K == 2880 ? 12 : 8;
+}
+
 template <int K, int MODE>
-__global__ __launch_bounds__(kThreads) void q8_matvec_kernel(const uint8_t *__restrict__ codes,
-                                                             const uint16_t *__restrict__ scales, uint32_t rows,
-                                                             stage::Input in, const float *__restrict__ bias,
-                                                             const float *__restrict__ residual,
-                                                             float *__restrict__ y) {
+__global__ __launch_bounds__(waves_for<K>() * 64) void q8_matvec_kernel(const uint8_t *__restrict__ codes,
+                                                                        const uint16_t *__restrict__ scales,
+                                                                        uint32_t rows, stage::Input in,
+                                                                        const float *__restrict__ bias,
+                                                                        const float *__restrict__ residual,
+                                                                        float *__restrict__ y) {
+    constexpr int W = waves_for<K>();
     __shared__ __attribute__((aligned(16))) float xs[q8::Shape<K>::x_blocks * stage::x_stride];
     __shared__ float xsum[q8::Shape<K>::x_blocks];
     __shared__ float red[stage::red_floats(q8::Shape<K>::x_blocks)];
-    __shared__ float part[q8::waves][q8::tile_rows];
+    __shared__ float part[W][q8::tile_rows];
     const size_t tile = blockIdx.x;
     if (blockIdx.x != 0) {
         in.v_out = nullptr;
@@ -133,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(const uint8_t *__re
     const uint32_t row = uint32_t(tile) * q8::tile_rows + threadIdx.x % q8::tile_rows;
     const float bv = bias ? bias[row] : 0.0f;
     const float rv = residual ? residual[row] : 0.0f;
-    const float sum = tile_matvec<K, MODE>(codes, scales, tile, in, xs, xsum, red, part);
+    const float sum = tile_matvec<K, W, MODE>(codes, scales, tile, in, xs, xsum, red, part);
     if (threadIdx.x < q8::tile_rows) {
         // tensor.cpp:235: bias + sum; model.cpp:586-588: residual = x + projected
         const float projected = bias ? bv + sum : sum;
@@ -154,7 +163,7 @@ __host__ __device__ inline uint32_t qkv_dim(uint32_t tile, uint32_t r) {
 }
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads) void qkv_kernel(const uint8_t *__restrict__ codes,
+__global__ __launch_bounds__(waves_for<2880>() * 64) void qkv_kernel(const uint8_t *__restrict__ codes,
                                                        const uint16_t *__restrict__ scales, stage::Input in,
                                                        const float *__restrict__ bias,
                                                        const float2 *__restrict__ rope,
@@ -165,7 +174,8 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(const uint8_t *__restrict
     __shared__ __attribute__((aligned(16))) float xs[q8::Shape<2880>::x_blocks * stage::x_stride];
     __shared__ float xsum[q8::Shape<2880>::x_blocks];
     __shared__ float red[stage::red_floats(q8::Shape<2880>::x_blocks)];
-    __shared__ float part[q8::waves][q8::tile_rows];
+    constexpr int W = waves_for<2880>();
+    __shared__ float part[W][q8::tile_rows];
     __shared__ float vals[q8::tile_rows];
     const uint32_t tile = blockIdx.x;
     if (blockIdx.x != 0) {
@@ -182,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(const uint8_t *__restrict
     const uint32_t pair = r16 < 8 ? dim : dim - 32;
     const bool rotate = (is_q || is_k) && pos < capacity;
     const float2 cs = rotate ? rope[size_t(pos) * (kHead / 2) + pair] : make_float2(0.f, 0.f);
-    const float sum = tile_matvec<2880, MODE>(codes, scales, tile, in, xs, xsum, red, part);
+    const float sum = tile_matvec<2880, W, MODE>(codes, scales, tile, in, xs, xsum, red, part);
     if (r < q8::tile_rows) {
         vals[r] = bv + sum;
     }
@@ -357,10 +367,10 @@ int ttl_matvec_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
     stage::with_mode(s, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
         if (w->cols == 2880) {
-            q8_matvec_kernel<2880, M><<<w->tiles, kThreads, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s,
+            q8_matvec_kernel<2880, M><<<w->tiles, waves_for<2880>() * 64, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s,
                                                                              bias_dev, residual_dev, y_dev);
         } else {
-            q8_matvec_kernel<4096, M><<<w->tiles, kThreads, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s,
+            q8_matvec_kernel<4096, M><<<w->tiles, waves_for<4096>() * 64, 0, ctx->stream>>>(w->codes, w->scales, w->rows, s,
                                                                              bias_dev, residual_dev, y_dev);
         }
     });
@@ -384,7 +394,7 @@ int ttl_attn_qkv(ttl_ctx *ctx, const ttl_q8 *qkv, const float *bias_dev, const t
                 "ttl_attn_qkv: the QKV tensor must be 5120 x 2880 (q|k|v rows in ttl_qkv_row_source order)");
     const stage::Input s = stage::from_abi(in);
     stage::with_mode(s, [&](auto mode) {
-        qkv_kernel<decltype(mode)::value><<<qkv->tiles, kThreads, 0, ctx->stream>>>(
+        qkv_kernel<decltype(mode)::value><<<qkv->tiles, waves_for<2880>() * 64, 0, ctx->stream>>>(
             qkv->codes, qkv->scales, s, bias_dev, reinterpret_cast<const float2 *>(rope_dev), position_dev, capacity,
             q_dev, k_cache_dev, v_cache_dev);
     });

@@ -59,36 +59,44 @@ __host__ __device__ inline size_t scale_index(size_t tile, uint32_t block, uint3
     return tile * lanes_k * tile_rows * pad + (size_t(block % lanes_k) * tile_rows + row) * pad + block / lanes_k;
 }
 
-template <int K>
+// A tile's K range split over W waves (W divides the padded iteration count, which
+// the layout fixes at scale_pad): wave w takes iterations [w*PW, w*PW + PW).
+template <int K, int W>
+struct Split {
+    static constexpr int per_wave = Shape<K>::scale_pad / W;
+    static_assert(Shape<K>::scale_pad % W == 0, "the split must divide the padded iterations");
+    static_assert(per_wave % 2 == 0, "scales are loaded in fp16 pairs");
+};
+
+template <int K, int W = waves>
 struct TileRegs {
-    static_assert(Shape<K>::per_wave % 2 == 0, "scales are loaded in fp16 pairs");
-    uint4 c[Shape<K>::per_wave][2];
-    uint32_t s[Shape<K>::per_wave / 2];  // fp16 scales, two per word
+    uint4 c[Split<K, W>::per_wave][2];
+    uint32_t s[Split<K, W>::per_wave / 2];  // fp16 scales, two per word
 };
 
 // Issues the loads of wave `wave`'s share of one tile.
-template <int K>
+template <int K, int W = waves>
 __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *__restrict__ codes,
                                                                 const uint16_t *__restrict__ scales, size_t tile,
-                                                                uint32_t wave, uint32_t lane, TileRegs<K> &regs) {
+                                                                uint32_t wave, uint32_t lane, TileRegs<K, W> &regs) {
     using S = Shape<K>;
+    constexpr int PW = Split<K, W>::per_wave;
     const uint32_t r = lane % tile_rows, kl = lane / tile_rows;
-    const uint16_t *sp = scales + tile * S::tile_scales + (size_t(kl) * tile_rows + r) * S::scale_pad +
-                         wave * S::per_wave;
-    // the lane's per_wave fp16 scales are contiguous; loaded first, since every
+    const uint16_t *sp = scales + tile * S::tile_scales + (size_t(kl) * tile_rows + r) * S::scale_pad + wave * PW;
+    // the lane's per-wave fp16 scales are contiguous; loaded first, since every
     // iteration needs them
     const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sp);
 #pragma unroll
-    for (int j = 0; j < S::per_wave / 2; ++j) {
+    for (int j = 0; j < PW / 2; ++j) {
         regs.s[j] = s32[j];
     }
     // Unconditional loads (see tail_pad_bytes): blocks past the row end have a zero
     // scale in the padded scale layout, so their codes contribute nothing.
 #pragma unroll
-    for (int j = 0; j < S::per_wave; ++j) {
+    for (int j = 0; j < PW; ++j) {
         // blocks past the row end re-read the last block (a duplicate address within the
         // load, so no extra memory traffic); their scale is zero
-        const int i = int(wave) * S::per_wave + j;
+        const int i = int(wave) * PW + j;
         const uint32_t kb = min(uint32_t(4 * i) + kl, uint32_t(S::blocks - 1));
         const uint4 *p = reinterpret_cast<const uint4 *>(codes + ((tile * S::blocks + kb) * tile_rows + r) * 32);
         regs.c[j][0] = p[0];
@@ -113,17 +121,17 @@ __device__ inline float block_dot(const uint4 c0, const uint4 c1, const float *_
 }
 
 // Wave's partial dot products for the tile's 16 rows; valid in lanes 0..15.
-template <int K>
-__device__ __attribute__((always_inline)) inline float tile_compute(const TileRegs<K> &regs, uint32_t wave,
+template <int K, int W = waves>
+__device__ __attribute__((always_inline)) inline float tile_compute(const TileRegs<K, W> &regs, uint32_t wave,
                                                                    uint32_t lane, const float *xs,
                                                                    const float *xsum) {
-    using S = Shape<K>;
+    constexpr int PW = Split<K, W>::per_wave;
     const uint32_t kl = lane / tile_rows;
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < S::per_wave; ++j) {
+    for (int j = 0; j < PW; ++j) {
         // no bounds test: padding iterations have zero x and a zero scale
-        const int i = int(wave) * S::per_wave + j;
+        const int i = int(wave) * PW + j;
         const uint32_t kb = 4 * i + kl;
         const uint16_t bits = uint16_t(regs.s[j / 2] >> (16 * (j % 2)));
         const float d = __half2float(__ushort_as_half(bits));
