@@ -315,6 +315,19 @@ int ttl_synth_q8_0_gguf(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t blo
 int ttl_matvec_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const ttl_stage_input *in,
                     const float *residual_dev, float *y_dev);
 
+/* matmul_add_q8_0 (tensor.h:36-37, tensor.cpp:529-566) for `tokens` tokens, as
+ * GptOssModel::prefill runs the attention projections (model.cpp:493-498, 519-520):
+ * out[t][r] = bias[r] + sum_k W[r][k] x[t][k] (+ residual[t][r] when residual_dev is
+ * non-NULL, the residual add of model.cpp:521-529).  x_dev f32 [tokens][cols] (cols
+ * 2880 or 4096), out_dev f32 [tokens][rows] in the tensor's row order; bias_dev may
+ * be NULL.  bf16 MFMA with exact products (int8 codes; the activations as three bf16
+ * planes) and the block scale applied per block: results agree with the reference to
+ * f32 rounding.  workspace_dev (16-byte aligned) holds
+ * ttl_matmul_q8_0_workspace_bytes(tokens, cols). */
+size_t ttl_matmul_q8_0_workspace_bytes(uint32_t tokens, uint32_t cols);
+int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev, uint32_t tokens,
+                    const float *residual_dev, float *out_dev, void *workspace_dev, size_t workspace_bytes);
+
 /* The row order ttl_attn_qkv expects of its 5120-row tensor: rows of attn_q (0..4095),
  * attn_k (4096..4607) and attn_v (4608..5119) stacked, reordered so each RoPE pair
  * (d, d+32) of a head shares a tile.  Fills row_source[5120]. */

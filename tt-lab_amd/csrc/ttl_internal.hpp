@@ -45,6 +45,7 @@ struct ttl_q8 {
     uint32_t tiles = 0;          // rows / 16
     uint8_t *codes = nullptr;    // [tiles][blocks][16 rows][32 B]
     uint16_t *scales = nullptr;  // [tiles][4 lanes_k][16 rows][scale_pad] fp16
+    uint16_t *row_scales = nullptr;  // [rows][blocks] fp16, for the batched matmul
     size_t code_bytes = 0;
     size_t scale_bytes = 0;
 };

@@ -17,7 +17,7 @@ constexpr int kQRows = kQHeads * kHead, kKvRows = kKvHeads * kHead, kQkvRows = k
 
 __global__ void q8_repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows, uint32_t cols,
                                  const int32_t *__restrict__ row_source, uint8_t *__restrict__ codes,
-                                 uint16_t *__restrict__ scales) {
+                                 uint16_t *__restrict__ scales, uint16_t *__restrict__ row_scales) {
     const uint32_t blocks = cols / 32;
     const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (gid >= size_t(rows) * blocks) {
@@ -37,7 +37,9 @@ __global__ void q8_repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows
     uint4 *dst = reinterpret_cast<uint4 *>(codes + q8::code_offset(tile, block, r, int(cols)));
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
     dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-    scales[q8::scale_index(tile, block, r, int(cols))] = uint16_t(src[0] | (src[1] << 8));
+    const uint16_t d = uint16_t(src[0] | (src[1] << 8));
+    scales[q8::scale_index(tile, block, r, int(cols))] = d;
+    row_scales[size_t(row) * q8::row_scale_stride(int(cols)) + block] = d;
 }
 
 __global__ void q8_unpack_kernel(const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
@@ -243,6 +245,13 @@ int ttl_q8_upload_dev(ttl_ctx *ctx, const void *gguf_dev, uint32_t rows, uint32_
     if (err == hipSuccess) {
         err = hipMalloc(&t->scales, t->scale_bytes);
     }
+    const size_t row_scale_bytes = size_t(rows) * q8::row_scale_stride(int(cols)) * sizeof(uint16_t);
+    if (err == hipSuccess) {
+        err = hipMalloc(&t->row_scales, row_scale_bytes);
+    }
+    if (err == hipSuccess) {
+        err = hipMemsetAsync(t->row_scales, 0, row_scale_bytes, ctx->stream);
+    }
     if (err == hipSuccess) {
         err = hipMemsetAsync(t->scales, 0, t->scale_bytes, ctx->stream);
     }
@@ -258,7 +267,8 @@ int ttl_q8_upload_dev(ttl_ctx *ctx, const void *gguf_dev, uint32_t rows, uint32_
     if (err == hipSuccess) {
         const size_t n = size_t(rows) * (cols / 32);
         q8_repack_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>((const uint8_t *)gguf_dev, rows, cols,
-                                                                            perm, t->codes, t->scales);
+                                                                            perm, t->codes, t->scales,
+                                                                            t->row_scales);
         err = hipGetLastError();
     }
     if (err == hipSuccess) {
@@ -322,11 +332,13 @@ void ttl_q8_free(ttl_ctx *ctx, ttl_q8 *t) {
     }
     (void)hipFree(t->codes);
     (void)hipFree(t->scales);
+    (void)hipFree(t->row_scales);
     delete t;
 }
 
 size_t ttl_q8_bytes(const ttl_q8 *t) {
-    return t ? t->code_bytes + t->scale_bytes : 0;
+    return t ? t->code_bytes + t->scale_bytes + size_t(t->rows) * q8::row_scale_stride(int(t->cols)) * sizeof(uint16_t)
+             : 0;
 }
 
 int ttl_synth_q8_0_gguf(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t block_offset, size_t n,

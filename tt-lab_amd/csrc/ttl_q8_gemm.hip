@@ -1,0 +1,342 @@
+// Batched Q8_0 matmul on MFMA: matmul_add_q8_0 (tensor.cpp:529-566) for a batch of
+// tokens, as GptOssModel::prefill runs the attention projections (model.cpp:493-498,
+// 519-520).
+//
+// Operands of v_mfma_f32_16x16x32_bf16 (D = A B + C; lane l holds 8 bf16 of A row
+// l%16 and of B column l%16 for the K offsets of lane group g = l/16, and receives D
+// rows 4g..4g+3 of column l%16):
+//  - one K step is one Q8_0 block of 32 columns; lane group g holds offsets 8g..8g+7;
+//  - A is 16 tokens: the f32 activations split into three bf16 planes whose sum is
+//    each value exactly (mf::split_planes), staged through LDS;
+//  - B is 16 weight rows: the int8 codes, exact in bf16 (at most 8 significant bits);
+//  - D[token][row]: a lane holds four tokens of one row, so the block's fp16 scale is
+//    one value per lane, applied after the block: acc += d * (A0 B + A1 B + A2 B).
+// Every product q x is exact; the MFMA sums a block's products in f32 and d times that
+// sum is added to the accumulator.  The reference sums the same products
+// sequentially from the bias (d q rounds to nothing: it has at most 19 significant
+// bits), so results agree to f32 rounding, not bit for bit.
+//
+// Token fragments: [token tile of 64][plane][step][16-token sub-tile][lane][16 B];
+// steps past the last block (K = 2880 has 90 blocks, padded to 92) hold zero tokens,
+// and their row scales are zero.
+#include "ttl_mfma.hpp"
+
+#include <hip/hip_fp16.h>
+
+namespace {
+
+using mf::bf16x8;
+using mf::f32x4;
+
+constexpr int kPlanes = 3;
+constexpr int kSub = 4;  // 16-token sub-tiles per 64-token tile
+constexpr int kTileTokens = 16 * kSub;
+constexpr int kStageSteps = 2;  // K steps per LDS stage
+constexpr int kWaves = 4;
+constexpr int kRowTiles = 3;  // 16-row weight tiles per wave
+constexpr int kGroupTiles = kWaves * kRowTiles;
+constexpr int kLook = 4;  // token fragments read from LDS this many ahead
+
+template <int K>
+struct Shape {
+    static constexpr int blocks = K / 32;
+    static constexpr int quads = (blocks + 3) / 4;
+    static constexpr int steps = quads * 4;
+    static constexpr int stages = steps / kStageSteps;
+    static constexpr size_t plane_bytes = size_t(steps) * kSub * mf::frag_bytes;
+    static constexpr size_t tile_bytes = kPlanes * plane_bytes;
+    static constexpr int stage_frags = kPlanes * kStageSteps * kSub;
+    static constexpr int stage_chunks = stage_frags * 64;  // 16-byte pieces
+};
+
+// Token fragments of one (step, tile): thread (sub-tile m, lane (t, g)) converts
+// x[64 tile + 16 m + t][32 step + 8 g .. + 7] (zero past the tokens or the row end).
+template <int K>
+__global__ __launch_bounds__(kSub * 64) void q8_gather_kernel(const float *__restrict__ x, uint32_t tokens,
+                                                              uint8_t *__restrict__ frags) {
+    using S = Shape<K>;
+    const uint32_t step = blockIdx.x, tile = blockIdx.y;
+    const uint32_t m = threadIdx.x / 64, lane = threadIdx.x % 64, g = lane / 16;
+    const uint32_t token = tile * kTileTokens + m * 16 + lane % 16;
+    float v[8];
+    if (token < tokens && step < uint32_t(S::blocks)) {
+        const float4 *p = reinterpret_cast<const float4 *>(x + size_t(token) * K + step * 32 + 8 * g);
+        const float4 lo = p[0], hi = p[1];
+        v[0] = lo.x;
+        v[1] = lo.y;
+        v[2] = lo.z;
+        v[3] = lo.w;
+        v[4] = hi.x;
+        v[5] = hi.y;
+        v[6] = hi.z;
+        v[7] = hi.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = 0.0f;
+        }
+    }
+    uint4 out[kPlanes];
+    mf::split_planes<kPlanes>(v, out);
+    uint8_t *dst = frags + size_t(tile) * S::tile_bytes + (size_t(step) * kSub + m) * mf::frag_bytes + lane * 16;
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) {
+        *reinterpret_cast<uint4 *>(dst + size_t(p) * S::plane_bytes) = out[p];
+    }
+}
+
+// 8 int8 codes (K order) as bf16: exact, so the bf16 bits are the f32's top half.
+__device__ inline bf16x8 int8_bf16(uint2 c) {
+    mf::u32x4 r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t w = k < 2 ? c.x : c.y;
+        const uint32_t sh = 16 * (k % 2);
+        const float f0 = float(int32_t(w << (24 - sh)) >> 24);
+        const float f1 = float(int32_t(w << (16 - sh)) >> 24);
+        r[k] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+    }
+    return mf::as_bf16x8v(r);
+}
+
+struct GemmArgs {
+    const uint8_t *codes;        // repacked [tiles][blocks][16 rows][32 B]
+    const uint16_t *row_scales;  // [rows][steps] fp16 (zero past the blocks, q8::row_scale_stride)
+    const float *bias;           // [rows] or null
+    const float *residual;       // [tokens][rows] or null
+    float *out;                  // [tokens][rows]
+    const uint8_t *frags;        // token fragments
+    uint32_t rows, row_tiles, tokens;
+};
+
+// One workgroup: a 64-token tile x kGroupTiles weight-row tiles; wave w takes row
+// tiles (group * 4 + w) * 3 + j.  Token fragments go through LDS in stages of two K
+// steps (double-buffered); each wave's weight codes and scales are requested one
+// quad (4 steps) ahead.
+template <int K>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void q8_gemm_kernel(GemmArgs a) {
+    using S = Shape<K>;
+    constexpr int kThreads = kWaves * 64;
+    constexpr int kPer = S::stage_chunks / kThreads;
+    static_assert(S::stage_chunks % kThreads == 0, "the stager moves whole pieces");
+    __shared__ mf::u32x4 lds[2][S::stage_chunks];
+    const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64, n = lane % 16, g = lane / 16;
+    const uint32_t tile = blockIdx.y;
+    const uint8_t *frags = a.frags + size_t(tile) * S::tile_bytes;
+
+    // this wave's weight row tiles (tiles past the matrix re-read tile 0; not written)
+    const uint8_t *cp[kRowTiles];
+    const uint16_t *sp[kRowTiles];
+    bool ok[kRowTiles];
+    uint32_t row[kRowTiles];
+#pragma unroll
+    for (int j = 0; j < kRowTiles; ++j) {
+        const uint32_t rt = (blockIdx.x * kWaves + wave) * kRowTiles + j;
+        ok[j] = rt < a.row_tiles;
+        const uint32_t rts = ok[j] ? rt : 0;
+        row[j] = rts * 16 + n;
+        cp[j] = a.codes + (size_t(rts) * S::blocks * 16 + n) * 32 + 8 * g;
+        sp[j] = a.row_scales + size_t(row[j]) * S::steps;
+    }
+
+    // stage j: K steps 2j, 2j+1 of all planes and sub-tiles, LDS order [plane][step][sub][lane]
+    mf::u32x4 st[kPer];
+    auto stage_load = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t c = t + uint32_t(k) * kThreads;
+            const uint32_t p = c / (kStageSteps * kSub * 64), within = c % (kStageSteps * kSub * 64);
+            st[k] = *reinterpret_cast<const mf::u32x4 *>(frags + size_t(p) * S::plane_bytes +
+                                                       size_t(j) * kStageSteps * kSub * mf::frag_bytes +
+                                                       size_t(within) * 16);
+        }
+    };
+    auto stage_store = [&](mf::u32x4 *dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            dst[t + uint32_t(k) * kThreads] = st[k];
+        }
+    };
+
+    // weight codes and scales of one quad: [row tile][step], [row tile] (4 fp16)
+    uint2 qc[2][kRowTiles][4];
+    uint2 qs[2][kRowTiles];
+    auto load_quad = [&](int q, uint2(&c)[kRowTiles][4], uint2(&s)[kRowTiles]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kRowTiles; ++j) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t b = min(uint32_t(4 * q + k), uint32_t(S::blocks - 1));
+                c[j][k] = *reinterpret_cast<const uint2 *>(cp[j] + size_t(b) * 16 * 32);
+            }
+            s[j] = *reinterpret_cast<const uint2 *>(sp[j] + 4 * q);
+        }
+    };
+
+    f32x4 acc[kSub][kRowTiles];
+#pragma unroll
+    for (int m = 0; m < kSub; ++m) {
+#pragma unroll
+        for (int j = 0; j < kRowTiles; ++j) {
+            acc[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    stage_load(0);
+    load_quad(0, qc[0], qs[0]);
+    stage_store(lds[0]);
+    __syncthreads();
+    stage_load(1);
+
+    // the MFMAs of quad q (stages 2q, 2q+1) with its codes c and scales s
+    auto compute_quad = [&](int q, const uint2(&c)[kRowTiles][4], const uint2(&s)[kRowTiles])
+                            __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 4 / kStageSteps; ++h) {
+            const int stage = 2 * q + h;
+            const mf::u32x4 *buf = lds[stage % 2];
+            constexpr int SF = S::stage_frags;  // fragments per stage, order (step, sub, plane)
+            auto frag = [&](int f) __attribute__((always_inline)) {
+                const int ls = f / (kSub * kPlanes), m = (f / kPlanes) % kSub, p = f % kPlanes;
+                return mf::as_bf16x8v(buf[((p * kStageSteps + ls) * kSub + m) * 64 + lane]);
+            };
+            bf16x8 ring[kLook];
+#pragma unroll
+            for (int d = 0; d < kLook; ++d) {
+                ring[d] = frag(d);
+            }
+            bf16x8 w[kRowTiles];
+            float d[kRowTiles];
+            f32x4 part[kRowTiles];
+#pragma unroll
+            for (int f = 0; f < SF; ++f) {
+                const bf16x8 av = ring[f % kLook];
+                if (f + kLook < SF) {
+                    ring[f % kLook] = frag(f + kLook);
+                }
+                const int ls = f / (kSub * kPlanes), m = (f / kPlanes) % kSub, p = f % kPlanes;
+                const int k = h * kStageSteps + ls;  // step within the quad
+                if (f % (kSub * kPlanes) == 0) {
+#pragma unroll
+                    for (int j = 0; j < kRowTiles; ++j) {
+                        w[j] = int8_bf16(c[j][k]);
+                        const uint32_t word = k < 2 ? s[j].x : s[j].y;
+                        d[j] = __half2float(__ushort_as_half(uint16_t(word >> (16 * (k % 2)))));
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < kRowTiles; ++j) {
+                    part[j] = mf::mfma(av, w[j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : part[j]);
+                    if (p == kPlanes - 1) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            acc[m][j][e] = fmaf(d[j], part[j][e], acc[m][j][e]);
+                        }
+                        // an empty statement that takes the sum in registers here: the
+                        // compiler otherwise sinks these updates below the stage's MFMAs
+                        // and keeps every block product live
+                        asm volatile("" : "+v"(acc[m][j]));
+                    }
+                }
+                // keep the ring's order: without this the scheduler hoists every LDS
+                // read of the stage and runs out of registers
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // end of stage: publish the next, fetch the one after
+            if (stage + 1 < S::stages) {
+                stage_store(lds[(stage + 1) % 2]);
+            }
+            __syncthreads();
+            if (stage + 2 < S::stages) {
+                stage_load(stage + 2);
+            }
+        }
+    };
+
+#pragma unroll 1
+    for (int q = 0; q < S::quads; q += 2) {
+        load_quad(min(q + 1, S::quads - 1), qc[1], qs[1]);
+        compute_quad(q, qc[0], qs[0]);
+        if (q + 1 < S::quads) {
+            load_quad(min(q + 2, S::quads - 1), qc[0], qs[0]);
+            compute_quad(q + 1, qc[1], qs[1]);
+        }
+    }
+
+    // D rows 4g..4g+3 of sub-tile m are tokens; the lane's column is row[j]
+#pragma unroll
+    for (int j = 0; j < kRowTiles; ++j) {
+        if (!ok[j]) {
+            continue;
+        }
+        const float bv = a.bias ? a.bias[row[j]] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < kSub; ++m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t token = tile * kTileTokens + m * 16 + 4 * g + e;
+                if (token < a.tokens) {
+                    const size_t o = size_t(token) * a.rows + row[j];
+                    float v = a.bias ? bv + acc[m][j][e] : acc[m][j][e];
+                    if (a.residual) {
+                        v = a.residual[o] + v;
+                    }
+                    a.out[o] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int K>
+size_t workspace_for(uint32_t tokens) {
+    return size_t((tokens + kTileTokens - 1) / kTileTokens) * Shape<K>::tile_bytes;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ttl_matmul_q8_0_workspace_bytes(uint32_t tokens, uint32_t cols) {
+    return cols == 4096 ? workspace_for<4096>(tokens) : workspace_for<2880>(tokens);
+}
+
+int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev, uint32_t tokens,
+                    const float *residual_dev, float *out_dev, void *workspace_dev, size_t workspace_bytes) {
+    TTL_REQUIRE(ctx && w && w->codes && w->row_scales && x_dev && out_dev && workspace_dev, TTL_ERR_INVALID,
+                "ttl_matmul_q8_0: null argument");
+    TTL_REQUIRE(w->cols == 2880 || w->cols == 4096, TTL_ERR_SHAPE, "ttl_matmul_q8_0: cols must be 2880 or 4096");
+    TTL_REQUIRE(tokens < (1u << 20), TTL_ERR_SHAPE, "ttl_matmul_q8_0: at most %u tokens per call", (1u << 20) - 1);
+    const size_t need = ttl_matmul_q8_0_workspace_bytes(tokens, w->cols);
+    TTL_REQUIRE(workspace_bytes >= need, TTL_ERR_SHAPE, "ttl_matmul_q8_0: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace_dev) & 15) == 0,
+                TTL_ERR_INVALID, "ttl_matmul_q8_0: x and the workspace must be 16-byte aligned");
+    if (tokens == 0) {
+        return TTL_OK;
+    }
+    const uint32_t tiles = (tokens + kTileTokens - 1) / kTileTokens;
+    GemmArgs a;
+    a.codes = w->codes;
+    a.row_scales = w->row_scales;
+    a.bias = bias_dev;
+    a.residual = residual_dev;
+    a.out = out_dev;
+    a.frags = static_cast<const uint8_t *>(workspace_dev);
+    a.rows = w->rows;
+    a.row_tiles = w->tiles;
+    a.tokens = tokens;
+    const dim3 grid((w->tiles + kGroupTiles - 1) / kGroupTiles, tiles);
+    uint8_t *frags = static_cast<uint8_t *>(workspace_dev);
+    if (w->cols == 2880) {
+        q8_gather_kernel<2880><<<dim3(Shape<2880>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, frags);
+        q8_gemm_kernel<2880><<<grid, kWaves * 64, 0, ctx->stream>>>(a);
+    } else {
+        q8_gather_kernel<4096><<<dim3(Shape<4096>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, frags);
+        q8_gemm_kernel<4096><<<grid, kWaves * 64, 0, ctx->stream>>>(a);
+    }
+    TTL_LAUNCHED("q8 gemm kernels");
+    return TTL_OK;
+}
+
+}  // extern "C"

@@ -51,6 +51,11 @@ __host__ __device__ inline size_t tail_pad_bytes(int cols) {
     const int covered = ((iters + waves - 1) / waves) * waves * lanes_k;
     return size_t(covered - cols / 32) * tile_rows * 32;
 }
+// fp16 scales per row of the row-major copy used by the batched matmul: the blocks
+// rounded up to a multiple of 4 (zero padding), so a quad's four are one 8-byte load.
+__host__ __device__ inline int row_scale_stride(int cols) {
+    return (cols / 32 + 3) / 4 * 4;
+}
 __host__ __device__ inline size_t code_offset(size_t tile, uint32_t block, uint32_t row, int cols) {
     return ((tile * blocks_of(cols) + block) * tile_rows + row) * 32;
 }

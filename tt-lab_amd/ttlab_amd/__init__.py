@@ -285,6 +285,8 @@ def load_library():
         "ttl_moe_prefill": (i32, [vp, C.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp, vp, sz]),
         "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
         "ttl_stream_read": (i32, [vp, vp, sz, vp]),
+        "ttl_matmul_q8_0_workspace_bytes": (sz, [u32, u32]),
+        "ttl_matmul_q8_0": (i32, [vp, vp, vp, vp, u32, vp, vp, vp, sz]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
@@ -562,6 +564,17 @@ class Device:
     def matvec_q8_0(self, w, bias, stage, residual, y):
         _check(self.lib.ttl_matvec_q8_0(self.ctx, w.handle, bias.ptr if bias else None, C.byref(stage),
                                         residual.ptr if residual else None, y.ptr), "ttl_matvec_q8_0")
+
+    def matmul_q8_0(self, w, bias, x, tokens, residual, out):
+        """matmul_add_q8_0 for `tokens` rows of x on the device; allocates its workspace."""
+        ws = self.alloc(max(16, self.lib.ttl_matmul_q8_0_workspace_bytes(tokens, w.cols)))
+        try:
+            _check(self.lib.ttl_matmul_q8_0(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, tokens,
+                                            residual.ptr if residual else None, out.ptr, ws.ptr, ws.nbytes),
+                   "ttl_matmul_q8_0")
+            self.sync()
+        finally:
+            ws.free()
 
     def attn_qkv(self, qkv, bias, stage, rope, position, capacity, q, kc, vc):
         _check(self.lib.ttl_attn_qkv(self.ctx, qkv.handle, bias.ptr, C.byref(stage), rope.ptr, position.ptr, capacity,
