@@ -837,6 +837,74 @@ void orc_layer_forward(const orc_layer *layer, size_t layer_index, size_t positi
     free(scores);
 }
 
+/* model.cpp:484-553 for positions first .. first + count - 1. */
+void orc_layer_prefill(const orc_layer *layer, size_t layer_index, size_t first, size_t count, const float *x_in,
+                       const float *rope_frequencies, float *key_cache, float *value_cache, int body, float *x_out,
+                       float *residual_out) {
+    enum { H = 2880, QW = ORC_QHEADS * ORC_HEAD, KW = ORC_KVHEADS * ORC_HEAD };
+    if (count == 0) {
+        return;
+    }
+    float *normalized = calloc(count * H, sizeof(float));
+    float *query = malloc(sizeof(float) * count * QW);
+    float *key = malloc(sizeof(float) * count * KW);
+    float *value = malloc(sizeof(float) * count * KW);
+    float *attended = malloc(sizeof(float) * count * QW);
+    float *projected = malloc(sizeof(float) * count * H);
+    float *residual = malloc(sizeof(float) * count * H);
+    float *moe_out = malloc(sizeof(float) * count * H);
+    float *workspace = malloc(sizeof(float) * count);
+    float *transposed = malloc(sizeof(float) * count * QW);
+    float *scores = malloc(sizeof(float) * (first + count));
+
+    for (size_t p = 0; p < count; ++p) {
+        orc_rms_norm(x_in + p * H, layer->attention_norm, H, 1.0e-5f, normalized + p * H);
+    }
+    orc_matmul_add_q8_0(layer->query_weight, layer->query_bias, QW, H, normalized, count, query, workspace,
+                        transposed);
+    orc_matmul_add_q8_0(layer->key_weight, layer->key_bias, KW, H, normalized, count, key, workspace, transposed);
+    orc_matmul_add_q8_0(layer->value_weight, layer->value_bias, KW, H, normalized, count, value, workspace,
+                        transposed);
+    for (size_t p = 0; p < count; ++p) {
+        orc_apply_rope(query + p * QW, ORC_QHEADS, first + p, rope_frequencies);
+        orc_apply_rope(key + p * KW, ORC_KVHEADS, first + p, rope_frequencies);
+        memcpy(key_cache + (first + p) * KW, key + p * KW, sizeof(float) * KW); /* store_kv */
+        memcpy(value_cache + (first + p) * KW, value + p * KW, sizeof(float) * KW);
+    }
+    for (size_t p = 0; p < count; ++p) {
+        orc_attention(query + p * QW, key_cache, value_cache, layer->sinks, layer_index, first + p, attended + p * QW,
+                      scores);
+    }
+    orc_matmul_add_q8_0(layer->output_weight, layer->output_bias, H, QW, attended, count, projected, workspace,
+                        transposed);
+    for (size_t p = 0; p < count; ++p) {
+        for (size_t j = 0; j < H; ++j) {
+            residual[p * H + j] = x_in[p * H + j] + projected[p * H + j];
+        }
+        orc_rms_norm(residual + p * H, layer->post_attention_norm, H, 1.0e-5f, normalized + p * H);
+    }
+    orc_moe_batch(&layer->moe, normalized, count, moe_out, body);
+    for (size_t p = 0; p < count; ++p) {
+        for (size_t j = 0; j < H; ++j) {
+            x_out[p * H + j] = residual[p * H + j] + moe_out[p * H + j];
+        }
+    }
+    if (residual_out) {
+        memcpy(residual_out, residual, sizeof(float) * count * H);
+    }
+    free(normalized);
+    free(query);
+    free(key);
+    free(value);
+    free(attended);
+    free(projected);
+    free(residual);
+    free(moe_out);
+    free(workspace);
+    free(transposed);
+    free(scores);
+}
+
 /* ------------------------------------------------------------------------- */
 /* synthetic inputs                                                          */
 /* ------------------------------------------------------------------------- */

@@ -176,6 +176,17 @@ void orc_layer_forward(const orc_layer *layer, size_t layer_index, size_t positi
                        float *query, float *attended, float *residual, float *router, int64_t *indices,
                        float *weights);
 
+/* The body of GptOssModel::prefill's layer loop (model.cpp:484-553) for `count`
+ * tokens at positions first .. first+count-1 (the reference's prefill has first = 0):
+ * per-token RMSNorm, the batched Q8_0 matmuls (matmul_add_q8_0), RoPE and the KV
+ * store of every token, then attention per token, the output matmul, the residual,
+ * moe_batch and the second residual.  x_in/x_out f32 [count][2880]; the caches as in
+ * orc_layer_forward.  residual_out [count][2880] may be NULL.  Parity unpinned as a
+ * composition: checked against orc_layer_forward token by token within tolerance. */
+void orc_layer_prefill(const orc_layer *layer, size_t layer_index, size_t first, size_t count, const float *x_in,
+                       const float *rope_frequencies, float *key_cache, float *value_cache, int body, float *x_out,
+                       float *residual_out);
+
 /* ---- synthetic inputs (shared specification with tt-lab_amd/csrc/ttl_synth.hip) */
 uint64_t orc_hash(uint64_t seed, uint64_t stream, uint64_t index);
 /* N(0,1) drawn as an Irwin-Hall sum of 12 24-bit uniforms in exact integer arithmetic,

@@ -91,6 +91,8 @@ def _load():
         "orc_matmul_add_q8_0": (None, [_u8p, _f32p, _sz, _sz, _f32p, _sz, _f32p, _f32p, _f32p]),
         "orc_matvec_bf16": (None, [_u16p, _sz, _sz, _f32p, _f32p]),
         "orc_greedy": (C.c_int32, [_f32p, _sz]),
+        "orc_layer_prefill": (None, [C.POINTER(OrcLayer), _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, C.c_int, _f32p,
+                                     C.c_void_p]),
         "orc_layer_forward": (None, [C.POINTER(OrcLayer), _sz, _sz, _f32p, _f32p, _f32p, _f32p, C.c_int, _f32p,
                                      _f32p, _f32p, _f32p, _f32p, _i64p, _f32p]),
         "orc_hash": (C.c_uint64, [_u64, _u64, _u64]),

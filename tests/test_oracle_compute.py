@@ -416,3 +416,46 @@ def test_moe_batch_routes_then_runs_experts():
         lib.orc_matvec_add_f32(k["router_w"], k["router_b"], s.experts, s.hidden, np.ascontiguousarray(x[p]), logits)
         idx[p], w[p] = O.router_topk(logits, s.used)
     assert np.array_equal(out.reshape(count, s.hidden), _moe_batch_experts(s, x, idx, w))
+
+
+@pytest.mark.parametrize("layer_index", [0, 1])
+def test_layer_prefill_matches_token_by_token_and_chunks(layer_index):
+    """orc_layer_prefill (model.cpp:484-553, batched matmuls and moe_batch) against
+    orc_layer_forward per token (model.cpp:571-595, matvecs and moe): the same
+    arithmetic summed in other orders, so rel L2 <= 1e-5 per token unless the routing
+    is a near-tie.  A prefill split into chunks (positions 0..2, then 3..5) writes the
+    same keys and values bit for bit (the Q8_0 matmul sums each token on its own); its
+    outputs agree to tolerance only, since moe_batch sends an expert with at most 4
+    tokens through the matvec and others through the selected matmul
+    (model.cpp:404,435), which round differently."""
+    from model_fixtures import HostModelLayer
+    host = HostModelLayer(0x77000031, layer_index, 8)
+    s = host.struct()
+    count, KW, N = 6, 512, 2880
+    freqs = np.empty(32, np.float32)
+    lib.orc_rope_frequencies(freqs)
+    x = O.synth_normal(0x78000031, layer_index, count * N, sigma=1.0)
+    kc, vc = np.zeros(count * KW, np.float32), np.zeros(count * KW, np.float32)
+    out = np.empty(count * N, np.float32)
+    lib.orc_layer_prefill(C.byref(s), layer_index, 0, count, x, freqs, kc, vc, O.BODY_V4, out, None)
+    kc2, vc2 = np.zeros(count * KW, np.float32), np.zeros(count * KW, np.float32)
+    out2 = np.empty(count * N, np.float32)
+    lib.orc_layer_prefill(C.byref(s), layer_index, 0, 3, x[:3 * N], freqs, kc2, vc2, O.BODY_V4, out2[:3 * N], None)
+    lib.orc_layer_prefill(C.byref(s), layer_index, 3, 3, x[3 * N:], freqs, kc2, vc2, O.BODY_V4, out2[3 * N:], None)
+    assert np.array_equal(kc.view(np.uint32), kc2.view(np.uint32))
+    assert np.array_equal(vc.view(np.uint32), vc2.view(np.uint32))
+    for p in range(count):
+        assert O.rel_l2(out2[p * N:(p + 1) * N], out[p * N:(p + 1) * N]) <= 1e-5, p
+    kc3, vc3 = np.zeros(count * KW, np.float32), np.zeros(count * KW, np.float32)
+    for p in range(count):
+        ref = np.empty(N, np.float32)
+        router = np.empty(8, np.float32)
+        idx, w = np.empty(4, np.int64), np.empty(4, np.float32)
+        q, att, res = np.empty(4096, np.float32), np.empty(4096, np.float32), np.empty(N, np.float32)
+        lib.orc_layer_forward(C.byref(s), layer_index, p, np.ascontiguousarray(x[p * N:(p + 1) * N]), freqs, kc3,
+                              vc3, O.BODY_V4, ref, q, att, res, router, idx, w)
+        assert O.rel_l2(kc[p * KW:(p + 1) * KW], kc3[p * KW:(p + 1) * KW]) <= 1e-5
+        top = np.sort(router.astype(np.float64))[::-1]
+        if np.any(np.abs(np.diff(top[:5])) < 1e-4):
+            continue
+        assert O.rel_l2(out[p * N:(p + 1) * N], ref) <= 1e-5, p

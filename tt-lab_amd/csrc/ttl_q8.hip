@@ -218,6 +218,72 @@ __global__ __launch_bounds__(waves_for<2880>() * 64) void qkv_kernel(const uint8
     }
 }
 
+// ---- batched prefill helpers -------------------------------------------------------
+
+// Bias, RoPE and the KV-cache store of a batch of tokens (model.cpp:499-507) from the
+// batched Q/K/V matmul (rows in ttl_qkv_row_source order, no bias): token t sits at
+// position first + t.  One thread per (row, token); a q/k row's RoPE partner is row
+// r ^ 8 of the same tile.  The rotation is qkv_kernel's, unfused.
+__global__ __launch_bounds__(256) void qkv_rope_store_kernel(const float *__restrict__ qkv, uint32_t first,
+                                                             const float *__restrict__ bias,
+                                                             const float2 *__restrict__ rope,
+                                                             float *__restrict__ q_out, float *__restrict__ k_cache,
+                                                             float *__restrict__ v_cache) {
+#pragma clang fp contract(off)
+    const uint32_t token = blockIdx.y, row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= uint32_t(kQkvRows)) {
+        return;
+    }
+    const uint32_t tile = row / q8::tile_rows, r16 = row % q8::tile_rows;
+    const bool is_q = tile < uint32_t(kQHeads) * 4, is_k = !is_q && tile < uint32_t(kQHeads + kKvHeads) * 4;
+    const uint32_t head = is_q ? tile / 4 : (is_k ? (tile - kQHeads * 4) / 4 : (tile - (kQHeads + kKvHeads) * 4) / 4);
+    const uint32_t base = is_q ? 0u : (is_k ? uint32_t(kQRows) : uint32_t(kQRows + kKvRows));
+    const uint32_t dim = qkv_dim(tile, r16);
+    const float *in = qkv + size_t(token) * kQkvRows;
+    const float value = bias[base + head * kHead + dim] + in[row];
+    const uint32_t pos = first + token;
+    if (!(is_q || is_k)) {
+        v_cache[(size_t(pos) * kKvHeads + head) * kHead + dim] = value;
+        return;
+    }
+    const uint32_t r2 = r16 ^ 8u, dim2 = qkv_dim(tile, r2);
+    const float partner = bias[base + head * kHead + dim2] + in[tile * q8::tile_rows + r2];
+    const uint32_t pair = r16 < 8 ? dim : dim - 32;
+    const float2 cs = rope[size_t(pos) * (kHead / 2) + pair];
+    const float x = r16 < 8 ? value : partner, y = r16 < 8 ? partner : value;
+    const float out = r16 < 8 ? x * cs.x - y * cs.y : x * cs.y + y * cs.x;
+    if (is_q) {
+        q_out[size_t(token) * kQRows + head * kHead + dim] = out;
+    } else {
+        k_cache[(size_t(pos) * kKvHeads + head) * kHead + dim] = out;
+    }
+}
+
+// rms_norm (tensor.cpp:568-580) of row blockIdx.x of x [rows][2880], in the staging's
+// canonical order (so a row normalizes to the same bits as in the decode kernels).
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                            float eps, float *__restrict__ out) {
+    using S = q8::Shape<2880>;
+    __shared__ __attribute__((aligned(16))) float xs[S::x_blocks * stage::x_stride];
+    __shared__ float red[stage::red_floats(S::x_blocks)];
+    stage::Input in{};
+    in.base = x + size_t(blockIdx.x) * 2880;
+    in.norm_w = w;
+    in.eps = eps;
+    stage::stage<2880, S::x_blocks, 256, stage::kNorm>(in, xs, red);
+    float *o = out + size_t(blockIdx.x) * 2880;
+    for (uint32_t c = threadIdx.x; c < 2880u; c += 256) {
+        o[c] = xs[(c / 32) * stage::x_stride + c % 32];
+    }
+}
+
+__global__ void add_kernel(const float *__restrict__ a, const float *__restrict__ b, size_t n, float *__restrict__ out) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) {
+        out[i] = a[i] + b[i];
+    }
+}
+
 int check_q8(const ttl_q8 *t, const char *who) {
     TTL_REQUIRE(t && t->codes && t->scales, TTL_ERR_INVALID, "%s: null tensor", who);
     return TTL_OK;
@@ -411,6 +477,46 @@ int ttl_attn_qkv(ttl_ctx *ctx, const ttl_q8 *qkv, const float *bias_dev, const t
             q_dev, k_cache_dev, v_cache_dev);
     });
     TTL_LAUNCHED("qkv_kernel");
+    return TTL_OK;
+}
+
+int ttl_qkv_rope_store(ttl_ctx *ctx, const float *qkv_dev, uint32_t tokens, uint32_t first_position,
+                       const float *bias_dev, const float *rope_dev, uint32_t capacity, float *q_dev,
+                       float *k_cache_dev, float *v_cache_dev) {
+    TTL_REQUIRE(ctx && qkv_dev && bias_dev && rope_dev && q_dev && k_cache_dev && v_cache_dev, TTL_ERR_INVALID,
+                "ttl_qkv_rope_store: null argument");
+    TTL_REQUIRE(tokens <= 65535 && size_t(first_position) + tokens <= capacity, TTL_ERR_SHAPE,
+                "ttl_qkv_rope_store: positions past the capacity %u", capacity);
+    if (tokens == 0) {
+        return TTL_OK;
+    }
+    qkv_rope_store_kernel<<<dim3(kQkvRows / 256, tokens), 256, 0, ctx->stream>>>(
+        qkv_dev, first_position, bias_dev, reinterpret_cast<const float2 *>(rope_dev), q_dev, k_cache_dev, v_cache_dev);
+    TTL_LAUNCHED("qkv_rope_store_kernel");
+    return TTL_OK;
+}
+
+int ttl_rms_norm_rows(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev, float epsilon,
+                      float *out_dev) {
+    TTL_REQUIRE(ctx && x_dev && weight_dev && out_dev, TTL_ERR_INVALID, "ttl_rms_norm_rows: null argument");
+    TTL_REQUIRE(((uintptr_t)x_dev & 15) == 0 && ((uintptr_t)weight_dev & 15) == 0, TTL_ERR_INVALID,
+                "ttl_rms_norm_rows: x and weight must be 16-byte aligned");
+    TTL_REQUIRE(rows < (1u << 31), TTL_ERR_SHAPE, "ttl_rms_norm_rows: too many rows");
+    if (rows == 0) {
+        return TTL_OK;
+    }
+    rms_norm_rows_kernel<<<rows, 256, 0, ctx->stream>>>(x_dev, weight_dev, epsilon, out_dev);
+    TTL_LAUNCHED("rms_norm_rows_kernel");
+    return TTL_OK;
+}
+
+int ttl_add(ttl_ctx *ctx, const float *a_dev, const float *b_dev, size_t n, float *out_dev) {
+    TTL_REQUIRE(ctx && a_dev && b_dev && out_dev, TTL_ERR_INVALID, "ttl_add: null argument");
+    if (n == 0) {
+        return TTL_OK;
+    }
+    add_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>(a_dev, b_dev, n, out_dev);
+    TTL_LAUNCHED("add_kernel");
     return TTL_OK;
 }
 
