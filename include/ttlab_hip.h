@@ -353,12 +353,43 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
                          const float *sinks_dev, const int32_t *position_dev, uint32_t capacity, uint32_t layer_index,
                          float *workspace_dev, float *out_dev);
 
+/* attention_from_cache (model.cpp:255-290) for `tokens` tokens at positions
+ * first_position .. first_position + tokens - 1, as GptOssModel::prefill runs it per
+ * token (model.cpp:510-514): q_dev / out_dev f32 [tokens][4096]; the caches must hold
+ * every position up to the last token's.  workspace_dev holds
+ * ttl_attention_prefill_workspace_bytes(first_position, tokens). */
+size_t ttl_attention_prefill_workspace_bytes(uint32_t first_position, uint32_t tokens);
+int ttl_attention_prefill(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev, const float *v_cache_dev,
+                          const float *sinks_dev, uint32_t first_position, uint32_t tokens, uint32_t capacity,
+                          uint32_t layer_index, float *workspace_dev, size_t workspace_bytes, float *out_dev);
+
+/* ---- batched prefill helpers (GptOssModel::prefill, model.cpp:463-555) ------------- */
+
+/* rms_norm (tensor.cpp:568-580) of each of `rows` rows of 2880 (model.cpp:487-491,
+ * 524-526), in the decode kernels' summation order. */
+int ttl_rms_norm_rows(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev, float epsilon,
+                      float *out_dev);
+/* The bias, RoPE and KV-cache store of model.cpp:499-507 for `tokens` tokens at
+ * positions first_position .. : qkv_dev f32 [tokens][5120] is the output of
+ * ttl_matmul_q8_0 on a tensor in ttl_qkv_row_source order without its bias; bias_dev
+ * f32 [5120] in GGUF order (attn_q, attn_k, attn_v biases); rope_dev as for
+ * ttl_attn_qkv; q_dev f32 [tokens][4096]. */
+int ttl_qkv_rope_store(ttl_ctx *ctx, const float *qkv_dev, uint32_t tokens, uint32_t first_position,
+                       const float *bias_dev, const float *rope_dev, uint32_t capacity, float *q_dev,
+                       float *k_cache_dev, float *v_cache_dev);
+/* out = a + b elementwise over n floats (the residual adds of model.cpp:521-529,
+ * 545-551). */
+int ttl_add(ttl_ctx *ctx, const float *a_dev, const float *b_dev, size_t n, float *out_dev);
+
 /* ---- embedding, unembedding, greedy ------------------------------------------------ */
 
 /* load_token_embedding_q8_0 (tensor.cpp:171-184) for the token in token_dev; table_dev
  * holds the GGUF Q8_0 token_embd rows (vocab x 2880).  An out-of-range token gives NaNs. */
 int ttl_embedding_q8_0(ttl_ctx *ctx, const void *table_dev, uint32_t vocab, const int32_t *token_dev,
                        float *out_dev);
+/* The embeddings of `count` tokens (model.cpp:474-482): out_dev f32 [count][2880]. */
+int ttl_embedding_q8_0_batch(ttl_ctx *ctx, const void *table_dev, uint32_t vocab, const int32_t *tokens_dev,
+                             uint32_t count, float *out_dev);
 size_t ttl_logits_workspace_bytes(uint32_t vocab);
 /* logits = W in for a bf16 unembedding W [vocab][2880] (the synthetic configurations'
  * output.weight; the reference's is Q8_0, model.cpp:598-599), and per-group argmax

@@ -45,8 +45,17 @@ const char *ttlm_last_error(void);
 
 /* GptOssModel::forward (model.cpp:557-602): logits (host, f32 [vocab]) may be NULL. */
 int ttlm_forward(ttlm_model *model, int32_t token, uint32_t position, float *logits);
-/* GptOssModel::prefill (model.cpp:463-555) as consecutive decode steps: logits of the last token. */
+/* GptOssModel::prefill (model.cpp:463-555), layer-major on the device: per layer the
+ * batched Q8_0 matmuls (MFMA), RoPE and the KV store of every token, attention per
+ * token, and moe_batch (MFMA expert GEMMs); logits (host, f32 [vocab], may be NULL) of
+ * the last token.  Prompts longer than ttlm_prefill_batch() run in consecutive passes
+ * (a token's results do not depend on the cut).  Positions 0 .. count-1 are filled. */
 int ttlm_prefill(ttlm_model *model, const int32_t *tokens, uint32_t count, float *logits);
+/* Tokens per layer-major prefill pass. */
+uint32_t ttlm_prefill_batch(const ttlm_model *model);
+/* After a prefill: the inputs of `layer` (layer == layers: the final stream) of the
+ * last pass's first `count` tokens, f32 [count][2880] (host). */
+int ttlm_prefill_state(ttlm_model *model, uint32_t layer, uint32_t count, float *x_in);
 /* Greedy decode on the device: feeds token at position, then each step's argmax,
  * for `steps` steps; tokens (host, int32 [steps]) receives the chosen tokens. */
 int ttlm_generate(ttlm_model *model, int32_t token, uint32_t position, uint32_t steps, int32_t *tokens);

@@ -270,7 +270,9 @@ __global__ __launch_bounds__(kThreads) void embedding_kernel(const uint8_t *__re
                                                              const int32_t *__restrict__ token,
                                                              float *__restrict__ out) {
 #pragma clang fp contract(off)
-    const int32_t tok = *token;
+    // workgroup y embeds token[y] into out + y * 2880 (one token: y = 0)
+    const int32_t tok = token[blockIdx.y];
+    out += size_t(blockIdx.y) * kCols;
     const bool ok = tok >= 0 && uint32_t(tok) < vocab;
     const uint8_t *row = table + size_t(ok ? tok : 0) * (kCols / 32) * 34;
     for (uint32_t i = threadIdx.x; i < uint32_t(kCols); i += kThreads) {
@@ -351,6 +353,19 @@ int ttl_embedding_q8_0(ttl_ctx *ctx, const void *table_dev, uint32_t vocab, cons
                        float *out_dev) {
     TTL_REQUIRE(ctx && table_dev && token_dev && out_dev, TTL_ERR_INVALID, "ttl_embedding_q8_0: null argument");
     embedding_kernel<<<1, kThreads, 0, ctx->stream>>>((const uint8_t *)table_dev, vocab, token_dev, out_dev);
+    TTL_LAUNCHED("embedding_kernel");
+    return TTL_OK;
+}
+
+int ttl_embedding_q8_0_batch(ttl_ctx *ctx, const void *table_dev, uint32_t vocab, const int32_t *tokens_dev,
+                             uint32_t count, float *out_dev) {
+    TTL_REQUIRE(ctx && table_dev && tokens_dev && out_dev, TTL_ERR_INVALID, "ttl_embedding_q8_0_batch: null argument");
+    TTL_REQUIRE(count <= 65535, TTL_ERR_SHAPE, "ttl_embedding_q8_0_batch: at most 65535 tokens per call");
+    if (count == 0) {
+        return TTL_OK;
+    }
+    embedding_kernel<<<dim3(1, count), kThreads, 0, ctx->stream>>>((const uint8_t *)table_dev, vocab, tokens_dev,
+                                                                   out_dev);
     TTL_LAUNCHED("embedding_kernel");
     return TTL_OK;
 }

@@ -18,6 +18,7 @@ constexpr size_t kQueryWidth = HipGptOssModel::query_heads * HipGptOssModel::hea
 constexpr size_t kKvWidth = HipGptOssModel::kv_heads * HipGptOssModel::head_size;        // 512
 constexpr size_t kQkvRows = kQueryWidth + 2 * kKvWidth;                                  // 5120
 constexpr size_t kSlidingWindow = 128;                                                    // model.h:44
+constexpr size_t kPrefillBatch = 512;  // tokens per layer-major prefill pass
 constexpr size_t kQ8RowBytes2880 = 2880 / 32 * 34;
 constexpr size_t kQ8RowBytes4096 = 4096 / 32 * 34;
 constexpr size_t kMxfp4RowBytes = 2880 / 32 * 17;
@@ -130,6 +131,27 @@ void HipGptOssModel::finish_construction() {
         logits_ = static_cast<float *>(alloc(sizeof(float) * spec_.vocab));
         logits_workspace_ = alloc(ttl_logits_workspace_bytes(spec_.vocab));
         host_logits_.resize(spec_.vocab);
+
+        // layer-major prefill buffers for chunks of up to kPrefillBatch tokens
+        const size_t B = std::min<size_t>(kPrefillBatch, spec_.capacity);
+        prefill_batch_ = B;
+        prefill_tokens_ = static_cast<int32_t *>(alloc(sizeof(int32_t) * B));
+        x_seq_ = static_cast<float *>(alloc(sizeof(float) * (L + 1) * B * kHidden));
+        norm_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kHidden));
+        qkv_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kQkvRows));
+        q_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kQueryWidth));
+        attended_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kQueryWidth));
+        residual_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kHidden));
+        moe_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kHidden));
+        gemm_workspace_bytes_ = std::max(ttl_matmul_q8_0_workspace_bytes(uint32_t(B), 2880),
+                                         ttl_matmul_q8_0_workspace_bytes(uint32_t(B), 4096));
+        gemm_workspace_ = alloc(gemm_workspace_bytes_);
+        moe_workspace_bytes_ =
+            ttl_moe_prefill_batch_workspace_bytes(uint32_t(B), uint32_t(spec_.experts), uint32_t(kUsed));
+        moe_workspace_ = alloc(moe_workspace_bytes_);
+        attn_prefill_workspace_bytes_ =
+            ttl_attention_prefill_workspace_bytes(uint32_t(spec_.capacity - B), uint32_t(B));
+        attn_prefill_workspace_ = static_cast<float *>(alloc(attn_prefill_workspace_bytes_));
         check(ttl_sync(ctx_), "ttl_sync");
         record_step();
     }
@@ -362,6 +384,62 @@ const float *HipGptOssModel::forward(int32_t token, size_t position) {
     return host_logits_.data();
 }
 
+// One layer-major pass of GptOssModel::prefill (model.cpp:474-553) over the `count`
+// tokens already in prefill_tokens_, at positions first .. first + count - 1.  The
+// per-token results do not depend on how a prompt is cut into passes: each pass's
+// attention reads the earlier positions' keys and values from the caches.
+int HipGptOssModel::enqueue_prefill_chunk(size_t first, size_t count) {
+    const size_t L = spec_.layers, B = prefill_batch_;
+    const uint32_t n = uint32_t(count);
+    int status = ttl_embedding_q8_0_batch(ctx_, embedding_, spec_.vocab, prefill_tokens_, n, x_seq_);
+    for (size_t l = 0; l < L && status == TTL_OK; ++l) {
+        Layer &layer = layers_[l];
+        const float *x_in = x_seq_ + l * B * kHidden;
+        float *x_out = x_seq_ + (l + 1) * B * kHidden;
+        status = ttl_rms_norm_rows(ctx_, x_in, n, layer.attn_norm, norm_epsilon, norm_seq_);
+        if (status == TTL_OK) {
+            status = ttl_matmul_q8_0(ctx_, layer.qkv, nullptr, norm_seq_, n, nullptr, qkv_seq_, gemm_workspace_,
+                                     gemm_workspace_bytes_);
+        }
+        if (status == TTL_OK) {
+            status = ttl_qkv_rope_store(ctx_, qkv_seq_, n, uint32_t(first), layer.qkv_bias, rope_,
+                                        uint32_t(spec_.capacity), q_seq_, layer.key_cache, layer.value_cache);
+        }
+        if (status == TTL_OK) {
+            status = ttl_attention_prefill(ctx_, q_seq_, layer.key_cache, layer.value_cache, layer.sinks,
+                                           uint32_t(first), n, uint32_t(spec_.capacity), uint32_t(l),
+                                           attn_prefill_workspace_, attn_prefill_workspace_bytes_, attended_seq_);
+        }
+        if (status == TTL_OK) {
+            // model.cpp:519-529: output projection, then residual = x + projected
+            status = ttl_matmul_q8_0(ctx_, layer.attn_output, layer.attn_output_bias, attended_seq_, n, x_in,
+                                     residual_seq_, gemm_workspace_, gemm_workspace_bytes_);
+        }
+        if (status == TTL_OK) {
+            status = ttl_rms_norm_rows(ctx_, residual_seq_, n, layer.post_norm, norm_epsilon, norm_seq_);
+        }
+        if (status == TTL_OK) {
+            ttl_moe_layer moe = layer.moe;
+            moe.input_norm = nullptr;  // moe_batch receives the normalized sequence (model.cpp:531)
+            status = ttl_moe_prefill(ctx_, &moe, norm_seq_, n, moe_seq_, nullptr, nullptr, moe_workspace_,
+                                     moe_workspace_bytes_);
+        }
+        if (status == TTL_OK) {
+            status = ttl_add(ctx_, residual_seq_, moe_seq_, size_t(n) * kHidden, x_out);
+        }
+    }
+    if (status == TTL_OK) {
+        // model.cpp:555-559: the logits of the last token
+        ttl_stage_input f{};
+        f.base = x_seq_ + (L * B + count - 1) * kHidden;
+        f.norm_weight = output_norm_;
+        f.epsilon = norm_epsilon;
+        status = unembedding_q8_ ? ttl_logits_q8_0(ctx_, unembedding_q8_, spec_.vocab, &f, logits_, logits_workspace_)
+                                 : ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits_, logits_workspace_);
+    }
+    return status;
+}
+
 const float *HipGptOssModel::prefill(const int32_t *tokens, size_t count) {
     // model.cpp:464-472
     if (count == 0) {
@@ -376,12 +454,21 @@ const float *HipGptOssModel::prefill(const int32_t *tokens, size_t count) {
     for (size_t p = 0; p < count; ++p) {
         validate(tokens[p], p);
     }
-    for (size_t p = 0; p < count; ++p) {
-        set_position(tokens[p], p);
-        run_step();
+    for (size_t first = 0; first < count; first += prefill_batch_) {
+        const size_t n = std::min(prefill_batch_, count - first);
+        check(ttl_memcpy_h2d(ctx_, prefill_tokens_, tokens + first, sizeof(int32_t) * n), "ttl_memcpy_h2d");
+        check(enqueue_prefill_chunk(first, n), "prefill");
     }
     check(ttl_memcpy_d2h(ctx_, host_logits_.data(), logits_, sizeof(float) * spec_.vocab), "ttl_memcpy_d2h");
     return host_logits_.data();
+}
+
+void HipGptOssModel::prefill_state(size_t layer, size_t count, float *x_in) const {
+    if (layer > spec_.layers || count > prefill_batch_) {
+        throw std::runtime_error("prefill_state: layer or count out of range");
+    }
+    check(ttl_memcpy_d2h(ctx_, x_in, x_seq_ + layer * prefill_batch_ * kHidden, sizeof(float) * count * kHidden),
+          "ttl_memcpy_d2h");
 }
 
 int32_t HipGptOssModel::greedy(const float *logits) const {

@@ -112,6 +112,13 @@ class HipGptOssModel {
 
     // Last step's state, for layer-by-layer checks.
     void layer_state(size_t layer, float *x_in, float *residual, int32_t *indices, float *weights) const;
+    // The last prefill chunk's inputs of `layer` (layer == layers: the final stream),
+    // f32 [count][2880] for its first `count` tokens.
+    void prefill_state(size_t layer, size_t count, float *x_in) const;
+    // Tokens a prefill processes per layer-major pass (longer prompts run in chunks).
+    size_t prefill_batch() const {
+        return prefill_batch_;
+    }
     void final_state(float *x_final) const;
     void kv_cache(size_t layer, size_t positions, float *keys, float *values) const;
     size_t device_bytes() const {
@@ -143,6 +150,7 @@ class HipGptOssModel {
     void upload_gguf(const GgufFile &file);
     void finish_construction();
     int enqueue_step();
+    int enqueue_prefill_chunk(size_t first, size_t count);
     void record_step();
     void run_step();
     void set_position(int32_t token, size_t position);
@@ -170,6 +178,15 @@ class HipGptOssModel {
     ttl_graph *step_ = nullptr;
     bool use_graph_ = true;
     std::vector<float> host_logits_;
+    // layer-major prefill (model.cpp:463-555), chunks of prefill_batch_ tokens
+    size_t prefill_batch_ = 0;
+    int32_t *prefill_tokens_ = nullptr;
+    float *x_seq_ = nullptr;         // [layers + 1][batch][2880]
+    float *norm_seq_ = nullptr, *qkv_seq_ = nullptr, *q_seq_ = nullptr, *attended_seq_ = nullptr;
+    float *residual_seq_ = nullptr, *moe_seq_ = nullptr;
+    void *gemm_workspace_ = nullptr, *moe_workspace_ = nullptr;
+    float *attn_prefill_workspace_ = nullptr;
+    size_t gemm_workspace_bytes_ = 0, moe_workspace_bytes_ = 0, attn_prefill_workspace_bytes_ = 0;
 };
 
 }  // namespace ttlab

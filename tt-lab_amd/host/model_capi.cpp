@@ -111,6 +111,14 @@ int ttlm_prefill(ttlm_model *model, const int32_t *tokens, uint32_t count, float
     });
 }
 
+int ttlm_prefill_state(ttlm_model *model, uint32_t layer, uint32_t count, float *x_in) {
+    return guarded([&] { model->model->prefill_state(layer, count, x_in); });
+}
+
+uint32_t ttlm_prefill_batch(const ttlm_model *model) {
+    return uint32_t(model->model->prefill_batch());
+}
+
 int ttlm_generate(ttlm_model *model, int32_t token, uint32_t position, uint32_t steps, int32_t *tokens) {
     return guarded([&] {
         const std::vector<int32_t> out = model->model->generate(token, position, steps);

@@ -100,6 +100,8 @@ def load_model_library():
         "ttlm_kv_cache": (i32, [vp, u32, u32, vp, vp]),
         "ttlm_device_bytes": (C.c_size_t, [vp]),
         "ttlm_step_bytes": (C.c_double, [vp, u32]),
+        "ttlm_prefill_state": (i32, [vp, u32, u32, vp]),
+        "ttlm_prefill_batch": (u32, [vp]),
         "ttlm_gguf_inspect": (i32, [C.c_char_p, i32, C.POINTER(GgufInfo)]),
         "ttlm_create_from_gguf": (i32, [C.c_char_p, i32, u32, i32, C.POINTER(vp)]),
     }
@@ -169,6 +171,15 @@ class Model:
         out = np.empty(self.vocab, np.float32)
         _mcheck(self.lib.ttlm_prefill(self.h, t.ctypes.data, t.size, out.ctypes.data), "ttlm_prefill")
         return out
+
+    def prefill_state(self, layer, count):
+        out = np.empty(count * 2880, np.float32)
+        _mcheck(self.lib.ttlm_prefill_state(self.h, layer, count, out.ctypes.data), "ttlm_prefill_state")
+        return out.reshape(count, 2880)
+
+    @property
+    def prefill_batch(self):
+        return int(self.lib.ttlm_prefill_batch(self.h))
 
     def generate(self, token, position, steps):
         out = np.empty(steps, np.int32)
