@@ -26,6 +26,10 @@ distinct resident layers, value = token-layers/s.
 --workload prefill runs benchmark config 2: the batched prefill experts of one MoE
 layer for 512 bf16 tokens with balanced given routing (bf16 MFMA), value =
 token-layers/s; roofline on the larger of the gate/up and down GEMM launches.
+
+--workload model-prefill runs the full synthetic gpt-oss-20b model's layer-major
+prefill (GptOssModel::prefill) of a 512-token prompt, value = prompt tokens/s;
+roofline = the pass's algorithmic MFMA rate (2 x active weights x tokens).
 """
 import argparse
 import json
@@ -314,6 +318,50 @@ def gpu_prefill(args):
     }
 
 
+PROMPT_TOKENS = 512
+# Multiply-adds per token and layer of the prefill pass: 4 experts x 3 matrices of
+# 2880 x 2880, the Q/K/V (5120 x 2880) and output (2880 x 4096) projections, the router.
+PREFILL_MACS_PER_TOKEN_LAYER = USED * 3 * N * N + 5120 * N + N * 4096 + EXPERTS * N
+
+
+def gpu_model_prefill(args):
+    import numpy as np
+
+    import ttlab_amd
+
+    t0 = time.time()
+    model = ttlab_amd.Model(args.layers, args.experts, VOCAB, PROMPT_TOKENS + 16, SEED)
+    log(f"model resident: {model.device_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
+    tokens = [int(t) for t in np.random.default_rng(0x79000010).integers(0, VOCAB, PROMPT_TOKENS)]
+    for _ in range(max(1, min(args.warmup, 3))):
+        model.prefill(tokens)
+    reps = max(3, args.steps // 20)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        model.prefill(tokens)
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    model.close()
+    flop = 2.0 * PREFILL_MACS_PER_TOKEN_LAYER * PROMPT_TOKENS * args.layers
+    tflops = flop / (ms * 1e-3) / 1e12
+    log(f"prefill of {PROMPT_TOKENS} tokens: {ms:.2f} ms, {PROMPT_TOKENS / ms * 1e3:.0f} tok/s, "
+        f"{tflops:.0f} TFLOP/s algorithmic")
+    return {
+        "value": PROMPT_TOKENS / (ms * 1e-3),
+        "unit": "prompt tok/s",
+        "ms_per_step": ms,
+        "dtype": "bf16 MFMA, exact products (f32 activations as three bf16 planes), f32 accumulate",
+        "config": {"workload": f"full synthetic gpt-oss-{'20b' if args.config == 3 else '120b'} layer-major prefill "
+                               f"of a {PROMPT_TOKENS}-token prompt (GptOssModel::prefill); step = one prefill "
+                               "(host tokens in, last-token logits out)",
+                   "layers": args.layers, "experts": args.experts, "tokens": PROMPT_TOKENS,
+                   "algorithmic_TFLOP_per_step": round(flop / 1e12, 3)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "whole prefill pass (MoE and Q8_0 GEMMs, attention, norms)",
+                     "flop_per_step": flop},
+    }
+
+
 def cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
     """The oracle (restated reference CPU path) on one host core, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -352,6 +400,32 @@ def cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
                           f"matmuls) in {per_expert * 1e3:.0f} ms each, times 32 experts = one 512-token layer; "
                           f"oracle restatement of tensor.cpp:319-495 / model.cpp:378-460 (the matmul's token loop "
                           f"auto-vectorized, -O3 -ffp-contract=off -march=x86-64-v3)"}
+    if workload == "model-prefill":
+        from model_fixtures import HostModelLayer
+
+        # one sliding-window and one full layer (4 experts, all selected) of the oracle's
+        # layer-major prefill over a 32-token sample; a token costs the mean of the two
+        # per layer, times the model's layers
+        host_layers = [HostModelLayer(SEED, l, 4) for l in (0, 1)]
+        freqs = np.empty(32, np.float32)
+        O.lib.orc_rope_frequencies(freqs)
+        sample = 32
+        x = O.synth_normal(0x78000310, 0, sample * N)
+        out = np.empty(sample * N, np.float32)
+        kc, vc = np.zeros(sample * 512, np.float32), np.zeros(sample * 512, np.float32)
+        runs, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds or runs == 0:
+            for l in (0, 1):
+                s = host_layers[l].struct()
+                O.lib.orc_layer_prefill(C.byref(s), l, 0, sample, x, freqs, kc, vc, body, out, None)
+            runs += 1
+        per_token_layer = (time.perf_counter() - t0) / (runs * 2 * sample)
+        return {"value": round(1.0 / (per_token_layer * layers), 3), "unit": "prompt tok/s", "cores": 1,
+                "kind": "port",
+                "sample": f"{runs} x (one window + one full layer) of the oracle's prefill (model.cpp:484-553) over "
+                          f"{sample} tokens, {per_token_layer * 1e3:.2f} ms per token-layer, times {layers} layers; "
+                          f"MXFP4 {isa}, Q8_0 matmuls as the reference's C loops"}
+
     if workload == "moe":
         from moe_fixtures import HostLayer
 
@@ -410,7 +484,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "moe", "prefill"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "moe", "prefill", "model-prefill"], default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -450,7 +524,8 @@ def main():
         src.free()
         dst.free()
         dev.close()
-    runner = {"decode": gpu_decode, "moe": gpu_moe, "prefill": gpu_prefill}[args.workload]
+    runner = {"decode": gpu_decode, "moe": gpu_moe, "prefill": gpu_prefill,
+              "model-prefill": gpu_model_prefill}[args.workload]
     res = runner(args)
     base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.workload, args.layers, args.context)
     if base:
