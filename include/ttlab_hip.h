@@ -356,12 +356,11 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
 /* attention_from_cache (model.cpp:255-290) for `tokens` tokens at positions
  * first_position .. first_position + tokens - 1, as GptOssModel::prefill runs it per
  * token (model.cpp:510-514): q_dev / out_dev f32 [tokens][4096]; the caches must hold
- * every position up to the last token's.  workspace_dev holds
- * ttl_attention_prefill_workspace_bytes(first_position, tokens). */
-size_t ttl_attention_prefill_workspace_bytes(uint32_t first_position, uint32_t tokens);
+ * every position up to the last token's.  Needs no workspace: each workgroup takes 16
+ * tokens of one kv head and streams their positions through LDS with an online softmax. */
 int ttl_attention_prefill(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev, const float *v_cache_dev,
                           const float *sinks_dev, uint32_t first_position, uint32_t tokens, uint32_t capacity,
-                          uint32_t layer_index, float *workspace_dev, size_t workspace_bytes, float *out_dev);
+                          uint32_t layer_index, float *out_dev);
 
 /* ---- batched prefill helpers (GptOssModel::prefill, model.cpp:463-555) ------------- */
 

@@ -167,6 +167,47 @@ def test_attention_with_sinks_matches_oracle(dev, layer_index, position):
         b.free()
 
 
+# (first position, tokens): a prompt from 0 (ragged last block), one continued past the
+# window, one token, and a block boundary inside the window.
+@pytest.mark.parametrize("layer_index", [0, 1])
+@pytest.mark.parametrize("first,tokens", [(0, 200), (300, 37), (1023, 1), (113, 16)])
+def test_attention_prefill_matches_oracle_per_token(dev, layer_index, first, tokens):
+    """ttl_attention_prefill over a run of tokens against orc_attention of each token
+    (attention_from_cache as GptOssModel::prefill runs it per token, model.cpp:510-514)."""
+    capacity = 1088
+    last = first + tokens - 1
+    q = O.synth_normal(51, first, tokens * 4096, sigma=2.0)
+    k = O.synth_normal(52, first, capacity * 512, sigma=2.0)
+    v = O.synth_normal(53, first, capacity * 512)
+    sinks = O.synth_normal(54, 0, 64, sigma=2.0)
+    qb, kb, vb, sb = dev.upload(q), dev.upload(k), dev.upload(v), dev.upload(sinks)
+    out = dev.alloc(tokens * 4096 * 4)
+    dev.attention_prefill(qb, kb, vb, sb, first, tokens, capacity, layer_index, out)
+    got = out.download(np.float32).reshape(tokens, 4096)
+    ref = np.empty(4096, np.float32)
+    scores = np.empty(last + 1, np.float32)
+    worst = 0.0
+    for t in range(tokens):
+        O.lib.orc_attention(np.ascontiguousarray(q[t * 4096:(t + 1) * 4096]), k, v, sinks, layer_index, first + t,
+                            ref, scores)
+        worst = max(worst, O.rel_l2(got[t], ref))
+    print(f"attention prefill layer {layer_index} positions {first}..{last}: worst rel_l2 {worst:.2e}")
+    assert worst <= TOL
+    for b in (qb, kb, vb, sb, out):
+        b.free()
+
+
+def test_attention_prefill_rejects_bad_shapes(dev):
+    buf = dev.alloc(4096 * 4)
+    cache = dev.alloc(64 * 512 * 4)
+    with pytest.raises(ttlab_amd.TtlError, match="capacity"):
+        dev.attention_prefill(buf, cache, cache, buf, 60, 5, 64, 0, buf)
+    with pytest.raises(ttlab_amd.TtlError, match="capacity"):
+        dev.attention_prefill(buf, cache, cache, buf, 0, 0, 64, 0, buf)
+    buf.free()
+    cache.free()
+
+
 def test_logits_and_greedy_match_oracle(dev):
     vocab = 5003
     w = O.synth_bf16(51, 0, vocab * N)

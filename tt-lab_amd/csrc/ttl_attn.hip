@@ -321,6 +321,130 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
     }
 }
 
+// Prefill: a block of kPfTokens consecutive tokens of one kv head per workgroup --
+// the 8 query heads of the group times the block's tokens are 128 (token, head)
+// pairs, two threads each.  The union of the pairs' spans streams through LDS in
+// chunks of 64 positions, and each pair keeps an online softmax: m starts at the
+// sink and l at exp(sink - sink) = 1 (the sink enters the max and the denominator,
+// model.cpp:270-281), o at 0; per chunk m' = max(m, scores), l and o are rescaled by
+// exp(m - m') and take the chunk's exp(s - m') terms; the output is o / l.
+constexpr int kPfTokens = 16;
+constexpr int kPfPairs = kPfTokens * kGroup;  // 128
+constexpr int kPfThreads = 2 * kPfPairs;      // 256
+
+__global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(const float *__restrict__ q,
+                                                                  const float *__restrict__ k_cache,
+                                                                  const float *__restrict__ v_cache,
+                                                                  const float *__restrict__ sinks, uint32_t first,
+                                                                  uint32_t tokens, uint32_t layer_index,
+                                                                  float *__restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float ks[kChunk * kRowStride];
+    __shared__ __attribute__((aligned(16))) float vs[kChunk * kRowStride];
+    __shared__ float e[kPfPairs][kChunk + 1];
+    const uint32_t t = threadIdx.x, pair = t / 2, half = t % 2;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t local = blockIdx.x * kPfTokens + pair / kGroup;  // token of this pair
+    const uint32_t head = kvh * kGroup + pair % kGroup;
+    const bool live = local < tokens;
+    const uint32_t pos = first + (live ? local : tokens - 1);
+    const Span sp = span_of(pos, layer_index);
+    // the block's positions: from the first token's span start to the last token
+    const uint32_t last_local = min(blockIdx.x * kPfTokens + kPfTokens, tokens) - 1;
+    const uint32_t lo = span_of(first + blockIdx.x * kPfTokens, layer_index).first;
+    const uint32_t hi = first + last_local;
+
+    float qv[kHead];
+    {
+        const float4 *q4 = reinterpret_cast<const float4 *>(q + (size_t(live ? local : 0) * kQHeads + head) * kHead);
+#pragma unroll
+        for (int d = 0; d < kHead / 4; ++d) {
+            const float4 v = q4[d];
+            qv[4 * d] = v.x;
+            qv[4 * d + 1] = v.y;
+            qv[4 * d + 2] = v.z;
+            qv[4 * d + 3] = v.w;
+        }
+    }
+    const float sink = sinks[head];
+    float m = sink, l = 1.0f;
+    float o[kHead / 2];
+#pragma unroll
+    for (int d = 0; d < kHead / 2; ++d) {
+        o[d] = 0.0f;
+    }
+
+    constexpr int kPer = kChunk * (kHead / 4) / kPfThreads;  // 4 float4 of K and of V per thread
+    for (uint32_t c0 = lo - lo % kChunk; c0 <= hi; c0 += kChunk) {
+        __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t f = t + uint32_t(k) * kPfThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
+            const uint32_t at = min(c0 + p, hi);  // positions past the block's last re-read it
+            const size_t row = (size_t(at) * kKvHeads + kvh) * kHead;
+            *reinterpret_cast<float4 *>(ks + p * kRowStride + 4 * d4) = reinterpret_cast<const float4 *>(k_cache + row)[d4];
+            *reinterpret_cast<float4 *>(vs + p * kRowStride + 4 * d4) = reinterpret_cast<const float4 *>(v_cache + row)[d4];
+        }
+        __syncthreads();
+        // scores of positions half, half + 2, ... of the chunk (this pair's span only)
+        float cmax = -INFINITY;
+        for (uint32_t j = half; j < uint32_t(kChunk); j += 2) {
+            const uint32_t at = c0 + j;
+            float a = 0.0f;
+#pragma unroll
+            for (int d = 0; d < kHead / 4; ++d) {
+                const float4 kv = *reinterpret_cast<const float4 *>(ks + j * kRowStride + 4 * d);
+                a = fmaf(qv[4 * d], kv.x, a);
+                a = fmaf(qv[4 * d + 1], kv.y, a);
+                a = fmaf(qv[4 * d + 2], kv.z, a);
+                a = fmaf(qv[4 * d + 3], kv.w, a);
+            }
+            const bool in = at >= sp.first && at <= pos;
+            const float s = in ? a * 0.125f : -INFINITY;  // 1/sqrt(64), exact
+            e[pair][j] = s;
+            cmax = fmaxf(cmax, s);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 1));
+        const float m2 = fmaxf(m, cmax);
+        const float scale = expf(m - m2);
+        __syncthreads();  // both halves' scores are in e
+        // exp terms and this thread's half of the dimensions of o
+        float lsum = 0.0f;
+        float acc[kHead / 2];
+#pragma unroll
+        for (int d = 0; d < kHead / 2; ++d) {
+            acc[d] = 0.0f;
+        }
+        for (uint32_t j = 0; j < uint32_t(kChunk); ++j) {
+            const float s = e[pair][j];
+            const float x = s == -INFINITY ? 0.0f : expf(s - m2);
+            lsum += x;
+            const float *vrow = vs + j * kRowStride + half * (kHead / 2);
+#pragma unroll
+            for (int d = 0; d < kHead / 8; ++d) {
+                const float4 v = *reinterpret_cast<const float4 *>(vrow + 4 * d);
+                acc[4 * d] = fmaf(x, v.x, acc[4 * d]);
+                acc[4 * d + 1] = fmaf(x, v.y, acc[4 * d + 1]);
+                acc[4 * d + 2] = fmaf(x, v.z, acc[4 * d + 2]);
+                acc[4 * d + 3] = fmaf(x, v.w, acc[4 * d + 3]);
+            }
+        }
+        l = l * scale + lsum;
+#pragma unroll
+        for (int d = 0; d < kHead / 2; ++d) {
+            o[d] = o[d] * scale + acc[d];
+        }
+        m = m2;
+    }
+    if (!live) {
+        return;
+    }
+    float *dst = out + (size_t(local) * kQHeads + head) * kHead + half * (kHead / 2);
+#pragma unroll
+    for (int d = 0; d < kHead / 2; ++d) {
+        dst[d] = o[d] / l;
+    }
+}
+
 }  // namespace
 
 namespace ttl {
@@ -352,9 +476,6 @@ void launch_attention(ttl_ctx *ctx, const float *q, const float *k_cache, const 
                                                                           layer_index, max_chunks, out);
 }
 
-size_t prefill_chunks(uint32_t first_position, uint32_t tokens) {
-    return (size_t(first_position) + tokens + kChunk - 1) / kChunk;
-}
 
 }  // namespace
 
@@ -380,30 +501,22 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
     return TTL_OK;
 }
 
-size_t ttl_attention_prefill_workspace_bytes(uint32_t first_position, uint32_t tokens) {
-    return size_t(tokens) * kQHeads * prefill_chunks(first_position, tokens) * (kHead + 2) * sizeof(float);
-}
 
 int ttl_attention_prefill(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev, const float *v_cache_dev,
                           const float *sinks_dev, uint32_t first_position, uint32_t tokens, uint32_t capacity,
-                          uint32_t layer_index, float *workspace_dev, size_t workspace_bytes, float *out_dev) {
-    TTL_REQUIRE(ctx && q_dev && k_cache_dev && v_cache_dev && sinks_dev && workspace_dev && out_dev, TTL_ERR_INVALID,
+                          uint32_t layer_index, float *out_dev) {
+    TTL_REQUIRE(ctx && q_dev && k_cache_dev && v_cache_dev && sinks_dev && out_dev, TTL_ERR_INVALID,
                 "ttl_attention_prefill: null argument");
     TTL_REQUIRE(capacity > 0 && capacity <= uint32_t(kMaxCombineChunks * kChunk), TTL_ERR_SHAPE,
                 "ttl_attention_prefill: capacity must be 1..%d", kMaxCombineChunks * kChunk);
     TTL_REQUIRE(tokens > 0 && tokens <= 65535 && size_t(first_position) + tokens <= capacity, TTL_ERR_SHAPE,
                 "ttl_attention_prefill: positions %u..%u do not fit the capacity %u", first_position,
                 first_position + tokens - 1, capacity);
-    TTL_REQUIRE(workspace_bytes >= ttl_attention_prefill_workspace_bytes(first_position, tokens), TTL_ERR_SHAPE,
-                "ttl_attention_prefill: workspace of %zu bytes, %zu needed", workspace_bytes,
-                ttl_attention_prefill_workspace_bytes(first_position, tokens));
     TTL_REQUIRE(((uintptr_t)q_dev & 15) == 0 && ((uintptr_t)k_cache_dev & 15) == 0 && ((uintptr_t)v_cache_dev & 15) == 0,
                 TTL_ERR_INVALID, "ttl_attention_prefill: q, k and v must be 16-byte aligned");
-    const uint32_t chunks = uint32_t(prefill_chunks(first_position, tokens));
-    const Tokens ts{nullptr, first_position, uint32_t(kQHeads * kHead), uint32_t(kQHeads * chunks * (kHead + 2))};
-    launch_attention(ctx, q_dev, k_cache_dev, v_cache_dev, sinks_dev, ts, tokens, capacity, layer_index, chunks,
-                     workspace_dev, out_dev);
-    TTL_LAUNCHED("attention kernels");
+    attn_prefill_kernel<<<dim3((tokens + kPfTokens - 1) / kPfTokens, kKvHeads), kPfThreads, 0, ctx->stream>>>(
+        q_dev, k_cache_dev, v_cache_dev, sinks_dev, first_position, tokens, layer_index, out_dev);
+    TTL_LAUNCHED("attn_prefill_kernel");
     return TTL_OK;
 }
 

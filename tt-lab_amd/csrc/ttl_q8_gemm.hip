@@ -33,8 +33,13 @@ constexpr int kSub = 4;  // 16-token sub-tiles per 64-token tile
 constexpr int kTileTokens = 16 * kSub;
 constexpr int kStageSteps = 2;  // K steps per LDS stage
 constexpr int kWaves = 4;
-constexpr int kRowTiles = 3;  // 16-row weight tiles per wave
-constexpr int kGroupTiles = kWaves * kRowTiles;
+// 16-row weight tiles per wave: one.  The projections have 2880 and 5120 rows, so more
+// tiles per workgroup leave CUs idle at a 512-token prompt (measured: one tile per wave
+// beat two and three in the layer-major prefill).
+template <int K>
+constexpr int row_tiles_for() {
+    return 1;
+}
 constexpr int kLook = 4;  // token fragments read from LDS this many ahead
 
 template <int K>
@@ -109,13 +114,14 @@ struct GemmArgs {
     uint32_t rows, row_tiles, tokens;
 };
 
-// One workgroup: a 64-token tile x kGroupTiles weight-row tiles; wave w takes row
-// tiles (group * 4 + w) * 3 + j.  Token fragments go through LDS in stages of two K
+// One workgroup: a 64-token tile x 4 * kRowTiles weight-row tiles; wave w takes row
+// tiles (group * 4 + w) * kRowTiles + j.  Token fragments go through LDS in stages of two K
 // steps (double-buffered); each wave's weight codes and scales are requested one
 // quad (4 steps) ahead.
 template <int K>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void q8_gemm_kernel(GemmArgs a) {
     using S = Shape<K>;
+    constexpr int kRowTiles = row_tiles_for<K>();
     constexpr int kThreads = kWaves * 64;
     constexpr int kPer = S::stage_chunks / kThreads;
     static_assert(S::stage_chunks % kThreads == 0, "the stager moves whole pieces");
@@ -326,7 +332,8 @@ int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
     a.rows = w->rows;
     a.row_tiles = w->tiles;
     a.tokens = tokens;
-    const dim3 grid((w->tiles + kGroupTiles - 1) / kGroupTiles, tiles);
+    const uint32_t group = uint32_t(kWaves * (w->cols == 2880 ? row_tiles_for<2880>() : row_tiles_for<4096>()));
+    const dim3 grid((w->tiles + group - 1) / group, tiles);
     uint8_t *frags = static_cast<uint8_t *>(workspace_dev);
     if (w->cols == 2880) {
         q8_gather_kernel<2880><<<dim3(Shape<2880>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, frags);

@@ -149,9 +149,6 @@ void HipGptOssModel::finish_construction() {
         moe_workspace_bytes_ =
             ttl_moe_prefill_batch_workspace_bytes(uint32_t(B), uint32_t(spec_.experts), uint32_t(kUsed));
         moe_workspace_ = alloc(moe_workspace_bytes_);
-        attn_prefill_workspace_bytes_ =
-            ttl_attention_prefill_workspace_bytes(uint32_t(spec_.capacity - B), uint32_t(B));
-        attn_prefill_workspace_ = static_cast<float *>(alloc(attn_prefill_workspace_bytes_));
         check(ttl_sync(ctx_), "ttl_sync");
         record_step();
     }
@@ -407,8 +404,7 @@ int HipGptOssModel::enqueue_prefill_chunk(size_t first, size_t count) {
         }
         if (status == TTL_OK) {
             status = ttl_attention_prefill(ctx_, q_seq_, layer.key_cache, layer.value_cache, layer.sinks,
-                                           uint32_t(first), n, uint32_t(spec_.capacity), uint32_t(l),
-                                           attn_prefill_workspace_, attn_prefill_workspace_bytes_, attended_seq_);
+                                           uint32_t(first), n, uint32_t(spec_.capacity), uint32_t(l), attended_seq_);
         }
         if (status == TTL_OK) {
             // model.cpp:519-529: output projection, then residual = x + projected

@@ -185,8 +185,7 @@ class HipGptOssModel {
     float *norm_seq_ = nullptr, *qkv_seq_ = nullptr, *q_seq_ = nullptr, *attended_seq_ = nullptr;
     float *residual_seq_ = nullptr, *moe_seq_ = nullptr;
     void *gemm_workspace_ = nullptr, *moe_workspace_ = nullptr;
-    float *attn_prefill_workspace_ = nullptr;
-    size_t gemm_workspace_bytes_ = 0, moe_workspace_bytes_ = 0, attn_prefill_workspace_bytes_ = 0;
+    size_t gemm_workspace_bytes_ = 0, moe_workspace_bytes_ = 0;
 };
 
 }  // namespace ttlab
