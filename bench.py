@@ -50,7 +50,7 @@ SEED = 0x77000003
 GATEUP_BYTES = USED * 2 * N * 1530 + USED * 2 * N * 4 + N * 4 + USED * N * 4
 # HBM bytes one gate/up launch moves, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE
 # (scaled on a 256 MiB copy): profiles/decode_cfg3_hbm_bytes.txt.
-GATEUP_TRAFFIC_BYTES = 35_889_000
+GATEUP_TRAFFIC_BYTES = 35_904_000
 
 
 def log(msg):
