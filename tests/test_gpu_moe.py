@@ -46,7 +46,9 @@ def run_router(dev, wbuf, bbuf, experts, x, k, force_exact=False):
     return out
 
 
-@pytest.mark.parametrize("experts", [32, 128])
+# 7, 32, 128, 192: the exact path's workgroup tiles hold 2, 8 and 12 float4 pieces per
+# thread (at most 32, 128 and 192 rows)
+@pytest.mark.parametrize("experts", [7, 32, 128, 192])
 def test_router_fast_and_exact_paths_match_reference(dev, experts):
     w = O.synth_normal_bf16(0x77000009, 20, experts * N, 0.02)
     b = O.synth_normal(0x77000009, 21, experts, sigma=0.05)

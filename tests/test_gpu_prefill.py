@@ -292,6 +292,36 @@ def test_moe_prefill_config2_router(dev):
         device.free()
 
 
+def test_moe_prefill_router_exact_path_in_a_batch(dev):
+    """Router rows 3, 5 and 9 are identical and lead, so every token's logits tie exactly
+    and every token of the batch takes the exact path (the reference's sequential sums
+    and selection sort); a few tokens without the tie take the certified path.  Indices
+    equal the oracle's for every token, weights to f32 rounding."""
+    count = 40
+    host = HostLayer(32, 4, biases=False, seed=0x7700000C, fill_experts=[])  # no bias: the rows tie
+    x0 = O.synth_normal(0x78000005, 0, N)
+    x = (x0[None, :] + np.float32(0.25) * O.synth_normal(0x78000005, 1, count * N).reshape(count, N))
+    x = x.astype(np.float32)
+    w = host.router_w.reshape(32, N).copy()
+    lead = np.sign(x0).astype(np.float32) * np.float32(0.05)
+    for r in (3, 5, 9):
+        w[r] = lead
+    for p in (7, 21):  # these tokens' inputs flip the lead rows' sign: no tie at the top
+        x[p] = -x[p]
+    host.router_w = np.ascontiguousarray(w.ravel())
+    device = DeviceLayer(dev, host)
+    try:
+        _, idx, wts = run_moe_prefill(dev, device, x)
+        logits, ref_idx, ref_w = oracle_routing(host, x)
+        for p in range(count):
+            assert list(idx[p]) == list(ref_idx[p]), (p, idx[p], ref_idx[p])
+            if p not in (7, 21):
+                assert list(idx[p][:3]) == [3, 5, 9], p
+        assert np.allclose(wts, ref_w, rtol=1e-5, atol=1e-7)
+    finally:
+        device.free()
+
+
 def test_moe_prefill_zero_tokens_and_input_norm(dev, layer8):
     host, device = layer8
     out, xb = dev.alloc(256), dev.alloc(256)

@@ -23,6 +23,7 @@
 #include "ttl_stage.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace {
 
@@ -267,74 +268,15 @@ __device__ void route_certified(uint32_t experts, uint32_t k, bool force_exact, 
     }
 }
 
-// CHUNKED: the sequential sums taken 16 columns at a time (faster, more registers;
-// the standalone selection kernel).  Both give the same bits.
-template <bool CHUNKED>
-__device__ void route_exact(const float *__restrict__ weight, const float *__restrict__ bias, uint32_t experts,
-                            uint32_t k, const float *xs, RouterScratch *scratch, RouteLds &lds,
-                            float *__restrict__ logits) {
+// The reference's selection sort (model.cpp:296-309) replayed on lds.ref_logits, then
+// the softmax of the selected logits.  Wave 0 only; ends with a barrier.
+__device__ __forceinline__ void replay_selection(uint32_t experts, uint32_t k, RouterScratch *scratch, RouteLds &lds,
+                                 bool count_exact) {
     const uint32_t t = threadIdx.x, lane = t % 64;
-    if (t < experts && !CHUNKED) {
-#pragma clang fp contract(off)
-        const float *w = weight + size_t(t) * kRouterCols;
-        float sum = bias[t];
-        for (int c = 0; c < kRouterCols; ++c) {
-            sum = sum + w[c] * xs[(c / 32) * mxt::x_stride + c % 32];
-        }
-        lds.ref_logits[t] = sum;
-        lds.order[t] = int32_t(t);
-        if (logits) {
-            logits[t] = sum;
-        }
-    }
-    if (t < experts && CHUNKED) {
-#pragma clang fp contract(off)
-        // sum = bias, then sum = sum + w[c] * x[c] for c = 0..2879 in order.  Taken 16
-        // columns at a time: the next chunk's weights are requested ahead and a
-        // chunk's products (each rounded, as the reference's) formed before its adds,
-        // so only the sequential adds wait on each other.
-        constexpr int kChunk = 16, kChunks = kRouterCols / kChunk;
-        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(t) * kRouterCols);
-        float sum = bias[t];
-        float4 next[kChunk / 4];
-#pragma unroll
-        for (int q = 0; q < kChunk / 4; ++q) {
-            next[q] = w4[q];
-        }
-        for (int b = 0; b < kChunks; ++b) {
-            float4 cur[kChunk / 4];
-#pragma unroll
-            for (int q = 0; q < kChunk / 4; ++q) {
-                cur[q] = next[q];
-                next[q] = w4[min(b + 1, kChunks - 1) * (kChunk / 4) + q];
-            }
-            const int c0 = b * kChunk;
-            const float4 *x4 = reinterpret_cast<const float4 *>(xs + (c0 / 32) * mxt::x_stride + c0 % 32);
-            float prod[kChunk];
-#pragma unroll
-            for (int q = 0; q < kChunk / 4; ++q) {
-                const float4 x = x4[q];
-                prod[4 * q + 0] = cur[q].x * x.x;
-                prod[4 * q + 1] = cur[q].y * x.y;
-                prod[4 * q + 2] = cur[q].z * x.z;
-                prod[4 * q + 3] = cur[q].w * x.w;
-            }
-#pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                sum = sum + prod[j];
-            }
-        }
-        lds.ref_logits[t] = sum;
-        lds.order[t] = int32_t(t);
-        if (logits) {
-            logits[t] = sum;
-        }
-    }
-    __syncthreads();
     if (t < 64) {
-        // model.cpp:296-309, one step per rank: best starts at position i and moves to
-        // j only if value[j] > value[best].  So best stays at i when value[order[i]] is
-        // NaN, and otherwise is the first position >= i holding the largest non-NaN value.
+        // one step per rank: best starts at position i and moves to j only if
+        // value[j] > value[best].  So best stays at i when value[order[i]] is NaN, and
+        // otherwise is the first position >= i holding the largest non-NaN value.
         for (uint32_t i = 0; i < k; ++i) {
             const bool start_nan = isnan(lds.ref_logits[lds.order[i]]);
             double m = -INFINITY;
@@ -380,7 +322,7 @@ __device__ void route_exact(const float *__restrict__ weight, const float *__res
                 lds.selected[r] = lds.ref_logits[lds.indices[r]];
             }
             softmax_selected(lds.selected, k, lds.weights);
-            if (logits) {
+            if (count_exact) {
                 scratch->exact_path_count += 1;
             }
         }
@@ -388,22 +330,118 @@ __device__ void route_exact(const float *__restrict__ weight, const float *__res
     __syncthreads();
 }
 
-template <int MODE, int NT>
+// The exact path inside the routed gate/up kernel: thread t < experts forms row t's
+// logit in the reference's order, sum = bias, then sum = sum + w[c] * x[c] for c =
+// 0..2879 (tensor.cpp:186-200), from the staged router input xs.  Few registers, so
+// the gate/up kernel keeps its occupancy; it runs for about 0.4% of decode tokens.
+__device__ void route_exact_serial(const float *__restrict__ weight, const float *__restrict__ bias,
+                                   uint32_t experts, uint32_t k, const float *xs, RouterScratch *scratch,
+                                   RouteLds &lds, float *__restrict__ logits) {
+    const uint32_t t = threadIdx.x;
+    if (t < experts) {
+#pragma clang fp contract(off)
+        const float *w = weight + size_t(t) * kRouterCols;
+        float sum = bias[t];
+        for (int c = 0; c < kRouterCols; ++c) {
+            sum = sum + w[c] * xs[(c / 32) * mxt::x_stride + c % 32];
+        }
+        lds.ref_logits[t] = sum;
+        lds.order[t] = int32_t(t);
+        if (logits) {
+            logits[t] = sum;
+        }
+    }
+    __syncthreads();
+    replay_selection(experts, k, scratch, lds, logits != nullptr);
+}
+
+// The exact path of the standalone selection (a batch can hold many tokens and one
+// uncertain token holds the whole launch, so its latency matters): the same sums, but
+// the workgroup forms the products w[c] * x[c] (each rounded to f32, as the
+// reference's) 64 columns at a time into LDS, every thread a few float4 pieces loaded
+// one tile ahead, and thread t < experts only adds its row's products in column order.
+constexpr int kProdCols = 64;
+constexpr int kProdStride = kProdCols + 1;  // the adders read down a column: no bank conflicts
+constexpr int kProdTiles = kRouterCols / kProdCols;
+
+// float4 pieces per thread of a 256-thread workgroup: experts * 16 pieces per tile
+template <int PER>
+__device__ __forceinline__ void route_exact_coop(const float *__restrict__ weight, const float *__restrict__ bias,
+                                 uint32_t experts, uint32_t k, const float *xs, RouterScratch *scratch,
+                                 RouteLds &lds, float *__restrict__ logits, float *prod) {
+    static_assert(kRouterCols % kProdCols == 0, "whole tiles");
+    const uint32_t t = threadIdx.x;
+    const uint32_t pieces = experts * (kProdCols / 4);
+    // piece i of a tile: expert i / 16, columns 4 (i % 16) .. + 3; pieces past the
+    // tile's last re-read the last one (all loads unconditional) and are not stored
+    auto piece = [&](int i) __attribute__((always_inline)) { return min(t + 256u * uint32_t(i), pieces - 1); };
+    auto load = [&](int tile, float4(&r)[PER]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const uint32_t e = piece(i) / 16, c = uint32_t(tile) * kProdCols + 4 * (piece(i) % 16);
+            r[i] = *reinterpret_cast<const float4 *>(weight + size_t(e) * kRouterCols + c);
+        }
+    };
+    float4 wv[PER];
+    load(0, wv);
+    float sum = t < experts ? bias[t] : 0.0f;
+#pragma unroll 1
+    for (int tile = 0; tile < kProdTiles; ++tile) {
+        __syncthreads();  // the adders are done with the previous tile
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+#pragma clang fp contract(off)
+            const uint32_t e = piece(i) / 16, c4 = 4 * (piece(i) % 16);
+            const uint32_t c = uint32_t(tile) * kProdCols + c4;
+            const float4 x = *reinterpret_cast<const float4 *>(xs + (c / 32) * mxt::x_stride + c % 32);
+            if (t + 256u * uint32_t(i) < pieces) {
+                float *dst = prod + e * kProdStride + c4;
+                dst[0] = wv[i].x * x.x;
+                dst[1] = wv[i].y * x.y;
+                dst[2] = wv[i].z * x.z;
+                dst[3] = wv[i].w * x.w;
+            }
+        }
+        if (tile + 1 < kProdTiles) {
+            load(tile + 1, wv);
+        }
+        __syncthreads();
+        if (t < experts) {
+#pragma clang fp contract(off)
+            const float *row = prod + t * kProdStride;
+#pragma unroll 16
+            for (int c = 0; c < kProdCols; ++c) {
+                sum = sum + row[c];
+            }
+        }
+    }
+    if (t < experts) {
+        lds.ref_logits[t] = sum;
+        lds.order[t] = int32_t(t);
+        if (logits) {
+            logits[t] = sum;
+        }
+    }
+    __syncthreads();
+    replay_selection(experts, k, scratch, lds, logits != nullptr);
+}
+
+template <int MODE, int PER>
 __device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
-                                float *red) {
+                                float *red, float *prod) {
     route_certified(experts, k, force_exact, scratch, lds, logits, true);
     if (!lds.certified) {
-        stage::stage<kRouterCols, mxt::x_blocks, NT, MODE>(in, xs, red);
-        route_exact<true>(weight, bias, experts, k, xs, scratch, lds, logits);
+        stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
+        route_exact_coop<PER>(weight, bias, experts, k, xs, scratch, lds, logits, prod);
     }
 }
 
 // Standalone routing (ttl_router_topk): one workgroup per token, publishes
 // everything.  Workgroup t of a batch routes token t: input in.base + t * x_stride,
 // scratch[t], outputs indices/weights_out + t * k (logits only for one token).
-template <int MODE>
+template <int MODE, int PER>
 __global__ __launch_bounds__(256) void router_select_kernel(const float *__restrict__ weight,
                                                             const float *__restrict__ bias, uint32_t experts,
                                                             stage::Input in, uint32_t k, uint32_t force_exact,
@@ -417,7 +455,9 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
     weights_out += size_t(blockIdx.x) * k;
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    route_workgroup<MODE, 256>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red);
+    __shared__ float prod[PER * 256 / (kProdCols / 4) * kProdStride];  // [experts][kProdStride]
+    route_workgroup<MODE, PER>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red,
+                               prod);
     if (threadIdx.x < k) {
         indices[threadIdx.x] = lds.indices[threadIdx.x];
         weights_out[threadIdx.x] = lds.weights[threadIdx.x];
@@ -487,7 +527,7 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
         if (!rl.certified) {
             // rare: the exact path needs the staged input first
             stage::stage_finish(a.in, pending, xs, red);
-            route_exact<false>(a.router_weight, a.router_bias, a.experts, a.k, xs, a.scratch, rl, logits);
+            route_exact_serial(a.router_weight, a.router_bias, a.experts, a.k, xs, a.scratch, rl, logits);
             staged = true;
         }
         e = rl.indices[slot];
@@ -723,6 +763,19 @@ stage::Input layer_input(const ttl_moe_layer &L, const float *x) {
     return in;
 }
 
+// Calls f(std::integral_constant<int, PER>) with the exact path's float4 pieces per
+// thread for `experts` rows (experts * 16 pieces per 64-column tile, 256 threads).
+template <typename F>
+void with_pieces(uint32_t experts, F &&f) {
+    if (experts <= 32) {
+        f(std::integral_constant<int, 2>{});
+    } else if (experts <= 128) {
+        f(std::integral_constant<int, 8>{});
+    } else {
+        f(std::integral_constant<int, 12>{});
+    }
+}
+
 // Router + top-k + softmax: the exact rows and their bounds (one workgroup per
 // expert), then the certified selection (one workgroup), which publishes indices,
 // weights and logits.
@@ -732,8 +785,10 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
     stage::with_mode(in, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
         router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch, 0u);
-        router_select_kernel<M><<<1, 256, 0, ctx->stream>>>(weight, bias, experts, in, k, force_exact ? 1u : 0u,
-                                                            scratch, logits, indices, weights, 0u);
+        with_pieces(experts, [&](auto per) {
+            router_select_kernel<M, decltype(per)::value><<<1, 256, 0, ctx->stream>>>(
+                weight, bias, experts, in, k, force_exact ? 1u : 0u, scratch, logits, indices, weights, 0u);
+        });
     });
 }
 
@@ -773,8 +828,10 @@ int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, ui
         router_rows_kernel<M><<<dim3(L.experts, count), kRouterThreads, 0, ctx->stream>>>(L.router_weight,
                                                                                           L.router_bias, in, s,
                                                                                           L.hidden);
-        router_select_kernel<M><<<count, 256, 0, ctx->stream>>>(L.router_weight, L.router_bias, L.experts, in,
-                                                                L.used, 0u, s, nullptr, indices, weights, L.hidden);
+        with_pieces(L.experts, [&](auto per) {
+            router_select_kernel<M, decltype(per)::value><<<count, 256, 0, ctx->stream>>>(
+                L.router_weight, L.router_bias, L.experts, in, L.used, 0u, s, nullptr, indices, weights, L.hidden);
+        });
     });
     TTL_LAUNCHED("moe_batch router kernels");
     return TTL_OK;

@@ -179,12 +179,19 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
         }
     };
 
-    f32x4 acc[kSub][kRowTiles];
+    // acc: the scaled sum so far.  The MFMAs of a K step go to cur; the scale FMAs of
+    // a step run one step later, from pend (the previous step's sums) and pend_d, so the
+    // VALU never waits on an MFMA result that was just issued.
+    f32x4 acc[kSub][kRowTiles], cur[kSub][kRowTiles], pend[kSub][kRowTiles];
+    float dcur[kRowTiles], pend_d[kRowTiles];
 #pragma unroll
-    for (int m = 0; m < kSub; ++m) {
+    for (int j = 0; j < kRowTiles; ++j) {
+        dcur[j] = 0.0f;
+        pend_d[j] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kRowTiles; ++j) {
+        for (int m = 0; m < kSub; ++m) {
             acc[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            pend[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
 
@@ -201,9 +208,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
         for (int h = 0; h < 4 / kStageSteps; ++h) {
             const int stage = 2 * q + h;
             const mf::u32x4 *buf = lds[stage % 2];
-            constexpr int SF = S::stage_frags;  // fragments per stage, order (step, sub, plane)
+            constexpr int SF = S::stage_frags;
+            // fragment order within a stage: step, plane, sub-tile (the four sub-tiles'
+            // MFMAs are independent, so consecutive MFMAs never wait on each other)
             auto frag = [&](int f) __attribute__((always_inline)) {
-                const int ls = f / (kSub * kPlanes), m = (f / kPlanes) % kSub, p = f % kPlanes;
+                const int ls = f / (kSub * kPlanes), p = (f / kSub) % kPlanes, m = f % kSub;
                 return mf::as_bf16x8v(buf[((p * kStageSteps + ls) * kSub + m) * 64 + lane]);
             };
             bf16x8 ring[kLook];
@@ -212,36 +221,37 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
                 ring[d] = frag(d);
             }
             bf16x8 w[kRowTiles];
-            float d[kRowTiles];
-            f32x4 part[kRowTiles];
 #pragma unroll
             for (int f = 0; f < SF; ++f) {
                 const bf16x8 av = ring[f % kLook];
                 if (f + kLook < SF) {
                     ring[f % kLook] = frag(f + kLook);
                 }
-                const int ls = f / (kSub * kPlanes), m = (f / kPlanes) % kSub, p = f % kPlanes;
+                const int ls = f / (kSub * kPlanes), p = (f / kSub) % kPlanes, m = f % kSub;
                 const int k = h * kStageSteps + ls;  // step within the quad
                 if (f % (kSub * kPlanes) == 0) {
 #pragma unroll
                     for (int j = 0; j < kRowTiles; ++j) {
                         w[j] = int8_bf16(c[j][k]);
                         const uint32_t word = k < 2 ? s[j].x : s[j].y;
-                        d[j] = __half2float(__ushort_as_half(uint16_t(word >> (16 * (k % 2)))));
+                        pend_d[j] = dcur[j];
+                        dcur[j] = __half2float(__ushort_as_half(uint16_t(word >> (16 * (k % 2)))));
                     }
                 }
 #pragma unroll
                 for (int j = 0; j < kRowTiles; ++j) {
-                    part[j] = mf::mfma(av, w[j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : part[j]);
+                    cur[m][j] = mf::mfma(av, w[j], p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : cur[m][j]);
                     if (p == kPlanes - 1) {
+                        // the previous step's block sum, scaled by its fp16 d
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            acc[m][j][e] = fmaf(d[j], part[j][e], acc[m][j][e]);
+                            acc[m][j][e] = fmaf(pend_d[j], pend[m][j][e], acc[m][j][e]);
                         }
                         // an empty statement that takes the sum in registers here: the
                         // compiler otherwise sinks these updates below the stage's MFMAs
                         // and keeps every block product live
                         asm volatile("" : "+v"(acc[m][j]));
+                        pend[m][j] = cur[m][j];
                     }
                 }
                 // keep the ring's order: without this the scheduler hoists every LDS
@@ -266,6 +276,17 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
         if (q + 1 < S::quads) {
             load_quad(min(q + 2, S::quads - 1), qc[0], qs[0]);
             compute_quad(q + 1, qc[1], qs[1]);
+        }
+    }
+    // the last step's sums
+#pragma unroll
+    for (int j = 0; j < kRowTiles; ++j) {
+#pragma unroll
+        for (int m = 0; m < kSub; ++m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[m][j][e] = fmaf(dcur[j], pend[m][j][e], acc[m][j][e]);
+            }
         }
     }
 
