@@ -358,60 +358,71 @@ __device__ void route_exact_serial(const float *__restrict__ weight, const float
 // The exact path of the standalone selection (a batch can hold many tokens and one
 // uncertain token holds the whole launch, so its latency matters): the same sums, but
 // the workgroup forms the products w[c] * x[c] (each rounded to f32, as the
-// reference's) 64 columns at a time into LDS, every thread a few float4 pieces loaded
-// one tile ahead, and thread t < experts only adds its row's products in column order.
-constexpr int kProdCols = 64;
-constexpr int kProdStride = kProdCols + 1;  // the adders read down a column: no bank conflicts
+// reference's) 60 columns at a time into LDS, and thread t < experts only adds its
+// row's products in column order.  Every thread holds a few float4 pieces of each
+// tile, loaded kAhead tiles before their products are formed (the router rows come
+// from L2 or the MALL, about a microsecond away).
+constexpr int kProdCols = 60;
+constexpr int kProdPieces = kProdCols / 4;  // float4 pieces of one row's tile
+constexpr int kProdStride = kProdCols + 1;  // odd: the adders read down a column without bank conflicts
 constexpr int kProdTiles = kRouterCols / kProdCols;
 
-// float4 pieces per thread of a 256-thread workgroup: experts * 16 pieces per tile
+// PER: float4 pieces per thread of a 256-thread workgroup (experts * 15 per tile)
 template <int PER>
 __device__ __forceinline__ void route_exact_coop(const float *__restrict__ weight, const float *__restrict__ bias,
-                                 uint32_t experts, uint32_t k, const float *xs, RouterScratch *scratch,
-                                 RouteLds &lds, float *__restrict__ logits, float *prod) {
-    static_assert(kRouterCols % kProdCols == 0, "whole tiles");
+                                                 uint32_t experts, uint32_t k, const float *xs,
+                                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits,
+                                                 float *prod) {
+    constexpr int kAhead = PER <= 2 ? 4 : (PER <= 4 ? 2 : 1);
+    static_assert(kRouterCols % kProdCols == 0 && kProdTiles % kAhead == 0, "whole tiles, whole rings");
     const uint32_t t = threadIdx.x;
-    const uint32_t pieces = experts * (kProdCols / 4);
-    // piece i of a tile: expert i / 16, columns 4 (i % 16) .. + 3; pieces past the
+    const uint32_t pieces = experts * kProdPieces;
+    // piece i of a tile: expert i / 15, columns 4 (i % 15) .. + 3; pieces past the
     // tile's last re-read the last one (all loads unconditional) and are not stored
     auto piece = [&](int i) __attribute__((always_inline)) { return min(t + 256u * uint32_t(i), pieces - 1); };
     auto load = [&](int tile, float4(&r)[PER]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const uint32_t e = piece(i) / 16, c = uint32_t(tile) * kProdCols + 4 * (piece(i) % 16);
+            const uint32_t e = piece(i) / kProdPieces, c = uint32_t(tile) * kProdCols + 4 * (piece(i) % kProdPieces);
             r[i] = *reinterpret_cast<const float4 *>(weight + size_t(e) * kRouterCols + c);
         }
     };
-    float4 wv[PER];
-    load(0, wv);
+    float4 wv[kAhead][PER];
+#pragma unroll
+    for (int d = 0; d < kAhead; ++d) {
+        load(d, wv[d]);
+    }
     float sum = t < experts ? bias[t] : 0.0f;
 #pragma unroll 1
-    for (int tile = 0; tile < kProdTiles; ++tile) {
-        __syncthreads();  // the adders are done with the previous tile
+    for (int base = 0; base < kProdTiles; base += kAhead) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        for (int d = 0; d < kAhead; ++d) {
+            const int tile = base + d;
+            __syncthreads();  // the adders are done with the previous tile
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
 #pragma clang fp contract(off)
-            const uint32_t e = piece(i) / 16, c4 = 4 * (piece(i) % 16);
-            const uint32_t c = uint32_t(tile) * kProdCols + c4;
-            const float4 x = *reinterpret_cast<const float4 *>(xs + (c / 32) * mxt::x_stride + c % 32);
-            if (t + 256u * uint32_t(i) < pieces) {
-                float *dst = prod + e * kProdStride + c4;
-                dst[0] = wv[i].x * x.x;
-                dst[1] = wv[i].y * x.y;
-                dst[2] = wv[i].z * x.z;
-                dst[3] = wv[i].w * x.w;
+                const uint32_t e = piece(i) / kProdPieces, c4 = 4 * (piece(i) % kProdPieces);
+                const uint32_t c = uint32_t(tile) * kProdCols + c4;
+                const float4 x = *reinterpret_cast<const float4 *>(xs + (c / 32) * mxt::x_stride + c % 32);
+                if (t + 256u * uint32_t(i) < pieces) {
+                    float *dst = prod + e * kProdStride + c4;
+                    dst[0] = wv[d][i].x * x.x;
+                    dst[1] = wv[d][i].y * x.y;
+                    dst[2] = wv[d][i].z * x.z;
+                    dst[3] = wv[d][i].w * x.w;
+                }
             }
-        }
-        if (tile + 1 < kProdTiles) {
-            load(tile + 1, wv);
-        }
-        __syncthreads();
-        if (t < experts) {
+            // refill this ring slot (past the last tile: re-read it, unused)
+            load(min(tile + kAhead, kProdTiles - 1), wv[d]);
+            __syncthreads();
+            if (t < experts) {
 #pragma clang fp contract(off)
-            const float *row = prod + t * kProdStride;
-#pragma unroll 16
-            for (int c = 0; c < kProdCols; ++c) {
-                sum = sum + row[c];
+                const float *row = prod + t * kProdStride;
+#pragma unroll 15
+                for (int c = 0; c < kProdCols; ++c) {
+                    sum = sum + row[c];
+                }
             }
         }
     }
@@ -455,7 +466,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
     weights_out += size_t(blockIdx.x) * k;
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    __shared__ float prod[PER * 256 / (kProdCols / 4) * kProdStride];  // [experts][kProdStride]
+    __shared__ float prod[PER * 256 / kProdPieces * kProdStride];  // [experts][kProdStride]
     route_workgroup<MODE, PER>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red,
                                prod);
     if (threadIdx.x < k) {
@@ -764,12 +775,14 @@ stage::Input layer_input(const ttl_moe_layer &L, const float *x) {
 }
 
 // Calls f(std::integral_constant<int, PER>) with the exact path's float4 pieces per
-// thread for `experts` rows (experts * 16 pieces per 64-column tile, 256 threads).
+// thread for `experts` rows (experts * 15 pieces per 60-column tile, 256 threads):
+// 2 up to 34 experts, 8 up to 136, 12 up to 204 (kMaxExperts is 192).
 template <typename F>
 void with_pieces(uint32_t experts, F &&f) {
-    if (experts <= 32) {
+    static_assert(kMaxExperts * kProdPieces <= 12 * 256, "the widest variant covers every row");
+    if (experts * kProdPieces <= 2 * 256) {
         f(std::integral_constant<int, 2>{});
-    } else if (experts <= 128) {
+    } else if (experts * kProdPieces <= 8 * 256) {
         f(std::integral_constant<int, 8>{});
     } else {
         f(std::integral_constant<int, 12>{});
