@@ -12,6 +12,7 @@
 // attn_window_kernel), odd layers all (model.cpp:260).  The position is read from device memory, so one captured
 // launch serves every decode step; chunks past the current length do nothing.
 #include "ttl_internal.hpp"
+#include "ttl_mfma.hpp"
 
 #include <cmath>
 
@@ -321,16 +322,32 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
     }
 }
 
-// Prefill: a block of kPfTokens consecutive tokens of one kv head per workgroup --
-// the 8 query heads of the group times the block's tokens are 128 (token, head)
-// pairs, two threads each.  The union of the pairs' spans streams through LDS in
-// chunks of 64 positions, and each pair keeps an online softmax: m starts at the
-// sink and l at exp(sink - sink) = 1 (the sink enters the max and the denominator,
-// model.cpp:270-281), o at 0; per chunk m' = max(m, scores), l and o are rescaled by
-// exp(m - m') and take the chunk's exp(s - m') terms; the output is o / l.
+// Prefill: attention of a run of tokens on f32 MFMA, v_mfma_f32_16x16x4_f32 (D 16x16
+// += A 16x4 B 4x16; lane l holds A[l%16][l/16] and B[l/16][l%16] and receives D rows
+// 4(l/16)..+3 of column l%16).  One workgroup per (kv head, 16 consecutive tokens):
+// the 8 query heads of the group times 16 tokens are 128 queries, in tiles of 16, two
+// tiles per wave.  The union of the block's spans streams through LDS in chunks of 64
+// positions, each K/V row loaded once per workgroup.  Per chunk and query tile:
+//  - S^T (positions x queries) = K Q^T: A is 16 K rows from LDS, B the tile's queries,
+//    held in registers for the whole launch; K step (s, j) covers dims 16s + 4k + j for
+//    lane group k, so each lane reads its K operands as float4;
+//  - an online softmax per query (a column of S^T: the lane's 4 rows of each position
+//    tile and the 4 lanes of its column).  m starts at the sink and l at
+//    exp(sink - sink) = 1, so the sink takes part in the max and the denominator
+//    (model.cpp:270-281); per chunk m' = max(m, scores), and l and O are rescaled by
+//    exp(m - m');
+//  - O^T (dims x queries) += V^T P^T: K step j of position tile p takes positions
+//    16p + 4k + j for lane group k, which is row j of the lane's own S^T tile, so the
+//    probabilities never leave their registers; A reads V rows from LDS.
+// The output is O / l.
 constexpr int kPfTokens = 16;
-constexpr int kPfPairs = kPfTokens * kGroup;  // 128
-constexpr int kPfThreads = 2 * kPfPairs;      // 256
+constexpr int kPfQueries = kPfTokens * kGroup;                // 128
+constexpr int kPfThreads = 256;
+constexpr int kPfTiles = kPfQueries / 16 / (kPfThreads / 64);  // query tiles per wave: 2
+
+__device__ inline mf::f32x4 mfma_f32(float a, float b, const mf::f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(const float *__restrict__ q,
                                                                   const float *__restrict__ k_cache,
@@ -338,39 +355,44 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(const float *_
                                                                   const float *__restrict__ sinks, uint32_t first,
                                                                   uint32_t tokens, uint32_t layer_index,
                                                                   float *__restrict__ out) {
+    using mf::f32x4;
     __shared__ __attribute__((aligned(16))) float ks[kChunk * kRowStride];
     __shared__ __attribute__((aligned(16))) float vs[kChunk * kRowStride];
-    __shared__ float e[kPfPairs][kChunk + 1];
-    const uint32_t t = threadIdx.x, pair = t / 2, half = t % 2;
-    const uint32_t kvh = blockIdx.y;
-    const uint32_t local = blockIdx.x * kPfTokens + pair / kGroup;  // token of this pair
-    const uint32_t head = kvh * kGroup + pair % kGroup;
-    const bool live = local < tokens;
-    const uint32_t pos = first + (live ? local : tokens - 1);
-    const Span sp = span_of(pos, layer_index);
+    const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64, n = lane % 16, g = lane / 16;
+    const uint32_t kvh = blockIdx.y, block0 = blockIdx.x * kPfTokens;
+    const uint32_t last_local = min(block0 + kPfTokens, tokens) - 1;
     // the block's positions: from the first token's span start to the last token
-    const uint32_t last_local = min(blockIdx.x * kPfTokens + kPfTokens, tokens) - 1;
-    const uint32_t lo = span_of(first + blockIdx.x * kPfTokens, layer_index).first;
+    const uint32_t lo = span_of(first + block0, layer_index).first;
     const uint32_t hi = first + last_local;
 
-    float qv[kHead];
-    {
-        const float4 *q4 = reinterpret_cast<const float4 *>(q + (size_t(live ? local : 0) * kQHeads + head) * kHead);
+    // this lane's query (column n) of each of the wave's tiles
+    float qv[kPfTiles][16];  // [4s + j] = Q[dim 16s + 4g + j]
+    uint32_t qpos[kPfTiles], qfirst[kPfTiles], qlocal[kPfTiles], qhead[kPfTiles];
+    float m[kPfTiles], l[kPfTiles];
+    f32x4 o[kPfTiles][4];  // O^T tiles: dims 16M + 4g + i of the query
 #pragma unroll
-        for (int d = 0; d < kHead / 4; ++d) {
-            const float4 v = q4[d];
-            qv[4 * d] = v.x;
-            qv[4 * d + 1] = v.y;
-            qv[4 * d + 2] = v.z;
-            qv[4 * d + 3] = v.w;
+    for (int qi = 0; qi < kPfTiles; ++qi) {
+        const uint32_t query = (wave * kPfTiles + qi) * 16 + n;
+        qlocal[qi] = block0 + query / kGroup;
+        qhead[qi] = kvh * kGroup + query % kGroup;
+        const uint32_t lc = min(qlocal[qi], last_local);  // past the last token: a stand-in, not written
+        qpos[qi] = first + lc;
+        qfirst[qi] = span_of(qpos[qi], layer_index).first;
+        const float4 *q4 = reinterpret_cast<const float4 *>(q + (size_t(lc) * kQHeads + qhead[qi]) * kHead);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const float4 v = q4[4 * s4 + g];
+            qv[qi][4 * s4] = v.x;
+            qv[qi][4 * s4 + 1] = v.y;
+            qv[qi][4 * s4 + 2] = v.z;
+            qv[qi][4 * s4 + 3] = v.w;
         }
-    }
-    const float sink = sinks[head];
-    float m = sink, l = 1.0f;
-    float o[kHead / 2];
+        m[qi] = sinks[qhead[qi]];
+        l[qi] = g == 0 ? 1.0f : 0.0f;  // the sink's exp(sink - m), counted once per column
 #pragma unroll
-    for (int d = 0; d < kHead / 2; ++d) {
-        o[d] = 0.0f;
+        for (int mt = 0; mt < 4; ++mt) {
+            o[qi][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     }
 
     constexpr int kPer = kChunk * (kHead / 4) / kPfThreads;  // 4 float4 of K and of V per thread
@@ -385,63 +407,102 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(const float *_
             *reinterpret_cast<float4 *>(vs + p * kRowStride + 4 * d4) = reinterpret_cast<const float4 *>(v_cache + row)[d4];
         }
         __syncthreads();
-        // scores of positions half, half + 2, ... of the chunk (this pair's span only)
-        float cmax = -INFINITY;
-        for (uint32_t j = half; j < uint32_t(kChunk); j += 2) {
-            const uint32_t at = c0 + j;
-            float a = 0.0f;
+
+        // S^T: [query tile][position tile], lane rows 4g..4g+3 = positions 16p + 4g + i
+        f32x4 sc[kPfTiles][4];
 #pragma unroll
-            for (int d = 0; d < kHead / 4; ++d) {
-                const float4 kv = *reinterpret_cast<const float4 *>(ks + j * kRowStride + 4 * d);
-                a = fmaf(qv[4 * d], kv.x, a);
-                a = fmaf(qv[4 * d + 1], kv.y, a);
-                a = fmaf(qv[4 * d + 2], kv.z, a);
-                a = fmaf(qv[4 * d + 3], kv.w, a);
+        for (int p = 0; p < 4; ++p) {
+#pragma unroll
+            for (int qi = 0; qi < kPfTiles; ++qi) {
+                sc[qi][p] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-            const bool in = at >= sp.first && at <= pos;
-            const float s = in ? a * 0.125f : -INFINITY;  // 1/sqrt(64), exact
-            e[pair][j] = s;
-            cmax = fmaxf(cmax, s);
-        }
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 1));
-        const float m2 = fmaxf(m, cmax);
-        const float scale = expf(m - m2);
-        __syncthreads();  // both halves' scores are in e
-        // exp terms and this thread's half of the dimensions of o
-        float lsum = 0.0f;
-        float acc[kHead / 2];
 #pragma unroll
-        for (int d = 0; d < kHead / 2; ++d) {
-            acc[d] = 0.0f;
-        }
-        for (uint32_t j = 0; j < uint32_t(kChunk); ++j) {
-            const float s = e[pair][j];
-            const float x = s == -INFINITY ? 0.0f : expf(s - m2);
-            lsum += x;
-            const float *vrow = vs + j * kRowStride + half * (kHead / 2);
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const float4 a = *reinterpret_cast<const float4 *>(ks + (16 * p + n) * kRowStride + 16 * s4 + 4 * g);
 #pragma unroll
-            for (int d = 0; d < kHead / 8; ++d) {
-                const float4 v = *reinterpret_cast<const float4 *>(vrow + 4 * d);
-                acc[4 * d] = fmaf(x, v.x, acc[4 * d]);
-                acc[4 * d + 1] = fmaf(x, v.y, acc[4 * d + 1]);
-                acc[4 * d + 2] = fmaf(x, v.z, acc[4 * d + 2]);
-                acc[4 * d + 3] = fmaf(x, v.w, acc[4 * d + 3]);
+                for (int qi = 0; qi < kPfTiles; ++qi) {
+                    sc[qi][p] = mfma_f32(a.x, qv[qi][4 * s4], sc[qi][p]);
+                }
+#pragma unroll
+                for (int qi = 0; qi < kPfTiles; ++qi) {
+                    sc[qi][p] = mfma_f32(a.y, qv[qi][4 * s4 + 1], sc[qi][p]);
+                }
+#pragma unroll
+                for (int qi = 0; qi < kPfTiles; ++qi) {
+                    sc[qi][p] = mfma_f32(a.z, qv[qi][4 * s4 + 2], sc[qi][p]);
+                }
+#pragma unroll
+                for (int qi = 0; qi < kPfTiles; ++qi) {
+                    sc[qi][p] = mfma_f32(a.w, qv[qi][4 * s4 + 3], sc[qi][p]);
+                }
             }
         }
-        l = l * scale + lsum;
+        // scores (1/sqrt(64) = 0.125, exact), mask, online softmax; sc becomes P^T
 #pragma unroll
-        for (int d = 0; d < kHead / 2; ++d) {
-            o[d] = o[d] * scale + acc[d];
+        for (int qi = 0; qi < kPfTiles; ++qi) {
+            float cmax = -INFINITY;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t at = c0 + 16 * p + 4 * g + i;
+                    const bool in = at >= qfirst[qi] && at <= qpos[qi];
+                    const float s = in ? sc[qi][p][i] * 0.125f : -INFINITY;
+                    sc[qi][p][i] = s;
+                    cmax = fmaxf(cmax, s);
+                }
+            }
+            cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+            cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+            const float m2 = fmaxf(m[qi], cmax);
+            const float scale = expf(m[qi] - m2);
+            float lsum = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float s = sc[qi][p][i];
+                    const float x = s == -INFINITY ? 0.0f : expf(s - m2);
+                    sc[qi][p][i] = x;
+                    lsum += x;
+                }
+            }
+            l[qi] = l[qi] * scale + lsum;
+            m[qi] = m2;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                o[qi][mt] *= scale;
+            }
         }
-        m = m2;
-    }
-    if (!live) {
-        return;
-    }
-    float *dst = out + (size_t(local) * kQHeads + head) * kHead + half * (kHead / 2);
+        // O^T += V^T P^T
 #pragma unroll
-    for (int d = 0; d < kHead / 2; ++d) {
-        dst[d] = o[d] / l;
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float a = vs[(16 * p + 4 * g + j) * kRowStride + 16 * mt + n];
+#pragma unroll
+                    for (int qi = 0; qi < kPfTiles; ++qi) {
+                        o[qi][mt] = mfma_f32(a, sc[qi][p][j], o[qi][mt]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int qi = 0; qi < kPfTiles; ++qi) {
+        float den = l[qi] + __shfl_xor(l[qi], 16);
+        den = den + __shfl_xor(den, 32);
+        if (qlocal[qi] < tokens) {
+            float *dst = out + (size_t(qlocal[qi]) * kQHeads + qhead[qi]) * kHead;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const f32x4 v = o[qi][mt];
+                *reinterpret_cast<float4 *>(dst + 16 * mt + 4 * g) =
+                    make_float4(v[0] / den, v[1] / den, v[2] / den, v[3] / den);
+            }
+        }
     }
 }
 
