@@ -80,17 +80,12 @@ struct RouterScratch {
     uint32_t exact_path_count;
 };
 
-// One workgroup per router row: the exact value of the row (f64) and the bound
-// on the reference's sequential-sum error.  180 lanes hold 16 columns each.
-// Grid y indexes tokens of a batch: token t reads in.base + t * x_stride and uses
-// scratch[t] (one token: grid y = 1).
+// One workgroup per router row of one token: the exact value of the row (f64) and
+// the bound on the reference's sequential-sum error.  180 lanes hold 16 columns each.
 template <int MODE>
 __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float *__restrict__ weight,
                                                                      const float *__restrict__ bias,
-                                                                     stage::Input in, RouterScratch *scratch,
-                                                                     uint32_t x_stride) {
-    in.base += size_t(blockIdx.y) * x_stride;
-    scratch += blockIdx.y;
+                                                                     stage::Input in, RouterScratch *scratch) {
     __shared__ double wave_part[3][3];
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
@@ -167,6 +162,99 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
         // u = 2^-24; 1.001 covers second-order terms (n u < 2e-4); the 1e-12 term
         // covers the f64 rounding of the exact sums; 1e-37 covers subnormal steps.
         scratch->bound[row] = 1.001 * 0x1p-24 * (abs_partials + abs_products) + 1e-12 * abs_products + 1e-37;
+    }
+}
+
+// Router rows of a batch (prefill): the same exact values and bounds as
+// router_rows_kernel, for kRbTokens tokens x kRbExperts experts per workgroup.  The
+// tokens are staged once; each wave takes kRbExperts / 4 experts, loads a row once and
+// runs it against every staged token.  Lane j < 60 holds columns 48j .. 48j+47, so a
+// row's scan over the columns stays within the wave (no barriers between pairs).
+constexpr int kRbTokens = 4;
+constexpr int kRbExperts = 8;
+constexpr int kRbLanes = 60;
+constexpr int kRbCols = kRouterCols / kRbLanes;  // 48
+static_assert(kRbLanes * kRbCols == kRouterCols && kRbCols % 4 == 0, "whole float4 per lane");
+
+template <int MODE>
+__global__ __launch_bounds__(256) void router_rows_batch_kernel(const float *__restrict__ weight,
+                                                                const float *__restrict__ bias, stage::Input in,
+                                                                RouterScratch *scratch, uint32_t x_stride,
+                                                                uint32_t count, uint32_t experts) {
+    __shared__ __attribute__((aligned(16))) float xs[kRbTokens][mxt::x_floats];
+    __shared__ float red[stage::red_floats(mxt::x_blocks)];
+    const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
+    const uint32_t token0 = blockIdx.x * kRbTokens;
+    const uint32_t tokens = min(uint32_t(kRbTokens), count - token0);
+#pragma unroll 1
+    for (uint32_t k = 0; k < uint32_t(kRbTokens); ++k) {
+        stage::Input ik = in;
+        ik.base += size_t(token0 + min(k, tokens - 1)) * x_stride;  // past the batch: a stand-in
+        stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(ik, xs[k], red);
+    }
+    __syncthreads();
+    const bool active = lane < uint32_t(kRbLanes);
+    const uint32_t c0 = (active ? lane : 0) * kRbCols;
+    auto xat = [&](uint32_t k, uint32_t c) __attribute__((always_inline)) {
+        return *reinterpret_cast<const float4 *>(xs[k] + (c / 32) * mxt::x_stride + c % 32);
+    };
+#pragma unroll 1
+    for (uint32_t r = 0; r < uint32_t(kRbExperts / 4); ++r) {
+        const uint32_t row = blockIdx.y * kRbExperts + wave * (kRbExperts / 4) + r;
+        if (row >= experts) {
+            break;
+        }
+        float4 w[kRbCols / 4];
+        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols + c0);
+#pragma unroll
+        for (int i = 0; i < kRbCols / 4; ++i) {
+            w[i] = w4[i];
+        }
+        const double b = double(bias[row]);
+#pragma unroll 1
+        for (uint32_t k = 0; k < tokens; ++k) {
+            // the lane's products (exact in f64: fma(w, x, s) rounds only the sum, as
+            // s + w x would), their sum and absolute sum
+            double local = 0.0, abs_products = 0.0;
+#pragma unroll
+            for (int i = 0; i < kRbCols / 4; ++i) {
+                const float4 x = xat(k, c0 + 4 * i);
+                const float wa[4] = {w[i].x, w[i].y, w[i].z, w[i].w}, xa[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    local = fma(double(wa[e]), double(xa[e]), local);
+                    abs_products = fma(fabs(double(wa[e])), fabs(double(xa[e])), abs_products);
+                }
+            }
+            if (!active) {
+                local = 0.0;
+                abs_products = 0.0;
+            }
+            const double incl = wave_inclusive_scan(local, lane);
+            // the partial sums S_c of the reference's order, from the bias
+            double running = b + (incl - local), abs_partials = 0.0;
+#pragma unroll
+            for (int i = 0; i < kRbCols / 4; ++i) {
+                const float4 x = xat(k, c0 + 4 * i);
+                const float wa[4] = {w[i].x, w[i].y, w[i].z, w[i].w}, xa[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    running = fma(double(wa[e]), double(xa[e]), running);
+                    abs_partials += fabs(running);
+                }
+            }
+            if (!active) {
+                abs_partials = 0.0;
+            }
+            const double total = __shfl(incl, 63);
+            const double s_partials = wave_sum(abs_partials), s_products = wave_sum(abs_products);
+            if (lane == 0 && k < tokens) {
+                RouterScratch *sk = scratch + token0 + k;
+                sk->exact[row] = b + total;
+                // the bound of router_rows_kernel
+                sk->bound[row] = 1.001 * 0x1p-24 * (s_partials + s_products) + 1e-12 * s_products + 1e-37;
+            }
+        }
     }
 }
 
@@ -797,7 +885,7 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
     RouterScratch *scratch = &workspace(ctx)->router;
     stage::with_mode(in, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
-        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch, 0u);
+        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch);
         with_pieces(experts, [&](auto per) {
             router_select_kernel<M, decltype(per)::value><<<1, 256, 0, ctx->stream>>>(
                 weight, bias, experts, in, k, force_exact ? 1u : 0u, scratch, logits, indices, weights, 0u);
@@ -811,7 +899,7 @@ void launch_router_rows(ttl_ctx *ctx, const ttl_moe_layer &L, const stage::Input
     RouterScratch *scratch = &workspace(ctx)->router;
     stage::with_mode(in, [&](auto mode) {
         router_rows_kernel<decltype(mode)::value>
-            <<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias, in, scratch, 0u);
+            <<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias, in, scratch);
     });
 }
 
@@ -838,9 +926,9 @@ int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, ui
     const stage::Input in = layer_input(L, x);
     stage::with_mode(in, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
-        router_rows_kernel<M><<<dim3(L.experts, count), kRouterThreads, 0, ctx->stream>>>(L.router_weight,
-                                                                                          L.router_bias, in, s,
-                                                                                          L.hidden);
+        router_rows_batch_kernel<M>
+            <<<dim3((count + kRbTokens - 1) / kRbTokens, (L.experts + kRbExperts - 1) / kRbExperts), 256, 0,
+               ctx->stream>>>(L.router_weight, L.router_bias, in, s, L.hidden, count, L.experts);
         with_pieces(L.experts, [&](auto per) {
             router_select_kernel<M, decltype(per)::value><<<count, 256, 0, ctx->stream>>>(
                 L.router_weight, L.router_bias, L.experts, in, L.used, 0u, s, nullptr, indices, weights, L.hidden);
