@@ -88,10 +88,11 @@ size_t align256(size_t v) {
     return (v + 255) & ~size_t(255);
 }
 
-// Upper bound on the tiles: sum_e ceil(c_e / 64) <= (S + 63 * nonempty) / 64.
+// Upper bound on the tiles: sum_e ceil(c_e / T) <= (S + (T - 1) * nonempty) / T for
+// tiles of T = mf::tile_slots slots.
 uint32_t max_tiles(uint32_t pairs, uint32_t experts) {
     const uint32_t nonempty = pairs < experts ? pairs : experts;
-    return uint32_t((uint64_t(pairs) + 63ull * nonempty) / mf::tile_slots) + 1;
+    return uint32_t((uint64_t(pairs) + uint64_t(mf::tile_slots - 1) * nonempty) / mf::tile_slots) + 1;
 }
 
 Layout make_layout(uint32_t pairs, uint32_t experts, int x_planes, bool with_hidden, uint32_t rows) {
@@ -270,7 +271,7 @@ __global__ void plan_selected_kernel(const int32_t *__restrict__ tokens, uint32_
 // fragment lane, as P bf16 planes.  Slots past the tile's count, tokens out of
 // range (NaN), and blocks 90/91 (zero) are filled so that every fragment is defined.
 template <bool BF16_IN, int P>
-__global__ __launch_bounds__(256) void gather_kernel(const void *__restrict__ x, uint32_t x_stride,
+__global__ __launch_bounds__(mf::col_tiles * 64) void gather_kernel(const void *__restrict__ x, uint32_t x_stride,
                                                      uint32_t x_rows, Plan plan) {
     const uint32_t tile = blockIdx.y;
     if (tile >= plan.header->tiles) {
@@ -898,7 +899,7 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     plan_selected_kernel<<<ttl::blocks_for(count > tiles ? count : tiles, 256), 256, 0, ctx->stream>>>(
         tokens_dev, count, expert, plan);
     TTL_LAUNCHED("plan_selected_kernel");
-    gather_kernel<false, 3><<<dim3(mf::steps, tiles), 256, 0, ctx->stream>>>(x_dev, x_stride, x_rows, plan);
+    gather_kernel<false, 3><<<dim3(mf::steps, tiles), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, x_stride, x_rows, plan);
     TTL_LAUNCHED("gather_kernel");
     MatmulArgs m;
     m.codes = w->codes;
@@ -965,9 +966,9 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     }
     if (stages & TTL_PREFILL_GATHER) {
         if (bf16) {
-            gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         } else {
-            gather_kernel<false, 3><<<dim3(mf::steps, lay.tmax), 256, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<false, 3><<<dim3(mf::steps, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         }
         TTL_LAUNCHED("gather_kernel");
     }
