@@ -158,3 +158,44 @@ def test_strict_load_refuses_the_small_model(loaded):
     _, _, path = loaded
     with pytest.raises(ttlab_amd.TtlError, match="only gpt-oss-20b and gpt-oss-120b are supported"):
         ttlab_amd.Model.from_gguf(path, CAPACITY, strict=True)
+
+
+def test_gguf_model_prefill_matches_oracle(loaded):
+    """Layer-major prefill (model.cpp:463-555) of the file's model: each layer's input
+    rows through the oracle's prefill layer, then the Q8_0 logits of the last token."""
+    gpu, host, _ = loaded
+    count = 21
+    tokens = [int(t) for t in np.random.default_rng(17).integers(0, VOCAB, count)]
+    logits = gpu.prefill(tokens)
+    x0 = gpu.prefill_state(0, count)
+    for p, tok in enumerate(tokens):
+        assert np.array_equal(x0[p].view(np.uint32), host.embedding(tok).view(np.uint32)), p
+    skipped = 0
+    for l in range(LAYERS):
+        x_in = gpu.prefill_state(l, count)
+        keys, values = gpu.kv_cache(l, count)
+        kc, vc = np.zeros(CAPACITY * KW, np.float32), np.zeros(CAPACITY * KW, np.float32)
+        out, res = np.empty(count * N, np.float32), np.empty(count * N, np.float32)
+        s = host.layer_struct(l)
+        O.lib.orc_layer_prefill(C.byref(s), l, 0, count, np.ascontiguousarray(x_in.ravel()), host.freqs, kc, vc,
+                                O.BODY_V4, out, res.ctypes.data)
+        assert O.rel_l2(keys, kc[:count * KW]) <= TOL
+        assert O.rel_l2(values, vc[:count * KW]) <= TOL
+        nxt = gpu.prefill_state(l + 1, count)
+        for p in range(count):
+            err = O.rel_l2(nxt[p], out[p * N:(p + 1) * N])
+            if err > TOL:
+                # only a token whose routing the oracle's own router logits leave near-tied
+                normed = np.empty(N, np.float32)
+                O.lib.orc_rms_norm(res[p * N:(p + 1) * N], host.t[f"blk.{l}.post_attention_norm.weight"], N, 1e-5,
+                                   normed)
+                router = np.empty(EXPERTS, np.float32)
+                O.lib.orc_matvec_add_f32(host.t[f"blk.{l}.ffn_gate_inp.weight"], host.t[f"blk.{l}.ffn_gate_inp.bias"],
+                                         EXPERTS, N, normed, router)
+                assert near_tie(router), (l, p, err)
+                skipped += 1
+    assert skipped <= 2
+    ref = host.logits(gpu.prefill_state(LAYERS, count)[count - 1])
+    err = O.rel_l2(logits, ref)
+    print(f"GGUF prefill of {count} tokens: Q8_0 logits rel_l2 {err:.2e}")
+    assert err <= TOL

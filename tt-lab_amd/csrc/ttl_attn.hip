@@ -26,20 +26,6 @@ struct Span {
     uint32_t first, count;
 };
 
-// The tokens of one launch: token z of the grid sits at position
-// (*position or first) + z; its query and output are q + z * q_stride and
-// out + z * q_stride, its chunk partials at z * ws_stride floats into the workspace.
-// A decode step is one token whose position is read from device memory.
-struct Tokens {
-    const int32_t *position;  // device position of token 0, or null
-    uint32_t first;           // position of token 0 when `position` is null
-    uint32_t q_stride, ws_stride;
-};
-
-__device__ inline uint32_t position_of(const Tokens &ts, uint32_t z) {
-    return (ts.position ? uint32_t(*ts.position) : ts.first) + z;
-}
-
 __device__ inline Span span_of(uint32_t pos, uint32_t layer_index) {
     const uint32_t first = (layer_index % 2 == 0 && pos + 1 > uint32_t(kWindow)) ? pos + 1 - kWindow : 0;
     return {first, pos + 1 - first};
@@ -67,7 +53,8 @@ constexpr int kRowStride = kHead + 4;
 
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__restrict__ q,
                                                                 const float *__restrict__ k_cache,
-                                                                const float *__restrict__ v_cache, Tokens ts,
+                                                                const float *__restrict__ v_cache,
+                                                                const int32_t *__restrict__ position,
                                                                 uint32_t capacity, uint32_t layer_index,
                                                                 uint32_t max_chunks, float *__restrict__ o_part,
                                                                 float2 *__restrict__ ml_part) {
@@ -76,10 +63,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
     __shared__ __attribute__((aligned(16))) float qs[kGroup][kHead];
     __shared__ float e[kGroup][kChunk];
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
-    const uint32_t pos = position_of(ts, blockIdx.z);
-    q += size_t(blockIdx.z) * ts.q_stride;
-    o_part += size_t(blockIdx.z) * ts.ws_stride;
-    ml_part = reinterpret_cast<float2 *>(reinterpret_cast<float *>(ml_part) + size_t(blockIdx.z) * ts.ws_stride);
+    const uint32_t pos = uint32_t(*position);
     if (pos >= capacity) {
         return;
     }
@@ -174,21 +158,28 @@ constexpr int kMaxCombineChunks = 256;  // capacity up to 16384 positions
 
 __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__restrict__ o_part,
                                                              const float2 *__restrict__ ml_part,
-                                                             const float *__restrict__ sinks, Tokens ts,
+                                                             const float *__restrict__ sinks,
+                                                             const int32_t *__restrict__ position,
                                                              uint32_t capacity, uint32_t layer_index,
                                                              uint32_t max_chunks, float *__restrict__ out) {
     __shared__ float fs[kMaxCombineChunks];
     const uint32_t head = blockIdx.x, d = threadIdx.x;
-    const uint32_t pos = position_of(ts, blockIdx.y);
-    o_part += size_t(blockIdx.y) * ts.ws_stride;
-    ml_part = reinterpret_cast<const float2 *>(reinterpret_cast<const float *>(ml_part) + size_t(blockIdx.y) * ts.ws_stride);
-    out += size_t(blockIdx.y) * ts.q_stride;
+    const uint32_t pos = uint32_t(*position);
     if (pos >= capacity) {
         return;
     }
     const Span sp = span_of(pos, layer_index);
     const uint32_t chunks = (sp.count + kChunk - 1) / kChunk;
     const float sink = sinks[head];
+    // the first kEarly chunks' outputs are requested with the statistics (addresses
+    // past the last chunk re-read it, weighted by 0 below)
+    constexpr int kEarly = 32;
+    const float *op = o_part + size_t(head) * max_chunks * kHead + d;
+    float early[kEarly];
+#pragma unroll
+    for (int c = 0; c < kEarly; ++c) {
+        early[c] = op[size_t(min(uint32_t(c), chunks - 1)) * kHead];
+    }
     constexpr int kPer = kMaxCombineChunks / kHead;
     float2 ml[kPer];
 #pragma unroll
@@ -213,9 +204,14 @@ __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__rest
     den = wave_sum(den) + expf(sink - m);
     __syncthreads();
     float acc = 0.0f;
-    const float *op = o_part + size_t(head) * max_chunks * kHead + d;
+#pragma unroll
+    for (int c = 0; c < kEarly; ++c) {
+        if (uint32_t(c) < chunks) {
+            acc = fmaf(early[c], fs[c], acc);
+        }
+    }
 #pragma unroll 8
-    for (uint32_t c = 0; c < chunks; ++c) {
+    for (uint32_t c = kEarly; c < chunks; ++c) {
         acc = fmaf(op[size_t(c) * kHead], fs[c], acc);
     }
     out[head * kHead + d] = acc / den;
@@ -229,7 +225,8 @@ constexpr int kWinThreads = 256;
 __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *__restrict__ q,
                                                                   const float *__restrict__ k_cache,
                                                                   const float *__restrict__ v_cache,
-                                                                  const float *__restrict__ sinks, Tokens ts,
+                                                                  const float *__restrict__ sinks,
+                                                                  const int32_t *__restrict__ position,
                                                                   uint32_t capacity, uint32_t layer_index,
                                                                   float *__restrict__ out) {
     __shared__ __attribute__((aligned(16))) float ks[kWindow * kRowStride];
@@ -239,9 +236,7 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
     __shared__ float stat[4];
     __shared__ float part[kWinThreads / kHead][kHead];
     const uint32_t head = blockIdx.x, kvh = head / kGroup, t = threadIdx.x;
-    const uint32_t pos = position_of(ts, blockIdx.y);
-    q += size_t(blockIdx.y) * ts.q_stride;
-    out += size_t(blockIdx.y) * ts.q_stride;
+    const uint32_t pos = uint32_t(*position);
     if (pos >= capacity) {
         return;
     }
@@ -518,23 +513,23 @@ size_t attention_partials_floats(uint32_t capacity) {
 
 namespace {
 
-// Attention for `tokens` tokens (grid slices); max_chunks = the chunks the partials of
+// Attention of the token at *position; max_chunks = the chunks the partials of
 // one token hold (at least those of its span).
 void launch_attention(ttl_ctx *ctx, const float *q, const float *k_cache, const float *v_cache, const float *sinks,
-                      const Tokens &ts, uint32_t tokens, uint32_t capacity, uint32_t layer_index,
-                      uint32_t max_chunks, float *workspace, float *out) {
+                      const int32_t *position, uint32_t capacity, uint32_t layer_index, uint32_t max_chunks,
+                      float *workspace, float *out) {
     if (layer_index % 2 == 0) {
         // the sliding window fits one workgroup per query head
-        attn_window_kernel<<<dim3(kQHeads, tokens), kWinThreads, 0, ctx->stream>>>(q, k_cache, v_cache, sinks, ts,
-                                                                                   capacity, layer_index, out);
+        attn_window_kernel<<<kQHeads, kWinThreads, 0, ctx->stream>>>(q, k_cache, v_cache, sinks, position, capacity,
+                                                                     layer_index, out);
         return;
     }
     float *o_part = workspace;
     float2 *ml_part = reinterpret_cast<float2 *>(workspace + size_t(kQHeads) * max_chunks * kHead);
-    attn_partial_kernel<<<dim3(max_chunks, kKvHeads, tokens), kThreads, 0, ctx->stream>>>(
-        q, k_cache, v_cache, ts, capacity, layer_index, max_chunks, o_part, ml_part);
-    attn_combine_kernel<<<dim3(kQHeads, tokens), kHead, 0, ctx->stream>>>(o_part, ml_part, sinks, ts, capacity,
-                                                                          layer_index, max_chunks, out);
+    attn_partial_kernel<<<dim3(max_chunks, kKvHeads), kThreads, 0, ctx->stream>>>(
+        q, k_cache, v_cache, position, capacity, layer_index, max_chunks, o_part, ml_part);
+    attn_combine_kernel<<<kQHeads, kHead, 0, ctx->stream>>>(o_part, ml_part, sinks, position, capacity, layer_index,
+                                                            max_chunks, out);
 }
 
 
@@ -555,8 +550,7 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
                 "ttl_attention_decode: capacity must be 1..%d", kMaxCombineChunks * kChunk);
     TTL_REQUIRE(((uintptr_t)q_dev & 15) == 0 && ((uintptr_t)k_cache_dev & 15) == 0 && ((uintptr_t)v_cache_dev & 15) == 0,
                 TTL_ERR_INVALID, "ttl_attention_decode: q, k and v must be 16-byte aligned");
-    const Tokens ts{position_dev, 0u, 0u, 0u};
-    launch_attention(ctx, q_dev, k_cache_dev, v_cache_dev, sinks_dev, ts, 1, capacity, layer_index,
+    launch_attention(ctx, q_dev, k_cache_dev, v_cache_dev, sinks_dev, position_dev, capacity, layer_index,
                      (capacity + kChunk - 1) / kChunk, workspace_dev, out_dev);
     TTL_LAUNCHED("attention kernels");
     return TTL_OK;
