@@ -216,6 +216,65 @@ def gpu_moe(args):
     }
 
 
+# Config 0: y = W x for the 5760 x 2880 MXFP4 matrix (gate and up stacked: the GGUF
+# {2880, 2880, 2} bytes are the same rows in the same order as one 5760-row matrix),
+# one ttl_matvec_mxfp4 launch.  The copies are distinct resident matrices replayed in
+# rotation, 1.13 GB in all (four times the 256 MB MALL), so every launch streams its
+# weights from HBM.
+MATVEC_COPIES = 128
+MATVEC_BYTES = 2 * N * 1530 + N * 4 + 2 * N * 4  # W, x, y: 8,847,360
+MATVEC_FLOP = 2 * 2 * N * N
+
+
+def gpu_matvec(args):
+    import ttlab_amd
+
+    dev = ttlab_amd.Device(0)
+    mats = [dev.mxfp4_synthetic(2 * N, N, 1, 0x77000000, 100 + i) for i in range(MATVEC_COPIES)]
+    x = dev.alloc(N * 4)
+    dev.synth_normal(x, 0x78000000, 0, N)
+    y = dev.alloc(2 * N * 4)
+    dev.sync()
+
+    def step():
+        for w in mats:
+            dev.matvec_mxfp4(w, None, x, y, 0)
+
+    graph = dev.capture(step)
+    for _ in range(max(args.warmup, 1)):
+        graph.launch()
+    dev.sync()
+    reps = max(20, args.steps)
+    dev.timer_start()
+    for _ in range(reps):
+        graph.launch()
+    ms = dev.timer_stop()
+    us = ms * 1e3 / (reps * MATVEC_COPIES)
+    gbs = MATVEC_BYTES / (us * 1e-6) / 1e9
+    log(f"config 0 matvec: {us:.3f} us per launch, {gbs:.0f} GB/s over {MATVEC_COPIES} rotated copies")
+    graph.free()
+    for w in mats:
+        w.free()
+    dev.close()
+    us_read = read_ceiling(MATVEC_BYTES, MATVEC_COPIES)
+    log(f"plain read of the same {MATVEC_BYTES / 1e6:.2f} MB per launch: {us_read:.2f} us, "
+        f"{MATVEC_BYTES / (us_read * 1e-6) / 1e9:.0f} GB/s")
+    return {
+        "value": gbs,
+        "unit": "GB/s",
+        "ms_per_step": us * 1e-3,
+        "config": {"workload": "config 0: one 5760x2880 MXFP4 matvec (gate|up stacked) per launch; "
+                               f"{MATVEC_COPIES} distinct resident matrices (1.13 GB) replayed in rotation; "
+                               "step = one launch",
+                   "rows": 2 * N, "cols": N, "bytes_per_launch": MATVEC_BYTES,
+                   "matvec_GFLOPs": round(MATVEC_FLOP / (us * 1e-6) / 1e9, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "matvec_kernel", "bytes_per_launch": MATVEC_BYTES, "launch_us": round(us, 3),
+                     "read_ceiling": ceiling_entry(gbs, MATVEC_BYTES, us_read)},
+    }
+
+
 PREFILL_TOKENS = 512
 PREFILL_LAYERS = 3  # distinct resident layers (1.27 GB of experts, beyond every cache)
 PREFILL_PAIRS = PREFILL_TOKENS * USED
@@ -426,6 +485,25 @@ def cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
                           f"{sample} tokens, {per_token_layer * 1e3:.2f} ms per token-layer, times {layers} layers; "
                           f"MXFP4 {isa}, Q8_0 matmuls as the reference's C loops"}
 
+    if workload == "matvec":
+        # config 0 on the CPU: the 5760 x 2880 matrix as two 2880-row experts
+        # (matvec_add_mxfp4_2880, tensor.cpp:239-304), over 16 copies (141 MB, beyond
+        # the host caches)
+        copies = 16
+        mats = [O.synth_mxfp4(0x77000000, 100 + i, 2 * N * 90) for i in range(copies)]
+        x = O.synth_normal(0x78000000, 0, N)
+        zero = np.zeros(2 * N, np.float32)
+        y = np.empty(N, np.float32)
+        count, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds or count == 0:
+            m = mats[count % copies]
+            O.lib.orc_matvec_add_mxfp4(m, zero, N, N, x, y, 0, body)
+            O.lib.orc_matvec_add_mxfp4(m, zero, N, N, x, y, 1, body)
+            count += 1
+        per = (time.perf_counter() - t0) / count
+        return {"value": round(MATVEC_BYTES / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{count} config-0 matvecs (two 2880-row experts each) over {copies} distinct matrices, "
+                          f"{per * 1e3:.2f} ms each; oracle restatement of tensor.cpp:239-304, {isa}"}
     if workload == "moe":
         from moe_fixtures import HostLayer
 
@@ -484,7 +562,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "moe", "prefill", "model-prefill"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "matvec", "moe", "prefill", "model-prefill"], default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -524,7 +602,7 @@ def main():
         src.free()
         dst.free()
         dev.close()
-    runner = {"decode": gpu_decode, "moe": gpu_moe, "prefill": gpu_prefill,
+    runner = {"decode": gpu_decode, "matvec": gpu_matvec, "moe": gpu_moe, "prefill": gpu_prefill,
               "model-prefill": gpu_model_prefill}[args.workload]
     res = runner(args)
     base = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.workload, args.layers, args.context)

@@ -153,6 +153,28 @@ def test_matvec_matches_oracle_config0(dev, emin, emax):
     t.free()
 
 
+def test_config0_as_one_5760_row_matrix(dev):
+    """The {2880, 2880, 2} bytes uploaded as one 5760-row matrix (the bench's config-0
+    launch) give bitwise the two experts' rows, and the oracle's values."""
+    blocks = O.synth_mxfp4(0x77000000, 0, 2 * N * 90)
+    x = O.synth_normal(0x78000000, 0, N)
+    one = dev.mxfp4_upload(blocks, 2 * N, N, 1)
+    two = dev.mxfp4_upload(blocks, N, N, 2)
+    xb, y1, y2 = dev.upload(x), dev.alloc(2 * N * 4), dev.alloc(2 * N * 4)
+    ids = dev.upload(np.array([0, 1], np.int32))
+    dev.matvec_mxfp4(one, None, xb, y1, 0)
+    dev.matvec_mxfp4_experts(two, None, xb, 0, ids, 2, y2)
+    a, b = y1.download(np.float32), y2.download(np.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    zero = np.zeros(2 * N, np.float32)
+    ref = np.concatenate([O.mxfp4_matvec(blocks, zero, N, N, x, expert=e, body=O.BODY_V4) for e in range(2)])
+    assert O.rel_l2(a, ref) <= TOL
+    for buf in (xb, y1, y2, ids):
+        buf.free()
+    one.free()
+    two.free()
+
+
 def test_expert_indexed_batch_reads_selected_experts(dev):
     E = 8
     blocks = O.synth_mxfp4(0x77000000, 7, E * N * 90)

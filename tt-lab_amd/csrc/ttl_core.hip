@@ -99,16 +99,6 @@ int ttl_create(int device, ttl_ctx **out) {
         err = hipEventCreate(&ctx->timer_stop);
     }
     if (err == hipSuccess) {
-        err = hipMalloc(&ctx->iota, sizeof(int32_t) * ttl::iota_size);
-    }
-    if (err == hipSuccess) {
-        int32_t host_iota[ttl::iota_size];
-        for (int i = 0; i < ttl::iota_size; ++i) {
-            host_iota[i] = i;
-        }
-        err = hipMemcpy(ctx->iota, host_iota, sizeof(host_iota), hipMemcpyHostToDevice);
-    }
-    if (err == hipSuccess) {
         err = hipMalloc(&ctx->moe_workspace, ttl::moe_workspace_bytes());
     }
     if (err == hipSuccess) {
@@ -138,9 +128,6 @@ void ttl_destroy(ttl_ctx *ctx) {
     }
     if (ctx->stream) {
         (void)hipStreamDestroy(ctx->stream);
-    }
-    if (ctx->iota) {
-        (void)hipFree(ctx->iota);
     }
     if (ctx->moe_workspace) {
         (void)hipFree(ctx->moe_workspace);

@@ -13,7 +13,6 @@ struct ttl_ctx {
     hipStream_t stream = nullptr;
     hipEvent_t timer_start = nullptr;
     hipEvent_t timer_stop = nullptr;
-    int32_t *iota = nullptr;  // device int32 [iota_size] = 0, 1, 2, ... (expert ids for single calls)
     void *moe_workspace = nullptr;  // device ttl::MoeWorkspace, zeroed at creation
     int compute_units = 0;
     double hbm_bytes = 0.0;
@@ -51,8 +50,6 @@ struct ttl_q8 {
 };
 
 namespace ttl {
-
-constexpr int iota_size = 1024;
 
 size_t moe_workspace_bytes();
 // Batched router of moe_batch (ttl_moe.hip): per-token exact rows in `scratch`

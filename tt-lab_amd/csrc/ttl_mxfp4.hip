@@ -2,6 +2,7 @@
 // expert-indexed MXFP4 matvec.  The per-tile inner loop is in ttl_mxfp4_tile.hpp.
 #include "ttl_mfma.hpp"
 #include "ttl_mxfp4_tile.hpp"
+#include "ttl_stage.hpp"
 
 #include <cmath>
 #include <vector>
@@ -12,7 +13,6 @@ int synth_mxfp4_repacked(ttl_ctx *ctx, ttl_mxfp4 *t, uint64_t seed, uint64_t str
 
 namespace {
 
-constexpr int kWaves = 4;  // tiles (waves) per workgroup
 
 // ---- layout conversion ------------------------------------------------------
 
@@ -131,38 +131,49 @@ __global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *_
 
 // ---- matvec ------------------------------------------------------------------
 
-// One wave = one 16-row tile of the expert selected for slot blockIdx.x / groups.
-__global__ __launch_bounds__(kWaves * 64) void matvec_kernel(
+// One workgroup per (slot, 16-row tile) of the expert selected for the slot
+// (expert_ids[slot], or expert_base + slot without ids: no dependent load): four
+// waves split the tile's K range (each wave's dependency chain is a quarter of the
+// row), and their partial sums are added in wave order.  The x loads are issued
+// first, then the weight loads, all unconditionally: an invalid expert reads expert
+// 0 and its rows become NaN.
+constexpr int kMvSplit = 4;
+using MvSplit = mxt::Split<kMvSplit>;
+
+__global__ __launch_bounds__(kMvSplit * 64) void matvec_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows, uint32_t tiles,
     uint32_t experts, const float *__restrict__ bias, const float *__restrict__ x, uint32_t x_stride,
-    const int32_t *__restrict__ expert_ids, float *__restrict__ y) {
-    __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
-    const uint32_t groups = (tiles + kWaves - 1) / kWaves;
-    const uint32_t slot = blockIdx.x / groups;
-    const uint32_t tile = (blockIdx.x % groups) * kWaves + threadIdx.x / 64;
-    const uint32_t lane = threadIdx.x % 64;
+    const int32_t *__restrict__ expert_ids, uint32_t expert_base, float *__restrict__ y) {
+    __shared__ __attribute__((aligned(16))) float xs[MvSplit::x_floats];
+    __shared__ float red[stage::red_floats(MvSplit::x_blocks)];
+    __shared__ float part[kMvSplit][mx::tile_rows];
+    const uint32_t slot = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+    const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
 
-    const int32_t e = expert_ids[slot];
-    const bool valid = tile < tiles && e >= 0 && uint32_t(e) < experts;
-    mxt::TileRegs regs;
-    if (valid) {
-        mxt::tile_load(codes, scales, size_t(e) * tiles + tile, lane, regs);
-    }
-    mxt::stage_x(x + size_t(slot) * x_stride, xs);
-    __syncthreads();
-    if (tile >= tiles) {
-        return;
-    }
+    stage::Input in{};
+    in.base = x + size_t(slot) * x_stride;
+    stage::Pending<mx::cols, MvSplit::x_blocks, kMvSplit * 64, stage::kPlain> pending;
+    stage::stage_load(in, pending);
+    const int32_t e = expert_ids ? expert_ids[slot] : int32_t(expert_base + slot);
+    const bool valid = e >= 0 && uint32_t(e) < experts;
+    const uint32_t e_safe = valid ? uint32_t(e) : 0u;
     const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
-    if (!valid) {
-        if (lane < mx::tile_rows) {
-            y[size_t(slot) * rows + row] = __builtin_nanf("");
-        }
-        return;
-    }
-    const float acc = mxt::tile_compute(regs, xs, lane);
+    const float bv = bias ? bias[size_t(e_safe) * rows + row] : 0.0f;
+    mxt::SplitRegs<kMvSplit> regs;
+    mxt::split_load<kMvSplit>(codes, scales, size_t(e_safe) * tiles + tile, w, lane, regs);
+    stage::stage_finish(in, pending, xs, red);
+    const float acc = mxt::split_compute<kMvSplit>(regs, xs, w, lane);
     if (lane < mx::tile_rows) {
-        y[size_t(slot) * rows + row] = bias ? acc + bias[size_t(e) * rows + row] : acc;
+        part[w][lane] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < uint32_t(mx::tile_rows)) {
+        float sum = part[0][threadIdx.x];
+#pragma unroll
+        for (int k = 1; k < kMvSplit; ++k) {
+            sum += part[k][threadIdx.x];
+        }
+        y[size_t(slot) * rows + row] = valid ? (bias ? sum + bv : sum) : __builtin_nanf("");
     }
 }
 
@@ -330,26 +341,31 @@ int ttl_matvec_mxfp4_experts(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias
     if (n == 0) {
         return TTL_OK;
     }
-    const uint32_t groups = (w->tiles + kWaves - 1) / kWaves;
-    const size_t grid = size_t(groups) * n;
+    const size_t grid = size_t(w->tiles) * n;
     TTL_REQUIRE(grid < (1u << 31), TTL_ERR_SHAPE, "ttl_matvec_mxfp4_experts: too many slots");
-    matvec_kernel<<<unsigned(grid), kWaves * 64, 0, ctx->stream>>>(w->codes, w->scales, w->rows,
-                                                                   w->tiles, w->experts, bias_dev, x_dev, x_stride,
-                                                                   experts_dev, y_dev);
+    matvec_kernel<<<unsigned(grid), kMvSplit * 64, 0, ctx->stream>>>(w->codes, w->scales, w->rows, w->tiles,
+                                                                     w->experts, bias_dev, x_dev, x_stride,
+                                                                     experts_dev, 0u, y_dev);
     TTL_LAUNCHED("matvec_kernel");
     return TTL_OK;
 }
 
 int ttl_matvec_mxfp4(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev, float *y_dev,
                      uint32_t expert) {
-    TTL_REQUIRE(ctx, TTL_ERR_INVALID, "ttl_matvec_mxfp4: null context");
+    TTL_REQUIRE(ctx && x_dev && y_dev, TTL_ERR_INVALID, "ttl_matvec_mxfp4: null argument");
     int rc = check_tensor(w, "ttl_matvec_mxfp4");
     if (rc != TTL_OK) {
         return rc;
     }
-    TTL_REQUIRE(expert < w->experts && expert < uint32_t(ttl::iota_size), TTL_ERR_INVALID,
-                "ttl_matvec_mxfp4: expert %u out of range (%u experts)", expert, w->experts);
-    return ttl_matvec_mxfp4_experts(ctx, w, bias_dev, x_dev, 0, ctx->iota + expert, 1, y_dev);
+    TTL_REQUIRE(expert < w->experts, TTL_ERR_INVALID, "ttl_matvec_mxfp4: expert %u out of range (%u experts)", expert,
+                w->experts);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0, TTL_ERR_INVALID,
+                "ttl_matvec_mxfp4: x must be 16-byte aligned");
+    // the expert is known here: the kernel takes it as an argument, with no id load
+    matvec_kernel<<<w->tiles, kMvSplit * 64, 0, ctx->stream>>>(w->codes, w->scales, w->rows, w->tiles, w->experts,
+                                                               bias_dev, x_dev, 0u, nullptr, expert, y_dev);
+    TTL_LAUNCHED("matvec_kernel");
+    return TTL_OK;
 }
 
 }  // extern "C"
