@@ -57,12 +57,19 @@ constexpr int kMmRows = kMmWaves * kMmTiles * 16;
 // Hidden planes between gate/up and down: three, exact (the hidden is f32).
 constexpr int kHiddenPlanes = 3;
 
+// A tile holding at most kNarrowSlots slots (the remainder of an expert's bucket) is
+// "narrow": its GEMMs run on the first kNarrowCols column tiles only, in a launch of
+// their own, so a bucket of 70 slots costs 64 + 32 columns instead of 64 + 64.
+constexpr int kNarrowCols = 2;
+constexpr uint32_t kNarrowSlots = kNarrowCols * 16;
+
 // ---- the plan ------------------------------------------------------------------
 
 struct PlanHeader {
     uint32_t tiles;    // token tiles in use
     uint32_t invalid;  // pairs whose expert index was out of range
-    uint32_t pad[62];
+    uint32_t wide;     // tiles [0, wide) hold more than kNarrowSlots slots, [wide, tiles) at most that
+    uint32_t pad[61];
 };
 
 // Device pointers into the caller's workspace.
@@ -150,7 +157,8 @@ Plan plan_at(void *workspace, const Layout &L) {
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__restrict__ indices,
                                                             const float *__restrict__ weights, uint32_t pairs,
                                                             uint32_t used, uint32_t experts, Plan plan) {
-    __shared__ uint32_t count[kMaxExperts], base[kMaxExperts], running[kMaxExperts];
+    __shared__ uint32_t count[kMaxExperts], base[kMaxExperts], running[kMaxExperts], narrow_of[kMaxExperts];
+    __shared__ uint32_t wide_total;
     __shared__ uint32_t wave_count[kPlanThreads / 64][kMaxExperts];
     __shared__ uint32_t invalid;
     const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
@@ -172,23 +180,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__res
     }
     __syncthreads();
     if (t == 0) {
-        uint32_t slots = 0, tiles = 0;
+        // wide tiles in expert order first, then the narrow ones (an expert's last tile
+        // when it holds at most kNarrowSlots slots), also in expert order
+        uint32_t slots = 0, wide = 0, narrow = 0;
         for (uint32_t e = 0; e < experts; ++e) {
             base[e] = slots;
             slots += count[e];
-            running[e] = tiles;  // first tile of expert e (reset below)
-            tiles += (count[e] + mf::tile_slots - 1) / mf::tile_slots;
+            const uint32_t tiles = (count[e] + mf::tile_slots - 1) / mf::tile_slots;
+            const bool last_narrow = tiles > 0 && count[e] - (tiles - 1) * mf::tile_slots <= kNarrowSlots;
+            running[e] = wide;  // first wide tile of expert e (reset below)
+            wide += tiles - (last_narrow ? 1 : 0);
+            narrow_of[e] = last_narrow ? narrow++ : ~0u;
         }
-        plan.header->tiles = tiles;
+        wide_total = wide;
+        plan.header->tiles = wide + narrow;
+        plan.header->wide = wide;
         plan.header->invalid = invalid;
     }
     __syncthreads();
     for (uint32_t e = t; e < experts; e += kPlanThreads) {
-        const uint32_t first_tile = running[e], n = count[e];
+        const uint32_t n = count[e];
         for (uint32_t j = 0; j * mf::tile_slots < n; ++j) {
-            plan.tile_expert[first_tile + j] = e;
-            plan.tile_first[first_tile + j] = base[e] + j * mf::tile_slots;
-            plan.tile_count[first_tile + j] = min(uint32_t(mf::tile_slots), n - j * mf::tile_slots);
+            const bool last = (j + 1) * mf::tile_slots >= n;
+            const uint32_t tile = last && narrow_of[e] != ~0u ? wide_total + narrow_of[e] : running[e] + j;
+            plan.tile_expert[tile] = e;
+            plan.tile_first[tile] = base[e] + j * mf::tile_slots;
+            plan.tile_count[tile] = min(uint32_t(mf::tile_slots), n - j * mf::tile_slots);
         }
     }
     __syncthreads();
@@ -251,6 +268,7 @@ __global__ void plan_selected_kernel(const int32_t *__restrict__ tokens, uint32_
     const uint32_t tiles = (count + mf::tile_slots - 1) / mf::tile_slots;
     if (i == 0) {
         plan.header->tiles = tiles;
+        plan.header->wide = tiles;  // one launch over every tile
         plan.header->invalid = 0;
     }
     if (i < tiles) {
@@ -432,14 +450,15 @@ struct AOperand {
 // next stage is readable only after the barrier that ends this one), so the wave
 // waits for LDS about once per stage rather than once per fragment.
 // decode(s, w) fills the M A fragments of step s of the quad; stage_end(stage)
-// runs after the last MFMA of each stage (publishes the next one).
-template <int P, int M, int LOOK, class Decode, class StageEnd>
+// runs after the last MFMA of each stage (publishes the next one).  Only the first
+// NC column tiles are multiplied (narrow tiles leave the others unread).
+template <int P, int M, int LOOK, int NC, class Decode, class StageEnd>
 __device__ __attribute__((always_inline)) inline void quad_mfma(const mf::u32x4 *buf0, const mf::u32x4 *buf1,
                                                                 int i, uint32_t lane, Decode &&decode,
-                                                                StageEnd &&stage_end,
-                                                                f32x4 (&acc)[M][mf::col_tiles]) {
+                                                                StageEnd &&stage_end, f32x4 (&acc)[M][NC]) {
     using SS = StageShape<P>;
-    constexpr int FPS = P * mf::col_tiles;  // fragments per K step
+    static_assert(NC >= 1 && NC <= mf::col_tiles, "column tiles");
+    constexpr int FPS = P * NC;  // fragments per K step
     constexpr int SF = SS::steps * FPS;     // fragments per stage
     constexpr int D = LOOK < SF ? LOOK : SF;
 #pragma unroll
@@ -505,7 +524,7 @@ struct GateUpArgs {
 // over the chip's 8 XCDs (each with its own L2), so consecutive logical indices
 // are taken from the same XCD: all row groups of one token tile then read its
 // activation fragments through one L2.  Workgroups past the tiles in use return.
-__device__ inline bool tile_of_workgroup(uint32_t tiles, uint32_t &tile, uint32_t &row_group) {
+__device__ inline bool tile_in_range(uint32_t tiles, uint32_t &tile, uint32_t &row_group) {
     const uint32_t groups = gridDim.x;
     const uint32_t id = blockIdx.y * groups + blockIdx.x;
     const uint32_t active = tiles * groups;
@@ -518,14 +537,28 @@ __device__ inline bool tile_of_workgroup(uint32_t tiles, uint32_t &tile, uint32_
     return true;
 }
 
-// Accumulators: [matrix (gate 0/1, up 2/3)][column tile]
-template <int PX>
+// NC = mf::col_tiles takes the plan's wide tiles, NC < mf::col_tiles its narrow ones.
+template <int NC>
+__device__ inline bool tile_of_workgroup(const PlanHeader *header, uint32_t &tile, uint32_t &row_group) {
+    const bool narrow = NC < mf::col_tiles;
+    const uint32_t first = narrow ? header->wide : 0u;
+    const uint32_t tiles = narrow ? header->tiles - header->wide : header->wide;
+    if (!tile_in_range(tiles, tile, row_group)) {
+        return false;
+    }
+    tile += first;
+    return true;
+}
+
+// Accumulators: [matrix (gate 0/1, up 2/3)][column tile]; NC column tiles (the plan's
+// wide tiles with all of them, or its narrow ones with kNarrowCols).
+template <int PX, int NC>
 __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void gateup_kernel(GateUpArgs a) {
     using SS = StageShape<PX>;
     constexpr int kThreads = kGuWaves * 64;
     __shared__ mf::u32x4 lds[2][Stager<PX, kThreads>::lds_chunks];
     uint32_t tile, row_group;
-    if (!tile_of_workgroup(a.plan.header->tiles, tile, row_group)) {
+    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
         return;
     }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
@@ -543,7 +576,7 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     ga.init(a.gate_codes, a.gate_scales, ti, lane);
     ua.init(a.up_codes, a.up_scales, ti, lane);
 
-    f32x4 acc[4][mf::col_tiles];
+    f32x4 acc[4][NC];
     {
         const uint32_t g = lane / 16;
 #pragma unroll
@@ -556,7 +589,7 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
                 b = f32x4{v.x, v.y, v.z, v.w};
             }
 #pragma unroll
-            for (int c = 0; c < mf::col_tiles; ++c) {
+            for (int c = 0; c < NC; ++c) {
                 acc[m][c] = b;
             }
         }
@@ -610,7 +643,7 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
             }
         };
         // three activation planes leave registers for a shorter lookahead only
-        quad_mfma<PX, 4, PX == 1 ? 4 : 2>(lds[0], lds[1], i, lane, decode, stage_end, acc);
+        quad_mfma<PX, 4, PX == 1 ? 4 : 2, NC>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
     rotate_quads(qa, load_quad, compute_quad);
@@ -625,7 +658,7 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     const uint32_t g = lane / 16, n16 = lane % 16;
     uint8_t *hb = a.plan.hb + size_t(tile) * kHiddenPlanes * mf::plane_bytes;
 #pragma unroll
-    for (int c = 0; c < mf::col_tiles; ++c) {
+    for (int c = 0; c < NC; ++c) {
         float h[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -662,13 +695,13 @@ struct MatmulArgs {
     uint32_t out_rows;   // SCATTER: rows of out (tokens beyond are skipped)
 };
 
-template <int P, bool SCATTER>
+template <int P, bool SCATTER, int NC>
 __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
     using SS = StageShape<P>;
     constexpr int kThreads = kMmWaves * 64;
     __shared__ mf::u32x4 lds[2][Stager<P, kThreads>::lds_chunks];
     uint32_t tile, row_group;
-    if (!tile_of_workgroup(a.plan.header->tiles, tile, row_group)) {
+    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
         return;
     }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
@@ -687,7 +720,7 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
     }
     wa.init(a.codes, a.scales, ti, lane);
 
-    f32x4 acc[kMmTiles][mf::col_tiles];
+    f32x4 acc[kMmTiles][NC];
     {
         const uint32_t g = lane / 16;
 #pragma unroll
@@ -699,7 +732,7 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
                 b = f32x4{v.x, v.y, v.z, v.w};
             }
 #pragma unroll
-            for (int c = 0; c < mf::col_tiles; ++c) {
+            for (int c = 0; c < NC; ++c) {
                 acc[m][c] = b;
             }
         }
@@ -739,7 +772,7 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
                 w[m] = mf::decode_step(word, sc[m]);
             }
         };
-        quad_mfma<P, kMmTiles, 4>(lds[0], lds[1], i, lane, decode, stage_end, acc);
+        quad_mfma<P, kMmTiles, 4, NC>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
     for (int i = 0; i < mf::quads; i += 3) {
@@ -761,7 +794,7 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
     const uint32_t cnt = a.plan.tile_count[tile], first = a.plan.tile_first[tile];
     const uint32_t g = lane / 16, n16 = lane % 16;
 #pragma unroll
-    for (int c = 0; c < mf::col_tiles; ++c) {
+    for (int c = 0; c < NC; ++c) {
         const uint32_t n = c * 16 + n16;
         if (n >= cnt) {
             continue;
@@ -911,7 +944,7 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     m.plan = plan;
     m.out = out_dev;
     m.out_rows = x_rows;
-    matmul_kernel<3, true><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
+    matmul_kernel<3, true, mf::col_tiles><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
     TTL_LAUNCHED("matmul_kernel");
     return TTL_OK;
 }
@@ -986,12 +1019,16 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     g.rows = L.expert_hidden;
     g.tiles_per_expert = L.gate->tiles;
     g.plan = plan;
-    const dim3 gu_grid((L.expert_hidden + kGuRows - 1) / kGuRows, lay.tmax);
+    // the wide tiles, then the narrow ones (at most one per expert)
+    const uint32_t gu_groups = (L.expert_hidden + kGuRows - 1) / kGuRows;
+    const dim3 gu_wide(gu_groups, lay.tmax), gu_narrow(gu_groups, min(lay.tmax, L.experts));
     if (stages & TTL_PREFILL_GATEUP) {
         if (bf16) {
-            gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<1, mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<1, kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
         } else {
-            gateup_kernel<3><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<3, mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<3, kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
         }
         TTL_LAUNCHED("gateup_kernel");
     }
@@ -1007,8 +1044,10 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     m.out = plan.down;
     m.out_rows = 0;
     if (stages & TTL_PREFILL_DOWN) {
-        matmul_kernel<kHiddenPlanes, false>
+        matmul_kernel<kHiddenPlanes, false, mf::col_tiles>
             <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
+        matmul_kernel<kHiddenPlanes, false, kNarrowCols>
+            <<<dim3(L.hidden / kMmRows, min(lay.tmax, L.experts)), kMmWaves * 64, 0, ctx->stream>>>(m);
         TTL_LAUNCHED("matmul_kernel");
     }
     if (stages & TTL_PREFILL_COMBINE) {
