@@ -85,6 +85,23 @@ def test_prefill_matches_oracle_layer_by_layer(host):
         gpu.close()
 
 
+@pytest.mark.parametrize("count", [1, 17])
+def test_prefill_short_prompts(host, count):
+    """One token (every GEMM tile narrow, one attention block) and 17 (a second attention
+    block of one token), teacher-forced against the oracle's prefill layers."""
+    capacity = 32
+    gpu = ttlab_amd.Model(LAYERS, EXPERTS, VOCAB, capacity, SEED)
+    try:
+        tokens = [int(t) for t in np.random.default_rng(43 + count).integers(0, VOCAB, count)]
+        logits = gpu.prefill(tokens)
+        checked = check_pass(gpu, host, 0, count, capacity)
+        assert checked >= LAYERS * count - 1
+        ref = host.logits(gpu.prefill_state(LAYERS, count)[count - 1])
+        assert O.rel_l2(logits, ref) <= TOL
+    finally:
+        gpu.close()
+
+
 def test_prefill_in_two_passes(host):
     capacity, count = 600, 530
     gpu = ttlab_amd.Model(LAYERS, EXPERTS, VOCAB, capacity, SEED)
