@@ -642,8 +642,9 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
                 w[m] = mf::decode_step(word, sc[m]);
             }
         };
-        // three activation planes leave registers for a shorter lookahead only
-        quad_mfma<PX, 4, PX == 1 ? 4 : 2, NC>(lds[0], lds[1], i, lane, decode, stage_end, acc);
+        // B fragments four ahead of their MFMAs for one plane and for three (with three
+        // planes this fits the 256 registers of two waves per SIMD without spilling)
+        quad_mfma<PX, 4, 4, NC>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
     rotate_quads(qa, load_quad, compute_quad);
