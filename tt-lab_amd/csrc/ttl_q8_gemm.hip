@@ -36,10 +36,7 @@ constexpr int kWaves = 4;
 // 16-row weight tiles per wave: one.  The projections have 2880 and 5120 rows, so more
 // tiles per workgroup leave CUs idle at a 512-token prompt (measured: one tile per wave
 // beat two and three in the layer-major prefill).
-template <int K>
-constexpr int row_tiles_for() {
-    return 1;
-}
+constexpr int kRowTiles = 1;
 constexpr int kLook = 4;  // token fragments read from LDS this many ahead
 
 template <int K>
@@ -121,7 +118,6 @@ struct GemmArgs {
 template <int K>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void q8_gemm_kernel(GemmArgs a) {
     using S = Shape<K>;
-    constexpr int kRowTiles = row_tiles_for<K>();
     constexpr int kThreads = kWaves * 64;
     constexpr int kPer = S::stage_chunks / kThreads;
     static_assert(S::stage_chunks % kThreads == 0, "the stager moves whole pieces");
@@ -353,7 +349,7 @@ int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
     a.rows = w->rows;
     a.row_tiles = w->tiles;
     a.tokens = tokens;
-    const uint32_t group = uint32_t(kWaves * (w->cols == 2880 ? row_tiles_for<2880>() : row_tiles_for<4096>()));
+    const uint32_t group = uint32_t(kWaves * kRowTiles);
     const dim3 grid((w->tiles + group - 1) / group, tiles);
     uint8_t *frags = static_cast<uint8_t *>(workspace_dev);
     if (w->cols == 2880) {
