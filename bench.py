@@ -240,19 +240,22 @@ def gpu_matvec(args):
         for w in mats:
             dev.matvec_mxfp4(w, None, x, y, 0)
 
-    graph = dev.capture(step)
+    # --eager launches one by one (for kernel tracers that do not follow graph launches)
+    graph = None if args.eager else dev.capture(step)
+    run = step if args.eager else graph.launch
     for _ in range(max(args.warmup, 1)):
-        graph.launch()
+        run()
     dev.sync()
     reps = max(20, args.steps)
     dev.timer_start()
     for _ in range(reps):
-        graph.launch()
+        run()
     ms = dev.timer_stop()
     us = ms * 1e3 / (reps * MATVEC_COPIES)
     gbs = MATVEC_BYTES / (us * 1e-6) / 1e9
     log(f"config 0 matvec: {us:.3f} us per launch, {gbs:.0f} GB/s over {MATVEC_COPIES} rotated copies")
-    graph.free()
+    if graph:
+        graph.free()
     for w in mats:
         w.free()
     dev.close()
