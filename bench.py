@@ -174,31 +174,35 @@ def gpu_moe(args):
         for L in layers:
             dev.moe_decode(L["desc"], L["x"], L["out"], L["idx"], L["w"])
 
-    graph = dev.capture(step)
-    for _ in range(max(args.warmup, 1)):
-        graph.launch()
-    dev.sync()
-    dev.timer_start()
-    for _ in range(args.steps):
-        graph.launch()
-    ms = dev.timer_stop() / args.steps
-
     def gateup():
         for L in layers:
             dev.moe_gateup_swiglu(L["desc"], L["x"], L["idx"], L["hidden"])
 
-    g2 = dev.capture(gateup)
+    # --eager launches one by one (for kernel tracers that do not follow graph launches)
+    graph = None if args.eager else dev.capture(step)
+    run = step if args.eager else graph.launch
+    for _ in range(max(args.warmup, 1)):
+        run()
+    dev.sync()
+    dev.timer_start()
+    for _ in range(args.steps):
+        run()
+    ms = dev.timer_stop() / args.steps
+
+    g2 = None if args.eager else dev.capture(gateup)
+    run2 = gateup if args.eager else g2.launch
     for _ in range(3):
-        g2.launch()
+        run2()
     dev.sync()
     reps = max(20, args.steps)
     dev.timer_start()
     for _ in range(reps):
-        g2.launch()
+        run2()
     us = dev.timer_stop() * 1e3 / (reps * LAYERS)
     achieved = GATEUP_BYTES / (us * 1e-6) / 1e9
-    graph.free()
-    g2.free()
+    for g in (graph, g2):
+        if g:
+            g.free()
     dev.close()
     layer_bytes = EXPERTS * N * 2 + USED * 3 * N * 1530 + N * 4 + N * 4 + 128
     return {
