@@ -135,6 +135,31 @@ def test_moe_decode_exact_routing_inside_gateup(dev):
     device.free()
 
 
+@pytest.mark.parametrize("experts,used", [(7, 4), (64, 16), (128, 4), (192, 8)])
+def test_moe_decode_routing_inside_gateup_at_other_widths(dev, experts, used):
+    """The gate/up kernel ranks the router rows in one wave, lane l holding experts l,
+    l+64 and l+128: one, two and three candidates per lane, and up to 16 ranks.  The
+    selected experts and weights must be the reference's."""
+    host = HostLayer(experts, used, biases=True, fill_experts=[])
+    device = DeviceLayer(dev, host)
+    out, ib, wb = dev.alloc(N * 4), dev.alloc(used * 4), dev.alloc(used * 4)
+    before = dev.router_exact_count()
+    for token in range(4):
+        x = O.synth_normal(X_SEED, 100 + token, N)
+        xb = dev.upload(x)
+        dev.moe_decode(device.desc, xb, out, ib, wb)
+        _, ref_idx, ref_w = oracle_router(host.router_w, host.router_b, x, used)
+        print(f"experts {experts} used {used} token {token}: {list(ref_idx)}", flush=True)
+        assert list(ib.download(np.int32)) == list(ref_idx)
+        assert np.allclose(wb.download(np.float32), ref_w, rtol=1e-5, atol=0)
+        xb.free()
+    # the certified ranking (not the exact fallback) decided most tokens
+    assert dev.router_exact_count() - before < 4
+    for b in (out, ib, wb):
+        b.free()
+    device.free()
+
+
 @pytest.mark.parametrize("body", [O.BODY_V4, O.BODY_DEFAULT])
 def test_moe_layer_config1_matches_oracle(dev, layer32, body):
     host, device = layer32

@@ -356,6 +356,149 @@ __device__ void route_certified(uint32_t experts, uint32_t k, bool force_exact, 
     }
 }
 
+// Order-preserving key of a double: a > b (neither NaN) gives key(a) >= key(b),
+// strictly for unequal values except -0.0 below +0.0.
+__device__ inline uint64_t order_key(double v) {
+    const uint64_t u = uint64_t(__double_as_longlong(v));
+    return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__device__ inline double key_value(uint64_t key) {
+    return __longlong_as_double((key >> 63) ? (long long)(key & 0x7fffffffffffffffull) : (long long)(~key));
+}
+
+__device__ inline uint64_t readlane_u64(uint64_t x, uint32_t lane) {
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(x)), int(lane)));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(x >> 32)), int(lane)));
+    return (uint64_t(hi) << 32) | lo;
+}
+
+// max(x, x of the lane that the DPP pattern CTRL names); every pattern used stays
+// inside a row of 16 lanes
+template <int CTRL>
+__device__ inline uint64_t max_dpp(uint64_t x) {
+    const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(x)), CTRL, 0xf, 0xf, false));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(x >> 32)), CTRL, 0xf, 0xf, false));
+    const uint64_t y = (uint64_t(hi) << 32) | lo;
+    return y > x ? y : x;
+}
+
+// Maximum over the 64 lanes of a wave (all lanes active); the result is uniform.
+// Quad swaps, then the half-row and row mirrors leave each row's maximum in all
+// its lanes; the four rows meet through lane reads.
+__device__ inline uint64_t wave_max_u64(uint64_t x) {
+    x = max_dpp<0xb1>(x);   // quad_perm [1,0,3,2]
+    x = max_dpp<0x4e>(x);   // quad_perm [2,3,0,1]
+    x = max_dpp<0x141>(x);  // row_half_mirror
+    x = max_dpp<0x140>(x);  // row_mirror
+    uint64_t m = readlane_u64(x, 0);
+#pragma unroll
+    for (uint32_t r = 1; r < 4; ++r) {
+        const uint64_t y = readlane_u64(x, 16 * r);
+        m = y > m ? y : m;
+    }
+    return m;
+}
+
+// The certified ranking of route_certified() computed by wave 0 alone, in
+// registers, for the routed gate/up kernel where every workgroup ranks the rows
+// itself.  Lane l holds experts l, l+64, l+128.  A candidate's key is the order
+// key of its exact value with the low byte replaced by 255 - expert, so one wave
+// maximum per rank picks the largest value (the lowest index among equal keys).
+// The truncated byte only matters for values the certificate rejects anyway:
+// the certificate compares the exact values and bounds, value - bound of rank r
+// > value + bound of every expert ranked below r, which holds only if the
+// values are strictly ordered as ranked (bounds are positive).  Checked as
+// up(r') < min(low of ranks before r') at each rank and max(up of the unselected)
+// < min(low of all selected) at the end.  Leaves indices, selected values and
+// lds.certified (and, when `publish`, weights and logits) in lds; ends with the
+// workgroup's one barrier.
+__device__ void route_certified_wave(uint32_t experts, uint32_t k, const RouterScratch *scratch, RouteLds &lds,
+                                     float *__restrict__ logits, bool publish) {
+    if (threadIdx.x < 64) {
+        const uint32_t lane = threadIdx.x;
+        uint64_t key[kPerLane];
+        double low[kPerLane], up[kPerLane];
+        float value[kPerLane];
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const uint32_t c = lane + 64 * j;
+            key[j] = 0;
+            low[j] = 0.0;
+            up[j] = -INFINITY;
+            value[j] = 0.0f;
+            if (c < experts) {
+                const double v = scratch->exact[c], b = scratch->bound[c];
+                bad = bad || !isfinite(v) || !isfinite(b);
+                key[j] = (order_key(v) & ~uint64_t(0xff)) | (0xff - c);
+                low[j] = v - b;
+                up[j] = v + b;
+                value[j] = float(v);
+            }
+        }
+        bool ok = __ballot(bad) == 0;
+        double min_low = INFINITY;
+        for (uint32_t r = 0; r < k; ++r) {
+            uint64_t m = key[0];
+#pragma unroll
+            for (int j = 1; j < kPerLane; ++j) {
+                m = key[j] > m ? key[j] : m;
+            }
+            const uint32_t c = 0xff - uint32_t(wave_max_u64(m) & 0xff);
+            const uint32_t owner = c % 64, piece = c / 64;
+            double lo_c = low[0], up_c = up[0];
+            float v_c = value[0];
+#pragma unroll
+            for (int j = 1; j < kPerLane; ++j) {
+                if (piece == uint32_t(j)) {
+                    lo_c = low[j];
+                    up_c = up[j];
+                    v_c = value[j];
+                }
+            }
+            const double w_low = __longlong_as_double((long long)readlane_u64(uint64_t(__double_as_longlong(lo_c)), owner));
+            const double w_up = __longlong_as_double((long long)readlane_u64(uint64_t(__double_as_longlong(up_c)), owner));
+            const float w_v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_c), int(owner)));
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                if (lane + 64 * j == c) {
+                    key[j] = 0;
+                    up[j] = -INFINITY;
+                }
+            }
+            ok = ok && (r == 0 || w_up < min_low);
+            min_low = fmin(min_low, w_low);
+            if (lane == 0) {
+                lds.indices[r] = int32_t(c);
+                lds.selected[r] = w_v;
+            }
+        }
+        uint64_t u = order_key(up[0]);
+#pragma unroll
+        for (int j = 1; j < kPerLane; ++j) {
+            const uint64_t y = order_key(up[j]);
+            u = y > u ? y : u;
+        }
+        ok = ok && min_low > key_value(wave_max_u64(u));
+        if (lane == 0) {
+            lds.certified = ok ? 1 : 0;
+            if (ok && publish) {
+                softmax_selected(lds.selected, k, lds.weights);
+            }
+        }
+        if (ok && publish && logits) {
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                if (lane + 64 * j < experts) {
+                    logits[lane + 64 * j] = value[j];
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // The reference's selection sort (model.cpp:296-309) replayed on lds.ref_logits, then
 // the softmax of the selected logits.  Wave 0 only; ends with a barrier.
 __device__ __forceinline__ void replay_selection(uint32_t experts, uint32_t k, RouterScratch *scratch, RouteLds &lds,
@@ -599,9 +742,10 @@ struct GateUpArgs {
     float *weights_out, *logits_out;
 };
 
-// ROUTE: every workgroup ranks the router rows itself (route_workgroup, the
-// certified selection or the exact fallback) instead of reading a separate
-// selection kernel's indices; the input loads are in flight meanwhile.
+// ROUTE: every workgroup ranks the router rows itself (route_certified_wave in
+// wave 0, or the exact fallback when the ranking is not certified) instead of
+// reading a separate selection kernel's indices; the input loads are in flight
+// meanwhile.
 template <int MODE, bool ROUTE>
 __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[GateUpSplit::x_floats];
@@ -622,7 +766,7 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
         // workgroup 0 publishes the routing; the others only need the indices
         const bool first = blockIdx.x == 0;
         float *logits = first ? a.logits_out : nullptr;
-        route_certified(a.experts, a.k, false, a.scratch, rl, logits, first);
+        route_certified_wave(a.experts, a.k, a.scratch, rl, logits, first);
         if (!rl.certified) {
             // rare: the exact path needs the staged input first
             stage::stage_finish(a.in, pending, xs, red);
