@@ -265,10 +265,6 @@ struct RouteLds {
     float selected[kMaxUsed];
     float ref_logits[kMaxExperts];
     int32_t order[kMaxExperts];
-    double value[kMaxExperts];  // exact logits
-    double bound[kMaxExperts];
-    double up[kMaxExperts];  // value + bound
-    uint32_t rank[kMaxExperts];
     int certified;
 };
 
@@ -278,82 +274,6 @@ __device__ inline double wave_max(double v) {
         v = fmax(v, __shfl_xor(v, d));
     }
     return v;
-}
-
-// Routing for one token, computed by the whole workgroup (blockDim.x >= experts),
-// in two parts.  route_certified() ranks the exact rows; when the ranking is
-// certified it leaves indices/weights in lds (and writes the logits when `logits`
-// is non-null -- only one workgroup of a launch does that) and lds.certified = 1.
-// Otherwise route_exact() recomputes the logits in the reference's order from the
-// staged router input xs (the same values the router rows saw) and replays the
-// reference's selection sort (it also bumps the exact-path counter when `logits`
-// is non-null).  Both end with a barrier, so lds.certified is uniform.
-__device__ void route_certified(uint32_t experts, uint32_t k, bool force_exact, const RouterScratch *scratch,
-                                RouteLds &lds, float *__restrict__ logits, bool publish) {
-    const uint32_t t = threadIdx.x;
-    // ---- certified path ------------------------------------------------------
-    // Thread c < experts ranks expert c by (exact value descending, index
-    // ascending) -- the order the reference's selection sort produces when no two
-    // values are within their error bounds -- and checks that separation for the
-    // top k: value - bound of rank r must exceed value + bound of every expert
-    // ranked below r.  Only LDS broadcast reads, no cross-lane chains.  The
-    // softmax weights (and logits) are computed only when `publish` is set, which
-    // must be the same for the whole workgroup; indices are always left in lds.
-    if (t == 0) {
-        lds.certified = force_exact ? 0 : 1;
-    }
-    if (t < experts) {
-        const double v = scratch->exact[t], b = scratch->bound[t];
-        lds.value[t] = v;
-        lds.bound[t] = b;
-        lds.up[t] = v + b;
-        if (!isfinite(v) || !isfinite(b)) {
-            lds.certified = 0;
-        }
-    }
-    __syncthreads();
-    if (t < experts) {
-        const double v = lds.value[t];
-        uint32_t rank = 0;
-#pragma unroll 8
-        for (uint32_t j = 0; j < experts; ++j) {
-            const double vj = lds.value[j];
-            rank += (vj > v || (vj == v && j < t)) ? 1u : 0u;
-        }
-        lds.rank[t] = rank;
-        if (rank < k) {
-            lds.indices[rank] = int32_t(t);
-            lds.selected[rank] = float(v);
-        }
-    }
-    __syncthreads();
-    if (t < experts && lds.rank[t] < k) {
-        const uint32_t rank = lds.rank[t];
-        const double low = lds.value[t] - lds.bound[t];
-        double up = -INFINITY;
-#pragma unroll 8
-        for (uint32_t j = 0; j < experts; ++j) {
-            // arithmetic masking (finite values here), so no branch holds back the
-            // LDS reads of the unrolled iterations
-            const double mask = lds.rank[j] > rank ? 0.0 : -INFINITY;
-            up = fmax(up, lds.up[j] + mask);
-        }
-        if (!(low > up)) {
-            lds.certified = 0;
-        }
-    }
-    __syncthreads();
-    if (publish) {
-        if (lds.certified) {
-            if (t == 0) {
-                softmax_selected(lds.selected, k, lds.weights);
-            }
-            if (logits && t < experts) {
-                logits[t] = float(lds.value[t]);
-            }
-        }
-        __syncthreads();
-    }
 }
 
 // Order-preserving key of a double: a > b (neither NaN) gives key(a) >= key(b),
@@ -400,9 +320,19 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
     return m;
 }
 
-// The certified ranking of route_certified() computed by wave 0 alone, in
-// registers, for the routed gate/up kernel where every workgroup ranks the rows
-// itself.  Lane l holds experts l, l+64, l+128.  A candidate's key is the order
+// Routing for one token comes in two parts.  route_certified_wave() ranks the
+// exact rows; when the ranking is certified it leaves the indices (and, when
+// `publish`, the softmax weights and -- if `logits` is non-null, in one workgroup
+// of a launch -- the logits) in lds with lds.certified = 1.  Otherwise (or with
+// force_exact) an exact path recomputes the logits in the reference's order from
+// the staged router input (the same values the router rows saw) and replays the
+// reference's selection sort.  Both end with a workgroup barrier, so
+// lds.certified is uniform.
+//
+// The ranking runs in wave 0 alone, in registers.  Thread c < experts would rank
+// expert c by (exact value descending, index ascending) -- the order the
+// reference's selection sort produces when no two values are within their error
+// bounds.  Lane l holds experts l, l+64, l+128.  A candidate's key is the order
 // key of its exact value with the low byte replaced by 255 - expert, so one wave
 // maximum per rank picks the largest value (the lowest index among equal keys).
 // The truncated byte only matters for values the certificate rejects anyway:
@@ -413,8 +343,8 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
 // < min(low of all selected) at the end.  Leaves indices, selected values and
 // lds.certified (and, when `publish`, weights and logits) in lds; ends with the
 // workgroup's one barrier.
-__device__ void route_certified_wave(uint32_t experts, uint32_t k, const RouterScratch *scratch, RouteLds &lds,
-                                     float *__restrict__ logits, bool publish) {
+__device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_exact, const RouterScratch *scratch,
+                                     RouteLds &lds, float *__restrict__ logits, bool publish) {
     if (threadIdx.x < 64) {
         const uint32_t lane = threadIdx.x;
         uint64_t key[kPerLane];
@@ -437,7 +367,7 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, const RouterS
                 value[j] = float(v);
             }
         }
-        bool ok = __ballot(bad) == 0;
+        bool ok = !force_exact && __ballot(bad) == 0;
         double min_low = INFINITY;
         for (uint32_t r = 0; r < k; ++r) {
             uint64_t m = key[0];
@@ -673,7 +603,7 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
                                 float *red, float *prod) {
-    route_certified(experts, k, force_exact, scratch, lds, logits, true);
+    route_certified_wave(experts, k, force_exact, scratch, lds, logits, true);
     if (!lds.certified) {
         stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
         route_exact_coop<PER>(weight, bias, experts, k, xs, scratch, lds, logits, prod);
@@ -766,7 +696,7 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
         // workgroup 0 publishes the routing; the others only need the indices
         const bool first = blockIdx.x == 0;
         float *logits = first ? a.logits_out : nullptr;
-        route_certified_wave(a.experts, a.k, a.scratch, rl, logits, first);
+        route_certified_wave(a.experts, a.k, false, a.scratch, rl, logits, first);
         if (!rl.certified) {
             // rare: the exact path needs the staged input first
             stage::stage_finish(a.in, pending, xs, red);
