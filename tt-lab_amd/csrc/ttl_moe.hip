@@ -343,7 +343,24 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
 // < min(low of all selected) at the end.  Leaves indices, selected values and
 // lds.certified (and, when `publish`, weights and logits) in lds; ends with the
 // workgroup's one barrier.
-__device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_exact, const RouterScratch *scratch,
+// Wave 0's share of the router rows (exact values and bounds), loaded ahead of
+// route_certified_wave() so a caller can issue the loads before others.
+struct RouteRows {
+    double v[kPerLane], b[kPerLane];
+};
+
+__device__ __forceinline__ void load_route_rows(uint32_t experts, const RouterScratch *scratch, RouteRows &rows) {
+    if (threadIdx.x < 64) {
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const uint32_t c = threadIdx.x + 64 * j;
+            rows.v[j] = c < experts ? scratch->exact[c] : 0.0;
+            rows.b[j] = c < experts ? scratch->bound[c] : 0.0;
+        }
+    }
+}
+
+__device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_exact, const RouteRows &rows,
                                      RouteLds &lds, float *__restrict__ logits, bool publish) {
     if (threadIdx.x < 64) {
         const uint32_t lane = threadIdx.x;
@@ -359,7 +376,7 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_ex
             up[j] = -INFINITY;
             value[j] = 0.0f;
             if (c < experts) {
-                const double v = scratch->exact[c], b = scratch->bound[c];
+                const double v = rows.v[j], b = rows.b[j];
                 bad = bad || !isfinite(v) || !isfinite(b);
                 key[j] = (order_key(v) & ~uint64_t(0xff)) | (0xff - c);
                 low[j] = v - b;
@@ -603,7 +620,9 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
                                 float *red, float *prod) {
-    route_certified_wave(experts, k, force_exact, scratch, lds, logits, true);
+    RouteRows rows;
+    load_route_rows(experts, scratch, rows);
+    route_certified_wave(experts, k, force_exact, rows, lds, logits, true);
     if (!lds.certified) {
         stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
         route_exact_coop<PER>(weight, bias, experts, k, xs, scratch, lds, logits, prod);
@@ -687,6 +706,12 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
 
     // input loads first (they depend on nothing), then the expert's weight loads;
     // the staging completes while those are in flight
+    // ROUTE: wave 0's router rows first (the ranking waits for them, and loads
+    // return in order), then the input loads, then the ranking
+    RouteRows rows;
+    if constexpr (ROUTE) {
+        load_route_rows(a.experts, a.scratch, rows);
+    }
     stage::Pending<mx::cols, GateUpSplit::x_blocks, kGateUpThreads, MODE> pending;
     stage::stage_load(a.in, pending);
     int32_t e;
@@ -696,7 +721,7 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
         // workgroup 0 publishes the routing; the others only need the indices
         const bool first = blockIdx.x == 0;
         float *logits = first ? a.logits_out : nullptr;
-        route_certified_wave(a.experts, a.k, false, a.scratch, rl, logits, first);
+        route_certified_wave(a.experts, a.k, false, rows, rl, logits, first);
         if (!rl.certified) {
             // rare: the exact path needs the staged input first
             stage::stage_finish(a.in, pending, xs, red);
