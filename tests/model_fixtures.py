@@ -73,14 +73,40 @@ class HostModelLayer:
         return s
 
 
+class _LazyLayers:
+    """Layer l of the host copy is generated the first time it is indexed, so a full
+    24- or 36-layer model costs only the layers a test reads."""
+
+    def __init__(self, seed, count, experts, lazy):
+        self.seed, self.count, self.experts, self.lazy = seed, count, experts, lazy
+        self.built = {}
+
+    def __len__(self):
+        return self.count
+
+    def __getitem__(self, l):
+        if not 0 <= l < self.count:
+            raise IndexError(l)
+        if l not in self.built:
+            self.built[l] = HostModelLayer(self.seed, l, self.experts, self.lazy)
+        return self.built[l]
+
+
 class HostModel:
     def __init__(self, seed, layers, experts, vocab, lazy=False):
         self.seed, self.vocab = seed, vocab
-        self.layers = [HostModelLayer(seed, l, experts, lazy) for l in range(layers)]
+        self.layers = _LazyLayers(seed, layers, experts, lazy)
         self.output_norm = O.synth_normal(seed, stream(-1, OUTPUT_NORM), N, sigma=0.05, mean=1.0)
-        self.unembedding = O.synth_bf16(seed, stream(-1, UNEMBEDDING), vocab * N)
+        self._unembedding = None
         self.freqs = np.empty(32, np.float32)
         O.lib.orc_rope_frequencies(self.freqs)
+
+    @property
+    def unembedding(self):
+        """bf16 [vocab][2880], generated on first use (1.16 GB at the full vocabulary)."""
+        if self._unembedding is None:
+            self._unembedding = O.synth_bf16(self.seed, stream(-1, UNEMBEDDING), self.vocab * N)
+        return self._unembedding
 
     def embedding(self, token):
         row = O.synth_q8_0(self.seed, stream(-1, EMBEDDING), 90, block_offset=token * 90)

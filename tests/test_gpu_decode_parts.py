@@ -143,10 +143,7 @@ def test_qkv_rope_kv_store_matches_oracle(dev, position):
     qkv.free()
 
 
-@pytest.mark.parametrize("layer_index,position", [(0, 0), (1, 0), (0, 63), (1, 64), (0, 127), (0, 128),
-                                                  (0, 129), (1, 129), (0, 300), (1, 300), (1, 1023)])
-def test_attention_with_sinks_matches_oracle(dev, layer_index, position):
-    capacity = 1088
+def check_attention(dev, layer_index, position, capacity):
     T = position + 1
     q = O.synth_normal(41, position, 4096, sigma=2.0)
     k = O.synth_normal(42, position, capacity * 512, sigma=2.0)
@@ -161,10 +158,24 @@ def test_attention_with_sinks_matches_oracle(dev, layer_index, position):
     scores = np.empty(T, np.float32)
     O.lib.orc_attention(q, k, v, sinks, layer_index, position, ref, scores)
     err = O.rel_l2(out.download(np.float32), ref)
-    print(f"attention layer {layer_index} position {position}: rel_l2 {err:.2e}")
+    print(f"attention layer {layer_index} position {position} capacity {capacity}: rel_l2 {err:.2e}")
     assert err <= TOL
     for b in (qb, kb, vb, sb, pb, ws, out):
         b.free()
+
+
+@pytest.mark.parametrize("layer_index,position", [(0, 0), (1, 0), (0, 63), (1, 64), (0, 127), (0, 128),
+                                                  (0, 129), (1, 129), (0, 300), (1, 300), (1, 1023)])
+def test_attention_with_sinks_matches_oracle(dev, layer_index, position):
+    check_attention(dev, layer_index, position, 1088)
+
+
+# The contexts of benchmark configurations 3 (2048) and 4 (4096): a full layer at 2048
+# positions and beyond has more than 32 chunks of 64, the combine's second loop.
+@pytest.mark.parametrize("layer_index,position", [(0, 2047), (1, 2047), (0, 2048), (1, 2048), (1, 2111),
+                                                  (0, 4095), (1, 4095), (1, 4096)])
+def test_attention_with_sinks_at_long_context(dev, layer_index, position):
+    check_attention(dev, layer_index, position, 4104)
 
 
 # (first position, tokens): a prompt from 0 (ragged last block), one continued past the
@@ -230,6 +241,66 @@ def test_logits_and_greedy_match_oracle(dev):
     assert pos.download(np.int32)[0] == 4
     assert hist.download(np.int32, 16)[3] == tok.download(np.int32)[0]
     for b in (wb, xb, nb, lb, ws, tok, pos, hist):
+        b.free()
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "q8_0"])
+def test_logits_full_vocabulary_and_argmax(dev, fmt):
+    """The unembedding and the greedy choice at the full gpt-oss vocabulary (201088 rows):
+    the logits kernels walk their rows grid-strided over 1024 workgroups, and the argmax
+    reduces every workgroup's partial best.  bf16 is the synthetic configurations'
+    unembedding; Q8_0 the reference's output.weight (matvec_q8_0, model.cpp:598-599).
+    Then rows are duplicated across workgroups to make exact ties: the first maximum
+    wins (model.cpp:604-612)."""
+    vocab = 201088
+    x = O.synth_normal(62, 0, N, sigma=5.0)
+    norm = O.synth_normal(63, 0, N, mean=1.0, sigma=0.05)
+    normed = np.empty(N, np.float32)
+    O.lib.orc_rms_norm(x, norm, N, 1e-5, normed)
+    ref = np.empty(vocab, np.float32)
+    if fmt == "bf16":
+        w = O.synth_bf16(61, 0, vocab * N)
+        O.lib.orc_matvec_bf16(w, vocab, N, normed, ref)
+        wt = dev.upload(w)
+        run = lambda: dev.logits_bf16(wt, vocab, ttlab_amd.stage_input(xb, norm=nb), lb, ws)
+        row_len = N  # uint16 elements
+    else:
+        w = O.synth_q8_0(61, 1, vocab * 90)
+        O.lib.orc_matvec_q8_0(w, vocab, N, normed, ref)
+        wt = dev.q8_upload(w, vocab, N)
+        run = lambda: dev.logits_q8_0(wt, vocab, ttlab_amd.stage_input(xb, norm=nb), lb, ws)
+        row_len = 90 * 34  # bytes
+    xb, nb = dev.upload(x), dev.upload(norm)
+    lb = dev.alloc(vocab * 4)
+    ws = dev.alloc(dev.lib.ttl_logits_workspace_bytes(vocab))
+    tok = dev.alloc(4)
+    run()
+    dev.argmax(vocab, ws, tok)
+    got = lb.download(np.float32)
+    err = O.rel_l2(got, ref)
+    print(f"{fmt} logits over {vocab} rows: rel_l2 {err:.2e}")
+    assert err <= TOL
+    token = int(tok.download(np.int32)[0])
+    assert token == int(O.lib.orc_greedy(got, vocab))
+    top = np.sort(ref.astype(np.float64))[-2:]
+    if top[1] - top[0] > 1e-4 * abs(top[1]):
+        assert token == int(O.lib.orc_greedy(ref, vocab))
+    # exact ties across workgroups: copy the winning row to a later row (the first
+    # stays the choice), then also to an earlier one (which becomes the choice)
+    rows = w.reshape(vocab, row_len)
+    for dst, expected in ((vocab - 1, token), (min(token, 1000) // 2, min(token, 1000) // 2)):
+        rows[dst] = rows[token]
+        if fmt == "bf16":
+            wt.upload(w)
+        else:
+            wt.free()
+            wt = dev.q8_upload(w, vocab, N)
+        run()
+        dev.argmax(vocab, ws, tok)
+        got = lb.download(np.float32)
+        assert got[dst] == got[token]
+        assert int(tok.download(np.int32)[0]) == expected == int(O.lib.orc_greedy(got, vocab))
+    for b in (xb, nb, lb, ws, tok, wt):
         b.free()
 
 

@@ -607,6 +607,10 @@ class Device:
         _check(self.lib.ttl_logits_bf16(self.ctx, weight.ptr, vocab, C.byref(stage), logits.ptr, workspace.ptr),
                "ttl_logits_bf16")
 
+    def logits_q8_0(self, weight, vocab, stage, logits, workspace):
+        _check(self.lib.ttl_logits_q8_0(self.ctx, weight.handle, vocab, C.byref(stage), logits.ptr, workspace.ptr),
+               "ttl_logits_q8_0")
+
     def argmax(self, vocab, workspace, token, position=None, history=None, history_len=0):
         _check(self.lib.ttl_argmax(self.ctx, vocab, workspace.ptr, token.ptr, position.ptr if position else None,
                                    history.ptr if history else None, history_len), "ttl_argmax")
