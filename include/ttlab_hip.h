@@ -100,7 +100,8 @@ int ttl_synth_mxfp4_gguf(ttl_ctx *ctx, uint64_t seed, uint64_t stream, size_t bl
 
 int ttl_mxfp4_upload(ttl_ctx *ctx, const void *gguf_blocks, uint32_t rows, uint32_t cols, uint32_t experts,
                      ttl_mxfp4 **out);
-/* Same, from GGUF-layout blocks already in device memory. */
+/* Same, from GGUF-layout blocks already in device memory.  Waits for the repack: it
+ * reads back whether any block has E8M0 scale 0 or 255 (ttl_mxfp4_edge_scales). */
 int ttl_mxfp4_upload_dev(ttl_ctx *ctx, const void *gguf_blocks_dev, uint32_t rows, uint32_t cols,
                          uint32_t experts, ttl_mxfp4 **out);
 /* Generates the tensor on the device: expert e is stream `stream + e` of the MXFP4
@@ -112,6 +113,14 @@ int ttl_mxfp4_download(ttl_ctx *ctx, const ttl_mxfp4 *tensor, void *gguf_blocks)
 void ttl_mxfp4_free(ttl_ctx *ctx, ttl_mxfp4 *tensor);
 int ttl_mxfp4_shape(const ttl_mxfp4 *tensor, uint32_t *rows, uint32_t *cols, uint32_t *experts);
 size_t ttl_mxfp4_bytes(const ttl_mxfp4 *tensor);
+/* 1 if some block of the tensor has E8M0 scale 255, or scale 0 with a code of nonzero
+ * magnitude, else 0 (negative: error).  The reference decodes those scales as 2^127 and
+ * 2^-128 per integer unit (tensor.cpp:36-44); the matvec entry points do too.  The
+ * batched MFMA entry points convert weights to bf16 with the scale folded in, which
+ * has no exact form for them: ttl_matmul_mxfp4_selected refuses such an expert and
+ * ttl_moe_prefill* such a tensor with TTL_ERR_SHAPE; HipGptOssModel then runs prefill
+ * as decode steps. */
+int ttl_mxfp4_edge_scales(const ttl_mxfp4 *tensor);
 
 /* Decodes expert `expert` to f32 [rows][cols] on the device (out_dev).
  * mode 0: the reference's table, weight = 2^(e-128) * int(code) (tensor.cpp:34-74).

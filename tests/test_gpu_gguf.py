@@ -199,3 +199,31 @@ def test_gguf_model_prefill_matches_oracle(loaded):
     err = O.rel_l2(logits, ref)
     print(f"GGUF prefill of {count} tokens: Q8_0 logits rel_l2 {err:.2e}")
     assert err <= TOL
+
+
+def test_edge_scales_make_prefill_run_as_decode_steps(tmp_path):
+    """A file whose expert weights hold a block with E8M0 scale 0 (or 255) loads, decodes
+    every scale exactly through the matvec kernels, and prefills as decode steps: the
+    batched MFMA kernels refuse such tensors.  The prompt's logits equal, bit for bit,
+    those of GptOssModel::forward run position by position."""
+    def with_edge(name, nbytes):
+        data = generated(name, nbytes)
+        if name == "blk.1.ffn_up_exps.weight":
+            data = data.copy()
+            data[17 * 12345] = 0  # one block's E8M0 byte
+        return data
+
+    tensors = gpt_oss_tensors(LAYERS, EXPERTS, VOCAB, with_edge, GGML_Q8_0)
+    path = os.path.join(tmp_path, "gpt-oss-edge.gguf")
+    write_gguf(path, gpt_oss_metadata(LAYERS, EXPERTS), tensors)
+    gpu = ttlab_amd.Model.from_gguf(path, CAPACITY, strict=False)
+    try:
+        tokens = [int(t) for t in np.random.default_rng(23).integers(0, VOCAB, 6)]
+        logits = gpu.prefill(tokens)
+        with pytest.raises(ttlab_amd.TtlError, match="decode steps"):
+            gpu.prefill_state(0, len(tokens))
+        for p, tok in enumerate(tokens):
+            last = gpu.forward(tok, p)
+        assert np.array_equal(logits.view(np.uint32), last.view(np.uint32))
+    finally:
+        gpu.close()

@@ -153,6 +153,124 @@ def test_matvec_matches_oracle_config0(dev, emin, emax):
     t.free()
 
 
+@pytest.mark.parametrize("emin,emax", [(250, 255), (255, 255)])
+def test_matvec_overflow_band_matches_oracle(dev, emin, emax):
+    """E8M0 250..255 with x ~ N(0, 1): partial sums pass 2^128, and every row mixes +inf
+    and -inf terms.  Both reference bodies give NaN in every row (model of the CPU
+    result for these inputs); the GPU's positions of NaN and infinity equal theirs.
+    (Between these and finite results, e.g. E8M0 240..250, the reference's own two
+    bodies disagree row by row on NaN, infinity or a finite value, so no per-row bar
+    exists there: test_oracle_compute.test_mxfp4_overflow_band_is_order_dependent.)"""
+    blocks = O.synth_mxfp4(0x77000000, 0, N * 90, emin, emax)
+    x = O.synth_normal(0x78000000, 0, N)
+    zero = np.zeros(N, np.float32)
+    t = dev.mxfp4_upload(blocks, N, N, 1)
+    assert t.edge_scales
+    xb, yb = dev.upload(x), dev.alloc(N * 4)
+    dev.matvec_mxfp4(t, None, xb, yb, 0)
+    got = yb.download(np.float32)
+    for body in (O.BODY_DEFAULT, O.BODY_V4):
+        ref = O.mxfp4_matvec(blocks, zero, N, N, x, expert=0, body=body)
+        assert np.isnan(ref).all()
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        assert np.array_equal(np.isinf(got), np.isinf(ref))
+    for b in (xb, yb):
+        b.free()
+    t.free()
+
+
+def test_matvec_top_and_bottom_exponents_match_oracle(dev):
+    """The decode matvec takes every E8M0 value exactly, E8M0 0 (2^-127) and 255 (2^127
+    per reference integer, tensor.cpp:36-44) included.  x is of order 2^-24 in columns
+    0..1439 and of order 1 in columns 1440..2879.  Rows 0..1439 hold E8M0 253..255 with
+    codes 0, 1, 8 or 9 (|E2M1| <= 0.5, so products stay finite) in the first 45 blocks;
+    rows 1440.. hold E8M0 0..2 with any codes in the last 45 blocks (subnormal products;
+    no bias, so they are the whole sum).  Every other block is zero codes at E8M0 127
+    (the reference's AVX-512 body scales x first, and 2^127 x would overflow there).
+    Relative L2 <= 1e-5 against both reference bodies."""
+    rng = np.random.default_rng(3)
+    half = N // 2
+    blocks = np.zeros((N, 90, 17), np.uint8)
+    blocks[:, :, 0] = 127
+    blocks[:half, :45, 0] = rng.integers(253, 256, (half, 45))
+    codes = rng.choice(np.array([0, 1, 8, 9], np.uint8), (half, 45, 32))
+    blocks[:half, :45, 1:] = codes[:, :, :16] | (codes[:, :, 16:] << 4)
+    blocks[half:, 45:, 0] = rng.integers(0, 3, (N - half, 45))
+    blocks[half:, 45:, 1:] = rng.integers(0, 256, (N - half, 45, 16))
+    blocks = blocks.ravel()
+    x = np.concatenate([O.synth_normal(5, 0, 1440) * np.float32(2.0 ** -24),
+                        O.synth_normal(5, 1, N - 1440)]).astype(np.float32)
+    zero = np.zeros(N, np.float32)
+    t = dev.mxfp4_upload(blocks, N, N, 1)
+    assert t.edge_scales
+    xb, yb = dev.upload(x), dev.alloc(N * 4)
+    dev.matvec_mxfp4(t, None, xb, yb, 0)
+    got = yb.download(np.float32)
+    assert np.isfinite(got).all()
+    for body in (O.BODY_DEFAULT, O.BODY_V4):
+        ref = O.mxfp4_matvec(blocks, zero, N, N, x, expert=0, body=body)
+        assert np.isfinite(ref).all()
+        for rows in (slice(0, half), slice(half, N)):
+            err = O.rel_l2(got[rows], ref[rows])
+            print(f"body {body} rows {rows.start}..{rows.stop}: rel_l2 {err:.2e}")
+            assert err <= TOL
+    for b in (xb, yb):
+        b.free()
+    t.free()
+
+
+def test_zero_code_rows_give_the_bias_bit_for_bit(dev):
+    """Rows made only of codes 0 and 8 (+0 and -0 in E2M1; the reference's table has +0
+    for both) give exactly the bias, as the reference's AVX-512 body does: the gfx950
+    conversion's -0 for code 8 never reaches an output, because every sum starts at +0
+    and +0 + (-0) is +0."""
+    rows = 64
+    blocks = np.zeros((rows, 90, 17), np.uint8)
+    blocks[:, :, 0] = 127
+    blocks[:, :, 1:] = np.random.default_rng(4).choice(np.array([0x00, 0x08, 0x80, 0x88], np.uint8), (rows, 90, 16))
+    blocks = blocks.ravel()
+    bias = O.synth_normal(6, 0, rows, sigma=2.0)
+    bias[:4] = [0.0, -0.0, 1e-30, -1e-30]
+    x = O.synth_normal(6, 1, N)
+    t = dev.mxfp4_upload(blocks, rows, N, 1)
+    bb, xb, yb = dev.upload(bias), dev.upload(x), dev.alloc(rows * 4)
+    dev.matvec_mxfp4(t, bb, xb, yb, 0)
+    got = yb.download(np.float32)
+    ref = O.mxfp4_matvec(blocks, bias, rows, N, x, expert=0, body=O.BODY_V4)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    for b in (bb, xb, yb):
+        b.free()
+    t.free()
+
+
+def test_mfma_entry_points_refuse_edge_scales(dev):
+    """A tensor with a block of E8M0 0 or 255 is flagged at upload, and the batched MFMA
+    entry points (whose bf16 weights cannot hold those scales exactly) refuse it
+    instead of computing a different result; ordinary scales are accepted."""
+    rows = 192
+    base = O.synth_mxfp4(0x77000000, 9, rows * 90)
+    x = dev.upload(O.synth_normal(7, 0, 4 * N))
+    tokens = dev.upload(np.array([0, 2], np.int32))
+    out = dev.alloc(4 * rows * 4)
+    ok = dev.mxfp4_upload(base, rows, N, 1)
+    assert not ok.edge_scales
+    dev.matmul_mxfp4_selected(ok, None, x, N, 4, tokens, 2, out, 0)
+    ok.free()
+    for e in (0, 255):
+        blocks = base.copy()
+        blocks[17 * 1000] = e
+        t = dev.mxfp4_upload(blocks, rows, N, 1)
+        assert t.edge_scales
+        with pytest.raises(ttlab_amd.TtlError, match="E8M0 scale 0 or 255"):
+            dev.matmul_mxfp4_selected(t, None, x, N, 4, tokens, 2, out, 0)
+        t.free()
+    syn = dev.mxfp4_synthetic(rows, N, 1, 1, 1, emin=0, emax=3)
+    assert syn.edge_scales
+    syn.free()
+    for b in (x, tokens, out):
+        b.free()
+
+
 def test_config0_as_one_5760_row_matrix(dev):
     """The {2880, 2880, 2} bytes uploaded as one 5760-row matrix (the bench's config-0
     launch) give bitwise the two experts' rows, and the oracle's values."""

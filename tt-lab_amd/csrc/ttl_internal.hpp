@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "../../include/ttlab_hip.h"
 
@@ -34,6 +35,19 @@ struct ttl_mxfp4 {
     uint8_t *scales = nullptr;   // [experts][tiles][lanes_k][tile_rows][scale_pad]
     size_t code_bytes = 0;
     size_t scale_bytes = 0;
+    // Per expert: some block has E8M0 scale 255, or scale 0 with a nonzero code.  The
+    // bf16 conversion of the MFMA kernels has no exact value for those (2^-127 is an
+    // f32 subnormal scale, 2^128 none at all), so the batched entry points refuse such
+    // experts; the matvec kernels decode every scale exactly.
+    std::vector<uint8_t> edge_experts;
+    bool edge_scales() const {
+        for (uint8_t f : edge_experts) {
+            if (f) {
+                return true;
+            }
+        }
+        return false;
+    }
 };
 
 // Q8_0 tensor in the repacked layout (see q8:: constants in ttl_q8_tile.hpp): rows of
@@ -106,6 +120,11 @@ constexpr int scale_pad = 24;                                 // per-lane scale 
 constexpr size_t tile_code_bytes = size_t(blocks) * tile_rows * 16;          // 23040
 constexpr size_t tile_scale_bytes = size_t(lanes_k) * tile_rows * scale_pad; // 1536
 constexpr uint8_t pad_scale = 127;                            // scale of padding blocks
+// One 32-bit word per expert after the scale plane, set by the repack for the edge
+// scales (ttl_mxfp4::edge_experts).
+inline size_t edge_flag_bytes(uint32_t experts) {
+    return (size_t(experts) * 4 + 15) / 16 * 16;
+}
 // Zero bytes after the last tile: iterations past the row end (blocks 90..95) read
 // there unconditionally (their x is zero, and E2M1 codes are all finite).
 constexpr size_t tail_pad_bytes = size_t(24 * lanes_k - blocks) * tile_rows * 16;  // 1536: up to block 95

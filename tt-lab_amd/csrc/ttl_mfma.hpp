@@ -35,7 +35,9 @@ __device__ inline f32x4 mfma(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
 
 // E8M0 byte -> the f32 scale 2^(e-127) of the gfx950 conversion (E2M1 values are
 // 0..6, half the reference's integer table, tensor.cpp:34-44).  e = 0 is the
-// subnormal 2^-127; e = 255 has no f32 value and gives infinity.
+// subnormal 2^-127 and e = 255 has no f32 value (infinity here); the conversion is
+// exact for e = 1..254 only, so the entry points refuse tensors holding 0 or 255
+// (ttl_mxfp4::edge_scales) before any kernel decodes them.
 __device__ inline float e8m0_scale(uint32_t e) {
     return e ? __uint_as_float(e << 23) : 0x1p-127f;
 }

@@ -17,7 +17,8 @@ namespace {
 // ---- layout conversion ------------------------------------------------------
 
 __global__ void repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows, uint32_t experts,
-                              uint4 *__restrict__ codes, uint8_t *__restrict__ scales) {
+                              uint4 *__restrict__ codes, uint8_t *__restrict__ scales,
+                              uint32_t *__restrict__ edge_flag) {
     const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const size_t per_expert = size_t(rows) * mx::blocks;
     if (gid >= per_expert * experts) {
@@ -35,7 +36,14 @@ __global__ void repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows, u
     }
     const size_t tile_index = size_t(e) * (rows / mx::tile_rows) + row / mx::tile_rows;
     codes[mx::code_chunk(tile_index, block, row % mx::tile_rows)] = make_uint4(w[0], w[1], w[2], w[3]);
-    scales[mx::scale_offset(tile_index, block, row % mx::tile_rows)] = src[0];
+    const uint8_t e8 = src[0];
+    scales[mx::scale_offset(tile_index, block, row % mx::tile_rows)] = e8;
+    // E8M0 255, or 0 with a code of nonzero magnitude (zero codes decode to 0 at any
+    // finite scale): the bf16 MFMA decode cannot represent the block
+    const bool nonzero = ((w[0] | w[1] | w[2] | w[3]) & 0x77777777u) != 0;
+    if (e8 == 255 || (e8 == 0 && nonzero)) {
+        edge_flag[e] = 1u;  // every writer stores the same value
+    }
 }
 
 __global__ void unpack_kernel(const uint4 *__restrict__ codes, const uint8_t *__restrict__ scales, uint32_t rows,
@@ -199,7 +207,7 @@ int alloc_tensor(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, t
     t->scale_bytes = tiles_total * mx::tile_scale_bytes;
     hipError_t err = hipMalloc(&t->codes, t->code_bytes + mx::tail_pad_bytes);
     if (err == hipSuccess) {
-        err = hipMalloc(&t->scales, t->scale_bytes);
+        err = hipMalloc(&t->scales, t->scale_bytes + mx::edge_flag_bytes(experts));
     }
     if (err != hipSuccess) {
         (void)hipFree(t->codes);
@@ -208,6 +216,9 @@ int alloc_tensor(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t experts, t
     }
     // Padding scale bytes must decode to a finite scale (their blocks are zero).
     int rc = ttl_fill_bytes(ctx, t->scales, mx::pad_scale, t->scale_bytes);
+    if (rc == TTL_OK) {
+        rc = ttl_fill_bytes(ctx, t->scales + t->scale_bytes, 0, mx::edge_flag_bytes(experts));
+    }
     if (rc == TTL_OK) {
         rc = ttl_fill_bytes(ctx, t->codes + t->code_bytes, 0, mx::tail_pad_bytes);
     }
@@ -232,9 +243,23 @@ int ttl_mxfp4_upload_dev(ttl_ctx *ctx, const void *gguf_blocks_dev, uint32_t row
     }
     ttl_mxfp4 *t = *out;
     const size_t n = size_t(rows) * mx::blocks * experts;
+    uint32_t *flag = reinterpret_cast<uint32_t *>(t->scales + t->scale_bytes);
     repack_kernel<<<ttl::blocks_for(n, 256), 256, 0, ctx->stream>>>((const uint8_t *)gguf_blocks_dev, rows, experts,
-                                                                     (uint4 *)t->codes, t->scales);
-    TTL_LAUNCHED("repack_kernel");
+                                                                     (uint4 *)t->codes, t->scales, flag);
+    hipError_t err = hipGetLastError();
+    std::vector<uint32_t> edge(experts, 0u);
+    if (err == hipSuccess) {
+        err = hipMemcpyAsync(edge.data(), flag, sizeof(uint32_t) * experts, hipMemcpyDeviceToHost, ctx->stream);
+    }
+    if (err == hipSuccess) {
+        err = hipStreamSynchronize(ctx->stream);
+    }
+    if (err != hipSuccess) {
+        ttl_mxfp4_free(ctx, t);
+        *out = nullptr;
+        return ttl::hip_fail(err, "ttl_mxfp4_upload_dev: repack_kernel");
+    }
+    t->edge_experts.assign(edge.begin(), edge.end());
     return TTL_OK;
 }
 
@@ -261,7 +286,14 @@ int ttl_mxfp4_synthetic(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t exp
     if (rc != TTL_OK) {
         return rc;
     }
+    // every expert then holds such blocks (a block of 32 zero codes has odds 2^-128)
+    (*out)->edge_experts.assign(experts, emin == 0 || emax == 255 ? 1 : 0);
     return ttl::synth_mxfp4_repacked(ctx, *out, seed, stream, emin, emax);
+}
+
+int ttl_mxfp4_edge_scales(const ttl_mxfp4 *t) {
+    TTL_REQUIRE(t, TTL_ERR_INVALID, "ttl_mxfp4_edge_scales: null tensor");
+    return t->edge_scales() ? 1 : 0;
 }
 
 int ttl_mxfp4_download(ttl_ctx *ctx, const ttl_mxfp4 *t, void *gguf_blocks) {

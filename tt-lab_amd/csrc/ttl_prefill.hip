@@ -889,6 +889,17 @@ void combine_for(uint32_t used, const Plan &plan, uint32_t count, uint32_t rows,
     }
 }
 
+// The MFMA kernels take weights as bf16 = E2M1 x 2^(e-127), exact for E8M0 1..254
+// (and for zero codes at E8M0 0) only.  expert < 0: every expert of the tensor.
+int check_bf16_scales(const ttl_mxfp4 *w, int64_t expert, const char *who) {
+    const bool edge = expert < 0 ? w->edge_scales() : w->edge_experts[size_t(expert)] != 0;
+    TTL_REQUIRE(!edge, TTL_ERR_SHAPE,
+                "%s: the expert tensor has blocks with E8M0 scale 0 or 255, which the bf16 MFMA decode cannot "
+                "represent exactly; use the matvec entry points for it",
+                who);
+    return TTL_OK;
+}
+
 int check_mxfp4(const ttl_mxfp4 *w, const char *who) {
     TTL_REQUIRE(w && w->codes && w->scales, TTL_ERR_INVALID, "%s: null tensor", who);
     TTL_REQUIRE(w->cols == uint32_t(mx::cols), TTL_ERR_SHAPE, "%s: cols must be %d", who, mx::cols);
@@ -915,6 +926,10 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     TTL_REQUIRE(w->rows % kMmRows == 0, TTL_ERR_SHAPE, "ttl_matmul_mxfp4_selected: rows must be a multiple of %d",
                 kMmRows);
     TTL_REQUIRE(expert < w->experts, TTL_ERR_INVALID, "ttl_matmul_mxfp4_selected: expert %u out of range", expert);
+    rc = check_bf16_scales(w, expert, "ttl_matmul_mxfp4_selected");
+    if (rc != TTL_OK) {
+        return rc;
+    }
     TTL_REQUIRE(x_stride >= uint32_t(mx::cols) && x_stride % 4 == 0, TTL_ERR_SHAPE,
                 "ttl_matmul_mxfp4_selected: x_stride must be >= %d and a multiple of 4", mx::cols);
     TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && (reinterpret_cast<uintptr_t>(out_dev) & 15) == 0,
@@ -973,6 +988,12 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
                 TTL_ERR_SHAPE, "ttl_moe_prefill_experts: expert tensor shapes do not match the layer");
     TTL_REQUIRE(L.gate->experts == L.experts && L.up->experts == L.experts && L.down->experts == L.experts,
                 TTL_ERR_SHAPE, "ttl_moe_prefill_experts: expert tensors must hold %u experts", L.experts);
+    for (const ttl_mxfp4 *t : {L.gate, L.up, L.down}) {
+        const int rc = check_bf16_scales(t, -1, "ttl_moe_prefill_experts");
+        if (rc != TTL_OK) {
+            return rc;
+        }
+    }
     TTL_REQUIRE(L.experts >= 1 && L.experts <= kMaxExperts, TTL_ERR_SHAPE,
                 "ttl_moe_prefill_experts: experts must be 1..%u", kMaxExperts);
     TTL_REQUIRE(L.used >= 1 && L.used <= kMaxUsed, TTL_ERR_SHAPE, "ttl_moe_prefill_experts: used must be 1..%u",
@@ -1073,6 +1094,13 @@ size_t ttl_moe_prefill_batch_workspace_bytes(uint32_t count, uint32_t experts, u
 int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, uint32_t count, float *out_dev,
                     int32_t *indices_dev, float *weights_dev, void *workspace_dev, size_t workspace_bytes) {
     TTL_REQUIRE(ctx && layer && x_dev && out_dev && workspace_dev, TTL_ERR_INVALID, "ttl_moe_prefill: null argument");
+    TTL_REQUIRE(layer->gate && layer->up && layer->down, TTL_ERR_INVALID, "ttl_moe_prefill: null expert tensor");
+    for (const ttl_mxfp4 *t : {layer->gate, layer->up, layer->down}) {
+        const int rc = check_bf16_scales(t, -1, "ttl_moe_prefill");  // before the router launches
+        if (rc != TTL_OK) {
+            return rc;
+        }
+    }
     TTL_REQUIRE(!layer->input_norm, TTL_ERR_INVALID,
                 "ttl_moe_prefill: x is the normalized MoE input (model.cpp:549-551); the layer's input_norm must be NULL");
     TTL_REQUIRE(layer->used >= 1 && layer->used <= kMaxUsed, TTL_ERR_SHAPE, "ttl_moe_prefill: used must be 1..%u",

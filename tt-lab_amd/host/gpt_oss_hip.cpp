@@ -99,6 +99,13 @@ HipGptOssModel::HipGptOssModel(const GgufFile &file, size_t token_capacity, int 
 // RoPE table, activations and the captured step: the part of construction that does
 // not depend on where the weights came from.
 void HipGptOssModel::finish_construction() {
+    for (const Layer &layer : layers_) {
+        for (const ttl_mxfp4 *t : {layer.gate, layer.up, layer.down}) {
+            if (ttl_mxfp4_edge_scales(t) != 0) {
+                prefill_by_decode_ = true;  // the MFMA prefill refuses E8M0 0 / 255
+            }
+        }
+    }
     {
         // RoPE coefficients per position and pair, as apply_rope computes them (model.cpp:230-245).
         const std::array<float, 32> f = rope_frequencies();
@@ -450,6 +457,16 @@ const float *HipGptOssModel::prefill(const int32_t *tokens, size_t count) {
     for (size_t p = 0; p < count; ++p) {
         validate(tokens[p], p);
     }
+    if (prefill_by_decode_) {
+        // Expert weights with E8M0 scale 0 or 255 have no exact bf16 form for the batched
+        // MFMA kernels; the decode kernels take every scale, so the prompt runs token by
+        // token (GptOssModel::forward at each position, model.cpp:557-602).
+        const float *logits = nullptr;
+        for (size_t p = 0; p < count; ++p) {
+            logits = forward(tokens[p], p);
+        }
+        return logits;
+    }
     for (size_t first = 0; first < count; first += prefill_batch_) {
         const size_t n = std::min(prefill_batch_, count - first);
         check(ttl_memcpy_h2d(ctx_, prefill_tokens_, tokens + first, sizeof(int32_t) * n), "ttl_memcpy_h2d");
@@ -462,6 +479,9 @@ const float *HipGptOssModel::prefill(const int32_t *tokens, size_t count) {
 void HipGptOssModel::prefill_state(size_t layer, size_t count, float *x_in) const {
     if (layer > spec_.layers || count > prefill_batch_) {
         throw std::runtime_error("prefill_state: layer or count out of range");
+    }
+    if (prefill_by_decode_) {
+        throw std::runtime_error("prefill_state: this model's prefill runs as decode steps (E8M0 scale 0 or 255)");
     }
     check(ttl_memcpy_d2h(ctx_, x_in, x_seq_ + layer * prefill_batch_ * kHidden, sizeof(float) * count * kHidden),
           "ttl_memcpy_d2h");

@@ -180,6 +180,7 @@ class HipGptOssModel {
     std::vector<float> host_logits_;
     // layer-major prefill (model.cpp:463-555), chunks of prefill_batch_ tokens
     size_t prefill_batch_ = 0;
+    bool prefill_by_decode_ = false;  // some expert tensor has E8M0 scale 0 or 255
     int32_t *prefill_tokens_ = nullptr;
     float *x_seq_ = nullptr;         // [layers + 1][batch][2880]
     float *norm_seq_ = nullptr, *qkv_seq_ = nullptr, *q_seq_ = nullptr, *attended_seq_ = nullptr;

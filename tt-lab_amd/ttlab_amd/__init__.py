@@ -260,6 +260,7 @@ def load_library():
         "ttl_mxfp4_free": (None, [vp, vp]),
         "ttl_mxfp4_shape": (i32, [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(u32)]),
         "ttl_mxfp4_bytes": (sz, [vp]),
+        "ttl_mxfp4_edge_scales": (i32, [vp]),
         "ttl_mxfp4_dequantize": (i32, [vp, vp, u32, i32, vp]),
         "ttl_matvec_mxfp4": (i32, [vp, vp, vp, vp, vp, u32]),
         "ttl_matvec_mxfp4_experts": (i32, [vp, vp, vp, vp, u32, vp, u32, vp]),
@@ -404,6 +405,14 @@ class Mxfp4:
     @property
     def nbytes(self):
         return self.dev.lib.ttl_mxfp4_bytes(self.handle)
+
+    @property
+    def edge_scales(self):
+        """True if some block has E8M0 scale 0 or 255 (the MFMA entry points refuse it)."""
+        rc = self.dev.lib.ttl_mxfp4_edge_scales(self.handle)
+        if rc < 0:
+            _check(rc, "ttl_mxfp4_edge_scales")
+        return bool(rc)
 
     def download_gguf(self):
         out = np.empty(self.rows * self.cols // 32 * 17 * self.experts, np.uint8)
