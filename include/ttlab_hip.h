@@ -362,6 +362,17 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
                          const float *sinks_dev, const int32_t *position_dev, uint32_t capacity, uint32_t layer_index,
                          float *workspace_dev, float *out_dev);
 
+/* ttl_attention_decode without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The full-context partials go to a
+ * static device array of 4,325,376 bytes per GPU (held until the process ends), so
+ * capacity is at most 16384 positions (larger is TTL_ERR_SHAPE).  Same kernels and
+ * results as ttl_attention_decode.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams or contexts) race. */
+int ttl_attention_decode_noalloc(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                                 const float *v_cache_dev, const float *sinks_dev, const int32_t *position_dev,
+                                 uint32_t capacity, uint32_t layer_index, float *out_dev);
+
 /* attention_from_cache (model.cpp:255-290) for `tokens` tokens at positions
  * first_position .. first_position + tokens - 1, as GptOssModel::prefill runs it per
  * token (model.cpp:510-514): q_dev / out_dev f32 [tokens][4096]; the caches must hold

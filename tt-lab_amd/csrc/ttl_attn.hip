@@ -15,6 +15,7 @@
 #include "ttl_mfma.hpp"
 
 #include <cmath>
+#include <mutex>
 
 namespace {
 
@@ -533,7 +534,42 @@ void launch_attention(ttl_ctx *ctx, const float *q, const float *k_cache, const 
 }
 
 
+// ---- ttl_attention_decode_noalloc: the partials in a static device array ------------
+//
+// For callers that cannot allocate (graph capture, serving loops): one array per GPU,
+// sized for the largest capacity the kernels take (kMaxCombineChunks chunks of 64
+// positions, 16384 positions: 64 x 256 x 66 floats = 4,325,376 bytes), which each GPU
+// the library runs on holds until the process ends.  Host code never passes the
+// array's name to a kernel: its device address is looked up once per device, with that
+// device current, when a context opens (ttl::attention_scratch_init, from ttl_create).
+constexpr size_t kScratchFloats = size_t(kQHeads) * kMaxCombineChunks * (kHead + 2);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxScratchDevices] = {};
+
+float *scratch_for(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    return device >= 0 && device < kMaxScratchDevices ? g_scratch_ptr[device] : nullptr;
+}
+
 }  // namespace
+
+namespace ttl {
+int attention_scratch_init(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    TTL_REQUIRE(device >= 0 && device < kMaxScratchDevices, TTL_ERR_NO_DEVICE,
+                "ttl_create: device ordinal %d above %d", device, kMaxScratchDevices - 1);
+    if (g_scratch_ptr[device]) {
+        return TTL_OK;
+    }
+    void *ptr = nullptr;
+    TTL_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[device] = static_cast<float *>(ptr);
+    return TTL_OK;
+}
+}  // namespace ttl
 
 extern "C" {
 
@@ -556,6 +592,28 @@ int ttl_attention_decode(ttl_ctx *ctx, const float *q_dev, const float *k_cache_
     return TTL_OK;
 }
 
+
+int ttl_attention_decode_noalloc(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                                 const float *v_cache_dev, const float *sinks_dev, const int32_t *position_dev,
+                                 uint32_t capacity, uint32_t layer_index, float *out_dev) {
+    TTL_REQUIRE(ctx && q_dev && k_cache_dev && v_cache_dev && sinks_dev && position_dev && out_dev, TTL_ERR_INVALID,
+                "ttl_attention_decode_noalloc: null argument");
+    TTL_REQUIRE(capacity > 0 && capacity <= uint32_t(kMaxCombineChunks * kChunk), TTL_ERR_SHAPE,
+                "ttl_attention_decode_noalloc: capacity must be 1..%d (the static partials hold %zu bytes)",
+                kMaxCombineChunks * kChunk, kScratchFloats * sizeof(float));
+    TTL_REQUIRE(((uintptr_t)q_dev & 15) == 0 && ((uintptr_t)k_cache_dev & 15) == 0 && ((uintptr_t)v_cache_dev & 15) == 0,
+                TTL_ERR_INVALID, "ttl_attention_decode_noalloc: q, k and v must be 16-byte aligned");
+    float *partials = scratch_for(ctx->device);
+    TTL_REQUIRE(partials, TTL_ERR_INVALID, "ttl_attention_decode_noalloc: no static partials on device %d",
+                ctx->device);
+    const uint32_t chunks = (capacity + kChunk - 1) / kChunk;
+    TTL_REQUIRE(ttl::attention_partials_floats(capacity) <= kScratchFloats, TTL_ERR_SHAPE,
+                "ttl_attention_decode_noalloc: %u chunks exceed the static partials", chunks);
+    launch_attention(ctx, q_dev, k_cache_dev, v_cache_dev, sinks_dev, position_dev, capacity, layer_index, chunks,
+                     partials, out_dev);
+    TTL_LAUNCHED("attention kernels");
+    return TTL_OK;
+}
 
 int ttl_attention_prefill(ttl_ctx *ctx, const float *q_dev, const float *k_cache_dev, const float *v_cache_dev,
                           const float *sinks_dev, uint32_t first_position, uint32_t tokens, uint32_t capacity,

@@ -108,6 +108,11 @@ int ttl_create(int device, ttl_ctx **out) {
         ttl_destroy(ctx);
         return ttl::hip_fail(err, "ttl_create");
     }
+    const int rc = ttl::attention_scratch_init(device);  // the device is current here
+    if (rc != TTL_OK) {
+        ttl_destroy(ctx);
+        return rc;
+    }
     *out = ctx;
     return TTL_OK;
 }

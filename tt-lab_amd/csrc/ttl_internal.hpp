@@ -66,6 +66,9 @@ struct ttl_q8 {
 namespace ttl {
 
 size_t moe_workspace_bytes();
+// Looks up the device address of the attention partials' static array (ttl_attn.hip)
+// for `device`, which must be current; once per device.
+int attention_scratch_init(int device);
 // Batched router of moe_batch (ttl_moe.hip): per-token exact rows in `scratch`
 // (router_scratch_bytes() each), indices/weights [count][used].
 size_t router_scratch_bytes();

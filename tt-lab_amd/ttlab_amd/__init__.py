@@ -284,6 +284,7 @@ def load_library():
         "ttl_attn_qkv": (i32, [vp, vp, vp, C.POINTER(StageInput), vp, vp, u32, vp, vp, vp]),
         "ttl_attention_workspace_bytes": (sz, [u32]),
         "ttl_attention_decode": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, vp, vp]),
+        "ttl_attention_decode_noalloc": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, vp]),
         "ttl_attention_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp]),
         "ttl_embedding_q8_0": (i32, [vp, vp, u32, vp, vp]),
         "ttl_logits_workspace_bytes": (sz, [u32]),
@@ -604,6 +605,10 @@ class Device:
     def attention_decode(self, q, kc, vc, sinks, position, capacity, layer_index, workspace, out):
         _check(self.lib.ttl_attention_decode(self.ctx, q.ptr, kc.ptr, vc.ptr, sinks.ptr, position.ptr, capacity,
                                              layer_index, workspace.ptr, out.ptr), "ttl_attention_decode")
+
+    def attention_decode_noalloc(self, q, kc, vc, sinks, position, capacity, layer_index, out):
+        _check(self.lib.ttl_attention_decode_noalloc(self.ctx, q.ptr, kc.ptr, vc.ptr, sinks.ptr, position.ptr,
+                                                     capacity, layer_index, out.ptr), "ttl_attention_decode_noalloc")
 
     def attention_prefill(self, q, kc, vc, sinks, first, tokens, capacity, layer_index, out):
         _check(self.lib.ttl_attention_prefill(self.ctx, q.ptr, kc.ptr, vc.ptr, sinks.ptr, first, tokens, capacity,
