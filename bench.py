@@ -48,9 +48,45 @@ SEED = 0x77000003
 # Algorithmic bytes of one gate/up+SwiGLU launch: 4 experts x (gate + up) x 2880 rows x
 # 1530 B, their f32 biases, x (f32 2880) read, hidden (f32 4x2880) written.
 GATEUP_BYTES = USED * 2 * N * 1530 + USED * 2 * N * 4 + N * 4 + USED * N * 4
-# HBM bytes one gate/up launch moves, measured with rocprofv3 FETCH_SIZE + WRITE_SIZE
-# (scaled on a 256 MiB copy): profiles/decode_cfg3_hbm_bytes.txt.
-GATEUP_TRAFFIC_BYTES = 35_904_000
+Q8_ROW_2880, Q8_ROW_4096 = 90 * 34, 128 * 34
+# The committed rocprofv3 summary the measured HBM bytes per launch come from
+# (FETCH_SIZE and WRITE_SIZE runs, scaled on a known-size copy).
+HBM_BYTES_PROFILE = os.path.join(ROOT, "profiles", "decode_cfg3_hbm_bytes.txt")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` (its name as rocprofv3 prints it) from the
+    committed counter summary, or None if the summary has no line for it."""
+    try:
+        with open(HBM_BYTES_PROFILE) as f:
+            for line in f:
+                if line.startswith("  ") and line.strip().startswith(kernel) and "total" in line:
+                    return int(round(float(line.split("total")[1].split()[0]) * 1e6))
+    except OSError:
+        pass
+    return None
+
+
+def step_kernel_bytes(kind, position, experts, vocab):
+    """Algorithmic bytes one launch of a decode-step kernel must move: the weights and
+    cache entries the reference's arithmetic reads, its f32 inputs and outputs."""
+    span_full = position + 1
+    if kind == "qkv":  # Q8_0 5120 x 2880, x, norm, bias, q out, k/v out, one RoPE row
+        return 5120 * Q8_ROW_2880 + 2 * N * 4 + 5120 * 4 + 4096 * 4 + 2 * 512 * 4 + 64 * 4
+    if kind in ("attention_window", "attention_full"):  # K and V of the span, q, out, sinks
+        span = min(span_full, 128) if kind == "attention_window" else span_full
+        return 2 * span * 512 * 4 + 2 * 4096 * 4 + 64 * 4
+    if kind == "output":  # Q8_0 2880 x 4096, attended, bias, residual in, out
+        return N * Q8_ROW_4096 + 4096 * 4 + 3 * N * 4
+    if kind == "router_rows":  # f32 router, bias, x, norm
+        return experts * N * 4 + experts * 4 + 2 * N * 4
+    if kind in ("gateup_routed", "gateup_given"):
+        return GATEUP_BYTES
+    if kind == "down_combine":  # 4 experts' down rows and biases, hidden, residual, out
+        return USED * N * 1530 + 2 * USED * N * 4 + 2 * N * 4
+    if kind == "logits":  # bf16 unembedding, x, norm, logits out
+        return vocab * N * 2 + 2 * N * 4 + vocab * 4
+    raise ValueError(kind)
 
 
 def log(msg):
@@ -119,13 +155,27 @@ def gpu_decode(args):
     step_bytes = model.step_bytes(mid)
     log(f"{ms:.4f} ms per token, {tok_s:.1f} tok/s, step {step_bytes / 1e9:.3f} GB -> "
         f"{step_bytes / (ms * 1e-3) / 1e9:.0f} GB/s algorithmic")
-    us = model.time_expert_kernel(max(20, args.steps // 5))
+    # every kind of the step's kernels, timed one kind at a time at the last step's position
+    last = context + args.warmup + args.steps - 1
+    reps = max(20, args.steps // 5)
+    kernels, total_us = {}, 0.0
+    for kind in ttlab_amd.Model.KERNELS:
+        us_k, n = model.time_kernel(kind, last, reps)
+        nbytes = step_kernel_bytes(kind, last, experts, VOCAB)
+        gbs = nbytes / (us_k * 1e-6) / 1e9
+        kernels[kind] = {"us": round(us_k, 3), "launches_per_step": n, "bytes_per_launch": nbytes,
+                         "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if kind != "gateup_given":
+            total_us += us_k * n
+        log(f"{kind:17s} {n:3d} launches x {us_k:7.2f} us, {gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
+    log(f"sum of the step's kernels timed one kind at a time: {total_us / 1000:.4f} ms (step {ms:.4f} ms)")
+    us = kernels["gateup_routed"]["us"]
     achieved = GATEUP_BYTES / (us * 1e-6) / 1e9
-    log(f"gateup_swiglu_kernel: {us:.2f} us per launch, {achieved:.0f} GB/s")
     model.close()
     us_read = read_ceiling(GATEUP_BYTES, args.layers)
     log(f"plain read of the same {GATEUP_BYTES / 1e6:.1f} MB per launch: {us_read:.2f} us, "
         f"{GATEUP_BYTES / (us_read * 1e-6) / 1e9:.0f} GB/s")
+    given = kernels["gateup_given"]
     return {
         "value": tok_s,
         "unit": "tok/s",
@@ -138,11 +188,18 @@ def gpu_decode(args):
                    "context": context, "unembedding": "bf16", "attention_weights": "Q8_0",
                    "step_algorithmic_bytes": int(step_bytes),
                    "step_algorithmic_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-                   "step_frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+                   "step_frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "kernels": kernels,
+                   "kernels_sum_ms": round(total_us / 1000, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
-                     "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
-                     "launch_us": round(us, 3), "read_ceiling": ceiling_entry(achieved, GATEUP_BYTES, us_read)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("void gateup_swiglu_kernel<1, true>"),
+                     "kernel": "gateup_swiglu_kernel<1, true> (top-4 ranking at its head, then gate/up of the 4 "
+                               "experts and the clamped SwiGLU; as the step runs it)",
+                     "bytes_per_launch": GATEUP_BYTES, "launch_us": round(us, 3),
+                     "given_indices": {"kernel": "gateup_swiglu_kernel<1, false>", "launch_us": given["us"],
+                                       "GBps": given["GBps"], "frac": given["frac"]},
+                     "read_ceiling": ceiling_entry(achieved, GATEUP_BYTES, us_read)},
     }
 
 
@@ -214,8 +271,9 @@ def gpu_moe(args):
                    "experts": EXPERTS, "used": USED, "hidden": N, "layers_per_step": LAYERS,
                    "layer_algorithmic_GBps": round(layer_bytes * LAYERS / (ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
-                     "kernel": "gateup_swiglu_kernel", "bytes_per_launch": GATEUP_BYTES,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("void gateup_swiglu_kernel<0, false>"),
+                     "kernel": "gateup_swiglu_kernel<0, false> (indices given)", "bytes_per_launch": GATEUP_BYTES,
                      "launch_us": round(us, 3)},
     }
 
@@ -428,8 +486,30 @@ def gpu_model_prefill(args):
     }
 
 
+def host_cpu():
+    """Model name, online cores and the x86 ISA extensions that matter to the oracle."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni") if f in flags]
+    return {"model": model, "nproc": os.cpu_count(), "allowed_cores": len(os.sched_getaffinity(0)), "isa": isa}
+
+
 def cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
     """The oracle (restated reference CPU path) on one host core, bounded sample."""
+    res = _cpu_baseline(seconds, workload, layers, context)
+    res["host"] = host_cpu()
+    return res
+
+
+def _cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import ctypes as C
 

@@ -203,6 +203,15 @@ int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float 
  * and weights f32 [used] (model.cpp:293-332). */
 int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
                          int32_t *indices_dev, float *weights_dev);
+/* ttl_moe_route_gateup split into its two launches, for callers that time them one
+ * by one: TTL_ROUTE_ROWS computes the exact router rows into the context's scratch,
+ * TTL_ROUTE_GATEUP ranks the rows last computed on this context and runs gate/up.
+ * No reference counterpart. */
+#define TTL_ROUTE_ROWS 1u
+#define TTL_ROUTE_GATEUP 2u
+#define TTL_ROUTE_ALL 3u
+int ttl_moe_route_gateup_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                                int32_t *indices_dev, float *weights_dev, uint32_t stages);
 int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
                  float *down_dev);
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,

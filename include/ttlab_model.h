@@ -68,6 +68,24 @@ int ttlm_time_decode(ttlm_model *model, int32_t token, uint32_t position, uint32
  * with the last step's routing, as one graph replayed `reps` times (HIP events). */
 int ttlm_time_expert_kernel(ttlm_model *model, uint32_t reps, double *us_per_launch);
 
+/* The decode step's kernels timed one kind at a time: every launch of `kind` that a step
+ * at `position` makes (all layers; the attention kinds only the layers of their parity;
+ * logits one), with the last step's inputs and scratch outputs, captured as one graph
+ * replayed `reps` times between HIP events.  us_per_launch: microseconds per launch
+ * (per partials + combine pair for TTLM_KERNEL_ATTENTION_FULL); launches (may be NULL):
+ * launches per replay.  The model's state is unchanged. */
+#define TTLM_KERNEL_QKV 0u               /* Q8_0 QKV + bias + RoPE + KV store (qkv_kernel)      */
+#define TTLM_KERNEL_ATTENTION_WINDOW 1u  /* even layers: attn_window_kernel                     */
+#define TTLM_KERNEL_ATTENTION_FULL 2u    /* odd layers: attn_partial_kernel + attn_combine_kernel */
+#define TTLM_KERNEL_OUTPUT 3u            /* O projection + residual (q8_matvec_kernel<4096>)     */
+#define TTLM_KERNEL_ROUTER_ROWS 4u       /* exact router rows and bounds (router_rows_kernel)    */
+#define TTLM_KERNEL_GATEUP_ROUTED 5u     /* gateup_swiglu_kernel with the top-k ranking, as run  */
+#define TTLM_KERNEL_GATEUP_GIVEN 6u      /* the same with the indices given                      */
+#define TTLM_KERNEL_DOWN_COMBINE 7u      /* down + bias + rank-order combine + residual          */
+#define TTLM_KERNEL_LOGITS 8u            /* unembedding + per-workgroup argmax                   */
+int ttlm_time_kernel(ttlm_model *model, uint32_t kind, uint32_t position, uint32_t reps, double *us_per_launch,
+                     uint32_t *launches);
+
 /* Decode steps (and the expert-kernel timer) replay captured HIP graphs when `enabled`
  * is nonzero (the default), else launch the same kernels one by one on the model's
  * stream -- for tools that cannot follow graph launches. */

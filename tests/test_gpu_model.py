@@ -128,6 +128,14 @@ def test_timers_leave_decode_state_intact(models):
     before = [gpu.layer_state(l) for l in range(LAYERS)]
     us = gpu.time_expert_kernel(5)
     assert 0.0 < us < 1e5
+    keys, values = gpu.kv_cache(0, 2)
+    for kind in ttlab_amd.Model.KERNELS:
+        us, launches = gpu.time_kernel(kind, 0, 3)
+        expected = {"attention_window": (LAYERS + 1) // 2, "attention_full": LAYERS // 2, "logits": 1}
+        assert launches == expected.get(kind, LAYERS), kind
+        assert 0.0 < us < 1e5, kind
+    k2, v2 = gpu.kv_cache(0, 2)
+    assert np.array_equal(keys, k2) and np.array_equal(values, v2)
     after = [gpu.layer_state(l) for l in range(LAYERS)]
     for b, a in zip(before, after):
         for u, v in zip(b, a):

@@ -1133,10 +1133,12 @@ int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_d
     return TTL_OK;
 }
 
-int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
-                         int32_t *indices_dev, float *weights_dev) {
+int ttl_moe_route_gateup_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                                int32_t *indices_dev, float *weights_dev, uint32_t stages) {
     TTL_REQUIRE(ctx && x_dev && hidden_dev && indices_dev && weights_dev, TTL_ERR_INVALID,
                 "ttl_moe_route_gateup: null argument");
+    TTL_REQUIRE((stages & ~uint32_t(TTL_ROUTE_ALL)) == 0, TTL_ERR_INVALID,
+                "ttl_moe_route_gateup_stages: unknown stage bits 0x%x", stages);
     int rc = check_layer(layer, "ttl_moe_route_gateup");
     if (rc != TTL_OK) {
         return rc;
@@ -1146,9 +1148,19 @@ int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
     if (rc != TTL_OK) {
         return rc;
     }
-    launch_router_rows(ctx, L, layer_input(L, x_dev));
-    TTL_LAUNCHED("router_rows_kernel");
-    return launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
+    if (stages & TTL_ROUTE_ROWS) {
+        launch_router_rows(ctx, L, layer_input(L, x_dev));
+        TTL_LAUNCHED("router_rows_kernel");
+    }
+    if (stages & TTL_ROUTE_GATEUP) {
+        return launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
+    }
+    return TTL_OK;
+}
+
+int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                         int32_t *indices_dev, float *weights_dev) {
+    return ttl_moe_route_gateup_stages(ctx, layer, x_dev, hidden_dev, indices_dev, weights_dev, TTL_ROUTE_ALL);
 }
 
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,

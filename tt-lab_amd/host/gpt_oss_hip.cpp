@@ -577,6 +577,141 @@ double HipGptOssModel::time_expert_kernel(size_t reps) {
     return double(ms) * 1000.0 / double(reps * spec_.layers);
 }
 
+double HipGptOssModel::time_kernel(uint32_t kind, size_t position, size_t reps, size_t *launches) {
+    if (kind >= kKernelKinds) {
+        throw std::runtime_error("time_kernel: unknown kernel kind");
+    }
+    if (position >= spec_.capacity || reps == 0) {
+        throw std::runtime_error("time_kernel: position beyond the token capacity, or no repetitions");
+    }
+    // Scratch outputs, so the step's state (layer inputs, residuals, routing, caches) is
+    // untouched; inputs are the last step's.
+    std::vector<void *> scratch;
+    const auto take = [&](size_t bytes) {
+        void *p = nullptr;
+        check(ttl_malloc(ctx_, bytes, &p), "ttl_malloc");
+        scratch.push_back(p);
+        return p;
+    };
+    const auto release_scratch = [&]() {
+        (void)ttl_sync(ctx_);
+        for (void *p : scratch) {
+            (void)ttl_free(ctx_, p);
+        }
+    };
+    ttl_graph *graph = nullptr;
+    float ms = 0.0f;
+    size_t count = 0;
+    try {
+        int32_t *pos = static_cast<int32_t *>(take(sizeof(int32_t)));
+        const int32_t p32 = int32_t(position);
+        check(ttl_memcpy_h2d(ctx_, pos, &p32, sizeof(p32)), "ttl_memcpy_h2d");
+        const size_t cache_bytes = sizeof(float) * spec_.capacity * kKvWidth;
+        float *q = static_cast<float *>(take(sizeof(float) * kQueryWidth));
+        float *kc = kind == kKernelQkv ? static_cast<float *>(take(cache_bytes)) : nullptr;
+        float *vc = kind == kKernelQkv ? static_cast<float *>(take(cache_bytes)) : nullptr;
+        float *vec = static_cast<float *>(take(sizeof(float) * kUsed * kHidden));
+        int32_t *idx = static_cast<int32_t *>(take(sizeof(int32_t) * kUsed));
+        float *w = static_cast<float *>(take(sizeof(float) * kUsed));
+        float *logits = kind == kKernelLogits ? static_cast<float *>(take(sizeof(float) * spec_.vocab)) : nullptr;
+        void *logits_ws = kind == kKernelLogits ? take(ttl_logits_workspace_bytes(spec_.vocab)) : nullptr;
+        const size_t L = spec_.layers;
+        const auto enqueue = [&]() {
+            int status = TTL_OK;
+            count = 0;
+            if (kind == kKernelLogits) {
+                ttl_stage_input f{};
+                f.base = x_ + L * kHidden;
+                f.norm_weight = output_norm_;
+                f.epsilon = norm_epsilon;
+                count = 1;
+                return unembedding_q8_ ? ttl_logits_q8_0(ctx_, unembedding_q8_, spec_.vocab, &f, logits, logits_ws)
+                                       : ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits, logits_ws);
+            }
+            for (size_t l = 0; l < L && status == TTL_OK; ++l) {
+                Layer &layer = layers_[l];
+                switch (kind) {
+                case kKernelQkv: {
+                    ttl_stage_input in{};
+                    in.base = x_ + l * kHidden;
+                    in.norm_weight = layer.attn_norm;
+                    in.epsilon = norm_epsilon;
+                    status = ttl_attn_qkv(ctx_, layer.qkv, layer.qkv_bias, &in, rope_, pos, spec_.capacity, q, kc, vc);
+                    ++count;
+                    break;
+                }
+                case kKernelAttentionWindow:
+                case kKernelAttentionFull:
+                    if ((l % 2 == 0) == (kind == kKernelAttentionWindow)) {
+                        status = ttl_attention_decode(ctx_, query_, layer.key_cache, layer.value_cache, layer.sinks,
+                                                      pos, spec_.capacity, uint32_t(l), attn_workspace_, q);
+                        ++count;
+                    }
+                    break;
+                case kKernelOutputProjection: {
+                    ttl_stage_input o{};
+                    o.base = attended_;
+                    status = ttl_matvec_q8_0(ctx_, layer.attn_output, layer.attn_output_bias, &o, x_ + l * kHidden,
+                                             vec);
+                    ++count;
+                    break;
+                }
+                case kKernelRouterRows:
+                case kKernelGateUpRouted:
+                    // the routed gate/up ranks the rows the last router launch left in the
+                    // context's scratch (the last layer's): the same work as in the step
+                    status = ttl_moe_route_gateup_stages(ctx_, &layer.moe, residual_ + l * kHidden, vec, idx, w,
+                                                         kind == kKernelRouterRows ? TTL_ROUTE_ROWS : TTL_ROUTE_GATEUP);
+                    ++count;
+                    break;
+                case kKernelGateUpGiven:
+                    status = ttl_moe_gateup_swiglu(ctx_, &layer.moe, residual_ + l * kHidden, indices_ + l * kUsed,
+                                                   vec);
+                    ++count;
+                    break;
+                case kKernelDownCombine:
+                    status = ttl_moe_down_combine(ctx_, &layer.moe, hidden_, indices_ + l * kUsed,
+                                                  weights_ + l * kUsed, residual_ + l * kHidden, vec, nullptr);
+                    ++count;
+                    break;
+                }
+            }
+            return status;
+        };
+        if (use_graph_) {
+            check(ttl_capture_begin(ctx_), "ttl_capture_begin");
+            const int status = enqueue();
+            const std::string error = status == TTL_OK ? "" : ttl_last_error();
+            check(ttl_capture_end(ctx_, &graph), "ttl_capture_end");
+            if (status != TTL_OK) {
+                throw std::runtime_error("recording the kernels to time: " + error);
+            }
+        }
+        const auto run = [&]() {
+            check(graph ? ttl_graph_launch(ctx_, graph) : enqueue(), "timed kernels");
+        };
+        for (int r = 0; r < 3; ++r) {
+            run();
+        }
+        check(ttl_sync(ctx_), "ttl_sync");
+        check(ttl_timer_start(ctx_), "ttl_timer_start");
+        for (size_t r = 0; r < reps; ++r) {
+            run();
+        }
+        check(ttl_timer_stop(ctx_, &ms), "ttl_timer_stop");
+    } catch (...) {
+        ttl_graph_free(graph);
+        release_scratch();
+        throw;
+    }
+    ttl_graph_free(graph);
+    release_scratch();
+    if (launches) {
+        *launches = count;
+    }
+    return count ? double(ms) * 1000.0 / double(reps * count) : 0.0;
+}
+
 void HipGptOssModel::layer_state(size_t layer, float *x_in, float *residual, int32_t *indices, float *weights) const {
     if (layer >= spec_.layers) {
         throw std::runtime_error("layer out of range");

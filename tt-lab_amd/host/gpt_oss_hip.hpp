@@ -103,6 +103,24 @@ class HipGptOssModel {
     // Microseconds per launch of the MXFP4 gate/up + SwiGLU kernel (all layers, the
     // last step's routing, replayed `reps` times; HIP events on the model's stream).
     double time_expert_kernel(size_t reps);
+    // The decode step's kernels, one kind at a time (TTLM_KERNEL_* in ttlab_model.h).
+    enum KernelKind : uint32_t {
+        kKernelQkv = 0,
+        kKernelAttentionWindow = 1,  // the even (sliding-window) layers
+        kKernelAttentionFull = 2,    // the odd layers: partials + combine
+        kKernelOutputProjection = 3,
+        kKernelRouterRows = 4,
+        kKernelGateUpRouted = 5,     // top-k ranking at its head, as the step runs it
+        kKernelGateUpGiven = 6,      // the same kernel with the indices given
+        kKernelDownCombine = 7,
+        kKernelLogits = 8,
+        kKernelKinds = 9,
+    };
+    // Microseconds per launch (for kKernelAttentionFull: per partials + combine pair) of
+    // every launch of `kind` one step at `position` makes, with the last step's inputs
+    // and scratch outputs (the model's state is unchanged), captured as one graph and
+    // replayed `reps` times between HIP events.  *launches = launches per replay.
+    double time_kernel(uint32_t kind, size_t position, size_t reps, size_t *launches);
 
     // Decode steps replay the captured step graph (default) or launch its kernels
     // one by one on the model's stream (same kernels, same order).

@@ -137,6 +137,17 @@ int ttlm_time_expert_kernel(ttlm_model *model, uint32_t reps, double *us_per_lau
     return guarded([&] { *us_per_launch = model->model->time_expert_kernel(reps); });
 }
 
+int ttlm_time_kernel(ttlm_model *model, uint32_t kind, uint32_t position, uint32_t reps, double *us_per_launch,
+                     uint32_t *launches) {
+    return guarded([&] {
+        size_t n = 0;
+        *us_per_launch = model->model->time_kernel(kind, position, reps, &n);
+        if (launches) {
+            *launches = uint32_t(n);
+        }
+    });
+}
+
 int ttlm_set_graph_replay(ttlm_model *model, int enabled) {
     return guarded([&] { model->model->set_graph_replay(enabled != 0); });
 }

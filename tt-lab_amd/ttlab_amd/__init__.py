@@ -95,6 +95,7 @@ def load_model_library():
         "ttlm_time_decode": (i32, [vp, C.c_int32, u32, u32, u32, C.POINTER(C.c_double)]),
         "ttlm_time_expert_kernel": (i32, [vp, u32, C.POINTER(C.c_double)]),
         "ttlm_set_graph_replay": (i32, [vp, i32]),
+        "ttlm_time_kernel": (i32, [vp, u32, u32, u32, C.POINTER(C.c_double), C.POINTER(u32)]),
         "ttlm_layer_state": (i32, [vp, u32, vp, vp, vp, vp]),
         "ttlm_final_state": (i32, [vp, vp]),
         "ttlm_kv_cache": (i32, [vp, u32, u32, vp, vp]),
@@ -198,6 +199,17 @@ class Model:
 
     def set_graph_replay(self, enabled):
         _mcheck(self.lib.ttlm_set_graph_replay(self.h, 1 if enabled else 0), "ttlm_set_graph_replay")
+
+    KERNELS = ("qkv", "attention_window", "attention_full", "output", "router_rows", "gateup_routed",
+               "gateup_given", "down_combine", "logits")
+
+    def time_kernel(self, kind, position, reps):
+        """Microseconds per launch of one kind of the step's kernels (KERNELS names them), and
+        the launches per step."""
+        us, n = C.c_double(), C.c_uint32()
+        _mcheck(self.lib.ttlm_time_kernel(self.h, self.KERNELS.index(kind), position, reps, C.byref(us), C.byref(n)),
+                "ttlm_time_kernel")
+        return us.value, n.value
 
     def layer_state(self, layer):
         x = np.empty(2880, np.float32)
