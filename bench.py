@@ -71,8 +71,9 @@ def step_kernel_bytes(kind, position, experts, vocab):
     """Algorithmic bytes one launch of a decode-step kernel must move: the weights and
     cache entries the reference's arithmetic reads, its f32 inputs and outputs."""
     span_full = position + 1
-    if kind == "qkv":  # Q8_0 5120 x 2880, x, norm, bias, q out, k/v out, one RoPE row
-        return 5120 * Q8_ROW_2880 + 2 * N * 4 + 5120 * 4 + 4096 * 4 + 2 * 512 * 4 + 64 * 4
+    if kind == "qkv":  # Q8_0 5120 x 2880; the previous layer's residual, 4 down outputs and
+        # weights (the combine staged in), norm; bias, q out, k/v out, one RoPE row
+        return 5120 * Q8_ROW_2880 + (2 + USED) * N * 4 + 5120 * 4 + 4096 * 4 + 2 * 512 * 4 + 64 * 4
     if kind in ("attention_window", "attention_full"):  # K and V of the span, q, out, sinks
         span = min(span_full, 128) if kind == "attention_window" else span_full
         return 2 * span * 512 * 4 + 2 * 4096 * 4 + 64 * 4
@@ -82,10 +83,10 @@ def step_kernel_bytes(kind, position, experts, vocab):
         return experts * N * 4 + experts * 4 + 2 * N * 4
     if kind in ("gateup_routed", "gateup_given"):
         return GATEUP_BYTES
-    if kind == "down_combine":  # 4 experts' down rows and biases, hidden, residual, out
-        return USED * N * 1530 + 2 * USED * N * 4 + 2 * N * 4
-    if kind == "logits":  # bf16 unembedding, x, norm, logits out
-        return vocab * N * 2 + 2 * N * 4 + vocab * 4
+    if kind == "down":  # 4 experts' down rows and biases, hidden in, 4 outputs
+        return USED * N * 1530 + 3 * USED * N * 4
+    if kind == "logits":  # bf16 unembedding; residual, 4 down outputs, norm; logits out
+        return vocab * N * 2 + (2 + USED) * N * 4 + vocab * 4
     raise ValueError(kind)
 
 

@@ -74,14 +74,15 @@ int ttlm_time_expert_kernel(ttlm_model *model, uint32_t reps, double *us_per_lau
  * replayed `reps` times between HIP events.  us_per_launch: microseconds per launch
  * (per partials + combine pair for TTLM_KERNEL_ATTENTION_FULL); launches (may be NULL):
  * launches per replay.  The model's state is unchanged. */
-#define TTLM_KERNEL_QKV 0u               /* Q8_0 QKV + bias + RoPE + KV store (qkv_kernel)      */
+#define TTLM_KERNEL_QKV 0u               /* combine + residual + norm staged, Q8_0 QKV + bias +
+                                          * RoPE + KV store (qkv_kernel)                         */
 #define TTLM_KERNEL_ATTENTION_WINDOW 1u  /* even layers: attn_window_kernel                     */
 #define TTLM_KERNEL_ATTENTION_FULL 2u    /* odd layers: attn_partial_kernel + attn_combine_kernel */
 #define TTLM_KERNEL_OUTPUT 3u            /* O projection + residual (q8_matvec_kernel<4096>)     */
 #define TTLM_KERNEL_ROUTER_ROWS 4u       /* exact router rows and bounds (router_rows_kernel)    */
 #define TTLM_KERNEL_GATEUP_ROUTED 5u     /* gateup_swiglu_kernel with the top-k ranking, as run  */
 #define TTLM_KERNEL_GATEUP_GIVEN 6u      /* the same with the indices given                      */
-#define TTLM_KERNEL_DOWN_COMBINE 7u      /* down + bias + rank-order combine + residual          */
+#define TTLM_KERNEL_DOWN 7u              /* the 4 experts' down projections + bias (down_kernel) */
 #define TTLM_KERNEL_LOGITS 8u            /* unembedding + per-workgroup argmax                   */
 int ttlm_time_kernel(ttlm_model *model, uint32_t kind, uint32_t position, uint32_t reps, double *us_per_launch,
                      uint32_t *launches);

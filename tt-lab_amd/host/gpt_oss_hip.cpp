@@ -129,6 +129,7 @@ void HipGptOssModel::finish_construction() {
         history_ = static_cast<int32_t *>(alloc(sizeof(int32_t) * spec_.capacity));
         x_ = static_cast<float *>(alloc(sizeof(float) * (L + 1) * kHidden));
         residual_ = static_cast<float *>(alloc(sizeof(float) * L * kHidden));
+        down_ = static_cast<float *>(alloc(sizeof(float) * L * kUsed * kHidden));
         indices_ = static_cast<int32_t *>(alloc(sizeof(int32_t) * L * kUsed));
         weights_ = static_cast<float *>(alloc(sizeof(float) * L * kUsed));
         hidden_ = static_cast<float *>(alloc(sizeof(float) * kUsed * kHidden));
@@ -296,15 +297,34 @@ void HipGptOssModel::generate_weights() {
 //   output projection + residual, router (+ post-attention norm), gate/up +
 //   SwiGLU, down + combine + residual; output norm + logits; greedy argmax
 //   (writes the next token, advances the position).
+// The input of layer l's QKV projection (l == layers: of the unembedding) as the
+// staging computes it: for l > 0 the previous layer's output is never materialized
+// by a kernel of its own -- the MoE combine and the residual add (model.cpp:323-337,
+// 592-594) run in the consumer's staging, x_l = residual_{l-1} + (0 + w_0 d_0 + ...
+// + w_3 d_3) in the reference's rank order, and workgroup 0 stores x_l for the
+// state readers (and for the O projection's residual add).
+ttl_stage_input HipGptOssModel::layer_input(size_t l, const float *norm_weight) const {
+    ttl_stage_input in{};
+    in.norm_weight = norm_weight;
+    in.epsilon = norm_epsilon;
+    if (l == 0) {
+        in.base = x_;
+        return in;
+    }
+    in.base = residual_ + (l - 1) * kHidden;
+    in.add = down_ + (l - 1) * kUsed * kHidden;
+    in.add_weights = weights_ + (l - 1) * kUsed;
+    in.add_count = kUsed;
+    in.sum_out = x_ + l * kHidden;
+    return in;
+}
+
 int HipGptOssModel::enqueue_step() {
     const size_t L = spec_.layers;
     int status = ttl_embedding_q8_0(ctx_, embedding_, spec_.vocab, token_, x_);
     for (size_t l = 0; l < L && status == TTL_OK; ++l) {
         Layer &layer = layers_[l];
-        ttl_stage_input in{};
-        in.base = x_ + l * kHidden;
-        in.norm_weight = layer.attn_norm;
-        in.epsilon = norm_epsilon;
+        const ttl_stage_input in = layer_input(l, layer.attn_norm);
         status = ttl_attn_qkv(ctx_, layer.qkv, layer.qkv_bias, &in, rope_, position_, spec_.capacity, query_,
                               layer.key_cache, layer.value_cache);
         if (status == TTL_OK) {
@@ -322,17 +342,13 @@ int HipGptOssModel::enqueue_step() {
                                           weights_ + l * kUsed);
         }
         if (status == TTL_OK) {
-            // the MoE output's combine and the residual add (model.cpp:592-594) are fused
-            // into the down projection; its output is the next layer's input
-            status = ttl_moe_down_combine(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, weights_ + l * kUsed,
-                                          residual_ + l * kHidden, x_ + (l + 1) * kHidden, nullptr);
+            // the four experts' down projections (+ bias), one workgroup per (slot, tile);
+            // the combine and the residual add run in the next consumer's staging
+            status = ttl_moe_down(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, down_ + l * kUsed * kHidden);
         }
     }
     if (status == TTL_OK) {
-        ttl_stage_input f{};
-        f.base = x_ + L * kHidden;
-        f.norm_weight = output_norm_;
-        f.epsilon = norm_epsilon;
+        const ttl_stage_input f = layer_input(L, output_norm_);
         status = unembedding_q8_ ? ttl_logits_q8_0(ctx_, unembedding_q8_, spec_.vocab, &f, logits_, logits_workspace_)
                                  : ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits_, logits_workspace_);
     }
@@ -620,10 +636,8 @@ double HipGptOssModel::time_kernel(uint32_t kind, size_t position, size_t reps, 
             int status = TTL_OK;
             count = 0;
             if (kind == kKernelLogits) {
-                ttl_stage_input f{};
-                f.base = x_ + L * kHidden;
-                f.norm_weight = output_norm_;
-                f.epsilon = norm_epsilon;
+                ttl_stage_input f = layer_input(L, output_norm_);
+                f.sum_out = nullptr;
                 count = 1;
                 return unembedding_q8_ ? ttl_logits_q8_0(ctx_, unembedding_q8_, spec_.vocab, &f, logits, logits_ws)
                                        : ttl_logits_bf16(ctx_, unembedding_, spec_.vocab, &f, logits, logits_ws);
@@ -632,10 +646,8 @@ double HipGptOssModel::time_kernel(uint32_t kind, size_t position, size_t reps, 
                 Layer &layer = layers_[l];
                 switch (kind) {
                 case kKernelQkv: {
-                    ttl_stage_input in{};
-                    in.base = x_ + l * kHidden;
-                    in.norm_weight = layer.attn_norm;
-                    in.epsilon = norm_epsilon;
+                    ttl_stage_input in = layer_input(l, layer.attn_norm);
+                    in.sum_out = nullptr;
                     status = ttl_attn_qkv(ctx_, layer.qkv, layer.qkv_bias, &in, rope_, pos, spec_.capacity, q, kc, vc);
                     ++count;
                     break;
@@ -669,9 +681,8 @@ double HipGptOssModel::time_kernel(uint32_t kind, size_t position, size_t reps, 
                                                    vec);
                     ++count;
                     break;
-                case kKernelDownCombine:
-                    status = ttl_moe_down_combine(ctx_, &layer.moe, hidden_, indices_ + l * kUsed,
-                                                  weights_ + l * kUsed, residual_ + l * kHidden, vec, nullptr);
+                case kKernelDown:
+                    status = ttl_moe_down(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, vec);
                     ++count;
                     break;
                 }

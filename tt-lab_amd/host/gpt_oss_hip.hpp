@@ -112,7 +112,7 @@ class HipGptOssModel {
         kKernelRouterRows = 4,
         kKernelGateUpRouted = 5,     // top-k ranking at its head, as the step runs it
         kKernelGateUpGiven = 6,      // the same kernel with the indices given
-        kKernelDownCombine = 7,
+        kKernelDown = 7,             // the four experts' down projections (+ bias)
         kKernelLogits = 8,
         kKernelKinds = 9,
     };
@@ -168,6 +168,7 @@ class HipGptOssModel {
     void upload_gguf(const GgufFile &file);
     void finish_construction();
     int enqueue_step();
+    ttl_stage_input layer_input(size_t layer, const float *norm_weight) const;
     int enqueue_prefill_chunk(size_t first, size_t count);
     void record_step();
     void run_step();
@@ -188,6 +189,7 @@ class HipGptOssModel {
     int32_t *token_ = nullptr, *position_ = nullptr, *history_ = nullptr;
     float *x_ = nullptr;             // [layers + 1][2880]: layer inputs, then the final stream
     float *residual_ = nullptr;      // [layers][2880]
+    float *down_ = nullptr;          // [layers][4][2880]: each layer's expert down outputs
     int32_t *indices_ = nullptr;     // [layers][4]
     float *weights_ = nullptr;       // [layers][4]
     float *hidden_ = nullptr, *query_ = nullptr, *attended_ = nullptr, *attn_workspace_ = nullptr;

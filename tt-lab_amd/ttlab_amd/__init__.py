@@ -201,7 +201,7 @@ class Model:
         _mcheck(self.lib.ttlm_set_graph_replay(self.h, 1 if enabled else 0), "ttlm_set_graph_replay")
 
     KERNELS = ("qkv", "attention_window", "attention_full", "output", "router_rows", "gateup_routed",
-               "gateup_given", "down_combine", "logits")
+               "gateup_given", "down", "logits")
 
     def time_kernel(self, kind, position, reps):
         """Microseconds per launch of one kind of the step's kernels (KERNELS names them), and
