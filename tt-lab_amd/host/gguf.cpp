@@ -1,6 +1,16 @@
 // GGUF v3 reader (see gguf.hpp).
+//
+// Design: one parser walks the header once.  What it needs to know about a
+// metadata value -- how many bytes a scalar occupies, whether it is an integer and
+// signed, whether it is a float -- comes from one table indexed by the value kind,
+// so scalars, arrays of scalars and the typed accessors all share that table instead
+// of a switch per kind.  Tensor descriptors are only collected during the walk;
+// their data is placed and bounds-checked in a second pass, once the header's end
+// and general.alignment are known.  The format rules and error messages are the
+// reference's (gguf.cpp:145-239, 275-336), since callers match on them.
 #include "gguf.hpp"
 
+#include <array>
 #include <cerrno>
 #include <cstring>
 #include <fcntl.h>
@@ -16,129 +26,145 @@ namespace {
     throw std::runtime_error(message);
 }
 
-// Bounds-checked little-endian reads over the mapping.
-class Reader {
-  public:
-    Reader(const uint8_t *p, size_t n) : base_(p), at_(0), size_(n) {}
+// Per value kind (GgufKind order, gguf.h:13-27): scalar width in bytes (0: not a
+// fixed-size scalar), integer, signed, floating point.
+struct KindTraits {
+    uint8_t width;
+    bool integer, is_signed, floating;
+};
+constexpr std::array<KindTraits, 13> kKinds = {{
+    {1, true, false, false},   // u8
+    {1, true, true, false},    // i8
+    {2, true, false, false},   // u16
+    {2, true, true, false},    // i16
+    {4, true, false, false},   // u32
+    {4, true, true, false},    // i32
+    {4, false, false, true},   // f32
+    {1, false, false, false},  // bool
+    {0, false, false, false},  // string
+    {0, false, false, false},  // array
+    {8, true, false, false},   // u64
+    {8, true, true, false},    // i64
+    {8, false, false, true},   // f64
+}};
 
-    template <class T>
-    T get() {
-        T v;
-        std::memcpy(&v, need(sizeof(T)), sizeof(T));
-        return v;
+const KindTraits &traits(GgufKind kind) {
+    return kKinds[size_t(kind)];
+}
+
+// A little-endian scalar of `width` bytes as a 64-bit two's-complement value.
+uint64_t widen(const uint8_t *p, const KindTraits &t) {
+    uint64_t v = 0;
+    for (int i = t.width - 1; i >= 0; --i) {
+        v = (v << 8) | p[i];
     }
-    const uint8_t *need(size_t n) {
-        if (n > size_ - at_) {
+    if (t.is_signed && t.width < 8 && (v >> (8 * t.width - 1)) & 1) {
+        v |= ~uint64_t(0) << (8 * t.width);  // sign extension
+    }
+    return v;
+}
+
+// The header walk: a window [at, end) over the mapping that only ever shrinks from
+// the front; every read checks the window first.
+class HeaderParser {
+  public:
+    HeaderParser(const uint8_t *begin, size_t size) : begin_(begin), at_(begin), end_(begin + size) {}
+
+    size_t consumed() const {
+        return size_t(at_ - begin_);
+    }
+
+    const uint8_t *bytes(uint64_t n) {
+        if (n > uint64_t(end_ - at_)) {
             fail("truncated GGUF file");
         }
-        const uint8_t *p = base_ + at_;
+        const uint8_t *p = at_;
         at_ += n;
         return p;
     }
-    std::string_view str() {
-        const uint64_t n = get<uint64_t>();
-        if (n > size_) {
+
+    template <class T>
+    T scalar() {
+        T v;
+        std::memcpy(&v, bytes(sizeof(T)), sizeof(T));
+        return v;
+    }
+
+    std::string_view text() {
+        const uint64_t n = scalar<uint64_t>();
+        if (n > uint64_t(end_ - begin_)) {
             fail("GGUF string is too large");
         }
-        return {reinterpret_cast<const char *>(need(size_t(n))), size_t(n)};
+        return {reinterpret_cast<const char *>(bytes(n)), size_t(n)};
     }
-    size_t pos() const {
-        return at_;
+
+    GgufKind kind() {
+        const uint32_t raw = scalar<uint32_t>();
+        if (raw >= kKinds.size()) {
+            fail("unknown GGUF metadata type " + std::to_string(raw));
+        }
+        return GgufKind(raw);
+    }
+
+    // One metadata value of `kind`: scalars and arrays of scalars keep a pointer to
+    // their bytes in the mapping; strings a view; string arrays (the tokenizer's
+    // vocabulary) are walked over and not kept.
+    GgufEntry value(GgufKind kind) {
+        GgufEntry e;
+        e.kind = kind;
+        if (kind == GgufKind::string) {
+            e.text = text();
+        } else if (kind != GgufKind::array) {
+            e.raw = bytes(traits(kind).width);
+        } else {
+            e.element = this->kind();
+            e.count = scalar<uint64_t>();
+            if (e.element == GgufKind::array) {
+                fail("nested GGUF arrays are invalid");
+            }
+            if (e.element == GgufKind::string) {
+                if (e.count > uint64_t(end_ - at_) / sizeof(uint64_t)) {
+                    fail("GGUF string array is too large");
+                }
+                for (uint64_t i = 0; i < e.count; ++i) {
+                    text();
+                }
+            } else {
+                const uint64_t w = traits(e.element).width;
+                if (e.count > uint64_t(end_ - at_) / w) {
+                    fail("GGUF array is too large");
+                }
+                e.raw = bytes(e.count * w);
+            }
+        }
+        return e;
     }
 
   private:
-    const uint8_t *base_;
-    size_t at_, size_;
+    const uint8_t *begin_, *at_, *end_;
 };
-
-size_t scalar_width(GgufKind kind) {
-    switch (kind) {
-    case GgufKind::u8:
-    case GgufKind::i8:
-    case GgufKind::boolean:
-        return 1;
-    case GgufKind::u16:
-    case GgufKind::i16:
-        return 2;
-    case GgufKind::u32:
-    case GgufKind::i32:
-    case GgufKind::f32:
-        return 4;
-    case GgufKind::u64:
-    case GgufKind::i64:
-    case GgufKind::f64:
-        return 8;
-    default:
-        fail("GGUF value is not a fixed-size primitive");
-    }
-}
-
-GgufKind kind_of(Reader &r) {
-    const uint32_t raw = r.get<uint32_t>();
-    if (raw > uint32_t(GgufKind::f64)) {
-        fail("unknown GGUF metadata type " + std::to_string(raw));
-    }
-    return GgufKind(raw);
-}
-
-GgufEntry read_entry(Reader &r, GgufKind kind) {
-    GgufEntry e;
-    e.kind = kind;
-    if (kind == GgufKind::string) {
-        e.text = r.str();
-        return e;
-    }
-    if (kind != GgufKind::array) {
-        e.raw = r.need(scalar_width(kind));
-        return e;
-    }
-    e.element = kind_of(r);
-    e.count = r.get<uint64_t>();
-    if (e.element == GgufKind::array) {
-        fail("nested GGUF arrays are invalid");
-    }
-    if (e.element == GgufKind::string) {
-        for (uint64_t i = 0; i < e.count; ++i) {
-            r.str();  // string arrays (the tokenizer vocabulary) are skipped
-        }
-        return e;
-    }
-    const size_t w = scalar_width(e.element);
-    if (e.count > SIZE_MAX / w) {
-        fail("GGUF array is too large");
-    }
-    e.raw = r.need(size_t(e.count) * w);
-    return e;
-}
-
-template <class T>
-T value_as(const GgufEntry &e) {
-    T v;
-    std::memcpy(&v, e.raw, sizeof(T));
-    return v;
-}
 
 }  // namespace
 
 size_t gguf_row_bytes(uint32_t type, uint64_t n) {
-    switch (type) {
-    case kGgmlF32:
-        return size_t(n) * 4;
-    case kGgmlBf16:
-        return size_t(n) * 2;
-    case kGgmlQ8_0:
-        if (n % 32) {
-            fail("Q8_0 row is not a multiple of 32");
-        }
-        return size_t(n / 32) * 34;
-    case kGgmlMxfp4:
-        if (n % 32) {
-            fail("MXFP4 row is not a multiple of 32");
-        }
-        return size_t(n / 32) * 17;
-    default:
+    // elements per block and bytes per block of each supported type (tensor.cpp:136-157)
+    uint64_t per = 1, block = 0;
+    const char *name = nullptr;
+    if (type == kGgmlF32) {
+        block = 4;
+    } else if (type == kGgmlBf16) {
+        block = 2;
+    } else if (type == kGgmlQ8_0) {
+        per = 32, block = 34, name = "Q8_0";
+    } else if (type == kGgmlMxfp4) {
+        per = 32, block = 17, name = "MXFP4";
+    } else {
         fail("unsupported tensor type " + std::to_string(type));
     }
+    if (n % per) {
+        fail(std::string(name) + " row is not a multiple of 32");
+    }
+    return size_t(n / per * block);
 }
 
 GgufFile::GgufFile(const std::string &path) {
@@ -161,83 +187,94 @@ GgufFile::GgufFile(const std::string &path) {
     }
     bytes_ = static_cast<const uint8_t *>(map);
     try {
-        Reader r(bytes_, size_);
-        if (r.get<uint32_t>() != 0x46554747u) {  // "GGUF"
-            fail("not a GGUF file");
-        }
-        version_ = r.get<uint32_t>();
-        if (version_ != 3) {
-            fail("unsupported GGUF version " + std::to_string(version_));
-        }
-        const uint64_t ntensors = r.get<uint64_t>();
-        const uint64_t nkeys = r.get<uint64_t>();
-        if (ntensors > size_ || nkeys > size_) {
-            fail("GGUF header counts are too large");
-        }
-        for (uint64_t i = 0; i < nkeys; ++i) {
-            const std::string_view key = r.str();
-            GgufEntry e = read_entry(r, kind_of(r));
-            if (!entry_index_.emplace(key, entries_.size()).second) {
-                fail("duplicate GGUF key: " + std::string(key));
-            }
-            entries_.emplace_back(key, e);
-        }
-        for (uint64_t i = 0; i < ntensors; ++i) {
-            GgufTensorInfo t;
-            t.name = r.str();
-            const uint32_t dims = r.get<uint32_t>();
-            if (dims == 0 || dims > 4) {
-                fail("invalid tensor rank");
-            }
-            for (uint32_t d = 0; d < dims; ++d) {
-                t.shape.push_back(r.get<uint64_t>());
-            }
-            t.type = r.get<uint32_t>();
-            t.offset = r.get<uint64_t>();
-            if (!tensor_index_.emplace(t.name, tensors_.size()).second) {
-                fail("duplicate tensor: " + std::string(t.name));
-            }
-            tensors_.push_back(std::move(t));
-        }
-        uint64_t alignment = 32;
-        if (const GgufEntry *a = find("general.alignment")) {
-            if (a->kind != GgufKind::u32) {
-                fail("general.alignment is not uint32");
-            }
-            alignment = value_as<uint32_t>(*a);
-        }
-        if (alignment == 0 || (alignment & (alignment - 1)) != 0) {
-            fail("invalid GGUF alignment");
-        }
-        const uint64_t data = (uint64_t(r.pos()) + alignment - 1) & ~(alignment - 1);
-        if (data > size_) {
-            fail("GGUF tensor data starts past end of file");
-        }
-        for (GgufTensorInfo &t : tensors_) {
-            if (t.offset > size_ - data) {
-                fail("tensor starts past end of GGUF file");
-            }
-            size_t rows = 1;
-            for (size_t d = 1; d < t.shape.size(); ++d) {
-                if (t.shape[d] != 0 && rows > SIZE_MAX / t.shape[d]) {
-                    fail("tensor " + std::string(t.name) + " is too large");
-                }
-                rows *= size_t(t.shape[d]);
-            }
-            const size_t row = gguf_row_bytes(t.type, t.shape[0]);
-            if (rows != 0 && row > SIZE_MAX / rows) {
-                fail("tensor " + std::string(t.name) + " is too large");
-            }
-            t.bytes = row * rows;
-            if (t.bytes > size_ - data - t.offset) {
-                fail("tensor extends past end of GGUF file");
-            }
-            t.data = bytes_ + data + t.offset;
-        }
+        parse_header();
+        place_tensor_data();
     } catch (...) {
         munmap(const_cast<uint8_t *>(bytes_), size_);
         close(fd_);
         throw;
+    }
+}
+
+// Pass 1: magic, version, counts, the key/value table and the tensor descriptors.
+void GgufFile::parse_header() {
+    HeaderParser p(bytes_, size_);
+    if (p.scalar<uint32_t>() != 0x46554747u) {  // the bytes "GGUF"
+        fail("not a GGUF file");
+    }
+    version_ = p.scalar<uint32_t>();
+    if (version_ != 3) {
+        fail("unsupported GGUF version " + std::to_string(version_));
+    }
+    const uint64_t tensor_count = p.scalar<uint64_t>();
+    const uint64_t key_count = p.scalar<uint64_t>();
+    if (tensor_count > size_ || key_count > size_) {
+        fail("GGUF header counts are too large");
+    }
+    for (uint64_t i = 0; i < key_count; ++i) {
+        const std::string_view key = p.text();
+        const GgufKind kind = p.kind();
+        if (!entry_index_.emplace(key, entries_.size()).second) {
+            fail("duplicate GGUF key: " + std::string(key));
+        }
+        entries_.emplace_back(key, p.value(kind));
+    }
+    tensors_.resize(size_t(tensor_count));
+    for (uint64_t i = 0; i < tensor_count; ++i) {
+        GgufTensorInfo &t = tensors_[size_t(i)];
+        t.name = p.text();
+        const uint32_t rank = p.scalar<uint32_t>();
+        if (rank == 0 || rank > 4) {
+            fail("invalid tensor rank");
+        }
+        t.shape.resize(rank);
+        for (uint64_t &extent : t.shape) {
+            extent = p.scalar<uint64_t>();
+        }
+        t.type = p.scalar<uint32_t>();
+        t.offset = p.scalar<uint64_t>();
+        if (!tensor_index_.emplace(t.name, size_t(i)).second) {
+            fail("duplicate tensor: " + std::string(t.name));
+        }
+    }
+    header_bytes_ = p.consumed();
+}
+
+// Pass 2: the data section starts at the header's end rounded up to
+// general.alignment (default 32); every tensor's bytes must lie inside the file.
+void GgufFile::place_tensor_data() {
+    uint64_t alignment = 32;
+    if (const GgufEntry *a = find("general.alignment")) {
+        if (a->kind != GgufKind::u32) {
+            fail("general.alignment is not uint32");
+        }
+        alignment = widen(a->raw, traits(a->kind));
+    }
+    if (alignment == 0 || (alignment & (alignment - 1)) != 0) {
+        fail("invalid GGUF alignment");
+    }
+    const uint64_t data = (uint64_t(header_bytes_) + alignment - 1) & ~(alignment - 1);
+    if (data > size_) {
+        fail("GGUF tensor data starts past end of file");
+    }
+    const uint64_t room = size_ - data;
+    for (GgufTensorInfo &t : tensors_) {
+        if (t.offset > room) {
+            fail("tensor starts past end of GGUF file");
+        }
+        // bytes = row bytes x the product of the other extents, without overflow
+        uint64_t total = gguf_row_bytes(t.type, t.shape[0]);
+        for (size_t d = 1; d < t.shape.size(); ++d) {
+            if (t.shape[d] != 0 && total > UINT64_MAX / t.shape[d]) {
+                fail("tensor " + std::string(t.name) + " is too large");
+            }
+            total *= t.shape[d];
+        }
+        if (total > room - t.offset) {
+            fail("tensor extends past end of GGUF file");
+        }
+        t.bytes = size_t(total);
+        t.data = bytes_ + data + t.offset;
     }
 }
 
@@ -256,56 +293,49 @@ const GgufTensorInfo *GgufFile::tensor(std::string_view name) const {
     return it == tensor_index_.end() ? nullptr : &tensors_[it->second];
 }
 
-std::string_view GgufFile::string(std::string_view key) const {
+const GgufEntry &GgufFile::require(std::string_view key) const {
     const GgufEntry *e = find(key);
     if (!e) {
         fail("missing GGUF key: " + std::string(key));
     }
-    if (e->kind != GgufKind::string) {
+    return *e;
+}
+
+std::string_view GgufFile::string(std::string_view key) const {
+    const GgufEntry &e = require(key);
+    if (e.kind != GgufKind::string) {
         fail("GGUF key is not a string: " + std::string(key));
     }
-    return e->text;
+    return e.text;
 }
 
 uint64_t GgufFile::integer(std::string_view key) const {
-    const GgufEntry *e = find(key);
-    if (!e) {
-        fail("missing GGUF key: " + std::string(key));
-    }
-    switch (e->kind) {
-    case GgufKind::u8:
-        return value_as<uint8_t>(*e);
-    case GgufKind::i8:
-        return uint64_t(int64_t(value_as<int8_t>(*e)));
-    case GgufKind::u16:
-        return value_as<uint16_t>(*e);
-    case GgufKind::i16:
-        return uint64_t(int64_t(value_as<int16_t>(*e)));
-    case GgufKind::u32:
-        return value_as<uint32_t>(*e);
-    case GgufKind::i32:
-        return uint64_t(int64_t(value_as<int32_t>(*e)));
-    case GgufKind::u64:
-        return value_as<uint64_t>(*e);
-    case GgufKind::i64:
-        return uint64_t(value_as<int64_t>(*e));
-    default:
+    const GgufEntry &e = require(key);
+    const KindTraits &t = traits(e.kind);
+    if (!t.integer) {
         fail("GGUF key is not an integer: " + std::string(key));
     }
+    return widen(e.raw, t);
 }
 
 double GgufFile::number(std::string_view key) const {
-    const GgufEntry *e = find(key);
-    if (!e) {
-        fail("missing GGUF key: " + std::string(key));
+    const GgufEntry &e = require(key);
+    if (e.kind == GgufKind::f32) {
+        float v;
+        std::memcpy(&v, e.raw, sizeof v);
+        return v;
     }
-    if (e->kind == GgufKind::f32) {
-        return value_as<float>(*e);
+    if (e.kind == GgufKind::f64) {
+        double v;
+        std::memcpy(&v, e.raw, sizeof v);
+        return v;
     }
-    if (e->kind == GgufKind::f64) {
-        return value_as<double>(*e);
+    const KindTraits &t = traits(e.kind);
+    if (!t.integer) {
+        fail("GGUF key is not an integer: " + std::string(key));
     }
-    return double(integer(key));
+    const uint64_t v = widen(e.raw, t);
+    return t.is_signed ? double(int64_t(v)) : double(v);
 }
 
 }  // namespace ttlab

@@ -63,9 +63,14 @@ class GgufFile {
     double number(std::string_view key) const;
 
   private:
+    void parse_header();       // magic, version, key/values, tensor descriptors
+    void place_tensor_data();  // data offset, tensor sizes and bounds
+    const GgufEntry &require(std::string_view key) const;
+
     int fd_ = -1;
     size_t size_ = 0;
     const uint8_t *bytes_ = nullptr;
+    size_t header_bytes_ = 0;
     uint32_t version_ = 0;
     std::vector<std::pair<std::string_view, GgufEntry>> entries_;
     std::unordered_map<std::string_view, size_t> entry_index_;
