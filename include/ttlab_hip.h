@@ -237,6 +237,19 @@ int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
 
 #define TTL_DTYPE_F32 0
 #define TTL_DTYPE_BF16 1
+/* f32 / bf16 input computed on the scaled path (ttl_moe_prefill_experts): the
+ * activations, and the SwiGLU hidden between the two GEMMs, quantized to MXFP8 (E4M3
+ * values with an E8M0 exponent per 32-element block, the smallest exponent at which
+ * the block's largest magnitude is at most 448; round to nearest even), then
+ * v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as they are stored.  The
+ * products are those of the dequantized values (ttl_mxfp8_dequantize), but the
+ * instruction's accumulation is not exact in f32 (one GEMM against the reference's
+ * f32 sum of the same dequantized products: relative L2 below 1e-5, measured 7.9e-6).
+ * The SwiGLU hidden is requantized too, so the MoE's output carries the format's own
+ * error (relative L2 about 7e-2 on random activations): the bf16 path stays the
+ * exact one.  No reference counterpart (the reference computes in f32). */
+#define TTL_DTYPE_F32_AS_MXFP8 2
+#define TTL_DTYPE_BF16_AS_MXFP8 3
 
 /* out[tokens[s]][r] = bias[expert][r] + sum_k W[expert][r][k] x[tokens[s]][k] for
  * s < count; other rows of out are untouched.  Replaces transpose_selected +
@@ -249,6 +262,20 @@ size_t ttl_matmul_mxfp4_selected_workspace_bytes(uint32_t count);
 int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
                               uint32_t x_stride, uint32_t x_rows, const int32_t *tokens_dev, uint32_t count,
                               float *out_dev, uint32_t expert, void *workspace_dev, size_t workspace_bytes);
+
+/* ttl_matmul_mxfp4_selected on the scaled path: the selected tokens' rows quantized to
+ * MXFP8 (see TTL_DTYPE_F32_AS_MXFP8), then v_mfma_scale with the MXFP4 weights; the
+ * products are exactly those of ttl_mxfp8_dequantize's values, their sum is the
+ * instruction's.  No reference counterpart (a faster, inexact form of
+ * matmul_add_mxfp4_selected_transposed, tensor.cpp:306-495). */
+size_t ttl_matmul_mxfp4_selected_mxfp8_workspace_bytes(uint32_t count);
+int ttl_matmul_mxfp4_selected_mxfp8(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
+                                    uint32_t x_stride, uint32_t x_rows, const int32_t *tokens_dev, uint32_t count,
+                                    float *out_dev, uint32_t expert, void *workspace_dev, size_t workspace_bytes);
+/* The values the scaled path multiplies: each 2880-wide row of x (f32 or bf16) in
+ * 32-element blocks quantized to MXFP8 and widened back to f32 (exact); a block with a
+ * non-finite value becomes NaN.  out_dev f32 [rows][2880].  No reference counterpart. */
+int ttl_mxfp8_dequantize(ttl_ctx *ctx, const void *x_dev, int x_dtype, uint32_t rows, float *out_dev);
 
 /* The expert half of GptOssModel::moe_batch (model.cpp:378-460) for `count` tokens
  * with given routing: indices_dev int32 [count][used] and weights_dev f32

@@ -158,3 +158,27 @@ def layer_prefill(layer, layer_index, first, xs, key_cache, value_cache, freqs32
         qs.append(q)
     return [after_attention(layer, x, attention(q, key_cache, value_cache, layer.sinks, layer_index, first + t))
             for t, (x, q) in enumerate(zip(xs, qs))]
+
+
+def mxfp8_dequantize(x):
+    """The MXFP8 values of x's 32-element blocks (the rule of include/ttlab_hip.h,
+    TTL_DTYPE_F32_AS_MXFP8), widened back to float32: exponent X = the smallest with
+    max|x| / 2^X <= 448 (0 for a zero block, -127 when the maximum is an f32
+    subnormal), elements OCP E4M3 of x / 2^X rounded to nearest even; a block with a
+    non-finite value becomes NaN."""
+    b = np.asarray(x, np.float32).reshape(-1, 32).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        m = np.abs(b).max(axis=1)
+    finite = np.isfinite(b).all(axis=1)
+    mant, e = np.frexp(np.where(finite, m, 1.0))  # m = mant 2^e, mant in [0.5, 1)
+    X = np.where(mant > 0.875, e - 8, e - 9)      # significand 2 mant > 1.75 -> one more
+    X = np.where(m < 2.0 ** -126, -127, X)
+    X = np.where(m > 0, X, 0)
+    v = np.ldexp(np.where(finite[:, None], b, 0.0), -X[:, None])
+    a = np.abs(v)
+    am, ae = np.frexp(np.maximum(a, 2.0 ** -6))
+    step = np.ldexp(1.0, ae - 1 - 3)              # 3 mantissa bits; subnormals step 2^-9
+    q = np.round(a / step) * step                  # numpy rounds half to even
+    out = np.sign(v) * np.ldexp(q, X[:, None])
+    out[~finite] = np.nan
+    return out.astype(np.float32).reshape(np.shape(x))

@@ -94,3 +94,90 @@ __device__ inline void split_planes(const float (&v)[8], uint4 (&out)[P]) {
 }
 
 }  // namespace mf
+
+// The scaled path: v_mfma_scale_f32_16x16x128_f8f6f4 with MXFP4 weights as A and
+// MXFP8 (E4M3 + an E8M0 scale per 32 values) activations as B.
+//
+// Operand layout, measured on gfx950 (one wave, structured operands):
+//  - A lane (row r, group g) holds 32 fp4 values, value v = nibble v of its 16 bytes;
+//    here that is the repacked code chunk of MXFP4 block 4i+g of row r, so value v is
+//    block element v/2 + 16 (v%2) (GGUF order: byte j = elements j and j+16).
+//  - A value (g, v) meets B lane group 2 (g&1) + v/16, byte 16 (g>>1) + v%16 (B lane
+//    (column n, group gb) holds 32 fp8 bytes).
+//  - K-block g (the 32 values of A lane group g) is scaled by the A scale of lane
+//    (r, g) and by the B scale of lane (n, g), whichever B lanes hold its values.
+//  - D as in the other 16x16 MFMAs: lane l gets rows 4(l/16)..+3 of column l%16.
+// So activation scale groups are the natural 32-element blocks, as for the weights;
+// only the placement of the fp8 bytes is permuted.  The instruction's accumulation is
+// not exact in f32: measured |D - exact| up to about 6e-5 x sum|a b| per instruction.
+namespace mx8 {
+
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int lane_bytes = 32;                  // fp8 values per B lane
+constexpr size_t frag_bytes = 64 * lane_bytes;  // one (quad, column tile) B fragment: 2 KiB
+constexpr int scale_pad = 24;                   // scale bytes per (column tile, lane): quads 0..22 + 1
+// One token tile's B operand for all of K: fragments [quad][column tile][lane][32 B],
+// then scales [column tile][lane][scale_pad].
+constexpr size_t tile_frag_bytes = size_t(mf::quads) * mf::col_tiles * frag_bytes;  // 188416
+constexpr size_t tile_scale_bytes = size_t(mf::col_tiles) * 64 * scale_pad;         // 6144
+constexpr size_t tile_bytes = tile_frag_bytes + tile_scale_bytes;
+static_assert(tile_bytes <= mf::plane_bytes, "an MXFP8 tile fits one bf16 plane of the workspace");
+
+// Block element held as value v of an A lane (and so of the B bytes it meets).
+__host__ __device__ inline uint32_t element_of_value(uint32_t v) {
+    return v / 2 + 16 * (v % 2);
+}
+// B placement of element e of K-block g: lane group and byte.
+__host__ __device__ inline uint32_t b_group(uint32_t g, uint32_t e) {
+    const uint32_t v = 2 * (e % 16) + e / 16;
+    return 2 * (g & 1) + v / 16;
+}
+__host__ __device__ inline uint32_t b_byte(uint32_t g, uint32_t e) {
+    const uint32_t v = 2 * (e % 16) + e / 16;
+    return 16 * (g >> 1) + v % 16;
+}
+
+// E8M0 exponent X of a block whose largest magnitude is m (finite): the smallest X
+// with m / 2^X <= 448, the E4M3 maximum, so no element saturates; -127 for a block of
+// zeros or f32 subnormals.  m / 2^(e-8) = significand x 256 exceeds 448 exactly when
+// the significand exceeds 1.75.
+__device__ inline int block_exponent(float m) {
+    const uint32_t u = __float_as_uint(m);
+    const int e = int((u >> 23) & 0xffu);
+    if (e == 0) {
+        return -127;
+    }
+    return e - 127 - 8 + ((u & 0x7fffffu) > 0x600000u ? 1 : 0);
+}
+
+// OCP E4M3 of a value with |v| <= 448, rounded to nearest even: subnormals m x 2^-9
+// (m = 8 carries into the smallest normal), normals (1 + m/8) x 2^(e-7).
+__device__ inline uint32_t e4m3(float v) {
+    const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+    const float a = fabsf(v);
+    if (a < 0x1p-6f) {
+        return sign | uint32_t(__builtin_rintf(a * 512.0f));
+    }
+    const uint32_t ua = __float_as_uint(a);
+    const uint32_t r = ua + 0x7ffffu + ((ua >> 20) & 1u);
+    return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+}
+constexpr uint32_t e4m3_nan = 0x7fu;
+
+__device__ inline float e4m3_value(uint32_t b) {
+    const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+    const float mag = e == 0 ? float(m) * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+    return (b & 0x80u) ? -mag : mag;
+}
+
+// D += A B with A = one MXFP4 code chunk per lane (16 bytes) and its E8M0 scale, B = 32
+// fp8 bytes per lane and the E8M0 scale of K-block (lane / 16).
+__device__ inline mf::f32x4 mfma(const uint4 &a, const i32x8 &b, uint32_t scale_a, uint32_t scale_b,
+                                 const mf::f32x4 &c) {
+    const i32x8 av = {int32_t(a.x), int32_t(a.y), int32_t(a.z), int32_t(a.w), 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, c, 4, 0, 0, int32_t(scale_a), 0,
+                                                            int32_t(scale_b));
+}
+
+}  // namespace mx8

@@ -432,6 +432,9 @@ struct AOperand {
     __device__ inline float scale(int a) const {
         return mf::e8m0_scale(sw[a][0] & 0xffu);
     }
+    __device__ inline uint32_t scale_byte(int a) const {
+        return sw[a][0] & 0xffu;
+    }
     __device__ inline void next_quad() {
 #pragma unroll
         for (int a = 0; a < NT; ++a) {
@@ -819,6 +822,450 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
     }
 }
 
+// ---- the scaled path: MXFP4 weights x MXFP8 activations on v_mfma_scale ------------------
+//
+// Activations (the gathered tokens, and the SwiGLU hidden between the two GEMMs) are
+// quantized per 32-element block to MXFP8: E8M0 exponent X = the smallest with
+// max|x| / 2^X <= 448 (mx8::block_exponent), elements E4M3 of x / 2^X rounded to
+// nearest even.  One instruction then takes a whole quad (4 blocks) of 16 rows x 16
+// tokens, with the weights' own bytes and scales as the A operand (no decode).  The
+// products are those of the dequantized activations, but the instruction does not
+// accumulate exactly in f32 (see mx8 in ttl_mfma.hpp): this path is the fast one,
+// the bf16 one the exact one.
+
+// The MXFP8 form of one block of 32 values: its exponent, or non-finite.
+struct Mx8Block {
+    int exponent;
+    bool finite;
+};
+
+__device__ inline Mx8Block mx8_block(const float (&v)[32]) {
+    float m = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        finite = finite && isfinite(v[j]);
+        m = fmaxf(m, fabsf(v[j]));
+    }
+    // a zero block takes scale 2^0; its codes are zero whatever the scale
+    return {m > 0.0f ? mx8::block_exponent(m) : 0, finite};
+}
+
+__device__ inline uint32_t mx8_code(float v, const Mx8Block &b) {
+    return b.finite ? mx8::e4m3(__builtin_amdgcn_ldexpf(v, -b.exponent)) : mx8::e4m3_nan;
+}
+
+// One thread per (token tile, quad, column tile, B lane (n, gb)): the lane's 32 fp8
+// bytes -- elements of blocks 4 quad + gb/2 (bytes 0..15) and 4 quad + 2 + gb/2
+// (bytes 16..31), each block quantized with its own exponent -- and the E8M0 byte of
+// K-block gb, which the MFMA reads from this lane.  Slots past the tile's count and
+// blocks 90/91 are zero; a token out of range is NaN.
+template <bool BF16_IN>
+__global__ __launch_bounds__(mf::col_tiles * 64) void gather_mx8_kernel(const void *__restrict__ x,
+                                                                        uint32_t x_stride, uint32_t x_rows,
+                                                                        Plan plan) {
+    const uint32_t tile = blockIdx.y;
+    if (tile >= plan.header->tiles) {
+        return;
+    }
+    const uint32_t quad = blockIdx.x;
+    const uint32_t ct = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t n = ct * 16 + lane % 16, gb = lane / 16;
+    const uint32_t cnt = plan.tile_count[tile];
+    const bool live = n < cnt;
+    uint32_t token = 0;
+    bool token_ok = false;
+    if (live) {
+        token = plan.slot_token[plan.tile_first[tile] + n];
+        token_ok = token < x_rows;
+    }
+    uint32_t words[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int exps[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t block = 4 * quad + gb / 2 + 2 * h;
+        float v[32];
+        if (live && token_ok && block < uint32_t(mx::blocks)) {
+            const size_t base = size_t(token) * x_stride + size_t(block) * 32;
+            if (BF16_IN) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + base);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint4 w = src[k];
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        v[8 * k + 2 * q] = __uint_as_float(ww[q] << 16);
+                        v[8 * k + 2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
+                    }
+                }
+            } else {
+                const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float4 w = src[k];
+                    v[4 * k] = w.x;
+                    v[4 * k + 1] = w.y;
+                    v[4 * k + 2] = w.z;
+                    v[4 * k + 3] = w.w;
+                }
+            }
+        } else {
+            const float fill = (live && !token_ok && block < uint32_t(mx::blocks)) ? __builtin_nanf("") : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) {
+                v[j] = fill;
+            }
+        }
+        const Mx8Block b = mx8_block(v);
+        exps[h] = b.finite ? b.exponent : 0;
+        // bytes 16 h + j hold value 16 (gb % 2) + j of the A lanes of this block
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            // element of value 16 (gb % 2) + j: a static index either way
+            const float val = (gb % 2) ? v[mx8::element_of_value(16 + j)] : v[mx8::element_of_value(j)];
+            words[(16 * h + j) / 4] |= mx8_code(val, b) << (8 * ((16 * h + j) % 4));
+        }
+    }
+    uint8_t *tb = plan.xb + size_t(tile) * mf::plane_bytes;
+    uint4 *dst = reinterpret_cast<uint4 *>(tb + ((size_t(quad) * mf::col_tiles + ct) * 64 + lane) * mx8::lane_bytes);
+    dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
+    dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
+    // K-block gb's exponent: gb 0 holds block 4q (h 0), gb 3 block 4q+3 (h 1); block 4q+1
+    // is h 0 of groups 2 and 3, block 4q+2 is h 1 of groups 0 and 1
+    const int from_g2 = __shfl(exps[0], int(lane % 16 + 32));
+    const int from_g0 = __shfl(exps[1], int(lane % 16));
+    const int mine = gb == 0 ? exps[0] : (gb == 1 ? from_g2 : (gb == 2 ? from_g0 : exps[1]));
+    tb[mx8::tile_frag_bytes + (size_t(ct) * 64 + lane) * mx8::scale_pad + quad] = uint8_t(mine + 127);
+}
+
+// B staging of the scaled kernels: kMx8StageQuads quads of all column tiles per LDS stage.
+constexpr int kMx8StageQuads = 2;
+constexpr int kMx8Stages = (mf::quads + kMx8StageQuads - 1) / kMx8StageQuads;  // 12, the last with one quad
+constexpr size_t kMx8StageBytes = size_t(kMx8StageQuads) * mf::col_tiles * mx8::frag_bytes;  // 16 KiB
+
+template <int THREADS>
+struct Mx8Stager {
+    static constexpr int pieces = int(kMx8StageBytes / 16);
+    static constexpr int per = pieces / THREADS;
+    static_assert(pieces % THREADS == 0, "whole pieces per thread");
+    mf::u32x4 r[per];
+    // pieces past the tile's last quad (the last stage's second half) re-read its last piece
+    __device__ inline void load(const uint8_t *__restrict__ tile_frags, int stage, uint32_t t) {
+#pragma unroll
+        for (int k = 0; k < per; ++k) {
+            const size_t off = min(size_t(stage) * kMx8StageBytes + (size_t(t) + size_t(k) * THREADS) * 16,
+                                   mx8::tile_frag_bytes - 16);
+            r[k] = *reinterpret_cast<const mf::u32x4 *>(tile_frags + off);
+        }
+    }
+    __device__ inline void store(mf::u32x4 *lds, uint32_t t) const {
+#pragma unroll
+        for (int k = 0; k < per; ++k) {
+            lds[t + uint32_t(k) * THREADS] = r[k];
+        }
+    }
+};
+
+// One quad of the scaled main loop: B fragments of quad i from LDS (stage buffer
+// i / 2 % 2), the A and B scale bytes of the quad, then M x NC instructions; at the end
+// of a stage (every kMx8StageQuads quads, and after the last) the next stage is
+// published and the one after requested.
+template <int M, int NC, int THREADS>
+__device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint4 (&q)[M], AOperand<M> &wa,
+                                                               uint32_t (&sb)[NC][6], Mx8Stager<THREADS> &st,
+                                                               const uint8_t *tile_frags,
+                                                               mf::u32x4 (*lds)[kMx8StageBytes / 16], uint32_t t,
+                                                               uint32_t lane, mf::f32x4 (&acc)[M][NC]) {
+    const int stage = i / kMx8StageQuads;
+    const mf::u32x4 *buf = lds[stage % 2] + size_t(i % kMx8StageQuads) * mf::col_tiles * 64 * 2;
+    mx8::i32x8 b[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const mf::u32x4 lo = buf[(c * 64 + lane) * 2], hi = buf[(c * 64 + lane) * 2 + 1];
+        b[c] = mx8::i32x8{int32_t(lo[0]), int32_t(lo[1]), int32_t(lo[2]), int32_t(lo[3]),
+                          int32_t(hi[0]), int32_t(hi[1]), int32_t(hi[2]), int32_t(hi[3])};
+    }
+    uint32_t sa[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        sa[m] = wa.scale_byte(m);
+    }
+    wa.next_quad();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t scb = sb[c][0] & 0xffu;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            acc[m][c] = mx8::mfma(q[m], b[c], sa[m], scb, acc[m][c]);
+        }
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            sb[c][j] = (sb[c][j] >> 8) | (sb[c][j + 1] << 24);
+        }
+        sb[c][5] >>= 8;
+    }
+    if (i % kMx8StageQuads == kMx8StageQuads - 1 || i == mf::quads - 1) {
+        if (stage + 1 < kMx8Stages) {
+            st.store(lds[(stage + 1) % 2], t);
+        }
+        __syncthreads();
+        if (stage + 2 < kMx8Stages) {
+            st.load(tile_frags, stage + 2, t);
+        }
+    }
+}
+
+// The scaled main loop of one wave: M 16-row A tiles (AOperand), NC column tiles, the
+// B fragments staged in LDS by every wave of the workgroup.  acc[m][c] += A_m B_c for
+// quads 0..22; weight codes are requested two quads ahead (three code buffers).
+template <int M, int NC, int THREADS>
+__device__ __attribute__((always_inline)) inline void mx8_main_loop(AOperand<M> &wa, const uint8_t *tile_frags,
+                                                                    const uint8_t *tile_scales,
+                                                                    mf::u32x4 (*lds)[kMx8StageBytes / 16], uint32_t t,
+                                                                    uint32_t lane, mf::f32x4 (&acc)[M][NC]) {
+    // the lane's B scale bytes per column tile (quads 0..22, shifted one byte per quad)
+    uint32_t sb[NC][6];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint2 *rec = reinterpret_cast<const uint2 *>(tile_scales + (size_t(c) * 64 + lane) * mx8::scale_pad);
+        const uint2 r0 = rec[0], r1 = rec[1], r2 = rec[2];
+        sb[c][0] = r0.x;
+        sb[c][1] = r0.y;
+        sb[c][2] = r1.x;
+        sb[c][3] = r1.y;
+        sb[c][4] = r2.x;
+        sb[c][5] = r2.y;
+    }
+    Mx8Stager<THREADS> st;
+    st.load(tile_frags, 0, t);
+    uint4 q0[M], q1[M], q2[M];
+    wa.load(0, lane, q0);
+    wa.load(1, lane, q1);
+    st.store(lds[0], t);
+    __syncthreads();
+    st.load(tile_frags, 1, t);
+    for (int i = 0; i < mf::quads; i += 3) {
+        wa.load(min(i + 2, mf::quads - 1), lane, q2);
+        mx8_quad<M, NC, THREADS>(i, q0, wa, sb, st, tile_frags, lds, t, lane, acc);
+        wa.load(min(i + 3, mf::quads - 1), lane, q0);
+        if (i + 1 < mf::quads) {
+            mx8_quad<M, NC, THREADS>(i + 1, q1, wa, sb, st, tile_frags, lds, t, lane, acc);
+            wa.load(min(i + 4, mf::quads - 1), lane, q1);
+        }
+        if (i + 2 < mf::quads) {
+            mx8_quad<M, NC, THREADS>(i + 2, q2, wa, sb, st, tile_frags, lds, t, lane, acc);
+        }
+    }
+}
+
+// Gate/up on the scaled path, the workgroup layout of gateup_kernel (4 waves x 32 rows:
+// gate and up of two 16-row tiles per wave).  The SwiGLU hidden of a wave's 32 rows is
+// one 32-element K-block beta of the down GEMM for each token: lanes (n, 0..3) hold its
+// rows 4g..4g+3 and 16+4g..16+4g+3, so the block's maximum takes two lane exchanges,
+// and each lane writes 8 contiguous fp8 bytes of the down GEMM's B fragment.
+template <int NC>
+__global__ __launch_bounds__(kGuWaves * 64) void mx8_gateup_kernel(GateUpArgs a) {
+    constexpr int kThreads = kGuWaves * 64;
+    __shared__ mf::u32x4 lds[2][kMx8StageBytes / 16];
+    uint32_t tile, row_group;
+    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
+        return;
+    }
+    const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const uint32_t expert = a.plan.tile_expert[tile];
+    const uint32_t row0 = row_group * kGuRows + wave * 32;
+    const bool rows_ok = row0 < a.rows;
+    const uint32_t row_base = rows_ok ? row0 : row_group * kGuRows;
+    const size_t tile0 = size_t(expert) * a.tiles_per_expert + row_base / 16;
+    const uint8_t *tb = a.plan.xb + size_t(tile) * mf::plane_bytes;
+
+    // A tiles: gate rows +0, +16, up rows +0, +16 (AOperand over both tensors)
+    AOperand<4> wa;
+    {
+        AOperand<2> ga, ua;
+        const size_t ti[2] = {tile0, tile0 + 1};
+        ga.init(a.gate_codes, a.gate_scales, ti, lane);
+        ua.init(a.up_codes, a.up_scales, ti, lane);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            wa.codes[k] = ga.codes[k];
+            wa.codes[2 + k] = ua.codes[k];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) {
+                wa.sw[k][j] = ga.sw[k][j];
+                wa.sw[2 + k][j] = ua.sw[k][j];
+            }
+        }
+    }
+    mf::f32x4 acc[4][NC];
+    {
+        const uint32_t g = lane / 16;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float *bias = m < 2 ? a.gate_bias : a.up_bias;
+            mf::f32x4 b = {0.f, 0.f, 0.f, 0.f};
+            if (bias) {
+                const float4 v = *reinterpret_cast<const float4 *>(bias + size_t(expert) * a.rows + row_base +
+                                                                   16 * (m % 2) + 4 * g);
+                b = mf::f32x4{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                acc[m][c] = b;
+            }
+        }
+    }
+    mx8_main_loop<4, NC, kThreads>(wa, tb, tb + mx8::tile_frag_bytes, lds, t, lane, acc);
+    if (!rows_ok) {
+        return;
+    }
+    // the hidden block beta = this wave's 32 rows: K-block g = beta % 4 of quad beta / 4
+    const uint32_t beta = row0 / 32, quad = beta / 4, gk = beta % 4;
+    const uint32_t gs = lane / 16, n16 = lane % 16;
+    uint8_t *hb = a.plan.hb + size_t(tile) * mf::plane_bytes;
+    // bytes 16 (g>>1) + 8 (gs%2) .. +7 of B lane (n, 2 (g&1) + gs/2)
+    const auto dest = [&](uint32_t g, uint32_t c) __attribute__((always_inline)) {
+        return hb + ((size_t(quad) * mf::col_tiles + c) * 64 + n16 + 16 * (2 * (g & 1) + gs / 2)) * mx8::lane_bytes +
+               16 * (g >> 1) + 8 * (gs % 2);
+    };
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float h[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[2 * i] = moe_math::clamped_swiglu(acc[0][c][i], acc[2][c][i]);      // element 4 gs + i
+            h[2 * i + 1] = moe_math::clamped_swiglu(acc[1][c][i], acc[3][c][i]);  // element 16 + 4 gs + i
+        }
+        float m = 0.0f;
+        bool finite = true;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            finite = finite && isfinite(h[j]);
+            m = fmaxf(m, fabsf(h[j]));
+        }
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        int fin = finite ? 1 : 0;
+        fin &= __shfl_xor(fin, 16);
+        fin &= __shfl_xor(fin, 32);
+        const Mx8Block blk{m > 0.0f ? mx8::block_exponent(m) : 0, fin != 0};
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            lo |= mx8_code(h[j], blk) << (8 * j);
+            hi |= mx8_code(h[4 + j], blk) << (8 * j);
+        }
+        *reinterpret_cast<uint2 *>(dest(gk, c)) = make_uint2(lo, hi);
+        if (gs == 0) {
+            hb[mx8::tile_frag_bytes + (size_t(c) * 64 + n16 + 16 * gk) * mx8::scale_pad + quad] =
+                uint8_t((blk.finite ? blk.exponent : 0) + 127);
+        }
+        // blocks 90 and 91 (K-blocks 2 and 3 of quad 22) hold no rows: zero, scale 2^0
+        if (beta + 2 >= uint32_t(mx::blocks) && beta < uint32_t(mx::blocks)) {
+            *reinterpret_cast<uint2 *>(dest(gk + 2, c)) = make_uint2(0u, 0u);
+            if (gs == 0) {
+                hb[mx8::tile_frag_bytes + (size_t(c) * 64 + n16 + 16 * (gk + 2)) * mx8::scale_pad + quad] = 127;
+            }
+        }
+    }
+}
+
+// Down projection and the selected-token matmul on the scaled path: matmul_kernel's
+// workgroup layout (4 waves x 48 rows) and epilogue; B from frags (gather or gate/up).
+template <bool SCATTER, int NC>
+__global__ __launch_bounds__(kMmWaves * 64) void mx8_matmul_kernel(MatmulArgs a) {
+    constexpr int kThreads = kMmWaves * 64;
+    __shared__ mf::u32x4 lds[2][kMx8StageBytes / 16];
+    uint32_t tile, row_group;
+    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
+        return;
+    }
+    const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const uint32_t expert = a.plan.tile_expert[tile];
+    const uint32_t row0 = row_group * kMmRows + wave * (kMmTiles * 16);
+    const bool rows_ok = row0 < a.rows;
+    const uint32_t row_base = rows_ok ? row0 : 0;
+    const size_t tile0 = size_t(expert) * a.tiles_per_expert + row_base / 16;
+    const uint8_t *tb = a.frags + size_t(tile) * mf::plane_bytes;
+    AOperand<kMmTiles> wa;
+    size_t ti[kMmTiles];
+#pragma unroll
+    for (int m = 0; m < kMmTiles; ++m) {
+        ti[m] = tile0 + m;
+    }
+    wa.init(a.codes, a.scales, ti, lane);
+    mf::f32x4 acc[kMmTiles][NC];
+    {
+        const uint32_t g = lane / 16;
+#pragma unroll
+        for (int m = 0; m < kMmTiles; ++m) {
+            mf::f32x4 b = {0.f, 0.f, 0.f, 0.f};
+            if (a.bias) {
+                const float4 v =
+                    *reinterpret_cast<const float4 *>(a.bias + size_t(expert) * a.rows + row_base + 16 * m + 4 * g);
+                b = mf::f32x4{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                acc[m][c] = b;
+            }
+        }
+    }
+    mx8_main_loop<kMmTiles, NC, kThreads>(wa, tb, tb + mx8::tile_frag_bytes, lds, t, lane, acc);
+    if (!rows_ok) {
+        return;
+    }
+    const uint32_t cnt = a.plan.tile_count[tile], first = a.plan.tile_first[tile];
+    const uint32_t g = lane / 16, n16 = lane % 16;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t n = c * 16 + n16;
+        if (n >= cnt) {
+            continue;
+        }
+        size_t out_row;
+        if (SCATTER) {
+            const uint32_t token = a.plan.slot_token[first + n];
+            if (token >= a.out_rows) {
+                continue;
+            }
+            out_row = token;
+        } else {
+            out_row = first + n;
+        }
+        float *dst = a.out + out_row * a.rows + row0 + 4 * g;
+#pragma unroll
+        for (int m = 0; m < kMmTiles; ++m) {
+            *reinterpret_cast<float4 *>(dst + 16 * m) = make_float4(acc[m][c][0], acc[m][c][1], acc[m][c][2],
+                                                                    acc[m][c][3]);
+        }
+    }
+}
+
+// The values the scaled path multiplies: each row's 32-element blocks quantized to
+// MXFP8 and widened back to f32 (one thread per block).
+template <bool BF16_IN>
+__global__ __launch_bounds__(256) void mx8_dequantize_kernel(const void *__restrict__ x, uint32_t rows,
+                                                             float *__restrict__ out) {
+    const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= size_t(rows) * mx::blocks) {
+        return;
+    }
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        v[j] = BF16_IN ? __uint_as_float(uint32_t(static_cast<const uint16_t *>(x)[gid * 32 + j]) << 16)
+                       : static_cast<const float *>(x)[gid * 32 + j];
+    }
+    const Mx8Block b = mx8_block(v);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const uint32_t code = mx8_code(v[j], b);
+        out[gid * 32 + j] = b.finite ? __builtin_amdgcn_ldexpf(mx8::e4m3_value(code), b.exponent) : __builtin_nanf("");
+    }
+}
+
 // ---- combine ----------------------------------------------------------------------------
 
 // out[p][i] = sum over token p's slots in slot order (= expert order) of
@@ -965,8 +1412,80 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     return TTL_OK;
 }
 
+size_t ttl_matmul_mxfp4_selected_mxfp8_workspace_bytes(uint32_t count) {
+    return make_layout(count, 1, 1, false, 0).total;
+}
+
+int ttl_matmul_mxfp4_selected_mxfp8(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bias_dev, const float *x_dev,
+                                    uint32_t x_stride, uint32_t x_rows, const int32_t *tokens_dev, uint32_t count,
+                                    float *out_dev, uint32_t expert, void *workspace_dev, size_t workspace_bytes) {
+    const char *who = "ttl_matmul_mxfp4_selected_mxfp8";
+    TTL_REQUIRE(ctx && x_dev && tokens_dev && out_dev && workspace_dev, TTL_ERR_INVALID, "%s: null argument", who);
+    int rc = check_mxfp4(w, who);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(w->rows % kMmRows == 0, TTL_ERR_SHAPE, "%s: rows must be a multiple of %d", who, kMmRows);
+    TTL_REQUIRE(expert < w->experts, TTL_ERR_INVALID, "%s: expert %u out of range", who, expert);
+    rc = check_bf16_scales(w, expert, who);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    TTL_REQUIRE(x_stride >= uint32_t(mx::cols) && x_stride % 4 == 0, TTL_ERR_SHAPE,
+                "%s: x_stride must be >= %d and a multiple of 4", who, mx::cols);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && (reinterpret_cast<uintptr_t>(out_dev) & 15) == 0,
+                TTL_ERR_INVALID, "%s: x and out must be 16-byte aligned", who);
+    TTL_REQUIRE(count <= kMaxEntries, TTL_ERR_SHAPE, "%s: count above %u", who, kMaxEntries);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 255) == 0, TTL_ERR_INVALID,
+                "%s: workspace must be 256-byte aligned", who);
+    if (count == 0) {
+        return TTL_OK;
+    }
+    const Layout L = make_layout(count, 1, 1, false, 0);
+    TTL_REQUIRE(workspace_bytes >= L.total, TTL_ERR_SHAPE, "%s: workspace of %zu bytes, %zu needed", who,
+                workspace_bytes, L.total);
+    const Plan plan = plan_at(workspace_dev, L);
+    const uint32_t tiles = (count + mf::tile_slots - 1) / mf::tile_slots;
+    plan_selected_kernel<<<ttl::blocks_for(count > tiles ? count : tiles, 256), 256, 0, ctx->stream>>>(
+        tokens_dev, count, expert, plan);
+    TTL_LAUNCHED("plan_selected_kernel");
+    gather_mx8_kernel<false><<<dim3(mf::quads, tiles), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, x_stride, x_rows,
+                                                                                             plan);
+    TTL_LAUNCHED("gather_mx8_kernel");
+    MatmulArgs m;
+    m.codes = w->codes;
+    m.scales = w->scales;
+    m.bias = bias_dev;
+    m.rows = w->rows;
+    m.tiles_per_expert = w->tiles;
+    m.frags = plan.xb;
+    m.plan = plan;
+    m.out = out_dev;
+    m.out_rows = x_rows;
+    mx8_matmul_kernel<true, mf::col_tiles><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
+    TTL_LAUNCHED("mx8_matmul_kernel");
+    return TTL_OK;
+}
+
+int ttl_mxfp8_dequantize(ttl_ctx *ctx, const void *x_dev, int x_dtype, uint32_t rows, float *out_dev) {
+    TTL_REQUIRE(ctx && x_dev && out_dev, TTL_ERR_INVALID, "ttl_mxfp8_dequantize: null argument");
+    TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16, TTL_ERR_INVALID,
+                "ttl_mxfp8_dequantize: x_dtype must be TTL_DTYPE_F32 or TTL_DTYPE_BF16");
+    const size_t blocks = size_t(rows) * mx::blocks;
+    if (blocks == 0) {
+        return TTL_OK;
+    }
+    if (x_dtype == TTL_DTYPE_BF16) {
+        mx8_dequantize_kernel<true><<<unsigned((blocks + 255) / 256), 256, 0, ctx->stream>>>(x_dev, rows, out_dev);
+    } else {
+        mx8_dequantize_kernel<false><<<unsigned((blocks + 255) / 256), 256, 0, ctx->stream>>>(x_dev, rows, out_dev);
+    }
+    TTL_LAUNCHED("mx8_dequantize_kernel");
+    return TTL_OK;
+}
+
 size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used, int x_dtype) {
-    const int planes = x_dtype == TTL_DTYPE_BF16 ? 1 : 3;
+    const int planes = x_dtype == TTL_DTYPE_F32 ? 3 : 1;  // bf16, or the MXFP8 fragments (one plane's room)
     return make_layout(count * used, experts, planes, true, uint32_t(mx::cols)).total;
 }
 
@@ -979,8 +1498,9 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
                 "ttl_moe_prefill_stages: unknown stage bits 0x%x", stages);
     const ttl_moe_layer &L = *layer;
     TTL_REQUIRE(L.gate && L.up && L.down, TTL_ERR_INVALID, "ttl_moe_prefill_experts: null expert tensor");
-    TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16, TTL_ERR_INVALID,
-                "ttl_moe_prefill_experts: x_dtype must be TTL_DTYPE_F32 or TTL_DTYPE_BF16");
+    TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_F32_AS_MXFP8 ||
+                    x_dtype == TTL_DTYPE_BF16_AS_MXFP8,
+                TTL_ERR_INVALID, "ttl_moe_prefill_experts: unknown x_dtype %d", x_dtype);
     TTL_REQUIRE(L.hidden == uint32_t(mx::cols) && L.expert_hidden == uint32_t(mx::cols), TTL_ERR_SHAPE,
                 "ttl_moe_prefill_experts: hidden and expert_hidden must be %d", mx::cols);
     TTL_REQUIRE(L.gate->rows == L.expert_hidden && L.up->rows == L.expert_hidden && L.down->rows == L.hidden &&
@@ -1008,8 +1528,9 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         return TTL_OK;
     }
     const uint32_t pairs = count * L.used;
-    const bool bf16 = x_dtype == TTL_DTYPE_BF16;
-    const Layout lay = make_layout(pairs, L.experts, bf16 ? 1 : 3, true, L.hidden);
+    const bool scaled = x_dtype == TTL_DTYPE_F32_AS_MXFP8 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
+    const bool bf16 = x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
+    const Layout lay = make_layout(pairs, L.experts, (bf16 || scaled) ? 1 : 3, true, L.hidden);
     TTL_REQUIRE(workspace_bytes >= lay.total, TTL_ERR_SHAPE,
                 "ttl_moe_prefill_experts: workspace of %zu bytes, %zu needed for this count and x_dtype",
                 workspace_bytes, lay.total);
@@ -1019,7 +1540,16 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(indices_dev, weights_dev, pairs, L.used, L.experts, plan);
         TTL_LAUNCHED("plan_kernel");
     }
-    if (stages & TTL_PREFILL_GATHER) {
+    if ((stages & TTL_PREFILL_GATHER) && scaled) {
+        if (bf16) {
+            gather_mx8_kernel<true><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden,
+                                                                                                    count, plan);
+        } else {
+            gather_mx8_kernel<false><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden,
+                                                                                                     count, plan);
+        }
+        TTL_LAUNCHED("gather_mx8_kernel");
+    } else if (stages & TTL_PREFILL_GATHER) {
         if (bf16) {
             gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         } else {
@@ -1044,7 +1574,11 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     // the wide tiles, then the narrow ones (at most one per expert)
     const uint32_t gu_groups = (L.expert_hidden + kGuRows - 1) / kGuRows;
     const dim3 gu_wide(gu_groups, lay.tmax), gu_narrow(gu_groups, min(lay.tmax, L.experts));
-    if (stages & TTL_PREFILL_GATEUP) {
+    if ((stages & TTL_PREFILL_GATEUP) && scaled) {
+        mx8_gateup_kernel<mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
+        mx8_gateup_kernel<kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
+        TTL_LAUNCHED("mx8_gateup_kernel");
+    } else if (stages & TTL_PREFILL_GATEUP) {
         if (bf16) {
             gateup_kernel<1, mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
             gateup_kernel<1, kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
@@ -1065,7 +1599,13 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     m.plan = plan;
     m.out = plan.down;
     m.out_rows = 0;
-    if (stages & TTL_PREFILL_DOWN) {
+    if ((stages & TTL_PREFILL_DOWN) && scaled) {
+        mx8_matmul_kernel<false, mf::col_tiles>
+            <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
+        mx8_matmul_kernel<false, kNarrowCols>
+            <<<dim3(L.hidden / kMmRows, min(lay.tmax, L.experts)), kMmWaves * 64, 0, ctx->stream>>>(m);
+        TTL_LAUNCHED("mx8_matmul_kernel");
+    } else if (stages & TTL_PREFILL_DOWN) {
         matmul_kernel<kHiddenPlanes, false, mf::col_tiles>
             <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
         matmul_kernel<kHiddenPlanes, false, kNarrowCols>

@@ -17,6 +17,8 @@ HEADER_PATH = os.path.join(REPO_DIR, "include", "ttlab_hip.h")
 TTL_OK = 0
 TTL_DTYPE_F32 = 0
 TTL_DTYPE_BF16 = 1
+TTL_DTYPE_F32_AS_MXFP8 = 2
+TTL_DTYPE_BF16_AS_MXFP8 = 3
 TTL_PREFILL_PLAN, TTL_PREFILL_GATHER, TTL_PREFILL_GATEUP, TTL_PREFILL_DOWN, TTL_PREFILL_COMBINE = 1, 2, 4, 8, 16
 TTL_PREFILL_ALL = 31
 
@@ -304,6 +306,9 @@ def load_library():
         "ttl_argmax": (i32, [vp, u32, vp, vp, vp, vp, u32]),
         "ttl_matmul_mxfp4_selected_workspace_bytes": (sz, [u32]),
         "ttl_matmul_mxfp4_selected": (i32, [vp, vp, vp, vp, u32, u32, vp, u32, vp, u32, vp, sz]),
+        "ttl_matmul_mxfp4_selected_mxfp8_workspace_bytes": (sz, [u32]),
+        "ttl_matmul_mxfp4_selected_mxfp8": (i32, [vp, vp, vp, vp, u32, u32, vp, u32, vp, u32, vp, sz]),
+        "ttl_mxfp8_dequantize": (i32, [vp, vp, i32, u32, vp]),
         "ttl_moe_prefill_workspace_bytes": (sz, [u32, u32, u32, i32]),
         "ttl_moe_prefill_experts": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz]),
         "ttl_moe_prefill_stages": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz, u32]),
@@ -641,6 +646,9 @@ class Device:
         _check(self.lib.ttl_argmax(self.ctx, vocab, workspace.ptr, token.ptr, position.ptr if position else None,
                                    history.ptr if history else None, history_len), "ttl_argmax")
 
+    def mxfp8_dequantize(self, x, x_dtype, rows, out):
+        _check(self.lib.ttl_mxfp8_dequantize(self.ctx, x.ptr, x_dtype, rows, out.ptr), "ttl_mxfp8_dequantize")
+
     # ---- graphs ----
     def capture(self, fn):
         """Records the launches fn() makes into a replayable graph."""
@@ -654,15 +662,17 @@ class Device:
         return Graph(self, g.value)
 
     # ---- batched prefill (MFMA) ----
-    def matmul_mxfp4_selected(self, w, bias, x, x_stride, x_rows, tokens, count, out, expert, workspace=None):
-        """out[tokens[s]] = W[expert] x[tokens[s]] + bias[expert]; allocates a workspace if none is given."""
+    def matmul_mxfp4_selected(self, w, bias, x, x_stride, x_rows, tokens, count, out, expert, workspace=None,
+                              mxfp8=False):
+        """out[tokens[s]] = W[expert] x[tokens[s]] + bias[expert]; allocates a workspace if none is given.
+        mxfp8: the scaled path (activations quantized to MXFP8, v_mfma_scale)."""
+        name = "ttl_matmul_mxfp4_selected_mxfp8" if mxfp8 else "ttl_matmul_mxfp4_selected"
         ws = workspace
         if ws is None:
-            ws = self.alloc(max(self.lib.ttl_matmul_mxfp4_selected_workspace_bytes(count), 256))
+            ws = self.alloc(max(getattr(self.lib, name + "_workspace_bytes")(count), 256))
         try:
-            _check(self.lib.ttl_matmul_mxfp4_selected(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride,
-                                                      x_rows, tokens.ptr, count, out.ptr, expert, ws.ptr, ws.nbytes),
-                   "ttl_matmul_mxfp4_selected")
+            _check(getattr(self.lib, name)(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, x_stride, x_rows,
+                                           tokens.ptr, count, out.ptr, expert, ws.ptr, ws.nbytes), name)
             if workspace is None:
                 self.sync()
         finally:
