@@ -24,8 +24,9 @@ is 12 of each plus the unembedding.
 distinct resident layers, value = token-layers/s.
 
 --workload prefill runs benchmark config 2: the batched prefill experts of one MoE
-layer for 512 bf16 tokens with balanced given routing (bf16 MFMA), value =
-token-layers/s; roofline on the larger of the gate/up and down GEMM launches.
+layer for 512 bf16 tokens with balanced given routing (bf16 MFMA; with
+--activations mxfp8 the scaled fp8 x fp4 MFMA path), value = token-layers/s;
+roofline on the larger of the gate/up and down GEMM launches.
 
 --workload model-prefill runs the full synthetic gpt-oss-20b model's layer-major
 prefill (GptOssModel::prefill) of a 512-token prompt, value = prompt tokens/s;
@@ -353,6 +354,15 @@ PF_DOWN_BYTES = EXPERTS * N * 1530 + 2 * PREFILL_PAIRS * N * 4
 PF_GATEUP_FLOP = 2 * 2 * PREFILL_PAIRS * N * N
 PF_DOWN_FLOP = 2 * PREFILL_PAIRS * N * N
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# The scaled path (--activations mxfp8) moves MXFP8 instead of bf16/f32 activations:
+# one byte per element plus one E8M0 byte per 32.  Gate/up reads the tokens' MXFP8
+# activations and writes the pairs' MXFP8 hidden; down reads that hidden and writes
+# the f32 down outputs.  Its MFMA peak is the fp8 one (the mixed fp4 x fp8 operands
+# run at the fp8 rate).
+MX8_ROW = N + N // 32
+PF_MX8_GATEUP_BYTES = EXPERTS * 2 * N * 1530 + PREFILL_TOKENS * MX8_ROW + PREFILL_PAIRS * MX8_ROW
+PF_MX8_DOWN_BYTES = EXPERTS * N * 1530 + PREFILL_PAIRS * MX8_ROW + PREFILL_PAIRS * N * 4
+MFMA_FP8_PEAK_TFLOPS = 5000.0
 
 
 def gpu_prefill(args):
@@ -377,7 +387,8 @@ def gpu_prefill(args):
     idx, w = ttlab_amd.balanced_routing(PREFILL_TOKENS, EXPERTS, USED, 0x79000002)
     ib, wb = dev.upload(idx), dev.upload(w)
     out = dev.alloc(PREFILL_TOKENS * N * 4)
-    dt = ttlab_amd.TTL_DTYPE_BF16
+    scaled = args.activations == "mxfp8"
+    dt = ttlab_amd.TTL_DTYPE_BF16_AS_MXFP8 if scaled else ttlab_amd.TTL_DTYPE_BF16
     ws = dev.alloc(dev.moe_prefill_workspace_bytes(PREFILL_TOKENS, EXPERTS, USED, dt))
 
     def run(stages, layers):
@@ -411,10 +422,16 @@ def gpu_prefill(args):
     dev.close()
     log(f"prefill layer: {ms * 1e3:.1f} us ({PREFILL_TOKENS / ms * 1e3:.0f} token-layers/s); gate/up "
         f"{us_gu:.1f} us, down {us_dn:.1f} us")
-    kernels = {
-        "gateup_kernel": (us_gu, PF_GATEUP_BYTES, PF_GATEUP_FLOP),
-        "matmul_kernel (down)": (us_dn, PF_DOWN_BYTES, PF_DOWN_FLOP),
-    }
+    if scaled:
+        kernels = {
+            "mx8_gateup_kernel": (us_gu, PF_MX8_GATEUP_BYTES, PF_GATEUP_FLOP),
+            "mx8_matmul_kernel (down)": (us_dn, PF_MX8_DOWN_BYTES, PF_DOWN_FLOP),
+        }
+    else:
+        kernels = {
+            "gateup_kernel": (us_gu, PF_GATEUP_BYTES, PF_GATEUP_FLOP),
+            "matmul_kernel (down)": (us_dn, PF_DOWN_BYTES, PF_DOWN_FLOP),
+        }
     name = max(kernels, key=lambda k: kernels[k][0])
     us, nbytes, flop = kernels[name]
     achieved = nbytes / (us * 1e-6) / 1e9
@@ -427,18 +444,20 @@ def gpu_prefill(args):
         "value": PREFILL_TOKENS / (ms * 1e-3),
         "unit": "token-layers/s",
         "ms_per_step": ms,
-        "dtype": "bf16 activations x MXFP4 weights, f32 accumulate (bf16 MFMA)",
+        "dtype": ("MXFP8 activations and hidden x MXFP4 weights, f32 accumulate (scaled fp8/fp4 MFMA)" if scaled
+                  else "bf16 activations x MXFP4 weights, f32 accumulate (bf16 MFMA)"),
         "config": {"workload": "config 2: batched prefill experts of one gpt-oss-20b MoE layer, 512 bf16 tokens, "
                                "top-4 of 32 experts, balanced given routing (64 tokens per expert); step = one layer "
                                f"(plan, gather, gate/up+SwiGLU, down, combine) over {PREFILL_LAYERS} distinct "
                                "resident layers (HIP graph)",
+                   "activations": args.activations,
                    "tokens": PREFILL_TOKENS, "experts": EXPERTS, "used": USED, "hidden": N,
                    "kernels": per_kernel},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
                      "bytes_per_launch": nbytes, "launch_us": round(us, 3),
                      "mfma_algorithmic_TFLOPs": round(flop / (us * 1e-6) / 1e12, 1),
-                     "mfma_peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS,
+                     "mfma_peak_TFLOPs": MFMA_FP8_PEAK_TFLOPS if scaled else MFMA_BF16_PEAK_TFLOPS,
                      "read_ceiling": ceiling_entry(achieved, nbytes, us_read)},
     }
 
@@ -651,6 +670,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", choices=["decode", "matvec", "moe", "prefill", "model-prefill"], default="decode")
+    ap.add_argument("--activations", choices=["bf16", "mxfp8"], default="bf16",
+                    help="prefill workload: bf16 MFMA on bf16 activations (exact), or the scaled path "
+                         "(activations and hidden quantized to MXFP8, fp8 x fp4 MFMA)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",

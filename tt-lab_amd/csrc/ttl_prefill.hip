@@ -220,27 +220,26 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__res
         const uint32_t j = round + t;
         const int32_t ej = j < pairs ? indices[j] : -1;
         const bool valid = ej >= 0 && uint32_t(ej) < experts;
-        // rank among the earlier lanes of this wave with the same expert
-        uint32_t rank = 0;
-        uint64_t remaining = __ballot(valid);
-        while (remaining) {
-            const uint32_t leader = uint32_t(__ffsll((long long)remaining) - 1);
-            const int32_t key = __shfl(ej, int(leader));
-            const uint64_t same = __ballot(valid && ej == key);
-            if (valid && ej == key) {
-                rank = uint32_t(__popcll(same & ((1ull << lane) - 1ull)));
-            }
-            if (lane == leader) {
-                wave_count[wave][key] = uint32_t(__popcll(same));
-            }
-            remaining &= ~same;
+        // the lanes of this wave with the same expert: one ballot per bit of the expert
+        // index (a lane matches where every bit agrees); rank = earlier lanes among them,
+        // and the lowest of them records the wave's count for the expert
+        uint64_t same = __ballot(valid);
+        for (uint32_t bit = 0; (1u << bit) < experts; ++bit) {
+            const bool one = valid && ((uint32_t(ej) >> bit) & 1u);
+            const uint64_t ones = __ballot(one);
+            same &= one ? ones : ~ones;
+        }
+        const uint32_t rank = uint32_t(__popcll(same & ((1ull << lane) - 1ull)));
+        if (valid && rank == 0) {
+            wave_count[wave][ej] = uint32_t(__popcll(same));
         }
         __syncthreads();
         if (j < pairs) {
             if (valid) {
                 uint32_t slot = base[ej] + running[ej] + rank;
-                for (uint32_t w = 0; w < wave; ++w) {
-                    slot += wave_count[w][ej];
+#pragma unroll
+                for (uint32_t w = 0; w < kPlanThreads / 64; ++w) {
+                    slot += w < wave ? wave_count[w][ej] : 0u;
                 }
                 plan.slot_token[slot] = j / used;
                 plan.slot_weight[slot] = weights[j];
@@ -855,93 +854,100 @@ __device__ inline uint32_t mx8_code(float v, const Mx8Block &b) {
     return b.finite ? mx8::e4m3(__builtin_amdgcn_ldexpf(v, -b.exponent)) : mx8::e4m3_nan;
 }
 
-// One thread per (token tile, quad, column tile, B lane (n, gb)): the lane's 32 fp8
-// bytes -- elements of blocks 4 quad + gb/2 (bytes 0..15) and 4 quad + 2 + gb/2
-// (bytes 16..31), each block quantized with its own exponent -- and the E8M0 byte of
-// K-block gb, which the MFMA reads from this lane.  Slots past the tile's count and
-// blocks 90/91 are zero; a token out of range is NaN.
+// One workgroup per (quad, column tile, token tile); 16 threads per slot, 4 per
+// 32-element block, each thread 8 consecutive elements (one 16-byte bf16 load, the
+// slot's 4 blocks of the quad contiguous across its 16 threads).  The block's largest
+// magnitude takes two lane exchanges.  Element e of K-block g belongs to B lane group
+// 2 (g & 1) + (e % 16) / 8, byte 16 (g >> 1) + 2 (e % 8) + e / 16, so the threads
+// holding elements 8r..8r+7 and 8r+16..8r+23 (r = 0, 1) interleave their codes and the
+// first writes 16 contiguous bytes; the block's first thread writes its E8M0 byte,
+// read by the MFMA from lane (n, g).  Slots past the tile's count and blocks 90/91 are
+// zero; a token out of range is NaN.
 template <bool BF16_IN>
-__global__ __launch_bounds__(mf::col_tiles * 64) void gather_mx8_kernel(const void *__restrict__ x,
-                                                                        uint32_t x_stride, uint32_t x_rows,
-                                                                        Plan plan) {
+__global__ __launch_bounds__(256) void gather_mx8_kernel(const void *__restrict__ x, uint32_t x_stride,
+                                                          uint32_t x_rows, Plan plan) {
     const uint32_t tile = blockIdx.y;
     if (tile >= plan.header->tiles) {
         return;
     }
-    const uint32_t quad = blockIdx.x;
-    const uint32_t ct = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const uint32_t n = ct * 16 + lane % 16, gb = lane / 16;
-    const uint32_t cnt = plan.tile_count[tile];
-    const bool live = n < cnt;
-    uint32_t token = 0;
-    bool token_ok = false;
-    if (live) {
-        token = plan.slot_token[plan.tile_first[tile] + n];
-        token_ok = token < x_rows;
-    }
-    uint32_t words[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int exps[2];
+    const uint32_t quad = blockIdx.x / mf::col_tiles, ct = blockIdx.x % mf::col_tiles;
+    const uint32_t t = threadIdx.x, n16 = t / 16, g = (t % 16) / 4, r = t % 4;
+    const uint32_t n = ct * 16 + n16, block = 4 * quad + g;
+    const bool live = n < plan.tile_count[tile];
+    float v[8];
+    bool in_range = true;
+    if (live && block < uint32_t(mx::blocks)) {
+        const uint32_t token = plan.slot_token[plan.tile_first[tile] + n];
+        in_range = token < x_rows;
+        const size_t base = size_t(in_range ? token : 0u) * x_stride + size_t(block) * 32 + 8 * r;
+        if (BF16_IN) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + base);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t block = 4 * quad + gb / 2 + 2 * h;
-        float v[32];
-        if (live && token_ok && block < uint32_t(mx::blocks)) {
-            const size_t base = size_t(token) * x_stride + size_t(block) * 32;
-            if (BF16_IN) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + base);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint4 w = src[k];
-                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        v[8 * k + 2 * q] = __uint_as_float(ww[q] << 16);
-                        v[8 * k + 2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
-                    }
-                }
-            } else {
-                const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float4 w = src[k];
-                    v[4 * k] = w.x;
-                    v[4 * k + 1] = w.y;
-                    v[4 * k + 2] = w.z;
-                    v[4 * k + 3] = w.w;
-                }
+            for (int k = 0; k < 4; ++k) {
+                v[2 * k] = __uint_as_float(ww[k] << 16);
+                v[2 * k + 1] = __uint_as_float(ww[k] & 0xffff0000u);
             }
         } else {
-            const float fill = (live && !token_ok && block < uint32_t(mx::blocks)) ? __builtin_nanf("") : 0.0f;
+            const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+            const float4 w0 = src[0], w1 = src[1];
+            const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int j = 0; j < 32; ++j) {
-                v[j] = fill;
+            for (int k = 0; k < 8; ++k) {
+                v[k] = ww[k];
             }
         }
-        const Mx8Block b = mx8_block(v);
-        exps[h] = b.finite ? b.exponent : 0;
-        // bytes 16 h + j hold value 16 (gb % 2) + j of the A lanes of this block
+    } else {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            // element of value 16 (gb % 2) + j: a static index either way
-            const float val = (gb % 2) ? v[mx8::element_of_value(16 + j)] : v[mx8::element_of_value(j)];
-            words[(16 * h + j) / 4] |= mx8_code(val, b) << (8 * ((16 * h + j) % 4));
+        for (int k = 0; k < 8; ++k) {
+            v[k] = 0.0f;
         }
     }
+    if (!in_range) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            v[k] = __builtin_nanf("");
+        }
+    }
+    float m = 0.0f;
+    int finite = 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        finite &= isfinite(v[k]) ? 1 : 0;
+        m = fmaxf(m, fabsf(v[k]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    finite &= __shfl_xor(finite, 1);
+    finite &= __shfl_xor(finite, 2);
+    const Mx8Block blk{m > 0.0f ? mx8::block_exponent(m) : 0, finite != 0};
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        lo |= mx8_code(v[k], blk) << (8 * k);
+        hi |= mx8_code(v[4 + k], blk) << (8 * k);
+    }
+    // the partner thread (r ^ 2) holds the elements 16 further on
+    const uint32_t plo = uint32_t(__shfl_xor(int(lo), 2)), phi = uint32_t(__shfl_xor(int(hi), 2));
     uint8_t *tb = plan.xb + size_t(tile) * mf::plane_bytes;
-    uint4 *dst = reinterpret_cast<uint4 *>(tb + ((size_t(quad) * mf::col_tiles + ct) * 64 + lane) * mx8::lane_bytes);
-    dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
-    dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
-    // K-block gb's exponent: gb 0 holds block 4q (h 0), gb 3 block 4q+3 (h 1); block 4q+1
-    // is h 0 of groups 2 and 3, block 4q+2 is h 1 of groups 0 and 1
-    const int from_g2 = __shfl(exps[0], int(lane % 16 + 32));
-    const int from_g0 = __shfl(exps[1], int(lane % 16));
-    const int mine = gb == 0 ? exps[0] : (gb == 1 ? from_g2 : (gb == 2 ? from_g0 : exps[1]));
-    tb[mx8::tile_frag_bytes + (size_t(ct) * 64 + lane) * mx8::scale_pad + quad] = uint8_t(mine + 127);
+    if (r < 2) {
+        // bytes 2j and 2j + 1 = this thread's element j and the partner's
+        const auto mix = [](uint32_t a, uint32_t b) __attribute__((always_inline)) {
+            return (a & 0xffu) | ((b & 0xffu) << 8) | ((a & 0xff00u) << 8) | ((b & 0xff00u) << 16);
+        };
+        const uint4 out = make_uint4(mix(lo, plo), mix(lo >> 16, plo >> 16), mix(hi, phi), mix(hi >> 16, phi >> 16));
+        const uint32_t dest = n16 + 16 * (2 * (g & 1) + r);
+        *reinterpret_cast<uint4 *>(tb + ((size_t(quad) * mf::col_tiles + ct) * 64 + dest) * mx8::lane_bytes +
+                                   16 * (g >> 1)) = out;
+    }
+    if (r == 0) {
+        tb[mx8::tile_frag_bytes + (size_t(ct) * 64 + n16 + 16 * g) * mx8::scale_pad + quad] =
+            uint8_t((blk.finite ? blk.exponent : 0) + 127);
+    }
 }
 
 // B staging of the scaled kernels: kMx8StageQuads quads of all column tiles per LDS stage.
 constexpr int kMx8StageQuads = 2;
-constexpr int kMx8Stages = (mf::quads + kMx8StageQuads - 1) / kMx8StageQuads;  // 12, the last with one quad
 constexpr size_t kMx8StageBytes = size_t(kMx8StageQuads) * mf::col_tiles * mx8::frag_bytes;  // 16 KiB
 
 template <int THREADS>
@@ -950,7 +956,8 @@ struct Mx8Stager {
     static constexpr int per = pieces / THREADS;
     static_assert(pieces % THREADS == 0, "whole pieces per thread");
     mf::u32x4 r[per];
-    // pieces past the tile's last quad (the last stage's second half) re-read its last piece
+    // pieces past the tile's last quad (the last stage's second half, and the stage after
+    // the last that the main loop requests) re-read its last piece
     __device__ inline void load(const uint8_t *__restrict__ tile_frags, int stage, uint32_t t) {
 #pragma unroll
         for (int k = 0; k < per; ++k) {
@@ -968,15 +975,16 @@ struct Mx8Stager {
 };
 
 // One quad of the scaled main loop: B fragments of quad i from LDS (stage buffer
-// i / 2 % 2), the A and B scale bytes of the quad, then M x NC instructions; at the end
-// of a stage (every kMx8StageQuads quads, and after the last) the next stage is
-// published and the one after requested.
+// i / 2 % 2), the A and B scale bytes of the quad, then M x NC instructions.  At the end
+// of a stage (stage_end, a constant after unrolling) the next stage is published and
+// the one after requested; past the last stage the request re-reads the plane's last
+// piece (no condition around a load: the compiler would wait for it at once).
 template <int M, int NC, int THREADS>
 __device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint4 (&q)[M], AOperand<M> &wa,
                                                                uint32_t (&sb)[NC][6], Mx8Stager<THREADS> &st,
                                                                const uint8_t *tile_frags,
                                                                mf::u32x4 (*lds)[kMx8StageBytes / 16], uint32_t t,
-                                                               uint32_t lane, mf::f32x4 (&acc)[M][NC]) {
+                                                               uint32_t lane, mf::f32x4 (&acc)[M][NC], bool stage_end) {
     const int stage = i / kMx8StageQuads;
     const mf::u32x4 *buf = lds[stage % 2] + size_t(i % kMx8StageQuads) * mf::col_tiles * 64 * 2;
     mx8::i32x8 b[NC];
@@ -1005,25 +1013,25 @@ __device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint
         }
         sb[c][5] >>= 8;
     }
-    if (i % kMx8StageQuads == kMx8StageQuads - 1 || i == mf::quads - 1) {
-        if (stage + 1 < kMx8Stages) {
-            st.store(lds[(stage + 1) % 2], t);
-        }
+    if (stage_end) {
+        st.store(lds[(stage + 1) % 2], t);
         __syncthreads();
-        if (stage + 2 < kMx8Stages) {
-            st.load(tile_frags, stage + 2, t);
-        }
+        st.load(tile_frags, stage + 2, t);
     }
 }
 
 // The scaled main loop of one wave: M 16-row A tiles (AOperand), NC column tiles, the
 // B fragments staged in LDS by every wave of the workgroup.  acc[m][c] += A_m B_c for
-// quads 0..22; weight codes are requested two quads ahead (three code buffers).
+// quads 0..22; weight codes are requested one quad ahead (two code buffers), which
+// with two workgroups per CU measured faster than two or three quads ahead at one.
+// Pairs of quads keep the buffer and stage-end positions static.
 template <int M, int NC, int THREADS>
 __device__ __attribute__((always_inline)) inline void mx8_main_loop(AOperand<M> &wa, const uint8_t *tile_frags,
                                                                     const uint8_t *tile_scales,
                                                                     mf::u32x4 (*lds)[kMx8StageBytes / 16], uint32_t t,
                                                                     uint32_t lane, mf::f32x4 (&acc)[M][NC]) {
+    static_assert(kMx8StageQuads == 2, "a stage ends at every second quad");
+    constexpr int full = mf::quads / 2 * 2;
     // the lane's B scale bytes per column tile (quads 0..22, shifted one byte per quad)
     uint32_t sb[NC][6];
 #pragma unroll
@@ -1039,24 +1047,19 @@ __device__ __attribute__((always_inline)) inline void mx8_main_loop(AOperand<M> 
     }
     Mx8Stager<THREADS> st;
     st.load(tile_frags, 0, t);
-    uint4 q0[M], q1[M], q2[M];
-    wa.load(0, lane, q0);
-    wa.load(1, lane, q1);
+    uint4 q[2][M];
+    wa.load(0, lane, q[0]);
     st.store(lds[0], t);
     __syncthreads();
     st.load(tile_frags, 1, t);
-    for (int i = 0; i < mf::quads; i += 3) {
-        wa.load(min(i + 2, mf::quads - 1), lane, q2);
-        mx8_quad<M, NC, THREADS>(i, q0, wa, sb, st, tile_frags, lds, t, lane, acc);
-        wa.load(min(i + 3, mf::quads - 1), lane, q0);
-        if (i + 1 < mf::quads) {
-            mx8_quad<M, NC, THREADS>(i + 1, q1, wa, sb, st, tile_frags, lds, t, lane, acc);
-            wa.load(min(i + 4, mf::quads - 1), lane, q1);
-        }
-        if (i + 2 < mf::quads) {
-            mx8_quad<M, NC, THREADS>(i + 2, q2, wa, sb, st, tile_frags, lds, t, lane, acc);
-        }
+    for (int i = 0; i < full; i += 2) {
+        wa.load(i + 1, lane, q[1]);
+        mx8_quad<M, NC, THREADS>(i, q[0], wa, sb, st, tile_frags, lds, t, lane, acc, false);
+        wa.load(min(i + 2, mf::quads - 1), lane, q[0]);
+        mx8_quad<M, NC, THREADS>(i + 1, q[1], wa, sb, st, tile_frags, lds, t, lane, acc, true);
     }
+    static_assert(mf::quads - full == 1, "one quad after the pairs");
+    mx8_quad<M, NC, THREADS>(full, q[0], wa, sb, st, tile_frags, lds, t, lane, acc, false);
 }
 
 // Gate/up on the scaled path, the workgroup layout of gateup_kernel (4 waves x 32 rows:
@@ -1449,8 +1452,8 @@ int ttl_matmul_mxfp4_selected_mxfp8(ttl_ctx *ctx, const ttl_mxfp4 *w, const floa
     plan_selected_kernel<<<ttl::blocks_for(count > tiles ? count : tiles, 256), 256, 0, ctx->stream>>>(
         tokens_dev, count, expert, plan);
     TTL_LAUNCHED("plan_selected_kernel");
-    gather_mx8_kernel<false><<<dim3(mf::quads, tiles), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, x_stride, x_rows,
-                                                                                             plan);
+    gather_mx8_kernel<false><<<dim3(mf::quads * mf::col_tiles, tiles), 256, 0, ctx->stream>>>(x_dev, x_stride,
+                                                                                                  x_rows, plan);
     TTL_LAUNCHED("gather_mx8_kernel");
     MatmulArgs m;
     m.codes = w->codes;
@@ -1542,11 +1545,11 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     }
     if ((stages & TTL_PREFILL_GATHER) && scaled) {
         if (bf16) {
-            gather_mx8_kernel<true><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden,
-                                                                                                    count, plan);
+            gather_mx8_kernel<true><<<dim3(mf::quads * mf::col_tiles, lay.tmax), 256, 0, ctx->stream>>>(
+                x_dev, L.hidden, count, plan);
         } else {
-            gather_mx8_kernel<false><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden,
-                                                                                                     count, plan);
+            gather_mx8_kernel<false><<<dim3(mf::quads * mf::col_tiles, lay.tmax), 256, 0, ctx->stream>>>(
+                x_dev, L.hidden, count, plan);
         }
         TTL_LAUNCHED("gather_mx8_kernel");
     } else if (stages & TTL_PREFILL_GATHER) {
