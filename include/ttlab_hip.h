@@ -245,9 +245,11 @@ int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
  * products are those of the dequantized values (ttl_mxfp8_dequantize), but the
  * instruction's accumulation is not exact in f32 (one GEMM against the reference's
  * f32 sum of the same dequantized products: relative L2 below 1e-5, measured 7.9e-6).
- * The SwiGLU hidden is requantized too, so the MoE's output carries the format's own
- * error (relative L2 about 7e-2 on random activations): the bf16 path stays the
- * exact one.  No reference counterpart (the reference computes in f32). */
+ * The SwiGLU hidden is requantized too (its exponential and division on the
+ * hardware's approximate instructions, a few ulp, ahead of the 3-bit rounding), so
+ * the MoE's output carries the format's own error (relative L2 about 7e-2 on random
+ * activations): the bf16 path stays the exact one.  No reference counterpart (the
+ * reference computes in f32). */
 #define TTL_DTYPE_F32_AS_MXFP8 2
 #define TTL_DTYPE_BF16_AS_MXFP8 3
 

@@ -1137,8 +1137,8 @@ __global__ __launch_bounds__(kGuWaves * 64) void mx8_gateup_kernel(GateUpArgs a)
         float h[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            h[2 * i] = moe_math::clamped_swiglu(acc[0][c][i], acc[2][c][i]);      // element 4 gs + i
-            h[2 * i + 1] = moe_math::clamped_swiglu(acc[1][c][i], acc[3][c][i]);  // element 16 + 4 gs + i
+            h[2 * i] = moe_math::clamped_swiglu_fast(acc[0][c][i], acc[2][c][i]);      // element 4 gs + i
+            h[2 * i + 1] = moe_math::clamped_swiglu_fast(acc[1][c][i], acc[3][c][i]);  // element 16 + 4 gs + i
         }
         float m = 0.0f;
         bool finite = true;
