@@ -70,6 +70,16 @@ int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes);
  * words equals a fixed constant. */
 int ttl_stream_read(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *sink_dev);
 
+/* The cost of handing 2880 floats from 180 producer workgroups to 32 consumer
+ * workgroups, each consumer needing all of them: mode 0 across a kernel boundary (a
+ * producer launch, then a consumer launch), mode 1 inside one launch (release fence and
+ * a flag per producer, bounded polling, acquire fence).  `launches` handoffs are
+ * captured into a graph and replayed; *us_per_handoff is the average, *wrong the
+ * consumers that read a wrong sum or gave up polling (0 when the handoff worked).
+ * Measurement only, with no counterpart in the reference: it is why the decode step
+ * keeps one kernel per dependency level. */
+int ttl_measure_handoff(ttl_ctx *ctx, int mode, uint32_t launches, float *us_per_handoff, uint32_t *wrong);
+
 /* ---- timing (HIP events on the context's stream) -------------------------------- */
 
 int ttl_timer_start(ttl_ctx *ctx);

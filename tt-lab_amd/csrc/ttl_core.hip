@@ -49,6 +49,99 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4 *
         *sink = acc;
     }
 }
+// ---- a device-wide handoff: a kernel boundary against a barrier inside one kernel ----
+//
+// 180 producer workgroups each write 16 floats (the shape of the 16-row matvec tiles);
+// 32 consumers then each need all 2880 values (the shape of the router rows).  Across a
+// kernel boundary the producers are one launch and the consumers the next.  Inside one
+// launch each producer publishes its values with an agent-scope release fence and a flag
+// (an epoch, so nothing is reset between launches); each consumer polls the 180 flags in
+// parallel, boundedly, then takes an agent-scope acquire fence and reads.  Every
+// workgroup of the one-launch form is resident at once (212 <= the CU count).
+constexpr int kHandoffProducers = 180, kHandoffConsumers = 32, kHandoffThreads = 256, kHandoffValues = 2880;
+constexpr unsigned kHandoffMaxSpin = 200000;
+
+struct HandoffState {
+    float data[kHandoffValues];
+    unsigned flags[kHandoffProducers * 16];  // one flag per 64-byte line
+    unsigned epoch, done, failures;
+    float out[kHandoffConsumers];
+};
+
+__device__ inline void handoff_produce(HandoffState *st) {
+    if (threadIdx.x < 16) {
+        st->data[blockIdx.x * 16 + threadIdx.x] = float(blockIdx.x * 16 + threadIdx.x) * 0.5f;
+    }
+}
+
+// Sums the values in a fixed order (exact: multiples of 0.5 below 2^22) and records it.
+__device__ inline void handoff_consume(HandoffState *st, uint32_t consumer, bool ok) {
+    __shared__ float red[kHandoffThreads];
+    float s = 0.0f;
+    for (int i = int(threadIdx.x); i < kHandoffValues; i += kHandoffThreads) {
+        s += st->data[i];
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float a = 0.0f;
+        for (int i = 0; i < kHandoffThreads; ++i) {
+            a += red[i];
+        }
+        st->out[consumer] = ok ? a : -1.0f;
+    }
+}
+
+__global__ __launch_bounds__(kHandoffThreads) void handoff_producers_kernel(HandoffState *st) {
+    handoff_produce(st);
+}
+
+__global__ __launch_bounds__(kHandoffThreads) void handoff_consumers_kernel(HandoffState *st) {
+    handoff_consume(st, blockIdx.x, true);
+}
+
+__global__ __launch_bounds__(kHandoffThreads) void handoff_in_kernel(HandoffState *st) {
+    const unsigned epoch = __hip_atomic_load(&st->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    if (blockIdx.x < uint32_t(kHandoffProducers)) {
+        handoff_produce(st);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __hip_atomic_store(&st->flags[blockIdx.x * 16], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    __shared__ int all;
+    if (threadIdx.x == 0) {
+        all = 1;
+    }
+    __syncthreads();
+    if (threadIdx.x < uint32_t(kHandoffProducers)) {
+        unsigned spins = 0;
+        while (__hip_atomic_load(&st->flags[threadIdx.x * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch &&
+               spins < kHandoffMaxSpin) {
+            __builtin_amdgcn_s_sleep(1);
+            ++spins;
+        }
+        if (spins == kHandoffMaxSpin) {
+            all = 0;  // gave up: recorded as a failure, never waits longer
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const uint32_t consumer = blockIdx.x - kHandoffProducers;
+    handoff_consume(st, consumer, all != 0);
+    if (threadIdx.x == 0) {
+        if (!all) {
+            __hip_atomic_fetch_add(&st->failures, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const unsigned d = __hip_atomic_fetch_add(&st->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == unsigned(kHandoffConsumers - 1)) {  // the last consumer opens the next epoch
+            __hip_atomic_store(&st->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&st->epoch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
 }  // namespace
 
 namespace ttl {
@@ -234,6 +327,76 @@ int ttl_stream_read(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *s
     stream_read_kernel<<<unsigned(blocks), kReadThreads, 0, ctx->stream>>>(static_cast<const uint4 *>(src_dev), words,
                                                                        sink_dev);
     TTL_LAUNCHED("stream_read_kernel");
+    return TTL_OK;
+}
+
+int ttl_measure_handoff(ttl_ctx *ctx, int mode, uint32_t launches, float *us_per_handoff, uint32_t *wrong) {
+    TTL_REQUIRE(ctx && us_per_handoff && wrong, TTL_ERR_INVALID, "ttl_measure_handoff: null argument");
+    TTL_REQUIRE(mode == 0 || mode == 1, TTL_ERR_INVALID, "ttl_measure_handoff: mode must be 0 or 1");
+    TTL_REQUIRE(launches >= 1 && launches <= 1000, TTL_ERR_INVALID, "ttl_measure_handoff: 1..1000 launches");
+    TTL_REQUIRE(ctx->compute_units >= kHandoffProducers + kHandoffConsumers, TTL_ERR_SHAPE,
+                "ttl_measure_handoff: needs %d resident workgroups", kHandoffProducers + kHandoffConsumers);
+    HandoffState *st = nullptr;
+    TTL_HIP(hipMalloc(&st, sizeof(HandoffState)));
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int rc = TTL_OK;
+    const auto fail = [&](hipError_t err, const char *what) {
+        if (rc == TTL_OK && err != hipSuccess) {
+            rc = ttl::hip_fail(err, what);
+        }
+    };
+    fail(hipMemsetAsync(st, 0, sizeof(HandoffState), ctx->stream), "hipMemsetAsync");
+    fail(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    // one graph of `launches` handoffs, replayed: first untimed, then timed
+    if (rc == TTL_OK) {
+        fail(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        for (uint32_t i = 0; i < launches && rc == TTL_OK; ++i) {
+            if (mode == 0) {
+                handoff_producers_kernel<<<kHandoffProducers, kHandoffThreads, 0, ctx->stream>>>(st);
+                handoff_consumers_kernel<<<kHandoffConsumers, kHandoffThreads, 0, ctx->stream>>>(st);
+            } else {
+                handoff_in_kernel<<<kHandoffProducers + kHandoffConsumers, kHandoffThreads, 0, ctx->stream>>>(st);
+            }
+        }
+        fail(hipStreamEndCapture(ctx->stream, &graph), "hipStreamEndCapture");
+    }
+    if (rc == TTL_OK) {
+        fail(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+    constexpr int kReps = 20;
+    float ms = 0.0f;
+    if (rc == TTL_OK) {
+        fail(hipGraphLaunch(exec, ctx->stream), "hipGraphLaunch");
+        fail(hipEventRecord(ctx->timer_start, ctx->stream), "hipEventRecord");
+        for (int r = 0; r < kReps && rc == TTL_OK; ++r) {
+            fail(hipGraphLaunch(exec, ctx->stream), "hipGraphLaunch");
+        }
+        fail(hipEventRecord(ctx->timer_stop, ctx->stream), "hipEventRecord");
+        fail(hipEventSynchronize(ctx->timer_stop), "hipEventSynchronize");
+        fail(hipEventElapsedTime(&ms, ctx->timer_start, ctx->timer_stop), "hipEventElapsedTime");
+    }
+    HandoffState host;
+    if (rc == TTL_OK) {
+        fail(hipMemcpy(&host, st, sizeof host, hipMemcpyDeviceToHost), "hipMemcpy");
+    }
+    if (exec) {
+        (void)hipGraphExecDestroy(exec);
+    }
+    if (graph) {
+        (void)hipGraphDestroy(graph);
+    }
+    (void)hipFree(st);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const float expected = 0.5f * float(kHandoffValues) * float(kHandoffValues - 1) / 2.0f;
+    uint32_t bad = host.failures;
+    for (int c = 0; c < kHandoffConsumers; ++c) {
+        bad += host.out[c] != expected ? 1u : 0u;
+    }
+    *wrong = bad;
+    *us_per_handoff = ms * 1000.0f / float(kReps * launches);
     return TTL_OK;
 }
 

@@ -316,6 +316,7 @@ def load_library():
         "ttl_moe_prefill": (i32, [vp, C.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp, vp, sz]),
         "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
         "ttl_stream_read": (i32, [vp, vp, sz, vp]),
+        "ttl_measure_handoff": (i32, [vp, i32, u32, C.POINTER(f32), C.POINTER(u32)]),
         "ttl_matmul_q8_0_workspace_bytes": (sz, [u32, u32]),
         "ttl_matmul_q8_0": (i32, [vp, vp, vp, vp, u32, vp, vp, vp, sz]),
         "ttl_capture_begin": (i32, [vp]),
@@ -532,6 +533,14 @@ class Device:
         ms = C.c_float()
         _check(self.lib.ttl_timer_stop(self.ctx, C.byref(ms)), "ttl_timer_stop")
         return ms.value
+
+    def measure_handoff(self, mode, launches=50):
+        """(microseconds per handoff, consumers that saw a wrong sum or gave up):
+        mode 0 across a kernel boundary, mode 1 inside one kernel."""
+        us, wrong = C.c_float(), C.c_uint32()
+        _check(self.lib.ttl_measure_handoff(self.ctx, mode, launches, C.byref(us), C.byref(wrong)),
+               "ttl_measure_handoff")
+        return us.value, wrong.value
 
     # ---- synthetic inputs ----
     def synth_normal(self, buf, seed, stream, n, sigma=1.0, mean=0.0, offset=0):
