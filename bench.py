@@ -163,6 +163,8 @@ def gpu_decode(args):
     kernels, total_us = {}, 0.0
     for kind in ttlab_amd.Model.KERNELS:
         us_k, n = model.time_kernel(kind, last, reps)
+        if n == 0:  # e.g. no full-context layer in a one-layer counter run
+            continue
         nbytes = step_kernel_bytes(kind, last, experts, VOCAB)
         gbs = nbytes / (us_k * 1e-6) / 1e9
         kernels[kind] = {"us": round(us_k, 3), "launches_per_step": n, "bytes_per_launch": nbytes,
