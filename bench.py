@@ -521,13 +521,15 @@ def host_cpu():
     except OSError:
         pass
     isa = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni") if f in flags]
+    # allowed_cores: the cores this process may run on; the sample itself uses one
     return {"model": model, "nproc": os.cpu_count(), "allowed_cores": len(os.sched_getaffinity(0)), "isa": isa}
 
 
 def cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
     """The oracle (restated reference CPU path) on one host core, bounded sample."""
+    host = host_cpu()  # before the sample pins this process to one core
     res = _cpu_baseline(seconds, workload, layers, context)
-    res["host"] = host_cpu()
+    res["host"] = host
     return res
 
 
