@@ -87,6 +87,33 @@ def test_f32_matvec_and_rmsnorm_kats():
     assert abs(out[0] - 6 * scale) <= 1e-6 and abs(out[1] - 12 * scale) <= 1e-6
 
 
+def test_f32_router_sums_are_sequential_from_the_bias():
+    """matvec_add_f32 and matmul_add_f32 (tensor.cpp:186-200, 497-527): per (row, token)
+    the sum starts at the bias and adds the rounded f32 products one column after the
+    other -- numpy's float32 cumulative sum of [bias, w0 x0, w1 x1, ...] bit for bit."""
+    rng = np.random.default_rng(31)
+    rows, cols, tokens = 5, 2880, 3
+    w = rng.standard_normal((rows, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    x = rng.standard_normal((tokens, cols)).astype(np.float32)
+    expect = np.empty((tokens, rows), np.float32)
+    for t in range(tokens):
+        for r in range(rows):
+            terms = np.concatenate([bias[r:r + 1], (w[r] * x[t]).astype(np.float32)])
+            expect[t, r] = np.cumsum(terms, dtype=np.float32)[-1]
+    out = np.empty(tokens * rows, np.float32)
+    ws, tr = np.empty(tokens, np.float32), np.empty(tokens * cols, np.float32)
+    lib.orc_matmul_add_f32(np.ascontiguousarray(w.ravel()), bias, rows, cols, np.ascontiguousarray(x.ravel()), tokens,
+                           out, ws, tr)
+    assert np.array_equal(out.reshape(tokens, rows).view(np.uint32), expect.view(np.uint32))
+    for t in range(tokens):
+        y = np.empty(rows, np.float32)
+        lib.orc_matvec_add_f32(np.ascontiguousarray(w.ravel()), bias, rows, cols, np.ascontiguousarray(x[t]), y)
+        assert np.array_equal(y.view(np.uint32), expect[t].view(np.uint32))
+    # a pairwise or fused sum would differ somewhere: the order is what is pinned
+    assert not np.array_equal(expect, (x @ w.T + bias).astype(np.float32))
+
+
 def test_q8_0_matvec_kats():
     # src/tests.cpp:214-234
     data = np.zeros(68, np.uint8)
