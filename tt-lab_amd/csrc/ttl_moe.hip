@@ -320,6 +320,26 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
     return m;
 }
 
+// Order-preserving key of a float: a > b (neither NaN) gives key(a) >= key(b),
+// strictly for unequal values except -0.0 below +0.0.
+__device__ inline uint32_t order_key32(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+
+// The 32-bit form of wave_max_u64: DPP within rows, then the four rows' lane reads.
+__device__ inline uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0xb1, 0xf, 0xf, false)));   // quad_perm [1,0,3,2]
+    x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x4e, 0xf, 0xf, false)));   // quad_perm [2,3,0,1]
+    x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x141, 0xf, 0xf, false)));  // row_half_mirror
+    x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x140, 0xf, 0xf, false)));  // row_mirror
+    const uint32_t a = uint32_t(__builtin_amdgcn_readlane(int(x), 0));
+    const uint32_t b = uint32_t(__builtin_amdgcn_readlane(int(x), 16));
+    const uint32_t c = uint32_t(__builtin_amdgcn_readlane(int(x), 32));
+    const uint32_t d = uint32_t(__builtin_amdgcn_readlane(int(x), 48));
+    return max(max(a, b), max(c, d));
+}
+
 // Routing for one token comes in two parts.  route_certified_wave() ranks the
 // exact rows; when the ranking is certified it leaves the indices (and, when
 // `publish`, the softmax weights and -- if `logits` is non-null, in one workgroup
@@ -332,27 +352,34 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
 // The ranking runs in wave 0 alone, in registers.  Thread c < experts would rank
 // expert c by (exact value descending, index ascending) -- the order the
 // reference's selection sort produces when no two values are within their error
-// bounds.  Lane l holds experts l, l+64, l+128.  A candidate's key is the order
-// key of its exact value with the low byte replaced by 255 - expert, so one wave
-// maximum per rank picks the largest value (the lowest index among equal keys).
-// The truncated byte only matters for values the certificate rejects anyway:
-// the certificate compares the exact values and bounds, value - bound of rank r
-// > value + bound of every expert ranked below r, which holds only if the
-// values are strictly ordered as ranked (bounds are positive).  Checked as
+// bounds.  Lane l holds experts l, l+64, l+128.  A candidate's key is the 32-bit
+// order key of its exact value rounded to f32: one wave maximum per rank gives the
+// largest key, and a ballot picks the lowest expert holding it.  The rounding only
+// merges values the certificate rejects anyway: two values with one f32 image are
+// less than one f32 ulp apart, and each bound is at least half an ulp of its value
+// (2^-24 of the sum of |products|), so they are never separated by their bounds.
+// The certificate compares the exact values and bounds, value - bound of rank r >
+// value + bound of every expert ranked below r, which holds only if the values are
+// strictly ordered as ranked (bounds are positive).  Checked as
 // up(r') < min(low of ranks before r') at each rank and max(up of the unselected)
 // < min(low of all selected) at the end.  Leaves indices, selected values and
 // lds.certified (and, when `publish`, weights and logits) in lds; ends with the
 // workgroup's one barrier.
 // Wave 0's share of the router rows (exact values and bounds), loaded ahead of
 // route_certified_wave() so a caller can issue the loads before others.
+// PL candidates per lane (lane l holds experts l, l + 64, ...), at most kPerLane: the
+// decode launch picks the smallest PL that holds the layer's experts, so the loops over
+// a lane's candidates are as short as the expert count allows.
+template <int PL = kPerLane>
 struct RouteRows {
-    double v[kPerLane], b[kPerLane];
+    double v[PL], b[PL];
 };
 
-__device__ __forceinline__ void load_route_rows(uint32_t experts, const RouterScratch *scratch, RouteRows &rows) {
+template <int PL>
+__device__ __forceinline__ void load_route_rows(uint32_t experts, const RouterScratch *scratch, RouteRows<PL> &rows) {
     if (threadIdx.x < 64) {
 #pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
+        for (int j = 0; j < PL; ++j) {
             const uint32_t c = threadIdx.x + 64 * j;
             rows.v[j] = c < experts ? scratch->exact[c] : 0.0;
             rows.b[j] = c < experts ? scratch->bound[c] : 0.0;
@@ -360,16 +387,17 @@ __device__ __forceinline__ void load_route_rows(uint32_t experts, const RouterSc
     }
 }
 
-__device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_exact, const RouteRows &rows,
+template <int PL>
+__device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_exact, const RouteRows<PL> &rows,
                                      RouteLds &lds, float *__restrict__ logits, bool publish) {
     if (threadIdx.x < 64) {
         const uint32_t lane = threadIdx.x;
-        uint64_t key[kPerLane];
-        double low[kPerLane], up[kPerLane];
-        float value[kPerLane];
+        uint32_t key[PL];
+        double low[PL], up[PL];
+        float value[PL];
         bool bad = false;
 #pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
+        for (int j = 0; j < PL; ++j) {
             const uint32_t c = lane + 64 * j;
             key[j] = 0;
             low[j] = 0.0;
@@ -378,7 +406,7 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_ex
             if (c < experts) {
                 const double v = rows.v[j], b = rows.b[j];
                 bad = bad || !isfinite(v) || !isfinite(b);
-                key[j] = (order_key(v) & ~uint64_t(0xff)) | (0xff - c);
+                key[j] = order_key32(float(v));
                 low[j] = v - b;
                 up[j] = v + b;
                 value[j] = float(v);
@@ -387,17 +415,28 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_ex
         bool ok = !force_exact && __ballot(bad) == 0;
         double min_low = INFINITY;
         for (uint32_t r = 0; r < k; ++r) {
-            uint64_t m = key[0];
+            uint32_t m = key[0];
 #pragma unroll
-            for (int j = 1; j < kPerLane; ++j) {
-                m = key[j] > m ? key[j] : m;
+            for (int j = 1; j < PL; ++j) {
+                m = max(m, key[j]);
             }
-            const uint32_t c = 0xff - uint32_t(wave_max_u64(m) & 0xff);
+            m = wave_max_u32(m);
+            // the lowest expert holding the largest key (candidates are numbered lane +
+            // 64 j, so the first piece with a match, then its lowest lane)
+            uint32_t c = ~0u;
+#pragma unroll
+            for (int j = PL - 1; j >= 0; --j) {
+                const uint64_t hit = __ballot(key[j] == m && m != 0u);
+                if (hit) {
+                    c = 64u * uint32_t(j) + uint32_t(__ffsll((long long)hit) - 1);
+                }
+            }
+            c = c == ~0u ? 0u : c;
             const uint32_t owner = c % 64, piece = c / 64;
             double lo_c = low[0], up_c = up[0];
             float v_c = value[0];
 #pragma unroll
-            for (int j = 1; j < kPerLane; ++j) {
+            for (int j = 1; j < PL; ++j) {
                 if (piece == uint32_t(j)) {
                     lo_c = low[j];
                     up_c = up[j];
@@ -408,7 +447,7 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_ex
             const double w_up = __longlong_as_double((long long)readlane_u64(uint64_t(__double_as_longlong(up_c)), owner));
             const float w_v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_c), int(owner)));
 #pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
+            for (int j = 0; j < PL; ++j) {
                 if (lane + 64 * j == c) {
                     key[j] = 0;
                     up[j] = -INFINITY;
@@ -423,7 +462,7 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_ex
         }
         uint64_t u = order_key(up[0]);
 #pragma unroll
-        for (int j = 1; j < kPerLane; ++j) {
+        for (int j = 1; j < PL; ++j) {
             const uint64_t y = order_key(up[j]);
             u = y > u ? y : u;
         }
@@ -436,7 +475,7 @@ __device__ void route_certified_wave(uint32_t experts, uint32_t k, bool force_ex
         }
         if (ok && publish && logits) {
 #pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
+            for (int j = 0; j < PL; ++j) {
                 if (lane + 64 * j < experts) {
                     logits[lane + 64 * j] = value[j];
                 }
@@ -620,9 +659,9 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
                                 float *red, float *prod) {
-    RouteRows rows;
-    load_route_rows(experts, scratch, rows);
-    route_certified_wave(experts, k, force_exact, rows, lds, logits, true);
+    RouteRows<kPerLane> rows;
+    load_route_rows<kPerLane>(experts, scratch, rows);
+    route_certified_wave<kPerLane>(experts, k, force_exact, rows, lds, logits, true);
     if (!lds.certified) {
         stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
         route_exact_coop<PER>(weight, bias, experts, k, xs, scratch, lds, logits, prod);
@@ -695,7 +734,7 @@ struct GateUpArgs {
 // wave 0, or the exact fallback when the ranking is not certified) instead of
 // reading a separate selection kernel's indices; the input loads are in flight
 // meanwhile.
-template <int MODE, bool ROUTE>
+template <int MODE, bool ROUTE, int PL = kPerLane>
 __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[GateUpSplit::x_floats];
     __shared__ float red[stage::red_floats(GateUpSplit::x_blocks)];
@@ -708,9 +747,9 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
     // the staging completes while those are in flight
     // ROUTE: wave 0's router rows first (the ranking waits for them, and loads
     // return in order), then the input loads, then the ranking
-    RouteRows rows;
+    RouteRows<PL> rows;
     if constexpr (ROUTE) {
-        load_route_rows(a.experts, a.scratch, rows);
+        load_route_rows<PL>(a.experts, a.scratch, rows);
     }
     stage::Pending<mx::cols, GateUpSplit::x_blocks, kGateUpThreads, MODE> pending;
     stage::stage_load(a.in, pending);
@@ -721,7 +760,7 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_swiglu_kernel(GateUpArg
         // workgroup 0 publishes the routing; the others only need the indices
         const bool first = blockIdx.x == 0;
         float *logits = first ? a.logits_out : nullptr;
-        route_certified_wave(a.experts, a.k, false, rows, rl, logits, first);
+        route_certified_wave<PL>(a.experts, a.k, false, rows, rl, logits, first);
         if (!rl.certified) {
             // rare: the exact path needs the staged input first
             stage::stage_finish(a.in, pending, xs, red);
@@ -1070,8 +1109,15 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
         if (expert_ids) {
             gateup_swiglu_kernel<decltype(mode)::value, false>
                 <<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
+        } else if (L.experts <= 64) {
+            gateup_swiglu_kernel<decltype(mode)::value, true, 1>
+                <<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
+        } else if (L.experts <= 128) {
+            gateup_swiglu_kernel<decltype(mode)::value, true, 2>
+                <<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
         } else {
-            gateup_swiglu_kernel<decltype(mode)::value, true><<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
+            gateup_swiglu_kernel<decltype(mode)::value, true, kPerLane>
+                <<<a.tiles * L.used, kGateUpThreads, 0, ctx->stream>>>(a);
         }
     });
     TTL_LAUNCHED("gateup_swiglu_kernel");
