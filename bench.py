@@ -197,11 +197,13 @@ def gpu_decode(args):
                    "kernels_sum_ms": round(total_us / 1000, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("void gateup_swiglu_kernel<1, true>"),
-                     "kernel": "gateup_swiglu_kernel<1, true> (top-4 ranking at its head, then gate/up of the 4 "
-                               "experts and the clamped SwiGLU; as the step runs it)",
+                     # the committed counters are config 3's (PL = 1: at most 64 experts)
+                     "traffic": measured_traffic("void gateup_swiglu_kernel<1, true, 1>") if args.config == 3 else None,
+                     "kernel": f"gateup_swiglu_kernel<1, true, {1 if experts <= 64 else 2 if experts <= 128 else 3}> "
+                               "(top-4 ranking at its head, then gate/up of the 4 experts and the clamped SwiGLU; "
+                               "as the step runs it)",
                      "bytes_per_launch": GATEUP_BYTES, "launch_us": round(us, 3),
-                     "given_indices": {"kernel": "gateup_swiglu_kernel<1, false>", "launch_us": given["us"],
+                     "given_indices": {"kernel": "gateup_swiglu_kernel<1, false, 3>", "launch_us": given["us"],
                                        "GBps": given["GBps"], "frac": given["frac"]},
                      "read_ceiling": ceiling_entry(achieved, GATEUP_BYTES, us_read)},
     }
@@ -276,8 +278,8 @@ def gpu_moe(args):
                    "layer_algorithmic_GBps": round(layer_bytes * LAYERS / (ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("void gateup_swiglu_kernel<0, false>"),
-                     "kernel": "gateup_swiglu_kernel<0, false> (indices given)", "bytes_per_launch": GATEUP_BYTES,
+                     "traffic": measured_traffic("void gateup_swiglu_kernel<0, false, 3>"),
+                     "kernel": "gateup_swiglu_kernel<0, false, 3> (indices given)", "bytes_per_launch": GATEUP_BYTES,
                      "launch_us": round(us, 3)},
     }
 
