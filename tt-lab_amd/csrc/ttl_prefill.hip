@@ -58,8 +58,8 @@ constexpr int kMmRows = kMmWaves * kMmTiles * 16;
 constexpr int kHiddenPlanes = 3;
 
 // A tile holding at most kNarrowSlots slots (the remainder of an expert's bucket) is
-// "narrow": its GEMMs run on the first kNarrowCols column tiles only, in a launch of
-// their own, so a bucket of 70 slots costs 64 + 32 columns instead of 64 + 64.
+// "narrow": its GEMMs run on the first kNarrowCols column tiles only (a branch of the
+// same launch), so a bucket of 70 slots costs 64 + 32 columns instead of 64 + 64.
 constexpr int kNarrowCols = 2;
 constexpr uint32_t kNarrowSlots = kNarrowCols * 16;
 
@@ -426,6 +426,11 @@ struct AOperand {
             q[a] = codes[a][size_t(block) * mx::tile_rows];
         }
     }
+    // The same for tile a alone.
+    __device__ inline uint4 load_one(int i, uint32_t lane, int a) const {
+        const uint32_t block = min(uint32_t(4 * i) + lane / mx::tile_rows, uint32_t(mx::blocks - 1));
+        return codes[a][size_t(block) * mx::tile_rows];
+    }
     // Scale of tile a for the current quad; next_quad() moves every record on by
     // one byte, so the indices stay static.
     __device__ inline float scale(int a) const {
@@ -498,7 +503,10 @@ __device__ __attribute__((always_inline)) inline void quad_mfma(const mf::u32x4 
 
 // Quads 0..22 with NB code buffers rotating under static indices: quad i's codes
 // are requested NB - 1 quads before they are used (requests past quad 22 repeat
-// it).  The caller has requested quads 0..NB-2 into buffers 0..NB-2.
+// it).  The caller has requested quads 0..NB-2 into buffers 0..NB-2.  Each request
+// is pinned before the quad's instructions (sched_barrier), and so are the stage
+// requests at every stage end: left to the scheduler, requests sank to just before
+// their first use and the wave waited for them there.
 template <int NB, int M, class Load, class Compute>
 __device__ __attribute__((always_inline)) inline void rotate_quads(uint4 (&qa)[NB][M], Load &&load,
                                                                    Compute &&compute) {
@@ -507,6 +515,7 @@ __device__ __attribute__((always_inline)) inline void rotate_quads(uint4 (&qa)[N
         for (int b = 0; b < NB; ++b) {
             if (i + b < mf::quads) {
                 load(min(i + b + NB - 1, mf::quads - 1), qa[(b + NB - 1) % NB]);
+                __builtin_amdgcn_sched_barrier(0);
                 compute(i + b, qa[b]);
             }
         }
@@ -539,30 +548,26 @@ __device__ inline bool tile_in_range(uint32_t tiles, uint32_t &tile, uint32_t &r
     return true;
 }
 
-// NC = mf::col_tiles takes the plan's wide tiles, NC < mf::col_tiles its narrow ones.
-template <int NC>
-__device__ inline bool tile_of_workgroup(const PlanHeader *header, uint32_t &tile, uint32_t &row_group) {
-    const bool narrow = NC < mf::col_tiles;
-    const uint32_t first = narrow ? header->wide : 0u;
-    const uint32_t tiles = narrow ? header->tiles - header->wide : header->wide;
-    if (!tile_in_range(tiles, tile, row_group)) {
+// One launch covers every tile of the plan: the wide tiles [0, wide) run with all
+// mf::col_tiles column tiles, the narrow ones [wide, tiles) with kNarrowCols (the
+// workgroup's branch is uniform, so the barriers inside are reached by all its waves).
+__device__ inline bool tile_of_workgroup(const PlanHeader *header, uint32_t &tile, uint32_t &row_group,
+                                         bool &narrow) {
+    if (!tile_in_range(header->tiles, tile, row_group)) {
         return false;
     }
-    tile += first;
+    narrow = tile >= header->wide;
     return true;
 }
 
 // Accumulators: [matrix (gate 0/1, up 2/3)][column tile]; NC column tiles (the plan's
 // wide tiles with all of them, or its narrow ones with kNarrowCols).
 template <int PX, int NC>
-__global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void gateup_kernel(GateUpArgs a) {
+__device__ __attribute__((always_inline)) inline void gateup_tile(
+    const GateUpArgs &a, uint32_t tile, uint32_t row_group,
+    mf::u32x4 (*lds)[Stager<PX, kGuWaves * 64>::lds_chunks]) {
     using SS = StageShape<PX>;
     constexpr int kThreads = kGuWaves * 64;
-    __shared__ mf::u32x4 lds[2][Stager<PX, kThreads>::lds_chunks];
-    uint32_t tile, row_group;
-    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
-        return;
-    }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
     const uint32_t row0 = row_group * kGuRows + wave * 32;  // this wave's 32 rows (one down K block)
@@ -599,7 +604,9 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
 
     Stager<PX, kThreads> st;
     st.load(frags, 0, t);
-    uint4 qa[kGuCodeBuffers][4];  // codes of the quads in flight: [buffer][gate0, gate1, up0, up1]
+    // three planes leave room for one code buffer less (the fourth spilled)
+    constexpr int NB = PX == 3 ? 3 : kGuCodeBuffers;
+    uint4 qa[NB][4];  // codes of the quads in flight: [buffer][gate0, gate1, up0, up1]
     auto load_quad = [&](int i, uint4(&q)[4]) __attribute__((always_inline)) {
         uint4 g2[2], u2[2];
         ga.load(i, lane, g2);
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
         q[3] = u2[1];
     };
 #pragma unroll
-    for (int b = 0; b < kGuCodeBuffers - 1; ++b) {
+    for (int b = 0; b < NB - 1; ++b) {
         load_quad(b, qa[b]);
     }
     st.store(lds[0], t);
@@ -628,6 +635,7 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
         if (stage + 2 < SS::count) {
             st.load(frags, stage + 2, t);
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto compute_quad = [&](int i, const uint4(&q)[4]) __attribute__((always_inline)) {
         float sc[4];
@@ -686,6 +694,21 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     }
 }
 
+template <int PX>
+__global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void gateup_kernel(GateUpArgs a) {
+    __shared__ mf::u32x4 lds[2][Stager<PX, kGuWaves * 64>::lds_chunks];
+    uint32_t tile, row_group;
+    bool narrow;
+    if (!tile_of_workgroup(a.plan.header, tile, row_group, narrow)) {
+        return;
+    }
+    if (narrow) {
+        gateup_tile<PX, kNarrowCols>(a, tile, row_group, lds);
+    } else {
+        gateup_tile<PX, mf::col_tiles>(a, tile, row_group, lds);
+    }
+}
+
 // ---- plain GEMM (down projection, selected matmul) -----------------------------------------
 
 struct MatmulArgs {
@@ -699,14 +722,11 @@ struct MatmulArgs {
 };
 
 template <int P, bool SCATTER, int NC>
-__global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
+__device__ __attribute__((always_inline)) inline void matmul_tile(const MatmulArgs &a, uint32_t tile,
+                                                                  uint32_t row_group,
+                                                                  mf::u32x4 (*lds)[Stager<P, kMmWaves * 64>::lds_chunks]) {
     using SS = StageShape<P>;
     constexpr int kThreads = kMmWaves * 64;
-    __shared__ mf::u32x4 lds[2][Stager<P, kThreads>::lds_chunks];
-    uint32_t tile, row_group;
-    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
-        return;
-    }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
     const uint32_t row0 = row_group * kMmRows + wave * (kMmTiles * 16);
@@ -760,6 +780,7 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
         if (stage + 2 < SS::count) {
             st.load(frags, stage + 2, t);
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto compute_quad = [&](int i, const uint4(&q)[kMmTiles]) __attribute__((always_inline)) {
         float sc[kMmTiles];
@@ -780,11 +801,14 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
 
     for (int i = 0; i < mf::quads; i += 3) {
         wa.load(min(i + 2, mf::quads - 1), lane, qa[2]);
+        __builtin_amdgcn_sched_barrier(0);
         compute_quad(i, qa[0]);
         wa.load(min(i + 3, mf::quads - 1), lane, qa[0]);
+        __builtin_amdgcn_sched_barrier(0);
         if (i + 1 < mf::quads) {
             compute_quad(i + 1, qa[1]);
             wa.load(min(i + 4, mf::quads - 1), lane, qa[1]);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (i + 2 < mf::quads) {
             compute_quad(i + 2, qa[2]);
@@ -818,6 +842,21 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
             *reinterpret_cast<float4 *>(dst + 16 * m) = make_float4(acc[m][c][0], acc[m][c][1], acc[m][c][2],
                                                                     acc[m][c][3]);
         }
+    }
+}
+
+template <int P, bool SCATTER>
+__global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
+    __shared__ mf::u32x4 lds[2][Stager<P, kMmWaves * 64>::lds_chunks];
+    uint32_t tile, row_group;
+    bool narrow;
+    if (!tile_of_workgroup(a.plan.header, tile, row_group, narrow)) {
+        return;
+    }
+    if (narrow) {
+        matmul_tile<P, SCATTER, kNarrowCols>(a, tile, row_group, lds);
+    } else {
+        matmul_tile<P, SCATTER, mf::col_tiles>(a, tile, row_group, lds);
     }
 }
 
@@ -966,21 +1005,29 @@ struct Mx8Stager {
             r[k] = *reinterpret_cast<const mf::u32x4 *>(tile_frags + off);
         }
     }
+    // LDS holds each (quad, column tile) fragment as its 64 lanes' first 16 bytes, then
+    // their last 16: a lane's two reads are then contiguous across the wave (the
+    // fragment's own order, 32 bytes per lane, puts two lanes on the same banks)
     __device__ inline void store(mf::u32x4 *lds, uint32_t t) const {
 #pragma unroll
         for (int k = 0; k < per; ++k) {
-            lds[t + uint32_t(k) * THREADS] = r[k];
+            const uint32_t piece = t + uint32_t(k) * THREADS, r16 = piece % 128;
+            lds[piece - r16 + (r16 % 2) * 64 + r16 / 2] = r[k];
         }
     }
 };
 
 // One quad of the scaled main loop: B fragments of quad i from LDS (stage buffer
-// i / 2 % 2), the A and B scale bytes of the quad, then M x NC instructions.  At the end
-// of a stage (stage_end, a constant after unrolling) the next stage is published and
-// the one after requested; past the last stage the request re-reads the plane's last
-// piece (no condition around a load: the compiler would wait for it at once).
+// i / 2 % 2), the A and B scale bytes of the quad, then M x NC instructions, tile by
+// tile: as soon as tile m's instructions are issued, its registers take the codes of
+// quad `next` (sched_barrier keeps each request at its place; left to the scheduler,
+// the requests sank below the next quad's instructions and every wave waited for all
+// of its loads, vmcnt(0), once per stage).  At the end of a stage (stage_end, a
+// constant after unrolling) the next stage is published and the one after requested;
+// past the last stage the request re-reads the plane's last piece (no condition
+// around a load: the compiler would wait for it at once).
 template <int M, int NC, int THREADS>
-__device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint4 (&q)[M], AOperand<M> &wa,
+__device__ __attribute__((always_inline)) inline void mx8_quad(int i, uint4 (&q)[M], int next, AOperand<M> &wa,
                                                                uint32_t (&sb)[NC][6], Mx8Stager<THREADS> &st,
                                                                const uint8_t *tile_frags,
                                                                mf::u32x4 (*lds)[kMx8StageBytes / 16], uint32_t t,
@@ -990,7 +1037,7 @@ __device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint
     mx8::i32x8 b[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const mf::u32x4 lo = buf[(c * 64 + lane) * 2], hi = buf[(c * 64 + lane) * 2 + 1];
+        const mf::u32x4 lo = buf[c * 128 + lane], hi = buf[c * 128 + 64 + lane];
         b[c] = mx8::i32x8{int32_t(lo[0]), int32_t(lo[1]), int32_t(lo[2]), int32_t(lo[3]),
                           int32_t(hi[0]), int32_t(hi[1]), int32_t(hi[2]), int32_t(hi[3])};
     }
@@ -999,14 +1046,25 @@ __device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint
     for (int m = 0; m < M; ++m) {
         sa[m] = wa.scale_byte(m);
     }
+    uint32_t scb[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        scb[c] = sb[c][0] & 0xffu;
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            acc[m][c] = mx8::mfma(q[m], b[c], sa[m], scb[c], acc[m][c]);
+        }
+        // tile m's codes are consumed: request quad `next` into the same registers
+        __builtin_amdgcn_sched_barrier(0);
+        q[m] = wa.load_one(next, lane, m);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     wa.next_quad();
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const uint32_t scb = sb[c][0] & 0xffu;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            acc[m][c] = mx8::mfma(q[m], b[c], sa[m], scb, acc[m][c]);
-        }
 #pragma unroll
         for (int j = 0; j < 5; ++j) {
             sb[c][j] = (sb[c][j] >> 8) | (sb[c][j + 1] << 24);
@@ -1017,13 +1075,14 @@ __device__ __attribute__((always_inline)) inline void mx8_quad(int i, const uint
         st.store(lds[(stage + 1) % 2], t);
         __syncthreads();
         st.load(tile_frags, stage + 2, t);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // The scaled main loop of one wave: M 16-row A tiles (AOperand), NC column tiles, the
 // B fragments staged in LDS by every wave of the workgroup.  acc[m][c] += A_m B_c for
-// quads 0..22; weight codes are requested one quad ahead (two code buffers), which
-// with two workgroups per CU measured faster than two or three quads ahead at one.
+// quads 0..22; two code buffers, each refilled tile by tile two quads ahead while the
+// other quad is multiplied (a third buffer would cost the second wave per SIMD).
 // Pairs of quads keep the buffer and stage-end positions static.
 template <int M, int NC, int THREADS>
 __device__ __attribute__((always_inline)) inline void mx8_main_loop(AOperand<M> &wa, const uint8_t *tile_frags,
@@ -1049,17 +1108,17 @@ __device__ __attribute__((always_inline)) inline void mx8_main_loop(AOperand<M> 
     st.load(tile_frags, 0, t);
     uint4 q[2][M];
     wa.load(0, lane, q[0]);
+    wa.load(1, lane, q[1]);
     st.store(lds[0], t);
     __syncthreads();
     st.load(tile_frags, 1, t);
     for (int i = 0; i < full; i += 2) {
-        wa.load(i + 1, lane, q[1]);
-        mx8_quad<M, NC, THREADS>(i, q[0], wa, sb, st, tile_frags, lds, t, lane, acc, false);
-        wa.load(min(i + 2, mf::quads - 1), lane, q[0]);
-        mx8_quad<M, NC, THREADS>(i + 1, q[1], wa, sb, st, tile_frags, lds, t, lane, acc, true);
+        mx8_quad<M, NC, THREADS>(i, q[0], i + 2, wa, sb, st, tile_frags, lds, t, lane, acc, false);
+        mx8_quad<M, NC, THREADS>(i + 1, q[1], min(i + 3, mf::quads - 1), wa, sb, st, tile_frags, lds, t, lane, acc,
+                                 true);
     }
     static_assert(mf::quads - full == 1, "one quad after the pairs");
-    mx8_quad<M, NC, THREADS>(full, q[0], wa, sb, st, tile_frags, lds, t, lane, acc, false);
+    mx8_quad<M, NC, THREADS>(full, q[0], full, wa, sb, st, tile_frags, lds, t, lane, acc, false);
 }
 
 // Gate/up on the scaled path, the workgroup layout of gateup_kernel (4 waves x 32 rows:
@@ -1068,13 +1127,10 @@ __device__ __attribute__((always_inline)) inline void mx8_main_loop(AOperand<M> 
 // rows 4g..4g+3 and 16+4g..16+4g+3, so the block's maximum takes two lane exchanges,
 // and each lane writes 8 contiguous fp8 bytes of the down GEMM's B fragment.
 template <int NC>
-__global__ __launch_bounds__(kGuWaves * 64) void mx8_gateup_kernel(GateUpArgs a) {
+__device__ __attribute__((always_inline)) inline void mx8_gateup_tile(const GateUpArgs &a, uint32_t tile,
+                                                                      uint32_t row_group,
+                                                                      mf::u32x4 (*lds)[kMx8StageBytes / 16]) {
     constexpr int kThreads = kGuWaves * 64;
-    __shared__ mf::u32x4 lds[2][kMx8StageBytes / 16];
-    uint32_t tile, row_group;
-    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
-        return;
-    }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
     const uint32_t row0 = row_group * kGuRows + wave * 32;
@@ -1174,16 +1230,27 @@ __global__ __launch_bounds__(kGuWaves * 64) void mx8_gateup_kernel(GateUpArgs a)
     }
 }
 
+__global__ __launch_bounds__(kGuWaves * 64) void mx8_gateup_kernel(GateUpArgs a) {
+    __shared__ mf::u32x4 lds[2][kMx8StageBytes / 16];
+    uint32_t tile, row_group;
+    bool narrow;
+    if (!tile_of_workgroup(a.plan.header, tile, row_group, narrow)) {
+        return;
+    }
+    if (narrow) {
+        mx8_gateup_tile<kNarrowCols>(a, tile, row_group, lds);
+    } else {
+        mx8_gateup_tile<mf::col_tiles>(a, tile, row_group, lds);
+    }
+}
+
 // Down projection and the selected-token matmul on the scaled path: matmul_kernel's
 // workgroup layout (4 waves x 48 rows) and epilogue; B from frags (gather or gate/up).
 template <bool SCATTER, int NC>
-__global__ __launch_bounds__(kMmWaves * 64) void mx8_matmul_kernel(MatmulArgs a) {
+__device__ __attribute__((always_inline)) inline void mx8_matmul_tile(const MatmulArgs &a, uint32_t tile,
+                                                                      uint32_t row_group,
+                                                                      mf::u32x4 (*lds)[kMx8StageBytes / 16]) {
     constexpr int kThreads = kMmWaves * 64;
-    __shared__ mf::u32x4 lds[2][kMx8StageBytes / 16];
-    uint32_t tile, row_group;
-    if (!tile_of_workgroup<NC>(a.plan.header, tile, row_group)) {
-        return;
-    }
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
     const uint32_t expert = a.plan.tile_expert[tile];
     const uint32_t row0 = row_group * kMmRows + wave * (kMmTiles * 16);
@@ -1243,6 +1310,21 @@ __global__ __launch_bounds__(kMmWaves * 64) void mx8_matmul_kernel(MatmulArgs a)
             *reinterpret_cast<float4 *>(dst + 16 * m) = make_float4(acc[m][c][0], acc[m][c][1], acc[m][c][2],
                                                                     acc[m][c][3]);
         }
+    }
+}
+
+template <bool SCATTER>
+__global__ __launch_bounds__(kMmWaves * 64) void mx8_matmul_kernel(MatmulArgs a) {
+    __shared__ mf::u32x4 lds[2][kMx8StageBytes / 16];
+    uint32_t tile, row_group;
+    bool narrow;
+    if (!tile_of_workgroup(a.plan.header, tile, row_group, narrow)) {
+        return;
+    }
+    if (narrow) {
+        mx8_matmul_tile<SCATTER, kNarrowCols>(a, tile, row_group, lds);
+    } else {
+        mx8_matmul_tile<SCATTER, mf::col_tiles>(a, tile, row_group, lds);
     }
 }
 
@@ -1410,7 +1492,7 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     m.plan = plan;
     m.out = out_dev;
     m.out_rows = x_rows;
-    matmul_kernel<3, true, mf::col_tiles><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
+    matmul_kernel<3, true><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
     TTL_LAUNCHED("matmul_kernel");
     return TTL_OK;
 }
@@ -1465,7 +1547,7 @@ int ttl_matmul_mxfp4_selected_mxfp8(ttl_ctx *ctx, const ttl_mxfp4 *w, const floa
     m.plan = plan;
     m.out = out_dev;
     m.out_rows = x_rows;
-    mx8_matmul_kernel<true, mf::col_tiles><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
+    mx8_matmul_kernel<true><<<dim3(w->rows / kMmRows, tiles), kMmWaves * 64, 0, ctx->stream>>>(m);
     TTL_LAUNCHED("mx8_matmul_kernel");
     return TTL_OK;
 }
@@ -1574,20 +1656,16 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     g.rows = L.expert_hidden;
     g.tiles_per_expert = L.gate->tiles;
     g.plan = plan;
-    // the wide tiles, then the narrow ones (at most one per expert)
-    const uint32_t gu_groups = (L.expert_hidden + kGuRows - 1) / kGuRows;
-    const dim3 gu_wide(gu_groups, lay.tmax), gu_narrow(gu_groups, min(lay.tmax, L.experts));
+    // one launch per GEMM over the wide tiles and the narrow ones (at most one per expert)
+    const dim3 gu_grid((L.expert_hidden + kGuRows - 1) / kGuRows, lay.tmax);
     if ((stages & TTL_PREFILL_GATEUP) && scaled) {
-        mx8_gateup_kernel<mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
-        mx8_gateup_kernel<kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
+        mx8_gateup_kernel<<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         TTL_LAUNCHED("mx8_gateup_kernel");
     } else if (stages & TTL_PREFILL_GATEUP) {
         if (bf16) {
-            gateup_kernel<1, mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
-            gateup_kernel<1, kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         } else {
-            gateup_kernel<3, mf::col_tiles><<<gu_wide, kGuWaves * 64, 0, ctx->stream>>>(g);
-            gateup_kernel<3, kNarrowCols><<<gu_narrow, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<3><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         }
         TTL_LAUNCHED("gateup_kernel");
     }
@@ -1603,16 +1681,10 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     m.out = plan.down;
     m.out_rows = 0;
     if ((stages & TTL_PREFILL_DOWN) && scaled) {
-        mx8_matmul_kernel<false, mf::col_tiles>
-            <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
-        mx8_matmul_kernel<false, kNarrowCols>
-            <<<dim3(L.hidden / kMmRows, min(lay.tmax, L.experts)), kMmWaves * 64, 0, ctx->stream>>>(m);
+        mx8_matmul_kernel<false><<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
         TTL_LAUNCHED("mx8_matmul_kernel");
     } else if (stages & TTL_PREFILL_DOWN) {
-        matmul_kernel<kHiddenPlanes, false, mf::col_tiles>
-            <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
-        matmul_kernel<kHiddenPlanes, false, kNarrowCols>
-            <<<dim3(L.hidden / kMmRows, min(lay.tmax, L.experts)), kMmWaves * 64, 0, ctx->stream>>>(m);
+        matmul_kernel<kHiddenPlanes, false><<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
         TTL_LAUNCHED("matmul_kernel");
     }
     if (stages & TTL_PREFILL_COMBINE) {
