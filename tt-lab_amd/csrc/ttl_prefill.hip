@@ -150,10 +150,27 @@ Plan plan_at(void *workspace, const Layout &L) {
     return p;
 }
 
+// Exclusive prefix sum over the 64 lanes of a wave (all lanes active).
+__device__ inline uint32_t wave_exclusive_sum(uint32_t v, uint32_t lane) {
+    uint32_t x = v;
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d);
+        x += lane >= d ? y : 0u;
+    }
+    return x - v;
+}
+
 // Buckets the (token, rank) pairs by expert in the reference's order and cuts the
 // buckets into 64-slot tiles.  One workgroup of 1024 threads; pairs are taken in
 // rounds of 1024 in pair order, and a pair's slot is its expert's base plus the
-// number of earlier pairs with the same expert.
+// number of earlier pairs with the same expert.  Each thread requests the indices and
+// weights of its first kPlanHeld rounds at once, at the start (a 512-token batch of
+// top-4 is two rounds), so the kernel waits for global memory once instead of once
+// per pass; later rounds load theirs as they come.
+constexpr uint32_t kPlanHeld = 2;
+constexpr uint32_t kPlanPerLane = kMaxExperts / 64;  // experts per lane in the bucket scan
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__restrict__ indices,
                                                             const float *__restrict__ weights, uint32_t pairs,
                                                             uint32_t used, uint32_t experts, Plan plan) {
@@ -162,40 +179,83 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__res
     __shared__ uint32_t wave_count[kPlanThreads / 64][kMaxExperts];
     __shared__ uint32_t invalid;
     const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
+    const uint32_t rounds = (pairs + kPlanThreads - 1) / kPlanThreads;
+    // expert of pair j, -1 for an index out of range or past the pairs
+    auto expert_of = [&](int32_t e, uint32_t j) __attribute__((always_inline)) {
+        return j < pairs && e >= 0 && uint32_t(e) < experts ? e : -1;
+    };
+    int32_t held_e[kPlanHeld];
+    float held_w[kPlanHeld];
+#pragma unroll
+    for (uint32_t k = 0; k < kPlanHeld; ++k) {
+        // unconditional (clamped) requests; pairs == 0 never launches
+        const uint32_t j = min(t + k * kPlanThreads, pairs - 1);
+        held_e[k] = indices[j];
+        held_w[k] = weights[j];
+    }
     for (uint32_t e = t; e < kMaxExperts; e += kPlanThreads) {
         count[e] = 0;
-        running[e] = 0;
     }
     if (t == 0) {
         invalid = 0;
     }
     __syncthreads();
-    for (uint32_t j = t; j < pairs; j += kPlanThreads) {
-        const int32_t e = indices[j];
-        if (e >= 0 && uint32_t(e) < experts) {
+    auto count_pair = [&](int32_t raw, uint32_t j) __attribute__((always_inline)) {
+        const int32_t e = expert_of(raw, j);
+        if (e >= 0) {
             atomicAdd(&count[e], 1u);
-        } else {
+        } else if (j < pairs) {
             atomicAdd(&invalid, 1u);
         }
+    };
+    // the held rounds with constant indices (a run-time index would put them in scratch)
+#pragma unroll
+    for (uint32_t k = 0; k < kPlanHeld; ++k) {
+        count_pair(held_e[k], k * kPlanThreads + t);
+    }
+    for (uint32_t r = kPlanHeld; r < rounds; ++r) {
+        const uint32_t j = r * kPlanThreads + t;
+        count_pair(indices[min(j, pairs - 1)], j);
     }
     __syncthreads();
-    if (t == 0) {
+    if (wave == 0) {
         // wide tiles in expert order first, then the narrow ones (an expert's last tile
-        // when it holds at most kNarrowSlots slots), also in expert order
-        uint32_t slots = 0, wide = 0, narrow = 0;
-        for (uint32_t e = 0; e < experts; ++e) {
-            base[e] = slots;
-            slots += count[e];
-            const uint32_t tiles = (count[e] + mf::tile_slots - 1) / mf::tile_slots;
-            const bool last_narrow = tiles > 0 && count[e] - (tiles - 1) * mf::tile_slots <= kNarrowSlots;
-            running[e] = wide;  // first wide tile of expert e (reset below)
-            wide += tiles - (last_narrow ? 1 : 0);
-            narrow_of[e] = last_narrow ? narrow++ : ~0u;
+        // when it holds at most kNarrowSlots slots), also in expert order: lane l takes
+        // experts kPlanPerLane l .. + kPlanPerLane - 1, and one prefix sum per quantity
+        // places them after the lanes before
+        uint32_t c[kPlanPerLane], slots = 0, wide = 0, narrow = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < kPlanPerLane; ++k) {
+            const uint32_t e = lane * kPlanPerLane + k;
+            c[k] = e < experts ? count[e] : 0u;
+            const uint32_t tiles = (c[k] + mf::tile_slots - 1) / mf::tile_slots;
+            const bool last_narrow = tiles > 0 && c[k] - (tiles - 1) * mf::tile_slots <= kNarrowSlots;
+            slots += c[k];
+            wide += tiles - (last_narrow ? 1u : 0u);
+            narrow += last_narrow ? 1u : 0u;
         }
-        wide_total = wide;
-        plan.header->tiles = wide + narrow;
-        plan.header->wide = wide;
-        plan.header->invalid = invalid;
+        uint32_t s0 = wave_exclusive_sum(slots, lane), w0 = wave_exclusive_sum(wide, lane),
+                 n0 = wave_exclusive_sum(narrow, lane);
+#pragma unroll
+        for (uint32_t k = 0; k < kPlanPerLane; ++k) {
+            const uint32_t e = lane * kPlanPerLane + k;
+            const uint32_t tiles = (c[k] + mf::tile_slots - 1) / mf::tile_slots;
+            const bool last_narrow = tiles > 0 && c[k] - (tiles - 1) * mf::tile_slots <= kNarrowSlots;
+            if (e < experts) {
+                base[e] = s0;
+                running[e] = w0;  // first wide tile of expert e (reset below)
+                narrow_of[e] = last_narrow ? n0 : ~0u;
+            }
+            s0 += c[k];
+            w0 += tiles - (last_narrow ? 1u : 0u);
+            n0 += last_narrow ? 1u : 0u;
+        }
+        if (lane == 63) {
+            wide_total = w0;
+            plan.header->tiles = w0 + n0;
+            plan.header->wide = w0;
+            plan.header->invalid = invalid;
+        }
     }
     __syncthreads();
     for (uint32_t e = t; e < experts; e += kPlanThreads) {
@@ -212,14 +272,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__res
     for (uint32_t e = t; e < kMaxExperts; e += kPlanThreads) {
         running[e] = 0;
     }
-    for (uint32_t round = 0; round < pairs; round += kPlanThreads) {
+    // one round of 1024 pairs (uniform across the workgroup: its barriers are reached by all)
+    auto place_round = [&](uint32_t r, int32_t raw, float wj) __attribute__((always_inline)) {
         for (uint32_t e = t; e < (kPlanThreads / 64) * kMaxExperts; e += kPlanThreads) {
             (&wave_count[0][0])[e] = 0;
         }
         __syncthreads();
-        const uint32_t j = round + t;
-        const int32_t ej = j < pairs ? indices[j] : -1;
-        const bool valid = ej >= 0 && uint32_t(ej) < experts;
+        const uint32_t j = r * kPlanThreads + t;
+        const int32_t ej = expert_of(raw, j);
+        const bool valid = ej >= 0;
         // the lanes of this wave with the same expert: one ballot per bit of the expert
         // index (a lane matches where every bit agrees); rank = earlier lanes among them,
         // and the lowest of them records the wave's count for the expert
@@ -242,7 +303,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__res
                     slot += w < wave ? wave_count[w][ej] : 0u;
                 }
                 plan.slot_token[slot] = j / used;
-                plan.slot_weight[slot] = weights[j];
+                plan.slot_weight[slot] = wj;
                 plan.pair_slot[j] = int32_t(slot);
             } else {
                 plan.pair_slot[j] = -1;
@@ -257,6 +318,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t *__res
             running[e] += add;
         }
         __syncthreads();
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < kPlanHeld; ++k) {
+        if (k < rounds) {
+            place_round(k, held_e[k], held_w[k]);
+        }
+    }
+    for (uint32_t r = kPlanHeld; r < rounds; ++r) {
+        const uint32_t jc = min(r * kPlanThreads + t, pairs - 1);
+        place_round(r, indices[jc], weights[jc]);
     }
 }
 
@@ -284,68 +355,83 @@ __global__ void plan_selected_kernel(const int32_t *__restrict__ tokens, uint32_
 
 // ---- activation fragments ------------------------------------------------------------
 
-// One thread per (tile, step, column tile, lane): the 8 activations of that B
-// fragment lane, as P bf16 planes.  Slots past the tile's count, tokens out of
-// range (NaN), and blocks 90/91 (zero) are filled so that every fragment is defined.
+// One workgroup per (quad, token tile); thread (column tile, lane) takes slot
+// 16 ct + lane % 16 and K-block 4 quad + lane / 16, i.e. the 8 activations of that B
+// fragment lane in each of the quad's four K steps: one 128-byte run of the row (f32;
+// 64 bytes for bf16), converted to P bf16 planes per step.  The tile's metadata and
+// the early exit are requested together, then the slot's token, then its row
+// (unconditional requests at clamped addresses, masked after).  Slots past the tile's
+// count, and blocks 90/91, are zero; a token out of range is NaN.
 template <bool BF16_IN, int P>
 __global__ __launch_bounds__(mf::col_tiles * 64) void gather_kernel(const void *__restrict__ x, uint32_t x_stride,
-                                                     uint32_t x_rows, Plan plan) {
-    const uint32_t tile = blockIdx.y;
-    if (tile >= plan.header->tiles) {
+                                                                    uint32_t x_rows, Plan plan) {
+    const uint32_t tile = blockIdx.y, quad = blockIdx.x;
+    // (tile < the layout's tmax: its metadata words exist, stale past the plan's tiles)
+    const uint32_t tiles = plan.header->tiles, cnt = plan.tile_count[tile], first = plan.tile_first[tile];
+    if (tile >= tiles) {
         return;
     }
-    const uint32_t step = blockIdx.x;  // 0..91
     const uint32_t ct = threadIdx.x / 64, lane = threadIdx.x % 64;
     const uint32_t n = ct * 16 + lane % 16;
-    const uint32_t block = (step / 4) * 4 + lane / 16, s = step % 4;
-    float v[8];
-    const uint32_t cnt = plan.tile_count[tile];
-    const bool live = n < cnt && block < uint32_t(mx::blocks);
-    uint32_t token = 0;
-    bool token_ok = false;
-    if (live) {
-        token = plan.slot_token[plan.tile_first[tile] + n];
-        token_ok = token < x_rows;
-    }
-    if (live && token_ok) {
-        const size_t base = size_t(token) * x_stride + size_t(block) * 32 + 4 * s;
-        if (BF16_IN) {
-            const uint2 lo = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + base);
-            const uint2 hi = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + base + 16);
-            v[0] = __uint_as_float(lo.x << 16);
-            v[1] = __uint_as_float(hi.x << 16);
-            v[2] = __uint_as_float(lo.x & 0xffff0000u);
-            v[3] = __uint_as_float(hi.x & 0xffff0000u);
-            v[4] = __uint_as_float(lo.y << 16);
-            v[5] = __uint_as_float(hi.y << 16);
-            v[6] = __uint_as_float(lo.y & 0xffff0000u);
-            v[7] = __uint_as_float(hi.y & 0xffff0000u);
-        } else {
-            const float4 lo = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
-            const float4 hi = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base + 16);
-            v[0] = lo.x;
-            v[1] = hi.x;
-            v[2] = lo.y;
-            v[3] = hi.y;
-            v[4] = lo.z;
-            v[5] = hi.z;
-            v[6] = lo.w;
-            v[7] = hi.w;
+    const uint32_t block = quad * 4 + lane / 16;
+    const bool block_ok = block < uint32_t(mx::blocks);
+    const uint32_t token = plan.slot_token[first + min(n, cnt - 1)];
+    const bool live = n < cnt && block_ok;
+    const bool token_ok = token < x_rows;
+    const size_t base = size_t(token_ok ? token : 0u) * x_stride + size_t(block_ok ? block : 0u) * 32;
+    // the block's 32 activations as f32
+    float e[32];
+    if (BF16_IN) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + base);
+        uint4 w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w[k] = src[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t ww[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                e[8 * k + 2 * h] = __uint_as_float(ww[h] << 16);
+                e[8 * k + 2 * h + 1] = __uint_as_float(ww[h] & 0xffff0000u);
+            }
         }
     } else {
-        const float fill = (live && !token_ok) ? __builtin_nanf("") : 0.0f;
+        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+        float4 w[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[j] = fill;
+        for (int k = 0; k < 8; ++k) {
+            w[k] = src[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            e[4 * k] = w[k].x;
+            e[4 * k + 1] = w[k].y;
+            e[4 * k + 2] = w[k].z;
+            e[4 * k + 3] = w[k].w;
         }
     }
-    uint4 out[P];
-    mf::split_planes<P>(v, out);
-    uint8_t *dst = plan.xb + size_t(tile) * P * mf::plane_bytes +
-                   (size_t(step) * mf::col_tiles + ct) * mf::frag_bytes + lane * 16;
+    const float fill = (live && !token_ok) ? __builtin_nanf("") : 0.0f;
+    const bool keep = live && token_ok;
+    uint8_t *dst = plan.xb + size_t(tile) * P * mf::plane_bytes + size_t(ct) * mf::frag_bytes + lane * 16;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        *reinterpret_cast<uint4 *>(dst + size_t(p) * mf::plane_bytes) = out[p];
+    for (int s = 0; s < 4; ++s) {
+        // step s of the quad: elements 4s..4s+3 and 16+4s..16+4s+3, interleaved
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = keep ? e[4 * s + k] : fill;
+            v[2 * k + 1] = keep ? e[16 + 4 * s + k] : fill;
+        }
+        uint4 out[P];
+        mf::split_planes<P>(v, out);
+        const size_t step = size_t(quad) * 4 + size_t(s);
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            *reinterpret_cast<uint4 *>(dst + size_t(p) * mf::plane_bytes + step * mf::col_tiles * mf::frag_bytes) =
+                out[p];
+        }
     }
 }
 
@@ -895,58 +981,55 @@ __device__ inline uint32_t mx8_code(float v, const Mx8Block &b) {
 
 // One workgroup per (quad, column tile, token tile); 16 threads per slot, 4 per
 // 32-element block, each thread 8 consecutive elements (one 16-byte bf16 load, the
-// slot's 4 blocks of the quad contiguous across its 16 threads).  The block's largest
-// magnitude takes two lane exchanges.  Element e of K-block g belongs to B lane group
-// 2 (g & 1) + (e % 16) / 8, byte 16 (g >> 1) + 2 (e % 8) + e / 16, so the threads
-// holding elements 8r..8r+7 and 8r+16..8r+23 (r = 0, 1) interleave their codes and the
-// first writes 16 contiguous bytes; the block's first thread writes its E8M0 byte,
-// read by the MFMA from lane (n, g).  Slots past the tile's count and blocks 90/91 are
-// zero; a token out of range is NaN.
+// slot's 4 blocks of the quad contiguous across its 16 threads).  The tile's metadata
+// and the early exit are requested together, then the slot's token, then its row
+// (unconditional requests at clamped addresses, masked after), so a thread waits for
+// three dependent loads in all.  (One workgroup for the four column tiles in turn was
+// slower: 10.2 against 8.5 us per launch.)  The block's largest magnitude takes two
+// lane exchanges.  Element e of K-block g belongs to B lane group 2 (g & 1) +
+// (e % 16) / 8, byte 16 (g >> 1) + 2 (e % 8) + e / 16, so the threads holding elements
+// 8r..8r+7 and 8r+16..8r+23 (r = 0, 1) interleave their codes and the first writes 16
+// contiguous bytes; the block's first thread writes its E8M0 byte, read by the MFMA
+// from lane (n, g).  Slots past the tile's count and blocks 90/91 are zero; a token out
+// of range is NaN.
 template <bool BF16_IN>
 __global__ __launch_bounds__(256) void gather_mx8_kernel(const void *__restrict__ x, uint32_t x_stride,
                                                           uint32_t x_rows, Plan plan) {
     const uint32_t tile = blockIdx.y;
-    if (tile >= plan.header->tiles) {
+    // (tile < the layout's tmax: its metadata words exist, stale past the plan's tiles)
+    const uint32_t tiles = plan.header->tiles, count = plan.tile_count[tile], first = plan.tile_first[tile];
+    if (tile >= tiles) {
         return;
     }
     const uint32_t quad = blockIdx.x / mf::col_tiles, ct = blockIdx.x % mf::col_tiles;
     const uint32_t t = threadIdx.x, n16 = t / 16, g = (t % 16) / 4, r = t % 4;
     const uint32_t n = ct * 16 + n16, block = 4 * quad + g;
-    const bool live = n < plan.tile_count[tile];
+    const bool block_ok = block < uint32_t(mx::blocks);
+    const bool live = n < count && block_ok;
+    const uint32_t token = plan.slot_token[first + min(n, count - 1)];
+    const size_t base = size_t(token < x_rows ? token : 0u) * x_stride + size_t(block_ok ? block : 0u) * 32 + 8 * r;
     float v[8];
-    bool in_range = true;
-    if (live && block < uint32_t(mx::blocks)) {
-        const uint32_t token = plan.slot_token[plan.tile_first[tile] + n];
-        in_range = token < x_rows;
-        const size_t base = size_t(in_range ? token : 0u) * x_stride + size_t(block) * 32 + 8 * r;
-        if (BF16_IN) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + base);
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    if (BF16_IN) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + base);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                v[2 * k] = __uint_as_float(ww[k] << 16);
-                v[2 * k + 1] = __uint_as_float(ww[k] & 0xffff0000u);
-            }
-        } else {
-            const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
-            const float4 w0 = src[0], w1 = src[1];
-            const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                v[k] = ww[k];
-            }
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = __uint_as_float(ww[k] << 16);
+            v[2 * k + 1] = __uint_as_float(ww[k] & 0xffff0000u);
         }
     } else {
+        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+        const float4 w0 = src[0], w1 = src[1];
+        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            v[k] = 0.0f;
+            v[k] = ww[k];
         }
     }
-    if (!in_range) {
+    const bool nan_row = live && token >= x_rows;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            v[k] = __builtin_nanf("");
-        }
+    for (int k = 0; k < 8; ++k) {
+        v[k] = nan_row ? __builtin_nanf("") : (live ? v[k] : 0.0f);
     }
     float m = 0.0f;
     int finite = 1;
@@ -1480,7 +1563,7 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     plan_selected_kernel<<<ttl::blocks_for(count > tiles ? count : tiles, 256), 256, 0, ctx->stream>>>(
         tokens_dev, count, expert, plan);
     TTL_LAUNCHED("plan_selected_kernel");
-    gather_kernel<false, 3><<<dim3(mf::steps, tiles), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, x_stride, x_rows, plan);
+    gather_kernel<false, 3><<<dim3(mf::quads, tiles), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, x_stride, x_rows, plan);
     TTL_LAUNCHED("gather_kernel");
     MatmulArgs m;
     m.codes = w->codes;
@@ -1636,9 +1719,9 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         TTL_LAUNCHED("gather_mx8_kernel");
     } else if (stages & TTL_PREFILL_GATHER) {
         if (bf16) {
-            gather_kernel<true, 1><<<dim3(mf::steps, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<true, 1><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         } else {
-            gather_kernel<false, 3><<<dim3(mf::steps, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<false, 3><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         }
         TTL_LAUNCHED("gather_kernel");
     }
