@@ -29,11 +29,12 @@ __global__ void copy16_kernel(const uint4 *__restrict__ src, uint4 *__restrict__
 
 // Plain streaming read, the bandwidth reference for the matvec kernels: a grid of at
 // most kReadBlocks workgroups strides over the words, each thread keeping four 16-byte
-// loads in flight per pass.  Measured at 35.4 MB per launch (24 buffers in a graph):
-// 6.96 us with 512 or 1024 workgroups, against 7.33 us for one pass of 4 loads per
-// thread over 2160 workgroups and 7.4-8.5 us for 8 or 16 loads per thread or 256
-// workgroups.  The XOR of the words is stored only when it equals a fixed constant, so
-// the loads stay live and nothing is written in practice.
+// loads in flight per pass, marked non-temporal like the weight loads of the kernels it
+// is the reference for (ttl::load_stream).  Measured at 35.4 MB per launch (24 buffers
+// in a graph, ordinary loads): 6.96 us with 512 or 1024 workgroups, against 7.33 us for
+// one pass of 4 loads per thread over 2160 workgroups and 7.4-8.5 us for 8 or 16 loads
+// per thread or 256 workgroups.  The XOR of the words is stored only when it equals a
+// fixed constant, so the loads stay live and nothing is written in practice.
 constexpr int kReadThreads = 256, kReadPerThread = 4, kReadBlocks = 1024;
 __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4 *__restrict__ src, size_t n,
                                                                    uint32_t *__restrict__ sink) {
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4 *
 #pragma unroll
         for (int k = 0; k < kReadPerThread; ++k) {
             const size_t i = base + size_t(k) * kReadThreads;
-            v[k] = src[i < n ? i : n - 1];
+            v[k] = ttl::load_stream(src + (i < n ? i : n - 1));
         }
 #pragma unroll
         for (int k = 0; k < kReadPerThread; ++k) {

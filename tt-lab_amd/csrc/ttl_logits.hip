@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void logits_kernel(const uint16_t *__rest
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
             const uint32_t c = j + 16 * i;
-            q[i] = src[c < uint32_t(kChunks) ? c : uint32_t(kChunks) - 1];
+            q[i] = ttl::load_stream(src + (c < uint32_t(kChunks) ? c : uint32_t(kChunks) - 1));
             __builtin_amdgcn_sched_barrier(0);
         }
         float acc = 0.0f;

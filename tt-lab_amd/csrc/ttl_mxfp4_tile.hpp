@@ -95,7 +95,7 @@ __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *_
     // last iteration re-read block 89 (zero x there).
 #pragma unroll
     for (int i = 0; i < mx::iters; ++i) {
-        regs.q[i] = tc[size_t(min(uint32_t(4 * i) + kl, uint32_t(mx::blocks - 1))) * mx::tile_rows];
+        regs.q[i] = ttl::load_stream(tc + size_t(min(uint32_t(4 * i) + kl, uint32_t(mx::blocks - 1))) * mx::tile_rows);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -160,7 +160,7 @@ __device__ __attribute__((always_inline)) inline void split_load(const uint8_t *
         // blocks past the row end re-read block 89 (same address as another lane of
         // the load: no extra memory traffic); their x is zero
         const uint32_t kb = min(uint32_t(4 * (w * P + j)) + kl, uint32_t(mx::blocks - 1));
-        regs.q[j] = tc[size_t(kb) * mx::tile_rows];
+        regs.q[j] = ttl::load_stream(tc + size_t(kb) * mx::tile_rows);
         __builtin_amdgcn_sched_barrier(0);
     }
 }

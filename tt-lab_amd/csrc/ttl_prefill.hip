@@ -509,13 +509,13 @@ struct AOperand {
         const uint32_t block = min(uint32_t(4 * i) + lane / mx::tile_rows, uint32_t(mx::blocks - 1));
 #pragma unroll
         for (int a = 0; a < NT; ++a) {
-            q[a] = codes[a][size_t(block) * mx::tile_rows];
+            q[a] = ttl::load_stream(codes[a] + size_t(block) * mx::tile_rows);
         }
     }
     // The same for tile a alone.
     __device__ inline uint4 load_one(int i, uint32_t lane, int a) const {
         const uint32_t block = min(uint32_t(4 * i) + lane / mx::tile_rows, uint32_t(mx::blocks - 1));
-        return codes[a][size_t(block) * mx::tile_rows];
+        return ttl::load_stream(codes[a] + size_t(block) * mx::tile_rows);
     }
     // Scale of tile a for the current quad; next_quad() moves every record on by
     // one byte, so the indices stay static.
