@@ -56,7 +56,7 @@ struct ttl_q8 {
     uint32_t rows = 0;
     uint32_t cols = 0;
     uint32_t tiles = 0;          // rows / 16
-    uint8_t *codes = nullptr;    // [tiles][blocks][16 rows][32 B]
+    uint8_t *codes = nullptr;    // [tiles][blocks][2 halves][16 rows][16 B]
     uint16_t *scales = nullptr;  // [tiles][4 lanes_k][16 rows][scale_pad] fp16
     uint16_t *row_scales = nullptr;  // [rows][blocks] fp16, for the batched matmul
     size_t code_bytes = 0;
@@ -86,8 +86,9 @@ inline unsigned blocks_for(size_t n, unsigned threads) {
 // A 16-byte load marked non-temporal (the instruction's nt bit), for weights that are
 // streamed once per pass: a plain read of 1.16 GB ran at 7.0 TB/s this way against
 // 6.2 TB/s with ordinary loads (gfx950, 1024-4096 workgroups, 4 or 8 loads in flight).
-// Only for loads whose wave covers whole 128-byte lines: the Q8_0 tiles, read as two
-// 16-byte halves of each 32-byte lane record, got slower with it (QKV 8.7 -> 9.4 us).
+// Only for loads whose wave covers whole 128-byte lines: Q8_0 tiles read as the two
+// 16-byte halves of each 32-byte lane record got slower with it (QKV 8.7 -> 9.4 us),
+// hence their layout of halves (q8::code_offset).
 __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));

@@ -34,9 +34,8 @@ __global__ void q8_repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows
         w[i] = uint32_t(src[2 + 4 * i]) | (uint32_t(src[3 + 4 * i]) << 8) | (uint32_t(src[4 + 4 * i]) << 16) |
                (uint32_t(src[5 + 4 * i]) << 24);
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(codes + q8::code_offset(tile, block, r, int(cols)));
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    *reinterpret_cast<uint4 *>(codes + q8::code_offset(tile, block, 0, r, int(cols))) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4 *>(codes + q8::code_offset(tile, block, 1, r, int(cols))) = make_uint4(w[4], w[5], w[6], w[7]);
     const uint16_t d = uint16_t(src[0] | (src[1] << 8));
     scales[q8::scale_index(tile, block, r, int(cols))] = d;
     row_scales[size_t(row) * q8::row_scale_stride(int(cols)) + block] = d;
@@ -52,13 +51,15 @@ __global__ void q8_unpack_kernel(const uint8_t *__restrict__ codes, const uint16
     const uint32_t row = uint32_t(gid / blocks), block = uint32_t(gid % blocks);
     const size_t tile = row / q8::tile_rows;
     const uint32_t r = row % q8::tile_rows;
-    const uint8_t *src = codes + q8::code_offset(tile, block, r, int(cols));
     const uint16_t s = scales[q8::scale_index(tile, block, r, int(cols))];
     uint8_t *dst = gguf + gid * 34;
     dst[0] = uint8_t(s);
     dst[1] = uint8_t(s >> 8);
-    for (int i = 0; i < 32; ++i) {
-        dst[2 + i] = src[i];
+    for (uint32_t h = 0; h < 2; ++h) {
+        const uint8_t *src = codes + q8::code_offset(tile, block, h, r, int(cols));
+        for (int i = 0; i < 16; ++i) {
+            dst[2 + 16 * h + i] = src[i];
+        }
     }
 }
 

@@ -102,7 +102,7 @@ __device__ inline bf16x8 int8_bf16(uint2 c) {
 }
 
 struct GemmArgs {
-    const uint8_t *codes;        // repacked [tiles][blocks][16 rows][32 B]
+    const uint8_t *codes;        // repacked [tiles][blocks][2 halves][16 rows][16 B]
     const uint16_t *row_scales;  // [rows][steps] fp16 (zero past the blocks, q8::row_scale_stride)
     const float *bias;           // [rows] or null
     const float *residual;       // [tokens][rows] or null
@@ -137,7 +137,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
         ok[j] = rt < a.row_tiles;
         const uint32_t rts = ok[j] ? rt : 0;
         row[j] = rts * 16 + n;
-        cp[j] = a.codes + (size_t(rts) * S::blocks * 16 + n) * 32 + 8 * g;
+        // bytes 8g..8g+7 of row n's block: half g / 2 (q8::code_offset), 8 (g % 2) into it
+        cp[j] = a.codes + size_t(rts) * S::blocks * 512 + (g / 2) * 256 + n * 16 + 8 * (g % 2);
         sp[j] = a.row_scales + size_t(row[j]) * S::steps;
     }
 
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint32_t b = min(uint32_t(4 * q + k), uint32_t(S::blocks - 1));
-                c[j][k] = *reinterpret_cast<const uint2 *>(cp[j] + size_t(b) * 16 * 32);
+                c[j][k] = *reinterpret_cast<const uint2 *>(cp[j] + size_t(b) * 512);
             }
             s[j] = *reinterpret_cast<const uint2 *>(sp[j] + 4 * q);
         }

@@ -1,9 +1,11 @@
 // Device building blocks of the Q8_0 matvec kernels.
 //
 // Layout (repacked on upload from GGUF Q8_0 rows of 34-byte blocks, fp16 scale
-// then 32 int8, tensor.cpp:94-114): a tile is 16 rows; code chunks are 32 bytes
-// ordered [tile][block][row]; scales are fp16 ordered so each lane's scales are
-// contiguous, [tile][block%4][row][block/4 padded].
+// then 32 int8, tensor.cpp:94-114): a tile is 16 rows; a block's 32 codes are two
+// 16-byte halves, ordered [tile][block][half][row], so each of a lane's two loads
+// covers whole 256-byte runs across the wave (16 rows x 16 bytes per block, four
+// blocks) and can be marked non-temporal; scales are fp16 ordered so each lane's
+// scales are contiguous, [tile][block%4][row][block/4 padded].
 //
 // Work split: one workgroup of 4 waves owns one tile.  Lane l handles row l%16
 // and blocks 4*i + l/16; wave w handles iterations i in [w*P, w*P + P), so the
@@ -56,8 +58,9 @@ __host__ __device__ inline size_t tail_pad_bytes(int cols) {
 __host__ __device__ inline int row_scale_stride(int cols) {
     return (cols / 32 + 3) / 4 * 4;
 }
-__host__ __device__ inline size_t code_offset(size_t tile, uint32_t block, uint32_t row, int cols) {
-    return ((tile * blocks_of(cols) + block) * tile_rows + row) * 32;
+// Byte offset of codes 16 h .. 16 h + 15 of (tile, block, row).
+__host__ __device__ inline size_t code_offset(size_t tile, uint32_t block, uint32_t half, uint32_t row, int cols) {
+    return ((tile * blocks_of(cols) + block) * 2 + half) * (tile_rows * 16) + row * 16;
 }
 __host__ __device__ inline size_t scale_index(size_t tile, uint32_t block, uint32_t row, int cols) {
     const int pad = scale_pad_of(cols);
@@ -103,9 +106,9 @@ __device__ __attribute__((always_inline)) inline void tile_load(const uint8_t *_
         // load, so no extra memory traffic); their scale is zero
         const int i = int(wave) * PW + j;
         const uint32_t kb = min(uint32_t(4 * i) + kl, uint32_t(S::blocks - 1));
-        const uint4 *p = reinterpret_cast<const uint4 *>(codes + ((tile * S::blocks + kb) * tile_rows + r) * 32);
-        regs.c[j][0] = p[0];
-        regs.c[j][1] = p[1];
+        const uint4 *p = reinterpret_cast<const uint4 *>(codes + ((tile * S::blocks + kb) * 2 * tile_rows + r) * 16);
+        regs.c[j][0] = ttl::load_stream(p);
+        regs.c[j][1] = ttl::load_stream(p + tile_rows);
         __builtin_amdgcn_sched_barrier(0);  // keep the issue order (see the compute)
     }
 }
