@@ -88,7 +88,9 @@ inline unsigned blocks_for(size_t n, unsigned threads) {
 // 6.2 TB/s with ordinary loads (gfx950, 1024-4096 workgroups, 4 or 8 loads in flight).
 // Only for loads whose wave covers whole 128-byte lines: Q8_0 tiles read as the two
 // 16-byte halves of each 32-byte lane record got slower with it (QKV 8.7 -> 9.4 us),
-// hence their layout of halves (q8::code_offset).
+// hence their layout of halves (q8::code_offset).  Not for data re-read soon: the
+// sliding-window attention's cached K/V rows (re-read every token) went from 5.7 to
+// 7.7 us per launch with it.
 __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
