@@ -178,6 +178,44 @@ def test_attention_with_sinks_at_long_context(dev, layer_index, position):
     check_attention(dev, layer_index, position, 4104)
 
 
+# A position at or past the capacity is the kernels' no-op: the host refuses it before a
+# step, and a replayed graph whose position ran past the caches must write nothing (the
+# kernels still issue their loads, clamped inside the buffers, before they read it).
+@pytest.mark.parametrize("layer_index", [0, 1])
+@pytest.mark.parametrize("past", [0, 5])
+def test_position_past_capacity_writes_nothing(dev, layer_index, past):
+    capacity = 200
+    position = capacity + past
+    q = O.synth_normal(51, 0, 4096, sigma=2.0)
+    k = O.synth_normal(52, 0, capacity * 512, sigma=2.0)
+    v = O.synth_normal(53, 0, capacity * 512)
+    sinks = O.synth_normal(54, 0, 64, sigma=2.0)
+    qb, kb, vb, sb = dev.upload(q), dev.upload(k), dev.upload(v), dev.upload(sinks)
+    pb = dev.upload(np.array([position], np.int32))
+    ws = dev.alloc(dev.lib.ttl_attention_workspace_bytes(capacity))
+    out = dev.alloc(4096 * 4)
+    dev.fill(out, 0x7f)
+    dev.attention_decode(qb, kb, vb, sb, pb, capacity, layer_index, ws, out)
+    assert (out.download(np.uint8) == 0x7f).all()
+    # Q/K/V: no query, no cache row
+    qw = O.synth_q8_0(55, 3, 4096 * 90)
+    kw = O.synth_q8_0(55, 4, 512 * 90)
+    vw = O.synth_q8_0(55, 5, 512 * 90)
+    bias = O.synth_normal(55, 6, 5120, sigma=0.05)
+    x = O.synth_normal(56, 0, N, sigma=20.0)
+    rows = np.empty(5120, np.int32)
+    ttlab_amd.load_library().ttl_qkv_row_source(rows.ctypes.data)
+    qkv = dev.q8_upload(np.concatenate([qw, kw, vw]), 5120, N, rows, 5120)
+    table, _ = rope_table(capacity)
+    xb, bb, tb = dev.upload(x), dev.upload(bias), dev.upload(table)
+    dev.attn_qkv(qkv, bb, ttlab_amd.stage_input(xb), tb, pb, capacity, out, kb, vb)
+    assert (out.download(np.uint8) == 0x7f).all()
+    assert np.array_equal(kb.download(np.float32), k) and np.array_equal(vb.download(np.float32), v)
+    for b in (qb, kb, vb, sb, pb, ws, out, xb, bb, tb):
+        b.free()
+    qkv.free()
+
+
 # (first position, tokens): a prompt from 0 (ragged last block), one continued past the
 # window, one token, and a block boundary inside the window.
 @pytest.mark.parametrize("layer_index", [0, 1])

@@ -61,27 +61,28 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
                                                                 float2 *__restrict__ ml_part) {
     __shared__ __attribute__((aligned(16))) float ks[kChunk * kRowStride];
     __shared__ __attribute__((aligned(16))) float vs[kChunk * kRowStride];
-    __shared__ __attribute__((aligned(16))) float qs[kGroup][kHead];
+    // every thread stores its query float4 (t % 128) in a slot of its own, so the store
+    // needs no branch (under one, the compiler places the K/V loads after it, and the
+    // store waits for q alone); the scores read slots 0..127
+    __shared__ float4 qs[kThreads];
     __shared__ float e[kGroup][kChunk];
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
+    // The 8 query heads first (every thread loads one of their 128 float4), then the position,
+    // then the chunk's K and V rows of head kvh (16 float4 per row; positions past n
+    // re-read the last valid one): two round trips in all.
+    // No early exit (the compiler would sink the query loads below it): a workgroup
+    // past the span, or of a position past the capacity, computes chunk 0 of a valid
+    // span and stores nothing.
+    const float4 qv = reinterpret_cast<const float4 *>(q + size_t(kvh) * kGroup * kHead)[t % (kGroup * kHead / 4)];
     const uint32_t pos = uint32_t(*position);
-    if (pos >= capacity) {
-        return;
-    }
-    const Span sp = span_of(pos, layer_index);
-    const uint32_t start = sp.first + chunk * kChunk;
-    if (chunk * kChunk >= sp.count) {
-        return;
-    }
-    const uint32_t n = min(uint32_t(kChunk), sp.count - chunk * kChunk);
+    const Span sp = span_of(pos < capacity ? pos : 0u, layer_index);
+    const bool live = pos < capacity && chunk * kChunk < sp.count;
+    const uint32_t c0 = live ? chunk * kChunk : 0u;
+    const uint32_t start = sp.first + c0;
+    const uint32_t n = min(uint32_t(kChunk), sp.count - c0);
 
-    // One round trip: the 8 query heads, and the chunk's K and V rows of head kvh
-    // (16 float4 per row; positions past n re-read the last valid one).
     constexpr int kPer = kChunk * (kHead / 4) / kThreads;  // 4 float4 of K and of V per thread
     float4 kr[kPer], vr[kPer];
-    const float4 qv = t < uint32_t(kGroup * kHead / 4)
-                          ? reinterpret_cast<const float4 *>(q + size_t(kvh) * kGroup * kHead)[t]
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t f = t + uint32_t(k) * kThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
@@ -89,9 +90,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
         kr[k] = reinterpret_cast<const float4 *>(k_cache + row)[d4];
         vr[k] = reinterpret_cast<const float4 *>(v_cache + row)[d4];
     }
-    if (t < uint32_t(kGroup * kHead / 4)) {
-        *reinterpret_cast<float4 *>(&qs[t / (kHead / 4)][4 * (t % (kHead / 4))]) = qv;
-    }
+    qs[t] = qv;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t f = t + uint32_t(k) * kThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
@@ -107,8 +106,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
 #pragma unroll
         for (int d = 0; d < kHead / 4; ++d) {
             const float4 kv = *reinterpret_cast<const float4 *>(ks + p * kRowStride + 4 * d);
-            const float4 qa = *reinterpret_cast<const float4 *>(&qs[g0][4 * d]);
-            const float4 qb = *reinterpret_cast<const float4 *>(&qs[g0 + 1][4 * d]);
+            const float4 qa = qs[g0 * (kHead / 4) + d];
+            const float4 qb = qs[(g0 + 1) * (kHead / 4) + d];
             a0 = fmaf(qa.x, kv.x, a0);
             a0 = fmaf(qa.y, kv.y, a0);
             a0 = fmaf(qa.z, kv.z, a0);
@@ -131,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
             const float x = lane < n ? expf(s - m) : 0.0f;
             const float l = wave_sum(x);
             e[g][lane] = x;
-            if (lane == 0) {
+            if (lane == 0 && live) {
                 ml_part[(size_t(kvh * kGroup + g)) * max_chunks + chunk] = make_float2(m, l);
             }
         }
@@ -147,9 +146,11 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
             o0 = fmaf(x, v.x, o0);
             o1 = fmaf(x, v.y, o1);
         }
-        float *dst = o_part + ((size_t(kvh * kGroup + g)) * max_chunks + chunk) * kHead + d;
-        dst[0] = o0;
-        dst[1] = o1;
+        if (live) {
+            float *dst = o_part + ((size_t(kvh * kGroup + g)) * max_chunks + chunk) * kHead + d;
+            dst[0] = o0;
+            dst[1] = o1;
+        }
     }
 }
 
@@ -165,28 +166,35 @@ __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__rest
                                                              uint32_t max_chunks, float *__restrict__ out) {
     __shared__ float fs[kMaxCombineChunks];
     const uint32_t head = blockIdx.x, d = threadIdx.x;
-    const uint32_t pos = uint32_t(*position);
-    if (pos >= capacity) {
-        return;
+    // The statistics and the first kEarly chunks' outputs are requested before the
+    // position (the chunk count) is known: every address below max_chunks is inside
+    // the partials, and chunks past the count are left out below by selection (their
+    // stale contents never enter an arithmetic operation).
+    constexpr int kPer = kMaxCombineChunks / kHead;
+    float2 ml[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        ml[k] = ml_part[size_t(head) * max_chunks + min(d + uint32_t(k) * kHead, max_chunks - 1)];
     }
-    const Span sp = span_of(pos, layer_index);
-    const uint32_t chunks = (sp.count + kChunk - 1) / kChunk;
-    const float sink = sinks[head];
-    // the first kEarly chunks' outputs are requested with the statistics (addresses
-    // past the last chunk re-read it, weighted by 0 below)
     constexpr int kEarly = 32;
     const float *op = o_part + size_t(head) * max_chunks * kHead + d;
     float early[kEarly];
 #pragma unroll
     for (int c = 0; c < kEarly; ++c) {
-        early[c] = op[size_t(min(uint32_t(c), chunks - 1)) * kHead];
+        early[c] = op[size_t(min(uint32_t(c), max_chunks - 1)) * kHead];
     }
-    constexpr int kPer = kMaxCombineChunks / kHead;
-    float2 ml[kPer];
+    __builtin_amdgcn_sched_barrier(0);  // all of them issued before the position is read
+    const float sink = sinks[head];
+    // no early exit (the compiler would sink the loads above below it): a position
+    // past the capacity combines position 0's span and stores nothing
+    const uint32_t pos = uint32_t(*position);
+    const Span sp = span_of(pos < capacity ? pos : 0u, layer_index);
+    const uint32_t chunks = (sp.count + kChunk - 1) / kChunk;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-        const uint32_t c = d + uint32_t(k) * kHead;
-        ml[k] = c < chunks ? ml_part[size_t(head) * max_chunks + c] : make_float2(-INFINITY, 0.0f);
+        if (d + uint32_t(k) * kHead >= chunks) {
+            ml[k] = make_float2(-INFINITY, 0.0f);
+        }
     }
     float m = sink;
 #pragma unroll
@@ -215,7 +223,9 @@ __global__ __launch_bounds__(kHead) void attn_combine_kernel(const float *__rest
     for (uint32_t c = kEarly; c < chunks; ++c) {
         acc = fmaf(op[size_t(c) * kHead], fs[c], acc);
     }
-    out[head * kHead + d] = acc / den;
+    if (pos < capacity) {
+        out[head * kHead + d] = acc / den;
+    }
 }
 
 // Sliding-window layers in one launch: workgroup = query head; the window (at most
@@ -232,23 +242,23 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
                                                                   float *__restrict__ out) {
     __shared__ __attribute__((aligned(16))) float ks[kWindow * kRowStride];
     __shared__ __attribute__((aligned(16))) float vs[kWindow * kRowStride];
-    __shared__ __attribute__((aligned(16))) float qs[kHead];
+    __shared__ float4 qs[kWinThreads];  // thread t's copy of q float4 t % 16 (no branch)
     __shared__ float e[kWindow];
     __shared__ float stat[4];
     __shared__ float part[kWinThreads / kHead][kHead];
     const uint32_t head = blockIdx.x, kvh = head / kGroup, t = threadIdx.x;
+    // q and the sink first (one of q's 16 float4 per thread), then the position, then the
+    // window's K and V rows (positions past n re-read the last): two round trips
+    const float4 qv = reinterpret_cast<const float4 *>(q + size_t(head) * kHead)[t % (kHead / 4)];
+    const float sink = sinks[head];
+    // no early exit (the compiler would sink the loads above below it): a position
+    // past the capacity attends over position 0 and stores nothing
     const uint32_t pos = uint32_t(*position);
-    if (pos >= capacity) {
-        return;
-    }
-    const Span sp = span_of(pos, layer_index);
+    const Span sp = span_of(pos < capacity ? pos : 0u, layer_index);
     const uint32_t n = sp.count;  // 1..128
 
-    // one round trip: q and the window's K and V rows (positions past n re-read the last)
     constexpr int kPer = kWindow * (kHead / 4) / kWinThreads;  // 8 float4 of K and of V per thread
     float4 kr[kPer], vr[kPer];
-    const float4 qv = t < uint32_t(kHead / 4) ? reinterpret_cast<const float4 *>(q + size_t(head) * kHead)[t]
-                                               : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t f = t + uint32_t(k) * kWinThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
@@ -256,9 +266,7 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
         kr[k] = reinterpret_cast<const float4 *>(k_cache + row)[d4];
         vr[k] = reinterpret_cast<const float4 *>(v_cache + row)[d4];
     }
-    if (t < uint32_t(kHead / 4)) {
-        *reinterpret_cast<float4 *>(&qs[4 * t]) = qv;
-    }
+    qs[t] = qv;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t f = t + uint32_t(k) * kWinThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
@@ -274,7 +282,7 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
 #pragma unroll
         for (int d = 0; d < kHead / 4; ++d) {
             const float4 kv = *reinterpret_cast<const float4 *>(ks + t * kRowStride + 4 * d);
-            const float4 qq = *reinterpret_cast<const float4 *>(&qs[4 * d]);
+            const float4 qq = qs[d];
             a = fmaf(qq.x, kv.x, a);
             a = fmaf(qq.y, kv.y, a);
             a = fmaf(qq.z, kv.z, a);
@@ -289,7 +297,6 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
     }
     __syncthreads();
     // model.cpp:270-281: the sink enters the max and the denominator only
-    const float sink = sinks[head];
     const float m = fmaxf(sink, fmaxf(stat[0], stat[1]));
     if (t < uint32_t(kWindow)) {
         const float x = t < n ? expf(e[t] - m) : 0.0f;
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
         part[g][d] = o;
     }
     __syncthreads();
-    if (t < uint32_t(kHead)) {
+    if (t < uint32_t(kHead) && pos < capacity) {
         const float o = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
         out[head * kHead + t] = o / den;
     }

@@ -84,14 +84,22 @@ __global__ void q8_synth_kernel(uint64_t seed, uint64_t stream, size_t block_off
 
 // ---- matvec kernels -------------------------------------------------------------
 
+struct NoLoads {
+    __device__ void operator()() const {}
+};
+
 // Common body: one workgroup = one 16-row tile; returns the row sum for row
 // threadIdx.x (valid for threadIdx.x < 16) after the wave-order reduction.
-template <int K, int W, int MODE>
+// late_loads() runs once the input and weight loads are issued: loads whose
+// addresses wait on another load (the qkv epilogue's RoPE pair waits on the
+// position) go there, so that wait does not hold back the weight stream.
+template <int K, int W, int MODE, class LateLoads = NoLoads>
 __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t *__restrict__ codes,
                                                                   const uint16_t *__restrict__ scales,
                                                                   size_t tile, const stage::Input &in,
                                                                   float *xs, float *xsum, float *red,
-                                                                  float (*part)[q8::tile_rows]) {
+                                                                  float (*part)[q8::tile_rows],
+                                                                  LateLoads &&late_loads = NoLoads{}) {
     using S = q8::Shape<K>;
     const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     // input loads first: the staging then waits for them alone while the weight
@@ -100,6 +108,7 @@ __device__ __attribute__((always_inline)) inline float tile_matvec(const uint8_t
     stage::stage_load(in, pending);
     q8::TileRegs<K, W> regs;
     q8::tile_load<K, W>(codes, scales, tile, wave, lane, regs);
+    late_loads();
     stage::stage_finish(in, pending, xs, red);
     q8::block_sums(xs, S::x_blocks, xsum);
     const float acc = q8::tile_compute<K, W>(regs, wave, lane, xs, xsum);
@@ -184,18 +193,23 @@ __global__ __launch_bounds__(waves_for<2880>() * 64) void qkv_kernel(const uint8
     if (blockIdx.x != 0) {
         in.v_out = nullptr;
     }
-    // epilogue operands first (bias, position, the RoPE pair), so no load waits at the end
+    // epilogue operands before the sum, so no load waits at the end: the bias first;
+    // the position and the RoPE pair it selects once the weight loads are issued
     const uint32_t r = threadIdx.x, r16 = r % q8::tile_rows;
-    const uint32_t pos = uint32_t(*position);
     const bool is_q = tile < uint32_t(kQHeads) * 4, is_k = !is_q && tile < uint32_t(kQHeads + kKvHeads) * 4;
     const uint32_t head = is_q ? tile / 4 : (is_k ? (tile - kQHeads * 4) / 4 : (tile - (kQHeads + kKvHeads) * 4) / 4);
     const uint32_t base = is_q ? 0u : (is_k ? uint32_t(kQRows) : uint32_t(kQRows + kKvRows));
     const uint32_t dim = qkv_dim(tile, r16);
     const float bv = bias[base + head * kHead + dim];
-    const uint32_t pair = r16 < 8 ? dim : dim - 32;
-    const bool rotate = (is_q || is_k) && pos < capacity;
-    const float2 cs = rotate ? rope[size_t(pos) * (kHead / 2) + pair] : make_float2(0.f, 0.f);
-    const float sum = tile_matvec<2880, W, MODE>(codes, scales, tile, in, xs, xsum, red, part);
+    const uint32_t pair = (r16 < 8 ? dim : dim - 32) % 32;  // v rows: any in-bounds pair, unused
+    uint32_t pos = 0;
+    float2 cs;
+    const float sum = tile_matvec<2880, W, MODE>(codes, scales, tile, in, xs, xsum, red, part, [&]() {
+        // unconditional (a clamped position), so the compiler need not wait for every
+        // load in flight at the end of a branch
+        pos = uint32_t(*position);
+        cs = rope[size_t(min(pos, capacity - 1)) * (kHead / 2) + pair];
+    });
     if (r < q8::tile_rows) {
         vals[r] = bv + sum;
     }

@@ -102,7 +102,7 @@ struct Pending {
     float4 v[per];
     float4 a[per][add ? kMaxAdd : 1];
     float4 w[per];
-    float aw[kMaxAdd];
+    float aw_lane;  // combine weight lane % kMaxAdd
 };
 
 // Issues every global load of the staging, unconditionally: base, the combine
@@ -113,10 +113,11 @@ __device__ __attribute__((always_inline)) inline void stage_load(const Input &in
     using P = Pending<N, XB, NT, MODE>;
     const float4 *b4 = reinterpret_cast<const float4 *>(in.base);
     if constexpr (P::add) {
-#pragma unroll
-        for (uint32_t r = 0; r < kMaxAdd; ++r) {
-            p.aw[r] = in.add_w[r < in.add_k ? r : 0];
-        }
+        // lane r of each wave loads weight r (a vector load, issued here; loads from
+        // one uniform address go to the scalar unit, and the compiler sinks those to
+        // their uses, each behind a wait of its own); stage_finish reads the lanes
+        const uint32_t r = threadIdx.x % kMaxAdd;
+        p.aw_lane = in.add_w[r < in.add_k ? r : 0];
     }
 #pragma unroll
     for (int j = 0; j < P::per; ++j) {
@@ -158,7 +159,7 @@ __device__ __attribute__((always_inline)) inline void stage_finish(const Input &
 #pragma unroll
             for (uint32_t r = 0; r < kMaxAdd; ++r) {
                 if (r < in.add_k) {
-                    const float w = p.aw[r];
+                    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.aw_lane), int(r)));
                     const float4 a = p.a[j][r];
                     m.x = m.x + w * a.x;
                     m.y = m.y + w * a.y;
