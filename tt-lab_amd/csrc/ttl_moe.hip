@@ -95,13 +95,14 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
 
     stage::Pending<kRouterCols, mxt::x_blocks, kRouterThreads, MODE> pending;
     stage::stage_load(in, pending);
+    // unconditional (idle lanes re-read lane 179's columns): loads under a branch make
+    // the compiler wait for them at its end, before the staging could overlap them
     float4 wv[4];
-    if (active) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols) + 4 * t;
+    const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols) +
+                       4 * (active ? t : uint32_t(kRouterCols / 16 - 1));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            wv[q] = w4[q];
-        }
+    for (int q = 0; q < 4; ++q) {
+        wv[q] = w4[q];
     }
     stage::stage_finish(in, pending, xs, red);
     double prod[16];
