@@ -576,72 +576,120 @@ __device__ void route_exact_serial(const float *__restrict__ weight, const float
 // The exact path of the standalone selection (a batch can hold many tokens and one
 // uncertain token holds the whole launch, so its latency matters): the same sums, but
 // the workgroup forms the products w[c] * x[c] (each rounded to f32, as the
-// reference's) 60 columns at a time into LDS, and thread t < experts only adds its
-// row's products in column order.  Every thread holds a few float4 pieces of each
-// tile, loaded kAhead tiles before their products are formed (the router rows come
-// from L2 or the MALL, about a microsecond away).
-constexpr int kProdCols = 60;
-constexpr int kProdPieces = kProdCols / 4;  // float4 pieces of one row's tile
-constexpr int kProdStride = kProdCols + 1;  // odd: the adders read down a column without bank conflicts
-constexpr int kProdTiles = kRouterCols / kProdCols;
+// reference's) a tile of TC columns at a time into LDS, and thread t < experts only adds
+// its row's products in column order.  The products of tile j + 1 are formed into the
+// other of two LDS buffers while the adders sum tile j (one barrier per tile), and the
+// adders read their row four products at a time.  Every thread holds 8 float4 pieces of
+// each tile, loaded kAhead tiles before their products are formed (the router rows come
+// from L2 or the MALL, about a microsecond away).  TC is chosen so a tile holds at most
+// 7680 products (32 experts: 240 columns, 12 tiles; 128: 60; 192: 40).
+template <int TC>
+struct ExactTile {
+    static constexpr int cols = TC;
+    static constexpr int quads = TC / 4;                               // float4 pieces of one row's tile
+    static constexpr int rows = 7680 / TC;                             // experts a tile holds
+    static constexpr int stride = quads % 2 == 0 ? TC + 4 : TC + 8;    // floats; stride / 4 odd: the
+                                                                       // adders' b128 reads miss each other's banks
+    static constexpr int tiles = kRouterCols / TC;
+    static constexpr int ahead = TC >= 240 ? 3 : 6;                    // tiles of loads in flight
+    static constexpr int per = 8;                                      // pieces per thread (<= 2048 per tile)
+    static constexpr int lds_floats = 2 * rows * stride;
+    static_assert(kRouterCols % TC == 0 && tiles % ahead == 0, "whole tiles, whole rings");
+    static_assert(rows * quads <= per * 256, "a tile's pieces fit the workgroup");
+    static_assert((stride / 4) % 2 == 1 && stride % 4 == 0, "aligned rows, odd in float4");
+};
 
-// PER: float4 pieces per thread of a 256-thread workgroup (experts * 15 per tile)
-template <int PER>
+template <int TC>
 __device__ __forceinline__ void route_exact_coop(const float *__restrict__ weight, const float *__restrict__ bias,
                                                  uint32_t experts, uint32_t k, const float *xs,
                                                  RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits,
                                                  float *prod) {
-    constexpr int kAhead = PER <= 2 ? 4 : (PER <= 4 ? 2 : 1);
-    static_assert(kRouterCols % kProdCols == 0 && kProdTiles % kAhead == 0, "whole tiles, whole rings");
+    using T = ExactTile<TC>;
+    constexpr int PER = T::per, D = T::ahead;
     const uint32_t t = threadIdx.x;
-    const uint32_t pieces = experts * kProdPieces;
-    // piece i of a tile: expert i / 15, columns 4 (i % 15) .. + 3; pieces past the
+    const uint32_t pieces = experts * T::quads;
+    // piece i of a tile: expert i / quads, columns 4 (i % quads) .. + 3; pieces past the
     // tile's last re-read the last one (all loads unconditional) and are not stored
     auto piece = [&](int i) __attribute__((always_inline)) { return min(t + 256u * uint32_t(i), pieces - 1); };
     auto load = [&](int tile, float4(&r)[PER]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const uint32_t e = piece(i) / kProdPieces, c = uint32_t(tile) * kProdCols + 4 * (piece(i) % kProdPieces);
+            const uint32_t e = piece(i) / T::quads, c = uint32_t(tile) * TC + 4 * (piece(i) % T::quads);
             r[i] = *reinterpret_cast<const float4 *>(weight + size_t(e) * kRouterCols + c);
         }
     };
-    float4 wv[kAhead][PER];
+    // forms tile `tile`'s products into buffer tile % 2
+    auto produce = [&](int tile, const float4(&r)[PER]) __attribute__((always_inline)) {
+        float *buf = prod + (tile % 2) * (T::rows * T::stride);
 #pragma unroll
-    for (int d = 0; d < kAhead; ++d) {
+        for (int i = 0; i < PER; ++i) {
+#pragma clang fp contract(off)
+            const uint32_t e = piece(i) / T::quads, c4 = 4 * (piece(i) % T::quads);
+            const uint32_t c = uint32_t(tile) * TC + c4;
+            const float4 x = *reinterpret_cast<const float4 *>(xs + (c / 32) * mxt::x_stride + c % 32);
+            if (t + 256u * uint32_t(i) < pieces) {
+                const float4 w = r[i];
+                *reinterpret_cast<float4 *>(buf + e * T::stride + c4) =
+                    make_float4(w.x * x.x, w.y * x.y, w.z * x.z, w.w * x.w);
+            }
+        }
+    };
+    float4 wv[D][PER];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
         load(d, wv[d]);
     }
     float sum = t < experts ? bias[t] : 0.0f;
+    produce(0, wv[0]);
+    load(D, wv[0]);
+    __syncthreads();
 #pragma unroll 1
-    for (int base = 0; base < kProdTiles; base += kAhead) {
+    for (int base = 0; base < T::tiles; base += D) {
 #pragma unroll
-        for (int d = 0; d < kAhead; ++d) {
+        for (int d = 0; d < D; ++d) {
             const int tile = base + d;
-            __syncthreads();  // the adders are done with the previous tile
-#pragma unroll
-            for (int i = 0; i < PER; ++i) {
-#pragma clang fp contract(off)
-                const uint32_t e = piece(i) / kProdPieces, c4 = 4 * (piece(i) % kProdPieces);
-                const uint32_t c = uint32_t(tile) * kProdCols + c4;
-                const float4 x = *reinterpret_cast<const float4 *>(xs + (c / 32) * mxt::x_stride + c % 32);
-                if (t + 256u * uint32_t(i) < pieces) {
-                    float *dst = prod + e * kProdStride + c4;
-                    dst[0] = wv[d][i].x * x.x;
-                    dst[1] = wv[d][i].y * x.y;
-                    dst[2] = wv[d][i].z * x.z;
-                    dst[3] = wv[d][i].w * x.w;
-                }
+            const int next_slot = (d + 1) % D;  // a constant once the loop is unrolled
+            if (tile + 1 < T::tiles) {
+                produce(tile + 1, wv[next_slot]);
+                // refill the slot (past the last tile: re-read it, unused)
+                load(min(tile + 1 + D, T::tiles - 1), wv[next_slot]);
             }
-            // refill this ring slot (past the last tile: re-read it, unused)
-            load(min(tile + kAhead, kProdTiles - 1), wv[d]);
-            __syncthreads();
             if (t < experts) {
+                // chunks of kChunk float4: the next chunk's reads are issued before this
+                // chunk's adds, so the LDS latency hides behind 4 kChunk dependent adds
+                const float4 *row = reinterpret_cast<const float4 *>(prod + (tile % 2) * (T::rows * T::stride) +
+                                                                     t * T::stride);
+                constexpr int kChunk = T::quads % 12 == 0 ? 12 : (T::quads % 10 == 0 ? 10 : 5);
+                constexpr int kChunks = T::quads / kChunk;
+                static_assert(T::quads % kChunk == 0, "whole chunks");
+                float4 pa[kChunk], pb[kChunk];
+#pragma unroll
+                for (int q = 0; q < kChunk; ++q) {
+                    pa[q] = row[q];
+                }
+#pragma unroll
+                for (int c = 0; c < kChunks; ++c) {
+                    float4(&cur)[kChunk] = c % 2 == 0 ? pa : pb;
+                    float4(&nxt)[kChunk] = c % 2 == 0 ? pb : pa;
+                    if (c + 1 < kChunks) {
+#pragma unroll
+                        for (int q = 0; q < kChunk; ++q) {
+                            nxt[q] = row[(c + 1) * kChunk + q];
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int q = 0; q < kChunk; ++q) {
 #pragma clang fp contract(off)
-                const float *row = prod + t * kProdStride;
-#pragma unroll 15
-                for (int c = 0; c < kProdCols; ++c) {
-                    sum = sum + row[c];
+                        sum = sum + cur[q].x;
+                        sum = sum + cur[q].y;
+                        sum = sum + cur[q].z;
+                        sum = sum + cur[q].w;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            __syncthreads();  // tile + 1 formed; the adders are done with tile's buffer
         }
     }
     if (t < experts) {
@@ -655,7 +703,7 @@ __device__ __forceinline__ void route_exact_coop(const float *__restrict__ weigh
     replay_selection(experts, k, scratch, lds, logits != nullptr);
 }
 
-template <int MODE, int PER>
+template <int MODE, int TC>
 __device__ void route_workgroup(const float *__restrict__ weight, const float *__restrict__ bias,
                                 const stage::Input &in, uint32_t experts, uint32_t k, bool force_exact,
                                 RouterScratch *scratch, RouteLds &lds, float *__restrict__ logits, float *xs,
@@ -665,14 +713,14 @@ __device__ void route_workgroup(const float *__restrict__ weight, const float *_
     route_certified_wave<kPerLane>(experts, k, force_exact, rows, lds, logits, true);
     if (!lds.certified) {
         stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(in, xs, red);
-        route_exact_coop<PER>(weight, bias, experts, k, xs, scratch, lds, logits, prod);
+        route_exact_coop<TC>(weight, bias, experts, k, xs, scratch, lds, logits, prod);
     }
 }
 
 // Standalone routing (ttl_router_topk): one workgroup per token, publishes
 // everything.  Workgroup t of a batch routes token t: input in.base + t * x_stride,
 // scratch[t], outputs indices/weights_out + t * k (logits only for one token).
-template <int MODE, int PER>
+template <int MODE, int TC>
 __global__ __launch_bounds__(256) void router_select_kernel(const float *__restrict__ weight,
                                                             const float *__restrict__ bias, uint32_t experts,
                                                             stage::Input in, uint32_t k, uint32_t force_exact,
@@ -686,9 +734,9 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
     weights_out += size_t(blockIdx.x) * k;
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    __shared__ float prod[PER * 256 / kProdPieces * kProdStride];  // [experts][kProdStride]
-    route_workgroup<MODE, PER>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red,
-                               prod);
+    __shared__ __attribute__((aligned(16))) float prod[ExactTile<TC>::lds_floats];  // [2][rows][stride]
+    route_workgroup<MODE, TC>(weight, bias, in, experts, k, force_exact != 0, scratch, lds, logits, xs, red,
+                              prod);
     if (threadIdx.x < k) {
         indices[threadIdx.x] = lds.indices[threadIdx.x];
         weights_out[threadIdx.x] = lds.weights[threadIdx.x];
@@ -1001,18 +1049,17 @@ stage::Input layer_input(const ttl_moe_layer &L, const float *x) {
     return in;
 }
 
-// Calls f(std::integral_constant<int, PER>) with the exact path's float4 pieces per
-// thread for `experts` rows (experts * 15 pieces per 60-column tile, 256 threads):
-// 2 up to 34 experts, 8 up to 136, 12 up to 204 (kMaxExperts is 192).
+// Calls f(std::integral_constant<int, TC>) with the exact path's tile width for
+// `experts` rows: 240 columns up to 32 experts, 60 up to 128, 40 up to 192.
 template <typename F>
-void with_pieces(uint32_t experts, F &&f) {
-    static_assert(kMaxExperts * kProdPieces <= 12 * 256, "the widest variant covers every row");
-    if (experts * kProdPieces <= 2 * 256) {
-        f(std::integral_constant<int, 2>{});
-    } else if (experts * kProdPieces <= 8 * 256) {
-        f(std::integral_constant<int, 8>{});
+void with_tile_cols(uint32_t experts, F &&f) {
+    static_assert(kMaxExperts <= uint32_t(ExactTile<40>::rows), "the narrowest tile holds every row");
+    if (experts <= uint32_t(ExactTile<240>::rows)) {
+        f(std::integral_constant<int, 240>{});
+    } else if (experts <= uint32_t(ExactTile<60>::rows)) {
+        f(std::integral_constant<int, 60>{});
     } else {
-        f(std::integral_constant<int, 12>{});
+        f(std::integral_constant<int, 40>{});
     }
 }
 
@@ -1025,8 +1072,8 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
     stage::with_mode(in, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
         router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch);
-        with_pieces(experts, [&](auto per) {
-            router_select_kernel<M, decltype(per)::value><<<1, 256, 0, ctx->stream>>>(
+        with_tile_cols(experts, [&](auto tc) {
+            router_select_kernel<M, decltype(tc)::value><<<1, 256, 0, ctx->stream>>>(
                 weight, bias, experts, in, k, force_exact ? 1u : 0u, scratch, logits, indices, weights, 0u);
         });
     });
@@ -1068,8 +1115,8 @@ int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, ui
         router_rows_batch_kernel<M>
             <<<dim3((count + kRbTokens - 1) / kRbTokens, (L.experts + kRbExperts - 1) / kRbExperts), 256, 0,
                ctx->stream>>>(L.router_weight, L.router_bias, in, s, L.hidden, count, L.experts);
-        with_pieces(L.experts, [&](auto per) {
-            router_select_kernel<M, decltype(per)::value><<<count, 256, 0, ctx->stream>>>(
+        with_tile_cols(L.experts, [&](auto tc) {
+            router_select_kernel<M, decltype(tc)::value><<<count, 256, 0, ctx->stream>>>(
                 L.router_weight, L.router_bias, L.experts, in, L.used, 0u, s, nullptr, indices, weights, L.hidden);
         });
     });
