@@ -6,6 +6,8 @@ Makefile as tt-lab_amd/build/facade_check), on a GGUF file written here.
   (ttlm_*, which test_gpu_gguf.py checks against the oracle), and the reference's
   error messages come back as std::runtime_error (model.cpp:463-472, 557-566,
   gguf.cpp:150-153).
+- ttlab_run (host/ttlab_run.cpp), the reference CLI's `run` loop on token ids: the same
+  tokens, and the generation ends at tokenizer.ggml.eos_token_id (main.cpp:373-411).
 - HipTensorBackend, the tensor.h functions: the embedding row and the F32 router
   matvec (the exact path) equal the oracle's bit for bit; rms_norm, the Q8_0 and
   MXFP4 matvecs and the selected-token matmul agree with it to relative L2 <= 1e-5;
@@ -19,13 +21,14 @@ import pytest
 
 import oracle_lib as O
 import ttlab_amd
-from gguf_writer import GGML_Q8_0, gpt_oss_metadata, gpt_oss_tensors, write_gguf
+from gguf_writer import GGML_Q8_0, U32, gpt_oss_metadata, gpt_oss_tensors, write_gguf
 from test_gpu_gguf import EXPERTS, LAYERS, VOCAB, generated
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
 N = 2880
 BINARY = os.path.join(os.path.dirname(ttlab_amd.LIB_PATH), "facade_check")
+CLI = os.path.join(os.path.dirname(ttlab_amd.LIB_PATH), "ttlab_run")
 PROMPT = [17, 300, 5, 941, 2, 77, 512]
 LIMIT = 5
 
@@ -123,3 +126,32 @@ def test_selected_matmul_against_oracle(run):
         assert O.rel_l2(got[s], ref[s]) <= TOL, s
     for s in (0, 2, 4):
         assert np.isnan(got[s]).all(), s
+
+
+def generate_cli(path, limit):
+    done = subprocess.run([CLI, "run", "-m", path, "--loose", "-t", ",".join(str(t) for t in PROMPT), "-n",
+                           str(limit)], capture_output=True, text=True, timeout=300)
+    print(done.stdout, done.stderr)
+    assert done.returncode == 0, done.stderr
+    return [int(v) for v in done.stdout.split()], done.stderr
+
+
+def test_command_line_generates_the_c_abi_tokens(run):
+    tmp, path, _ = run
+    tokens = [int(v) for v in open(os.path.join(tmp, "tokens.txt")).read().split()]
+    out, err = generate_cli(path, LIMIT)
+    assert out == tokens
+    assert f"prefill: {len(PROMPT)} tokens" in err and f"generated: {LIMIT} tokens" in err
+    assert f"decode: {LIMIT - 1} evals" in err
+
+
+def test_command_line_stops_at_end_of_sequence(run):
+    tmp, _, _ = run
+    tokens = [int(v) for v in open(os.path.join(tmp, "tokens.txt")).read().split()]
+    eos = tokens[2]
+    path = os.path.join(tmp, "gpt-oss-small-eos.gguf")
+    write_gguf(path, gpt_oss_metadata(LAYERS, EXPERTS) + [("tokenizer.ggml.eos_token_id", U32, eos)],
+               gpt_oss_tensors(LAYERS, EXPERTS, VOCAB, generated, GGML_Q8_0))
+    out, err = generate_cli(path, LIMIT)
+    assert out == tokens[:tokens.index(eos)]
+    assert f"generated: {len(out)} tokens" in err

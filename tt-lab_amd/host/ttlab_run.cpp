@@ -1,0 +1,188 @@
+// ttlab_run: the reference CLI's generation path (main.cpp:292-411, `tt-lab run`) on the
+// gfx950 backend.  The model, its checks and its decode loop are the reference's; the
+// prompt arrives as token ids (the tokenizer and the Harmony template stay on the
+// reference's side: `tt-lab tokenize` prints the ids of a formatted prompt).
+//
+//   ttlab_run run -m <model.gguf> -t <id,id,...> [-n <tokens>] [--device <ordinal>] [--loose]
+//   ttlab_run inspect -m <model.gguf> [--loose]
+//
+// `run` prefills the prompt, then repeats greedy / forward until the end-of-sequence id
+// (tokenizer.ggml.eos_token_id) or the generation limit, printing each generated id; the
+// timing lines on stderr have the reference's format.  `inspect` applies the model checks
+// (model.cpp:64-206) without a device and prints the shape it found.  Errors print
+// "error: <message>" and exit 1, usage errors exit 2, as main.cpp does.  --loose admits
+// the small test models (check_gguf_model(file, false)).
+#include "gguf.hpp"
+#include "gpt_oss_hip.hpp"
+
+#include <chrono>
+#include <cstdio>
+#include <iostream>
+#include <limits>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace {
+
+void usage(const char *argv0) {
+    std::cerr << "usage: " << argv0 << " run -m <model.gguf> -t <id,id,...> [-n <tokens>] [--device <ordinal>] [--loose]\n"
+              << "       " << argv0 << " inspect -m <model.gguf> [--loose]\n";
+}
+
+bool parse_size(const std::string &text, size_t *output) {
+    try {
+        size_t used = 0;
+        const unsigned long long parsed = std::stoull(text, &used);
+        if (used != text.size() || text.empty() || text[0] == '-' ||
+            parsed > std::numeric_limits<size_t>::max()) {
+            return false;
+        }
+        *output = size_t(parsed);
+        return true;
+    } catch (const std::exception &) {
+        return false;
+    }
+}
+
+bool parse_tokens(const std::string &text, std::vector<int32_t> *tokens) {
+    size_t start = 0;
+    while (start <= text.size()) {
+        const size_t comma = text.find(',', start);
+        const std::string item = text.substr(start, comma == std::string::npos ? std::string::npos : comma - start);
+        size_t value = 0;
+        if (!parse_size(item, &value) || value > size_t(std::numeric_limits<int32_t>::max())) {
+            return false;
+        }
+        tokens->push_back(int32_t(value));
+        if (comma == std::string::npos) {
+            break;
+        }
+        start = comma + 1;
+    }
+    return !tokens->empty();
+}
+
+double seconds(std::chrono::steady_clock::time_point begin, std::chrono::steady_clock::time_point end) {
+    return std::chrono::duration<double>(end - begin).count();
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc < 2) {
+        usage(argv[0]);
+        return 2;
+    }
+    const std::string command = argv[1];
+    if (command == "-h" || command == "--help") {
+        usage(argv[0]);
+        return 0;
+    }
+    if (command != "run" && command != "inspect") {
+        std::cerr << "unknown command: " << command << '\n';
+        usage(argv[0]);
+        return 2;
+    }
+    std::string model_path;
+    std::vector<int32_t> prompt;
+    bool tokens_set = false, predict_set = false, strict = true;
+    size_t predict = 0, device = 0;
+    for (int i = 2; i < argc; ++i) {
+        const std::string argument = argv[i];
+        if ((argument == "-m" || argument == "--model") && i + 1 < argc) {
+            model_path = argv[++i];
+        } else if ((argument == "-t" || argument == "--tokens") && i + 1 < argc) {
+            if (!parse_tokens(argv[++i], &prompt)) {
+                std::cerr << "invalid token list: " << argv[i] << '\n';
+                return 2;
+            }
+            tokens_set = true;
+        } else if ((argument == "-n" || argument == "--predict" || argument == "--n-predict") && i + 1 < argc) {
+            if (!parse_size(argv[++i], &predict)) {
+                std::cerr << "invalid generation limit: " << argv[i] << '\n';
+                return 2;
+            }
+            predict_set = true;
+        } else if (argument == "--device" && i + 1 < argc) {
+            if (!parse_size(argv[++i], &device) || device > 1024) {
+                std::cerr << "invalid device ordinal: " << argv[i] << '\n';
+                return 2;
+            }
+        } else if (argument == "--loose") {
+            strict = false;
+        } else {
+            std::cerr << "unknown argument: " << argument << '\n';
+            usage(argv[0]);
+            return 2;
+        }
+    }
+    if (model_path.empty() || (command == "run" && !tokens_set)) {
+        usage(argv[0]);
+        return 2;
+    }
+    if (command == "inspect" && (tokens_set || predict_set)) {
+        std::cerr << "-t and -n are only valid for 'run'\n";
+        usage(argv[0]);
+        return 2;
+    }
+
+    try {
+        const ttlab::GgufFile file(model_path);
+        const ttlab::GgufModelShape shape = ttlab::check_gguf_model(file, strict);
+        if (command == "inspect") {
+            std::cout << "gpt-oss model: " << shape.layers << " layers, " << shape.experts
+                      << " experts, vocabulary " << shape.vocab << ", output.weight type " << shape.output_type
+                      << '\n';
+            return 0;
+        }
+        constexpr size_t context = ttlab::HipGptOssModel::context_length;
+        if (prompt.size() > context) {
+            throw std::runtime_error("prompt exceeds the model context");
+        }
+        const size_t limit = predict_set ? predict : context - prompt.size();
+        if (limit > context - prompt.size()) {
+            throw std::runtime_error("prompt and generation exceed the model context");
+        }
+        // main.cpp:373-411: the end-of-sequence id ends the generation (a file without the
+        // key generates to the limit)
+        const int64_t eos = file.find("tokenizer.ggml.eos_token_id")
+                                ? int64_t(file.integer("tokenizer.ggml.eos_token_id"))
+                                : -1;
+        ttlab::HipGptOssModel model(file, prompt.size() + limit, int(device), strict);
+        const auto prefill_begin = std::chrono::steady_clock::now();
+        const float *logits = model.prefill(prompt.data(), prompt.size());
+        const auto prefill_end = std::chrono::steady_clock::now();
+        size_t generated = 0, evaluations = 0;
+        double decode_seconds = 0.0;
+        for (size_t i = 0; i < limit; ++i) {
+            const int32_t next = model.greedy(logits);
+            if (next == eos) {
+                break;
+            }
+            ++generated;
+            std::cout << (generated > 1 ? " " : "") << next << std::flush;
+            if (i + 1 < limit) {
+                const auto begin = std::chrono::steady_clock::now();
+                logits = model.forward(next, prompt.size() + i);
+                decode_seconds += seconds(begin, std::chrono::steady_clock::now());
+                ++evaluations;
+            }
+        }
+        std::cout << '\n' << std::flush;
+        const double prefill_seconds = seconds(prefill_begin, prefill_end);
+        std::fprintf(stderr, "prefill: %zu tokens, %.3f s, %.3f t/s\n", prompt.size(), prefill_seconds,
+                     double(prompt.size()) / prefill_seconds);
+        std::fprintf(stderr, "generated: %zu tokens\n", generated);
+        if (evaluations > 0) {
+            std::fprintf(stderr, "decode: %zu evals, %.3f s, %.3f t/s\n", evaluations, decode_seconds,
+                         double(evaluations) / decode_seconds);
+        } else {
+            std::fprintf(stderr, "decode: 0 evals, 0.000 s, n/a t/s\n");
+        }
+        return 0;
+    } catch (const std::exception &error) {
+        std::cerr << "error: " << error.what() << '\n';
+        return 1;
+    }
+}
