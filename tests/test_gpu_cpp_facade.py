@@ -154,4 +154,5 @@ def test_command_line_stops_at_end_of_sequence(run):
                gpt_oss_tensors(LAYERS, EXPERTS, VOCAB, generated, GGML_Q8_0))
     out, err = generate_cli(path, LIMIT)
     assert out == tokens[:tokens.index(eos)]
-    assert f"generated: {len(out)} tokens" in err
+    # main.cpp counts the forward that produced the end-of-sequence id
+    assert f"generated: {len(out)} tokens" in err and f"decode: {len(out)} evals" in err

@@ -6,7 +6,8 @@
 //   ttlab_run run -m <model.gguf> -t <id,id,...> [-n <tokens>] [--device <ordinal>] [--loose]
 //   ttlab_run inspect -m <model.gguf> [--loose]
 //
-// `run` prefills the prompt, then repeats greedy / forward until the end-of-sequence id
+// `run` prefills the prompt, then generates as the reference's greedy / forward loop does
+// (the forwards run on the device in chunks) until the end-of-sequence id
 // (tokenizer.ggml.eos_token_id) or the generation limit, printing each generated id; the
 // timing lines on stderr have the reference's format.  `inspect` applies the model checks
 // (model.cpp:64-206) without a device and prints the shape it found.  Errors print
@@ -15,6 +16,7 @@
 #include "gguf.hpp"
 #include "gpt_oss_hip.hpp"
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <iostream>
@@ -153,21 +155,35 @@ int main(int argc, char **argv) {
         const auto prefill_begin = std::chrono::steady_clock::now();
         const float *logits = model.prefill(prompt.data(), prompt.size());
         const auto prefill_end = std::chrono::steady_clock::now();
-        size_t generated = 0, evaluations = 0;
+        // The reference's loop (greedy, print, forward) with the forwards run on the device
+        // in chunks: generate() feeds each step's argmax (the same first-maximum rule as
+        // greedy) to the next step without a host round trip, and the chunk's tokens are
+        // then printed, stopping at the end-of-sequence id as the reference does.  Steps a
+        // chunk runs past that id are discarded and not counted.
+        constexpr size_t kChunk = 32;
+        std::vector<int32_t> pending{model.greedy(logits)};
+        size_t next_index = 0, generated = 0, evaluations = 0;
         double decode_seconds = 0.0;
+        int32_t last = -1;
         for (size_t i = 0; i < limit; ++i) {
-            const int32_t next = model.greedy(logits);
+            if (next_index == pending.size()) {
+                // token i follows token i - 1 at position prompt + i - 1
+                const size_t steps = std::min(kChunk, limit - i);
+                const auto begin = std::chrono::steady_clock::now();
+                pending = model.generate(last, prompt.size() + i - 1, steps);
+                decode_seconds += seconds(begin, std::chrono::steady_clock::now());
+                next_index = 0;
+            }
+            const int32_t next = pending[next_index++];
+            if (i > 0) {
+                ++evaluations;  // the forward that produced this token (main.cpp counts it)
+            }
             if (next == eos) {
                 break;
             }
             ++generated;
             std::cout << (generated > 1 ? " " : "") << next << std::flush;
-            if (i + 1 < limit) {
-                const auto begin = std::chrono::steady_clock::now();
-                logits = model.forward(next, prompt.size() + i);
-                decode_seconds += seconds(begin, std::chrono::steady_clock::now());
-                ++evaluations;
-            }
+            last = next;
         }
         std::cout << '\n' << std::flush;
         const double prefill_seconds = seconds(prefill_begin, prefill_end);
