@@ -208,14 +208,16 @@ int ttl_moe_decode(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
  * combine: out = sum_r weights[r] * down_r, unfused, r = 0..k-1 (model.cpp:323,334-336). */
 int ttl_moe_gateup_swiglu(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev,
                           const int32_t *indices_dev, float *hidden_dev);
-/* Router + top-k + gate/up + SwiGLU (three launches: router rows, the certified
- * selection, gate/up); writes hidden f32 [used][expert_hidden], indices int32 [used]
- * and weights f32 [used] (model.cpp:293-332). */
+/* Router + top-k + gate/up + SwiGLU (two launches: the router rows, then gate/up with
+ * the certified top-k ranking at its head); writes hidden f32 [used][expert_hidden],
+ * indices int32 [used] and weights f32 [used] (model.cpp:293-332). */
 int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
                          int32_t *indices_dev, float *weights_dev);
 /* ttl_moe_route_gateup split into its two launches, for callers that time them one
- * by one: TTL_ROUTE_ROWS computes the exact router rows into the context's scratch,
- * TTL_ROUTE_GATEUP ranks the rows last computed on this context and runs gate/up.
+ * by one: TTL_ROUTE_ROWS computes the exact router rows into the context's scratch
+ * (and, for a layer with an input norm, keeps the normalized input there),
+ * TTL_ROUTE_GATEUP ranks the rows last computed on this context and runs gate/up on
+ * that normalized input (x_dev itself for a layer without a norm).
  * No reference counterpart. */
 #define TTL_ROUTE_ROWS 1u
 #define TTL_ROUTE_GATEUP 2u

@@ -85,7 +85,8 @@ struct RouterScratch {
 template <int MODE>
 __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float *__restrict__ weight,
                                                                      const float *__restrict__ bias,
-                                                                     stage::Input in, RouterScratch *scratch) {
+                                                                     stage::Input in, RouterScratch *scratch,
+                                                                     float *__restrict__ normed_out) {
     __shared__ double wave_part[3][3];
     __shared__ __attribute__((aligned(16))) float xs[mxt::x_floats];
     __shared__ float red[stage::red_floats(mxt::x_blocks)];
@@ -105,6 +106,13 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
         wv[q] = w4[q];
     }
     stage::stage_finish(in, pending, xs, red);
+    // workgroup 0 hands the staged (normalized) input on: the routed gate/up launch stages
+    // it as it is instead of normalizing the same vector again in each of its workgroups
+    if (normed_out && row == 0) {
+        for (uint32_t c = t; c < uint32_t(kRouterCols); c += kRouterThreads) {
+            normed_out[c] = xs[(c / 32) * mxt::x_stride + c % 32];
+        }
+    }
     double prod[16];
     double local = 0.0, abs_sum = 0.0;
     if (active) {
@@ -992,6 +1000,7 @@ struct MoeWorkspace {
     float logits[kMaxExperts];
     int32_t indices[kMaxUsed];
     float weights[kMaxUsed];
+    alignas(256) float normed[2880];  // the router rows' normalized input, for the routed gate/up
     alignas(256) float hidden[kMaxUsed * 2880];
     alignas(256) float down[kMaxUsed * 2880];
 };
@@ -1071,7 +1080,7 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
     RouterScratch *scratch = &workspace(ctx)->router;
     stage::with_mode(in, [&](auto mode) {
         constexpr int M = decltype(mode)::value;
-        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch);
+        router_rows_kernel<M><<<experts, kRouterThreads, 0, ctx->stream>>>(weight, bias, in, scratch, nullptr);
         with_tile_cols(experts, [&](auto tc) {
             router_select_kernel<M, decltype(tc)::value><<<1, 256, 0, ctx->stream>>>(
                 weight, bias, experts, in, k, force_exact ? 1u : 0u, scratch, logits, indices, weights, 0u);
@@ -1084,8 +1093,8 @@ void launch_router(ttl_ctx *ctx, const float *weight, const float *bias, uint32_
 void launch_router_rows(ttl_ctx *ctx, const ttl_moe_layer &L, const stage::Input &in) {
     RouterScratch *scratch = &workspace(ctx)->router;
     stage::with_mode(in, [&](auto mode) {
-        router_rows_kernel<decltype(mode)::value>
-            <<<L.experts, kRouterThreads, 0, ctx->stream>>>(L.router_weight, L.router_bias, in, scratch);
+        router_rows_kernel<decltype(mode)::value><<<L.experts, kRouterThreads, 0, ctx->stream>>>(
+            L.router_weight, L.router_bias, in, scratch, in.norm_w ? workspace(ctx)->normed : nullptr);
     });
 }
 
@@ -1145,6 +1154,12 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
     a.experts = L.experts;
     a.k = L.used;
     a.in = layer_input(L, x);
+    if (!expert_ids && L.input_norm) {
+        // routed: the router rows launch before this one left the normalized input in the
+        // context's workspace (the same values: the staging's norm is order-fixed)
+        a.in.base = workspace(ctx)->normed;
+        a.in.norm_w = nullptr;
+    }
     a.expert_ids = expert_ids;
     a.hidden = hidden;
     a.router_weight = L.router_weight;
