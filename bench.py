@@ -198,10 +198,10 @@ def gpu_decode(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      # the committed counters are config 3's (PL = 1: at most 64 experts)
-                     "traffic": measured_traffic("void gateup_swiglu_kernel<1, true, 1>") if args.config == 3 else None,
-                     "kernel": f"gateup_swiglu_kernel<1, true, {1 if experts <= 64 else 2 if experts <= 128 else 3}> "
-                               "(top-4 ranking at its head, then gate/up of the 4 experts and the clamped SwiGLU; "
-                               "as the step runs it)",
+                     "traffic": measured_traffic("void gateup_swiglu_kernel<0, true, 1>") if args.config == 3 else None,
+                     "kernel": f"gateup_swiglu_kernel<0, true, {1 if experts <= 64 else 2 if experts <= 128 else 3}> "
+                               "(top-4 ranking at its head, then gate/up of the 4 experts and the clamped SwiGLU, "
+                               "on the router rows' normalized input; as the step runs it)",
                      "bytes_per_launch": GATEUP_BYTES, "launch_us": round(us, 3),
                      "given_indices": {"kernel": "gateup_swiglu_kernel<1, false, 3>", "launch_us": given["us"],
                                        "GBps": given["GBps"], "frac": given["frac"]},
