@@ -59,7 +59,24 @@ __global__ __launch_bounds__(kThreads) void logits_kernel(const uint16_t *__rest
     if (blockIdx.x != 0) {
         in.v_out = nullptr;
     }
-    stage::stage<kCols, kXBlocks, kThreads, MODE>(in, xs, red);
+    // unconditional loads of group g's rows (a row past the end re-reads the last row)
+    uint4 q[kIters];
+    auto load_group = [&](uint32_t g) __attribute__((always_inline)) {
+        const uint32_t row = g * kRowsPerGroup + wave * kRowsPerWave + lane / 16;
+        const uint4 *src = reinterpret_cast<const uint4 *>(w + size_t(row < rows ? row : rows - 1) * kCols);
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const uint32_t c = j + 16 * i;
+            q[i] = ttl::load_stream(src + (c < uint32_t(kChunks) ? c : uint32_t(kChunks) - 1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // the input's loads, then the first group's weight loads, which stream while the
+    // staging (the last layer's combine and the output norm) completes
+    stage::Pending<kCols, kXBlocks, kThreads, MODE> pending;
+    stage::stage_load(in, pending);
+    load_group(blockIdx.x < groups ? blockIdx.x : groups - 1);
+    stage::stage_finish(in, pending, xs, red);
     float bv = NAN;
     int32_t bi = 0x7fffffff;
     if (threadIdx.x == 0) {
@@ -68,14 +85,8 @@ __global__ __launch_bounds__(kThreads) void logits_kernel(const uint16_t *__rest
     for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
         const uint32_t row = g * kRowsPerGroup + wave * kRowsPerWave + lane / 16;
         const bool valid = row < rows;
-        // unconditional loads (a row past the end re-reads the last row)
-        const uint4 *src = reinterpret_cast<const uint4 *>(w + size_t(valid ? row : rows - 1) * kCols);
-        uint4 q[kIters];
-#pragma unroll
-        for (int i = 0; i < kIters; ++i) {
-            const uint32_t c = j + 16 * i;
-            q[i] = ttl::load_stream(src + (c < uint32_t(kChunks) ? c : uint32_t(kChunks) - 1));
-            __builtin_amdgcn_sched_barrier(0);
+        if (g != blockIdx.x) {
+            load_group(g);
         }
         float acc = 0.0f;
 #pragma unroll
