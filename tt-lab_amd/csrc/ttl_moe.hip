@@ -106,10 +106,13 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
         wv[q] = w4[q];
     }
     stage::stage_finish(in, pending, xs, red);
-    // workgroup 0 hands the staged (normalized) input on: the routed gate/up launch stages
-    // it as it is instead of normalizing the same vector again in each of its workgroups
-    if (normed_out && row == 0) {
-        for (uint32_t c = t; c < uint32_t(kRouterCols); c += kRouterThreads) {
+    // the workgroups hand the staged (normalized) input on, a slice each: the routed
+    // gate/up launch stages it as it is instead of normalizing the same vector again in
+    // each of its workgroups
+    if (normed_out) {
+        const uint32_t slice = (uint32_t(kRouterCols) + gridDim.x - 1) / gridDim.x;
+        const uint32_t end = min(uint32_t(kRouterCols), (row + 1) * slice);
+        for (uint32_t c = row * slice + t; c < end; c += kRouterThreads) {
             normed_out[c] = xs[(c / 32) * mxt::x_stride + c % 32];
         }
     }
