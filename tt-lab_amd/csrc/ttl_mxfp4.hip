@@ -142,7 +142,7 @@ __global__ void dequant_kernel(const uint4 *__restrict__ codes, const uint8_t *_
 // One workgroup per (slot, 16-row tile) of the expert selected for the slot
 // (expert_ids[slot], or expert_base + slot without ids: no dependent load): twelve
 // waves split the tile's K range (two 128-column iterations each, so the decode and
-// FMAs left after a wave's last load arrives are a twelfth of the row; 4.63 -> 4.43 us
+// FMAs left after a wave's last load arrives are a twelfth of the row; 4.63-4.70 -> 4.47 us
 // per 5760-row launch against four waves), and their partial sums are added in wave
 // order.  The x loads are issued first, then the weight loads, all unconditionally: an
 // invalid expert reads expert 0 and its rows become NaN.
