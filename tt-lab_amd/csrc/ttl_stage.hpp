@@ -138,13 +138,16 @@ __device__ __attribute__((always_inline)) inline void stage_load(const Input &in
 }
 
 // Completes a staging begun by stage_load(): writes blocks [0, XB) of the padded
-// layout (blocks >= N/32 are zero) and v_out, then applies the norm.
-// blockDim.x == NT.
+// layout (blocks >= N/32 are zero) and v_out, then applies the norm.  With the norm,
+// every wave takes the same sum of squares (the same order in each), so no wave waits
+// on another for the scale, and each thread writes its normalized values to LDS once,
+// from registers.  blockDim.x == NT.
 template <int N, int XB, int NT, int MODE>
 __device__ __attribute__((always_inline)) inline void stage_finish(const Input &in, const Pending<N, XB, NT, MODE> &p,
                                                                    float *xs, float *red) {
 #pragma clang fp contract(off)
     using P = Pending<N, XB, NT, MODE>;
+    float4 kept[P::norm ? P::per : 1];
 #pragma unroll
     for (int j = 0; j < P::per; ++j) {
         const uint32_t i = threadIdx.x + uint32_t(j) * NT;
@@ -182,42 +185,44 @@ __device__ __attribute__((always_inline)) inline void stage_finish(const Input &
                 red[i] = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
         }
-        *reinterpret_cast<float4 *>(xs + (i / 8) * x_stride + (i % 8) * 4) = v;
+        if constexpr (P::norm) {
+            kept[j] = v;
+        } else {
+            *reinterpret_cast<float4 *>(xs + (i / 8) * x_stride + (i % 8) * 4) = v;
+        }
     }
     __syncthreads();
     if constexpr (P::norm) {
-        if (threadIdx.x < 64) {
-            float s = 0.0f;
+        // tensor.cpp:568-580: scale = 1 / sqrt(mean(v^2) + eps); xs = v * scale * w
+        const uint32_t lane = threadIdx.x % 64;
+        float s = 0.0f;
 #pragma unroll
-            for (int k = 0; k < (P::groups + 63) / 64; ++k) {
-                const uint32_t i = threadIdx.x + 64u * uint32_t(k);
-                if (i < uint32_t(P::groups)) {
-                    s = s + red[i];
-                }
-            }
-#pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) {
-                s = s + __shfl_xor(s, d);
-            }
-            if (threadIdx.x == 0) {
-                red[XB * 8] = 1.0f / sqrtf(s / float(N) + in.eps);
+        for (int k = 0; k < (P::groups + 63) / 64; ++k) {
+            const uint32_t i = lane + 64u * uint32_t(k);
+            if (i < uint32_t(P::groups)) {
+                s = s + red[i];
             }
         }
-        __syncthreads();
-        const float scale = red[XB * 8];
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            s = s + __shfl_xor(s, d);
+        }
+        const float scale = 1.0f / sqrtf(s / float(N) + in.eps);
 #pragma unroll
         for (int j = 0; j < P::per; ++j) {
             const uint32_t i = threadIdx.x + uint32_t(j) * NT;
-            if (i < uint32_t(P::groups)) {
-                float4 *q = reinterpret_cast<float4 *>(xs + (i / 8) * x_stride + (i % 8) * 4);
-                float4 v = *q;
-                const float4 w = p.w[j];
-                v.x = v.x * scale * w.x;
-                v.y = v.y * scale * w.y;
-                v.z = v.z * scale * w.z;
-                v.w = v.w * scale * w.w;
-                *q = v;
+            if (i >= uint32_t(XB) * 8) {
+                continue;
             }
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < uint32_t(P::groups)) {
+                const float4 w = p.w[j];
+                v.x = kept[j].x * scale * w.x;
+                v.y = kept[j].y * scale * w.y;
+                v.z = kept[j].z * scale * w.z;
+                v.w = kept[j].w * scale * w.w;
+            }
+            *reinterpret_cast<float4 *>(xs + (i / 8) * x_stride + (i % 8) * 4) = v;
         }
         __syncthreads();
     }
