@@ -252,11 +252,15 @@ int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
 /* f32 / bf16 input computed on the scaled path (ttl_moe_prefill_experts): the
  * activations, and the SwiGLU hidden between the two GEMMs, quantized to MXFP8 (E4M3
  * values with an E8M0 exponent per 32-element block, the smallest exponent at which
- * the block's largest magnitude is at most 448; round to nearest even), then
+ * the block's largest magnitude is at most 448 but never below -127, the smallest
+ * E8M0 scale; round to nearest even), then
  * v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as they are stored.  The
  * products are those of the dequantized values (ttl_mxfp8_dequantize), but the
- * instruction's accumulation is not exact in f32 (one GEMM against the reference's
- * f32 sum of the same dequantized products: relative L2 below 1e-5, measured 7.9e-6).
+ * instruction's accumulation is not exact in f32: within each 32-element block it
+ * drops product bits below 2^-13 of the block's largest product (against the
+ * reference's f32 sum of the same dequantized products: |err| up to 5.3e-6 of
+ * sum |w x| per output; relative L2 7.9e-6 on normal activations, 1.6e-5 to 1.9e-5
+ * on the SwiGLU hidden, whose blocks span a wider range).
  * The SwiGLU hidden is requantized too (its exponential and division on the
  * hardware's approximate instructions, a few ulp, ahead of the 3-bit rounding), so
  * the MoE's output carries the format's own error (relative L2 about 7e-2 on random
@@ -330,6 +334,20 @@ int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev
 int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
                            uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
                            void *workspace_dev, size_t workspace_bytes, uint32_t stages);
+
+/* What a ttl_moe_prefill_experts (or _stages) call left in its workspace, per (token,
+ * rank) pair p = token * used + rank, for checking the stages one by one; call it
+ * after that call with the same layer, x_dtype, count and workspace.  hidden_dev f32
+ * [count * used][expert_hidden] receives the pair's clamped SwiGLU hidden as the down
+ * GEMM reads it (on the scaled path its MXFP8 values; hidden_scales_dev, if non-NULL,
+ * u8 [count * used][90] receives their E8M0 bytes), down_dev f32 [count * used][hidden]
+ * the pair's down row with its bias, before the routing weight.  A pair with an
+ * invalid expert index gets NaN rows.  The reference's moe_batch holds the same values
+ * in its per-expert hidden and down buffers (model.cpp:415-447); no reference
+ * counterpart as an entry point. */
+int ttl_moe_prefill_intermediates(ttl_ctx *ctx, const ttl_moe_layer *layer, int x_dtype, uint32_t count,
+                                  const void *workspace_dev, size_t workspace_bytes, float *hidden_dev,
+                                  float *down_dev, uint8_t *hidden_scales_dev);
 
 /* ---- matvec inputs ----------------------------------------------------------------- *
  * The vector a matvec reads, with the elementwise steps GptOssModel::forward runs

@@ -181,8 +181,9 @@ void orc_layer_forward(const orc_layer *layer, size_t layer_index, size_t positi
  * per-token RMSNorm, the batched Q8_0 matmuls (matmul_add_q8_0), RoPE and the KV
  * store of every token, then attention per token, the output matmul, the residual,
  * moe_batch and the second residual.  x_in/x_out f32 [count][2880]; the caches as in
- * orc_layer_forward.  residual_out [count][2880] may be NULL.  Parity unpinned as a
- * composition: checked against orc_layer_forward token by token within tolerance. */
+ * orc_layer_forward.  residual_out [count][2880] may be NULL.  Pinned against an
+ * independent float64 restatement of the same layer body (tests/brute_force.py,
+ * layer_prefill), with mutation checks on the norms and the attention window. */
 void orc_layer_prefill(const orc_layer *layer, size_t layer_index, size_t first, size_t count, const float *x_in,
                        const float *rope_frequencies, float *key_cache, float *value_cache, int body, float *x_out,
                        float *residual_out);

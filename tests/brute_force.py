@@ -160,25 +160,41 @@ def layer_prefill(layer, layer_index, first, xs, key_cache, value_cache, freqs32
             for t, (x, q) in enumerate(zip(xs, qs))]
 
 
-def mxfp8_dequantize(x):
-    """The MXFP8 values of x's 32-element blocks (the rule of include/ttlab_hip.h,
-    TTL_DTYPE_F32_AS_MXFP8), widened back to float32: exponent X = the smallest with
-    max|x| / 2^X <= 448 (0 for a zero block, -127 when the maximum is an f32
-    subnormal), elements OCP E4M3 of x / 2^X rounded to nearest even; a block with a
-    non-finite value becomes NaN."""
+def mxfp8_exponents(x):
+    """The E8M0 exponent X of each 32-element block of x (the rule of
+    include/ttlab_hip.h, TTL_DTYPE_F32_AS_MXFP8): the smallest X with
+    max|x| / 2^X <= 448, but at least -127 (0 for a zero block; -127 whenever the
+    maximum is at most 448 x 2^-127, f32 subnormals included).  Returns int64 X and
+    bool finite per block (a block with a non-finite value has no exponent)."""
     b = np.asarray(x, np.float32).reshape(-1, 32).astype(np.float64)
     with np.errstate(invalid="ignore"):
         m = np.abs(b).max(axis=1)
     finite = np.isfinite(b).all(axis=1)
     mant, e = np.frexp(np.where(finite, m, 1.0))  # m = mant 2^e, mant in [0.5, 1)
     X = np.where(mant > 0.875, e - 8, e - 9)      # significand 2 mant > 1.75 -> one more
-    X = np.where(m < 2.0 ** -126, -127, X)
-    X = np.where(m > 0, X, 0)
-    v = np.ldexp(np.where(finite[:, None], b, 0.0), -X[:, None])
+    X = np.maximum(X, -127)                       # E8M0 byte 0 (below it X wraps)
+    X = np.where(finite & (m > 0), X, 0)
+    return X.astype(np.int64), finite
+
+
+def e4m3_round(v):
+    """float64 v (|v| below 464) to the nearest OCP E4M3 value, ties to even:
+    3 fraction bits, subnormals in steps of 2^-9."""
     a = np.abs(v)
-    am, ae = np.frexp(np.maximum(a, 2.0 ** -6))
-    step = np.ldexp(1.0, ae - 1 - 3)              # 3 mantissa bits; subnormals step 2^-9
-    q = np.round(a / step) * step                  # numpy rounds half to even
-    out = np.sign(v) * np.ldexp(q, X[:, None])
+    _, ae = np.frexp(np.maximum(a, 2.0 ** -6))
+    step = np.ldexp(1.0, ae - 1 - 3)
+    return np.sign(v) * np.round(a / step) * step  # numpy rounds half to even
+
+
+def mxfp8_dequantize(x, exponents=None):
+    """The MXFP8 values of x's 32-element blocks (mxfp8_exponents), widened back to
+    float32: elements OCP E4M3 of x / 2^X rounded to nearest even; a block with a
+    non-finite value becomes NaN.  exponents (int per block) replaces the rule's X."""
+    b = np.asarray(x, np.float32).reshape(-1, 32).astype(np.float64)
+    X, finite = mxfp8_exponents(x)
+    if exponents is not None:
+        X = np.asarray(exponents, np.int64).reshape(-1)
+    v = np.ldexp(np.where(finite[:, None], b, 0.0), -X[:, None])
+    out = np.ldexp(e4m3_round(v), X[:, None])
     out[~finite] = np.nan
     return out.astype(np.float32).reshape(np.shape(x))

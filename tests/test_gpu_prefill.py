@@ -144,6 +144,40 @@ def test_moe_prefill_experts_matches_oracle(dev, layer8, dtype):
         assert O.rel_l2(got[p], ref[p]) <= TOL, p
 
 
+def test_moe_prefill_intermediates_exact_path(dev, layer8):
+    """The exact path's stages read back per pair (ttl_moe_prefill_intermediates):
+    the SwiGLU hidden against orc_swiglu of the oracle's gate and up, the down row
+    against the oracle's matvec on the device's own hidden (model.cpp:407-447), both
+    within 1e-5; a pair with an invalid expert index reads NaN."""
+    host, device = layer8
+    count, used = 40, 4
+    idx, w = balanced_routing(count, 8, used, 21)
+    idx[5, 2] = 8  # out of range
+    x = O.synth_normal(0x78000131, 0, count * N).reshape(count, N)
+    xb, ib, wb = dev.upload(x), dev.upload(idx), dev.upload(w)
+    dtype = ttlab_amd.TTL_DTYPE_F32
+    ws = dev.alloc(dev.moe_prefill_workspace_bytes(count, 8, used, dtype))
+    out, hid, dwn = dev.alloc(count * N * 4), dev.alloc(count * used * N * 4), dev.alloc(count * used * N * 4)
+    try:
+        dev.moe_prefill_experts(device.desc, xb, dtype, count, ib, wb, out, ws)
+        dev.moe_prefill_intermediates(device.desc, dtype, count, ws, hid, dwn)
+        hidden = hid.download(np.float32).reshape(count, used, N)
+        down = dwn.download(np.float32).reshape(count, used, N)
+        assert np.all(np.isnan(hidden[5, 2])) and np.all(np.isnan(down[5, 2]))
+        for p, r in ((0, 0), (3, 1), (17, 3), (39, 2), (5, 1)):
+            e = int(idx[p, r])
+            gate = O.mxfp4_matvec(host.gate, host.gate_b, N, N, x[p], expert=e, body=O.BODY_DEFAULT)
+            up = O.mxfp4_matvec(host.up, host.up_b, N, N, x[p], expert=e, body=O.BODY_DEFAULT)
+            h = np.empty(N, np.float32)
+            O.lib.orc_swiglu(gate, up, N, h)
+            assert O.rel_l2(hidden[p, r], h) <= TOL, (p, r)
+            d = O.mxfp4_matvec(host.down, host.down_b, N, N, hidden[p, r], expert=e, body=O.BODY_DEFAULT)
+            assert O.rel_l2(down[p, r], d) <= TOL, (p, r)
+    finally:
+        for b in (xb, ib, wb, ws, out, hid, dwn):
+            b.free()
+
+
 def test_moe_prefill_uneven_buckets_and_invalid_index(dev, layer8):
     # experts with 0, 1, 2 and 70 (two tiles) tokens; one pair with an index out of range
     host, device = layer8

@@ -153,3 +153,59 @@ def test_synthetic_q8_0_and_bf16():
     exps = (b >> 7) & 0xFF
     assert set(np.unique(exps)) == {120, 121, 122, 123}
     assert np.array_equal(O.synth_bf16(5, 3, 7, offset=1001), b[1001:1008])
+
+
+# ---- the MXFP8 quantizer of the scaled prefill path (tests/brute_force.py) ----------------
+
+def e4m3_table():
+    """Every finite OCP E4M3 value by code (bits S.EEEE.MMM; E = 0 subnormal m x 2^-9;
+    S.1111.111 is NaN), enumerated from the definition."""
+    vals = {}
+    for code in range(256):
+        e, m, s = (code >> 3) & 15, code & 7, -1.0 if code & 0x80 else 1.0
+        if e == 15 and m == 7:
+            continue
+        vals[code] = s * (m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
+    return vals
+
+
+def test_e4m3_rounding_against_brute_force_nearest():
+    import brute_force as B
+    table = e4m3_table()
+    codes = np.array(list(table), np.int64)
+    values = np.array([table[c] for c in codes])
+    assert values.max() == 448.0 and values[values > 0].min() == 2.0 ** -9
+    rng = np.random.default_rng(3)
+    v = np.concatenate([rng.uniform(-460, 460, 4000), rng.uniform(-0.03, 0.03, 4000),
+                        values, (values[:-1] + values[1:]) / 2])  # grid points and neighbours' midpoints
+    got = B.e4m3_round(v)
+    for x, g in zip(v, got):
+        d = np.abs(values - x)
+        near = codes[d == d.min()]
+        # ties go to the even code (an even mantissa); +0 and -0 are the same value
+        best = [c for c in near if c & 1 == 0] or list(near)
+        assert g == table[int(best[0])], (x, g)
+
+
+def test_mxfp8_exponent_rule_brute_force_and_e8m0_floor():
+    import brute_force as B
+    rng = np.random.default_rng(4)
+    m = np.concatenate([np.ldexp(rng.uniform(0.5, 1.0, 3000), rng.integers(-149, 128, 3000)),
+                        [448.0, np.nextafter(448.0, 500), 1.75, float(np.nextafter(np.float32(1.75), 2)),
+                         2.0 ** -120, 1.5 * 2.0 ** -121, 2.0 ** -126, 1e-40, 1.75 * 2.0 ** -119,
+                         float(np.nextafter(np.float32(1.75 * 2.0 ** -119), 1))]]).astype(np.float32)
+    blocks = np.zeros((m.size, 32), np.float32)
+    blocks[:, 5] = -m
+    blocks[:, 6] = m / 3
+    X, finite = B.mxfp8_exponents(blocks)
+    assert finite.all()
+    for mi, xi in zip(m.astype(np.float64), X):
+        want = next(k for k in range(-127, 200) if mi / 2.0 ** k <= 448.0)  # the smallest, floor -127
+        assert xi == want, (mi, xi, want)
+    # maxima at most 448 x 2^-127 = 1.75 x 2^-119 take E8M0 byte 0 (the rule without the floor
+    # gives -128..-134 below 1.75 x 2^-120) and stay finite, small and exact where E4M3 holds them
+    q = B.mxfp8_dequantize(blocks[-6:-1])
+    assert np.all(X[-6:-1] == -127)
+    assert np.array_equal(q[:3, 5], blocks[-6:-3, 5])  # 2^-120, 1.5 x 2^-121 and 2^-126 are E4M3 x 2^-127
+    assert np.all(np.abs(q[:, 5]) <= np.abs(blocks[-6:-1, 5]) * 1.07)
+    assert B.mxfp8_exponents(blocks[-1:])[0][0] == -126

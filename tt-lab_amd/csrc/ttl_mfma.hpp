@@ -109,7 +109,9 @@ __device__ inline void split_planes(const float (&v)[8], uint4 (&out)[P]) {
 //  - D as in the other 16x16 MFMAs: lane l gets rows 4(l/16)..+3 of column l%16.
 // So activation scale groups are the natural 32-element blocks, as for the weights;
 // only the placement of the fp8 bytes is permuted.  The instruction's accumulation is
-// not exact in f32: measured |D - exact| up to about 6e-5 x sum|a b| per instruction.
+// not exact in f32: within a 32-element K-block the products are aligned to the
+// block's largest and bits below 2^-13 of it are dropped (measured: 256 + 2^-5 kept,
+// 256 + 2^-6 gives 256); block sums and the accumulator are added in f32.
 namespace mx8 {
 
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
@@ -139,16 +141,16 @@ __host__ __device__ inline uint32_t b_byte(uint32_t g, uint32_t e) {
 }
 
 // E8M0 exponent X of a block whose largest magnitude is m (finite): the smallest X
-// with m / 2^X <= 448, the E4M3 maximum, so no element saturates; -127 for a block of
-// zeros or f32 subnormals.  m / 2^(e-8) = significand x 256 exceeds 448 exactly when
-// the significand exceeds 1.75.
+// with m / 2^X <= 448, the E4M3 maximum, so no element saturates, but never below
+// -127, the smallest scale E8M0 holds (byte 0).  m / 2^(e-8) = significand x 256
+// exceeds 448 exactly when the significand exceeds 1.75.  Every block whose maximum is
+// at most 448 x 2^-127 (f32 subnormals included) takes -127; without the floor those
+// with maxima up to 1.75 x 2^-120 would get -128..-134, which the E8M0 byte cannot hold.
 __device__ inline int block_exponent(float m) {
     const uint32_t u = __float_as_uint(m);
     const int e = int((u >> 23) & 0xffu);
-    if (e == 0) {
-        return -127;
-    }
-    return e - 127 - 8 + ((u & 0x7fffffu) > 0x600000u ? 1 : 0);
+    const int x = e - 127 - 8 + ((u & 0x7fffffu) > 0x600000u ? 1 : 0);
+    return x < -127 ? -127 : x;
 }
 
 // OCP E4M3 of a value with |v| <= 448, rounded to nearest even: subnormals m x 2^-9

@@ -1434,6 +1434,73 @@ __global__ __launch_bounds__(256) void mx8_dequantize_kernel(const void *__restr
     }
 }
 
+// ---- the intermediates, read back for inspection -----------------------------------------
+
+// One workgroup per (token, rank) pair p: the pair's SwiGLU hidden as the down GEMM
+// reads it (the MXFP8 codes times their E8M0 scale on the scaled path, the sum of the
+// three bf16 planes otherwise) and its down row (bias included, before the routing
+// weight), from the workspace a full prefill left.  A pair without a slot (invalid
+// expert index) gets NaN rows.  The slot's tile is found by a scan of the plan's tiles.
+template <bool SCALED>
+__global__ __launch_bounds__(256) void prefill_intermediates_kernel(Plan plan, uint32_t rows,
+                                                                    float *__restrict__ hidden_out,
+                                                                    float *__restrict__ down_out,
+                                                                    uint8_t *__restrict__ scales_out) {
+    const uint32_t p = blockIdx.x, t = threadIdx.x;
+    const int32_t slot = plan.pair_slot[p];
+    float *h = hidden_out + size_t(p) * mx::cols;
+    float *d = down_out + size_t(p) * rows;
+    if (slot < 0) {
+        for (uint32_t k = t; k < uint32_t(mx::cols); k += blockDim.x) {
+            h[k] = __builtin_nanf("");
+        }
+        for (uint32_t k = t; k < rows; k += blockDim.x) {
+            d[k] = __builtin_nanf("");
+        }
+        return;
+    }
+    const uint32_t s = uint32_t(slot), tiles = plan.header->tiles;
+    uint32_t tile = 0;
+    for (uint32_t i = 0; i < tiles; ++i) {
+        const uint32_t f = plan.tile_first[i];
+        tile = (s >= f && s < f + plan.tile_count[i]) ? i : tile;
+    }
+    const uint32_t n = s - plan.tile_first[tile], c = n / 16, n16 = n % 16;
+    for (uint32_t k = t; k < uint32_t(mx::cols); k += blockDim.x) {
+        const uint32_t beta = k / 32, e = k % 32, quad = beta / 4, g = beta % 4;
+        float v;
+        if (SCALED) {
+            const uint8_t *hb = plan.hb + size_t(tile) * mf::plane_bytes;
+            const uint32_t code =
+                hb[((size_t(quad) * mf::col_tiles + c) * 64 + n16 + 16 * mx8::b_group(g, e)) * mx8::lane_bytes +
+                   mx8::b_byte(g, e)];
+            const uint32_t sc = hb[mx8::tile_frag_bytes + (size_t(c) * 64 + n16 + 16 * g) * mx8::scale_pad + quad];
+            v = (code & 0x7fu) == mx8::e4m3_nan ? __builtin_nanf("")
+                                                : __builtin_amdgcn_ldexpf(mx8::e4m3_value(code), int(sc) - 127);
+            if (e == 0 && scales_out) {
+                scales_out[size_t(p) * mx::blocks + beta] = uint8_t(sc);
+            }
+        } else {
+            // element e of block beta: K step 4 quad + (e % 16) / 4, lane (beta % 4, n16),
+            // bf16 2 (e % 4) + e / 16 of the lane's 8
+            const uint8_t *hb = plan.hb + size_t(tile) * kHiddenPlanes * mf::plane_bytes;
+            const size_t off = ((size_t(quad) * 4 + (e % 16) / 4) * mf::col_tiles + c) * mf::frag_bytes +
+                               (g * 16 + n16) * 16 + 2 * (2 * (e % 4) + e / 16);
+            v = 0.0f;
+#pragma unroll
+            for (int pl = 0; pl < kHiddenPlanes; ++pl) {
+                v += __uint_as_float(uint32_t(*reinterpret_cast<const uint16_t *>(hb + size_t(pl) * mf::plane_bytes +
+                                                                                  off))
+                                     << 16);
+            }
+        }
+        h[k] = v;
+    }
+    for (uint32_t k = t; k < rows; k += blockDim.x) {
+        d[k] = plan.down[size_t(s) * rows + k];
+    }
+}
+
 // ---- combine ----------------------------------------------------------------------------
 
 // out[p][i] = sum over token p's slots in slot order (= expert order) of
@@ -1774,6 +1841,45 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         combine_for(L.used, plan, count, L.hidden, out_dev, ctx->stream);
         TTL_LAUNCHED("combine_kernel");
     }
+    return TTL_OK;
+}
+
+int ttl_moe_prefill_intermediates(ttl_ctx *ctx, const ttl_moe_layer *layer, int x_dtype, uint32_t count,
+                                  const void *workspace_dev, size_t workspace_bytes, float *hidden_dev,
+                                  float *down_dev, uint8_t *hidden_scales_dev) {
+    TTL_REQUIRE(ctx && layer && workspace_dev && hidden_dev && down_dev, TTL_ERR_INVALID,
+                "ttl_moe_prefill_intermediates: null argument");
+    TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_F32_AS_MXFP8 ||
+                    x_dtype == TTL_DTYPE_BF16_AS_MXFP8,
+                TTL_ERR_INVALID, "ttl_moe_prefill_intermediates: unknown x_dtype %d", x_dtype);
+    TTL_REQUIRE(layer->hidden == uint32_t(mx::cols) && layer->expert_hidden == uint32_t(mx::cols), TTL_ERR_SHAPE,
+                "ttl_moe_prefill_intermediates: hidden and expert_hidden must be %d", mx::cols);
+    TTL_REQUIRE(layer->used >= 1 && layer->used <= kMaxUsed && layer->experts >= 1 && layer->experts <= kMaxExperts,
+                TTL_ERR_SHAPE, "ttl_moe_prefill_intermediates: used must be 1..%u and experts 1..%u", kMaxUsed,
+                kMaxExperts);
+    TTL_REQUIRE(uint64_t(count) * layer->used <= kMaxEntries, TTL_ERR_SHAPE,
+                "ttl_moe_prefill_intermediates: count * used above %u", kMaxEntries);
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 255) == 0, TTL_ERR_INVALID,
+                "ttl_moe_prefill_intermediates: workspace must be 256-byte aligned");
+    if (count == 0) {
+        return TTL_OK;
+    }
+    const uint32_t pairs = count * layer->used;
+    const bool scaled = x_dtype == TTL_DTYPE_F32_AS_MXFP8 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
+    const bool bf16 = x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
+    const Layout lay = make_layout(pairs, layer->experts, (bf16 || scaled) ? 1 : 3, true, layer->hidden);
+    TTL_REQUIRE(workspace_bytes >= lay.total, TTL_ERR_SHAPE,
+                "ttl_moe_prefill_intermediates: workspace of %zu bytes, %zu needed for this count and x_dtype",
+                workspace_bytes, lay.total);
+    const Plan plan = plan_at(const_cast<void *>(workspace_dev), lay);
+    if (scaled) {
+        prefill_intermediates_kernel<true><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
+                                                                            down_dev, hidden_scales_dev);
+    } else {
+        prefill_intermediates_kernel<false><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
+                                                                             down_dev, hidden_scales_dev);
+    }
+    TTL_LAUNCHED("prefill_intermediates_kernel");
     return TTL_OK;
 }
 

@@ -312,6 +312,7 @@ def load_library():
         "ttl_moe_prefill_workspace_bytes": (sz, [u32, u32, u32, i32]),
         "ttl_moe_prefill_experts": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz]),
         "ttl_moe_prefill_stages": (i32, [vp, C.POINTER(MoeLayerDesc), vp, i32, u32, vp, vp, vp, vp, sz, u32]),
+        "ttl_moe_prefill_intermediates": (i32, [vp, C.POINTER(MoeLayerDesc), i32, u32, vp, sz, vp, vp, vp]),
         "ttl_moe_prefill_batch_workspace_bytes": (sz, [u32, u32, u32]),
         "ttl_moe_prefill": (i32, [vp, C.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp, vp, sz]),
         "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
@@ -700,6 +701,14 @@ class Device:
             _check(self.lib.ttl_moe_prefill_stages(self.ctx, C.byref(layer), x.ptr, x_dtype, count, indices.ptr,
                                                    weights.ptr, out.ptr, workspace.ptr, workspace.nbytes, stages),
                    "ttl_moe_prefill_stages")
+
+    def moe_prefill_intermediates(self, layer, x_dtype, count, workspace, hidden, down, hidden_scales=None):
+        """Each (token, rank) pair's SwiGLU hidden and down row from the workspace of a
+        moe_prefill_experts call with the same arguments."""
+        _check(self.lib.ttl_moe_prefill_intermediates(self.ctx, C.byref(layer), x_dtype, count, workspace.ptr,
+                                                      workspace.nbytes, hidden.ptr, down.ptr,
+                                                      hidden_scales.ptr if hidden_scales is not None else None),
+               "ttl_moe_prefill_intermediates")
 
     def moe_prefill(self, layer, x, count, out, indices=None, weights=None):
         """GptOssModel::moe_batch on the device (router + experts); allocates its workspace."""
