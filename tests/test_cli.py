@@ -48,3 +48,11 @@ def test_inspect_prints_the_shape(tmp_path):
     assert done.returncode == 0, done.stderr
     assert done.stdout.strip() == f"gpt-oss model: {LAYERS} layers, {EXPERTS} experts, vocabulary {VOCAB}, " \
                                   "output.weight type 8"
+
+
+def test_run_requires_the_end_of_sequence_id(tmp_path):
+    """main.cpp:379 reads tokenizer.ggml.eos_token_id with GgufFile::integer, which
+    throws for a missing key; the run loop does the same before it opens a device."""
+    done = cli("run", "-m", model_file(tmp_path), "--loose", "-t", "1,2", "-n", "2")
+    assert done.returncode == 1
+    assert done.stderr.strip() == "error: missing GGUF key: tokenizer.ggml.eos_token_id"

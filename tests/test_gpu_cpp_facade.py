@@ -11,7 +11,12 @@ Makefile as tt-lab_amd/build/facade_check), on a GGUF file written here.
 - HipTensorBackend, the tensor.h functions: the embedding row and the F32 router
   matvec (the exact path) equal the oracle's bit for bit; rms_norm, the Q8_0 and
   MXFP4 matvecs and the selected-token matmul agree with it to relative L2 <= 1e-5;
-  rows the selection does not name stay untouched.
+  rows the selection does not name stay untouched.  After the first file is closed,
+  the same MXFP4 call on a second file of the same shapes uses the second file's
+  weights.
+Every facade call in the caller goes through types shaped like the reference's
+GgufTensor and GgufFile (gguf.h:38-72), and the model is built with the reference's
+constructor arguments (model.h:19-20).
 """
 import os
 import subprocess
@@ -40,13 +45,25 @@ def run(tmp_path_factory):
     tensors = gpt_oss_tensors(LAYERS, EXPERTS, VOCAB, generated, GGML_Q8_0)
     tmp = tmp_path_factory.mktemp("facade")
     path = os.path.join(tmp, "gpt-oss-small.gguf")
-    write_gguf(path, gpt_oss_metadata(LAYERS, EXPERTS), tensors)
-    print(f"running {BINARY} on {path}", flush=True)
-    done = subprocess.run([BINARY, path, str(tmp), str(LIMIT)] + [str(t) for t in PROMPT], capture_output=True,
-                          text=True, timeout=300)
+    # an end-of-sequence id no argmax can produce (the run loop requires the key, as
+    # main.cpp does), so the command line generates to its limit
+    write_gguf(path, gpt_oss_metadata(LAYERS, EXPERTS) + [("tokenizer.ggml.eos_token_id", U32, VOCAB)], tensors)
+    # a second file of the same shapes with other weights
+    def moved(name, nbytes):
+        data = generated(name, nbytes)
+        # the expert blocks one block further on: valid MXFP4, other weights per row
+        return np.roll(data.reshape(-1, 17), 1, axis=0).ravel() if name.endswith("_exps.weight") else data
+
+    other = gpt_oss_tensors(LAYERS, EXPERTS, VOCAB, moved, GGML_Q8_0)
+    second = os.path.join(tmp, "gpt-oss-small-second.gguf")
+    write_gguf(second, gpt_oss_metadata(LAYERS, EXPERTS) + [("tokenizer.ggml.eos_token_id", U32, VOCAB)], other)
+    print(f"running {BINARY} on {path} (then {second})", flush=True)
+    done = subprocess.run([BINARY, "--second", second, path, str(tmp), str(LIMIT)] + [str(t) for t in PROMPT],
+                          capture_output=True, text=True, timeout=300)
     print(done.stdout, done.stderr)
     assert done.returncode == 0, done.stderr
     t = {name: data for name, _, _, data in tensors}
+    t.update({"second/" + name: data for name, _, _, data in other})
     return str(tmp), path, t
 
 
@@ -79,6 +96,8 @@ def test_reference_error_messages(run):
     assert lines[2] == "prefill exceeds startup batch capacity"
     assert lines[3] == "prefill needs at least one token"
     assert lines[4] == f"cannot open {tmp}/no-such-model.gguf: No such file or directory"
+    assert lines[5] == "tensor dumps are not supported by the gfx950 backend"
+    assert lines[6] == "batch capacity exceeds token capacity"  # model.cpp:105-107
 
 
 def test_tensor_functions_against_oracle(run):
@@ -108,6 +127,10 @@ def test_tensor_functions_against_oracle(run):
     O.lib.orc_matvec_add_mxfp4(t["blk.0.ffn_gate_exps.weight"], t["blk.0.ffn_gate_exps.bias"], N, N, normed, gate,
                                expert, O.BODY_DEFAULT)
     assert O.rel_l2(floats(tmp, "mxfp4.f32"), gate) <= TOL
+    # the second file's gate, on the same input, after the first file was closed
+    O.lib.orc_matvec_add_mxfp4(t["second/blk.0.ffn_gate_exps.weight"], t["second/blk.0.ffn_gate_exps.bias"], N, N,
+                               normed, gate, expert, O.BODY_DEFAULT)
+    assert O.rel_l2(floats(tmp, "mxfp4_second.f32"), gate) <= TOL
 
 
 def test_selected_matmul_against_oracle(run):

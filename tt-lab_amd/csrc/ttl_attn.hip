@@ -261,7 +261,8 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
     const Span sp = span_of(pos < capacity ? pos : 0u, layer_index);
     const uint32_t n = sp.count;  // 1..128
 
-    constexpr int kPer = kWindow * (kHead / 4) / kWinThreads;  // 8 float4 of K and of V per thread
+    constexpr int kPer = kWindow * (kHead / 4) / kWinThreads;  // 4 float4 of K and of V per thread
+    static_assert(kPer == 4, "the window of 128 positions over 512 threads");
     float4 kr[kPer], vr[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {

@@ -6,6 +6,8 @@
 // file.  Errors are std::runtime_error with the reference's messages.
 #pragma once
 
+#include "gguf_source.hpp"  // gguf_row_bytes
+
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -77,8 +79,5 @@ class GgufFile {
     std::vector<GgufTensorInfo> tensors_;
     std::unordered_map<std::string_view, size_t> tensor_index_;
 };
-
-// Bytes of one row (the first dimension) of a tensor of `type` (tensor.cpp:136-157).
-size_t gguf_row_bytes(uint32_t type, uint64_t n);
 
 }  // namespace ttlab

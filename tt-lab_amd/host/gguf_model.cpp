@@ -16,37 +16,46 @@ constexpr uint64_t kHidden = 2880, kQueryWidth = 4096, kKvWidth = 512, kQkvRows 
 constexpr uint64_t kLayerCapacity = 36, kExpertCapacity = 128, kVocabulary = 201088;
 
 // require_integer / require_number (model.cpp:24-34)
-void require_integer(const GgufFile &file, const char *key, uint64_t expected) {
+void require_integer(const GgufSource &file, const char *key, uint64_t expected) {
     if (file.integer(key) != expected) {
         throw std::runtime_error("unsupported " + std::string(key));
     }
 }
-void require_number(const GgufFile &file, const char *key, double expected) {
+void require_number(const GgufSource &file, const char *key, double expected) {
     if (file.number(key) != expected) {
         throw std::runtime_error("unsupported " + std::string(key));
     }
 }
 
 // require_tensor (model.cpp:209-228)
-const GgufTensorInfo &require_tensor(const GgufFile &file, const std::string &name, uint32_t type,
-                                     std::initializer_list<uint64_t> shape) {
-    const GgufTensorInfo *t = file.tensor(name);
-    if (!t) {
+TensorRef require_tensor(const GgufSource &file, const std::string &name, uint32_t type,
+                         std::initializer_list<uint64_t> shape) {
+    TensorRef t;
+    if (!file.tensor(name, &t)) {
         throw std::runtime_error("missing tensor " + name);
     }
-    if (t->type != type) {
+    if (t.type != type) {
         throw std::runtime_error("wrong type for tensor " + name);
     }
-    if (t->shape.size() != shape.size()) {
+    if (t.dims != shape.size()) {
         throw std::runtime_error("wrong rank for tensor " + name);
     }
     size_t i = 0;
     for (uint64_t expected : shape) {
-        if (t->shape[i++] != expected) {
+        if (t.shape[i++] != expected) {
             throw std::runtime_error("wrong shape for tensor " + name);
         }
     }
-    return *t;
+    return t;
+}
+
+// A tensor check_gguf_source() has already required.
+TensorRef checked_tensor(const GgufSource &file, const std::string &name) {
+    TensorRef t;
+    if (!file.tensor(name, &t)) {
+        throw std::runtime_error("missing tensor " + name);
+    }
+    return t;
 }
 
 std::string layer_prefix(size_t l) {
@@ -55,7 +64,7 @@ std::string layer_prefix(size_t l) {
 
 }  // namespace
 
-GgufModelShape check_gguf_model(const GgufFile &file, bool strict) {
+GgufModelShape check_gguf_source(const GgufSource &file, bool strict) {
     if (file.string("general.architecture") != "gpt-oss") {
         throw std::runtime_error("model architecture is not gpt-oss");
     }
@@ -88,10 +97,10 @@ GgufModelShape check_gguf_model(const GgufFile &file, bool strict) {
     GgufModelShape shape;
     shape.layers = uint32_t(layers);
     shape.experts = uint32_t(experts);
-    const GgufTensorInfo *embd = file.tensor("token_embd.weight");
+    TensorRef embd;
     uint64_t vocab = kVocabulary;
-    if (!strict && embd && embd->shape.size() == 2) {
-        vocab = embd->shape[1];
+    if (!strict && file.tensor("token_embd.weight", &embd) && embd.dims == 2) {
+        vocab = embd.shape[1];
         if (vocab < 16 || vocab % 16 != 0 || vocab > (1ull << 31)) {
             throw std::runtime_error("wrong shape for tensor token_embd.weight");
         }
@@ -99,8 +108,9 @@ GgufModelShape check_gguf_model(const GgufFile &file, bool strict) {
     shape.vocab = uint32_t(vocab);
     require_tensor(file, "token_embd.weight", kGgmlQ8_0, {kHidden, vocab});
     require_tensor(file, "output_norm.weight", kGgmlF32, {kHidden});
-    const GgufTensorInfo *out = file.tensor("output.weight");
-    const uint32_t out_type = (!strict && out && out->type == kGgmlBf16) ? kGgmlBf16 : kGgmlQ8_0;
+    TensorRef out;
+    const uint32_t out_type = (!strict && file.tensor("output.weight", &out) && out.type == kGgmlBf16) ? kGgmlBf16
+                                                                                                       : kGgmlQ8_0;
     require_tensor(file, "output.weight", out_type, {kHidden, vocab});
     shape.output_type = out_type;
     for (size_t l = 0; l < layers; ++l) {
@@ -128,10 +138,10 @@ GgufModelShape check_gguf_model(const GgufFile &file, bool strict) {
     return shape;
 }
 
-void HipGptOssModel::upload_gguf(const GgufFile &file) {
+void HipGptOssModel::upload_gguf(const GgufSource &file) {
     const uint32_t E = spec_.experts;
     auto f32 = [&](const std::string &name) {
-        const GgufTensorInfo &t = *file.tensor(name);
+        const TensorRef t = checked_tensor(file, name);
         float *p = static_cast<float *>(alloc(t.bytes));
         check(ttl_memcpy_h2d(ctx_, p, t.data, t.bytes), "ttl_memcpy_h2d");
         return p;
@@ -145,7 +155,7 @@ void HipGptOssModel::upload_gguf(const GgufFile &file) {
     };
     auto mxfp4 = [&](const std::string &name) {
         ttl_mxfp4 *t = nullptr;
-        check(ttl_mxfp4_upload(ctx_, file.tensor(name)->data, uint32_t(kHidden), uint32_t(kHidden), E, &t),
+        check(ttl_mxfp4_upload(ctx_, checked_tensor(file, name).data, uint32_t(kHidden), uint32_t(kHidden), E, &t),
               "ttl_mxfp4_upload");
         device_bytes_ += ttl_mxfp4_bytes(t);
         return t;
@@ -164,8 +174,8 @@ void HipGptOssModel::upload_gguf(const GgufFile &file) {
         layer.post_norm = f32(p + "post_attention_norm.weight");
         size_t at = 0, bat = 0;
         for (const char *part : {"attn_q", "attn_k", "attn_v"}) {
-            const GgufTensorInfo &w = *file.tensor(p + part + ".weight");
-            const GgufTensorInfo &b = *file.tensor(p + part + ".bias");
+            const TensorRef w = checked_tensor(file, p + part + ".weight");
+            const TensorRef b = checked_tensor(file, p + part + ".bias");
             std::memcpy(qkv.data() + at, w.data, w.bytes);
             std::memcpy(qkv_bias.data() + bat, b.data, b.bytes);
             at += w.bytes;
@@ -174,8 +184,8 @@ void HipGptOssModel::upload_gguf(const GgufFile &file) {
         layer.qkv = q8(qkv.data(), uint32_t(kQkvRows), uint32_t(kHidden), qkv_rows.data(), uint32_t(kQkvRows));
         layer.qkv_bias = static_cast<float *>(alloc(sizeof(float) * kQkvRows));
         check(ttl_memcpy_h2d(ctx_, layer.qkv_bias, qkv_bias.data(), sizeof(float) * kQkvRows), "ttl_memcpy_h2d");
-        layer.attn_output = q8(file.tensor(p + "attn_output.weight")->data, uint32_t(kHidden), uint32_t(kQueryWidth),
-                               nullptr, uint32_t(kHidden));
+        layer.attn_output = q8(checked_tensor(file, p + "attn_output.weight").data, uint32_t(kHidden),
+                               uint32_t(kQueryWidth), nullptr, uint32_t(kHidden));
         layer.attn_output_bias = f32(p + "attn_output.bias");
         layer.sinks = f32(p + "attn_sinks.weight");
         layer.router = f32(p + "ffn_gate_inp.weight");
@@ -207,11 +217,11 @@ void HipGptOssModel::upload_gguf(const GgufFile &file) {
         m.input_norm = layer.post_norm;  // model.cpp:590
         m.input_norm_epsilon = norm_epsilon;
     }
-    const GgufTensorInfo &embd = *file.tensor("token_embd.weight");
+    const TensorRef embd = checked_tensor(file, "token_embd.weight");
     embedding_ = static_cast<uint8_t *>(alloc(embd.bytes));
     check(ttl_memcpy_h2d(ctx_, embedding_, embd.data, embd.bytes), "ttl_memcpy_h2d");
     output_norm_ = f32("output_norm.weight");
-    const GgufTensorInfo &out = *file.tensor("output.weight");
+    const TensorRef out = checked_tensor(file, "output.weight");
     if (out.type == kGgmlBf16) {
         unembedding_ = static_cast<uint16_t *>(alloc(out.bytes));
         check(ttl_memcpy_h2d(ctx_, unembedding_, out.data, out.bytes), "ttl_memcpy_h2d");

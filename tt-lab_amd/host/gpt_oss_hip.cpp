@@ -4,6 +4,8 @@
 // with no host work and feeds its own greedy token to the next step.
 #include "gpt_oss_hip.hpp"
 
+#include "gguf.hpp"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -76,10 +78,25 @@ HipGptOssModel::HipGptOssModel(const SyntheticSpec &spec, int device) : spec_(sp
     }
 }
 
-HipGptOssModel::HipGptOssModel(const GgufFile &file, size_t token_capacity, int device, bool strict) {
-    const GgufModelShape shape = check_gguf_model(file, strict);
-    if (token_capacity < 1 || token_capacity > context_length) {
-        throw std::runtime_error("token capacity exceeds model context");  // model.cpp:99-101
+HipGptOssModel::HipGptOssModel(const GgufFile &file, size_t token_capacity, int device, bool strict)
+    : HipGptOssModel(GgufSourceOf<GgufFile>(file), token_capacity, std::string(), 0, device, strict) {}
+
+HipGptOssModel::HipGptOssModel(const GgufSource &file, size_t token_capacity, const std::string &dump_directory,
+                               size_t batch_capacity, int device, bool strict) {
+    const GgufModelShape shape = check_gguf_source(file, strict);
+    // model.cpp:99-107, in the reference's order
+    if (token_capacity > context_length) {
+        throw std::runtime_error("token capacity exceeds model context");
+    }
+    if (batch_capacity > token_capacity) {
+        throw std::runtime_error("batch capacity exceeds token capacity");
+    }
+    if (!dump_directory.empty()) {
+        throw std::runtime_error("tensor dumps are not supported by the gfx950 backend");
+    }
+    if (token_capacity < 1) {
+        // the reference builds a model without KV caches, which no forward can use
+        throw std::runtime_error("the gfx950 backend needs a token capacity of at least 1");
     }
     spec_.layers = shape.layers;
     spec_.experts = shape.experts;

@@ -3,6 +3,7 @@
 // device operation goes through the C ABI in include/ttlab_hip.h.
 #pragma once
 
+#include "gguf_source.hpp"
 #include "ttlab_hip.h"
 
 #include <array>
@@ -10,6 +11,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 namespace ttlab {
@@ -72,7 +74,13 @@ struct GgufModelShape {
     uint32_t layers = 0, experts = 0, vocab = 0;
     uint32_t output_type = 0;  // GGML type id of output.weight: 8 (Q8_0) or 30 (BF16)
 };
-GgufModelShape check_gguf_model(const GgufFile &file, bool strict);
+GgufModelShape check_gguf_source(const GgufSource &file, bool strict);
+// The same checks on any file class with the reference's accessors (ttlab::GgufFile,
+// the reference's GgufFile).
+template <class File>
+GgufModelShape check_gguf_model(const File &file, bool strict) {
+    return check_gguf_source(GgufSourceOf<File>(file), strict);
+}
 
 class HipGptOssModel {
   public:
@@ -87,6 +95,18 @@ class HipGptOssModel {
     // the device; the file may be closed afterwards.  token_capacity as the reference's
     // constructor (model.cpp:64, 99-101).
     HipGptOssModel(const GgufFile &file, size_t token_capacity, int device = 0, bool strict = true);
+    // The reference's constructor (model.h:19-20) for any file class with its accessors
+    // (the reference's own GgufFile included), so `GptOssModel model(file, capacity,
+    // dump_directory, batch)` compiles against this class, with the reference's
+    // capacity checks (model.cpp:99-107).  batch_capacity sizes the reference's prefill
+    // buffers; the device prefill picks its own chunk and otherwise ignores it.  Tensor
+    // dumps (dump_directory) are not part of this backend: a non-empty one throws, as
+    // does a capacity of 0 (a model no forward could use).  device and strict follow
+    // the reference's parameters, with its defaults.
+    template <class File, class = std::enable_if_t<!std::is_base_of_v<GgufSource, File>>>
+    explicit HipGptOssModel(const File &file, size_t token_capacity = 0, std::string dump_directory = {},
+                            size_t batch_capacity = 0, int device = 0, bool strict = true)
+        : HipGptOssModel(GgufSourceOf<File>(file), token_capacity, dump_directory, batch_capacity, device, strict) {}
     ~HipGptOssModel();
     HipGptOssModel(const HipGptOssModel &) = delete;
     HipGptOssModel &operator=(const HipGptOssModel &) = delete;
@@ -162,10 +182,12 @@ class HipGptOssModel {
         ttl_moe_layer moe{};
     };
 
+    HipGptOssModel(const GgufSource &file, size_t token_capacity, const std::string &dump_directory,
+                   size_t batch_capacity, int device, bool strict);
     void *alloc(size_t bytes);
     void release();
     void generate_weights();
-    void upload_gguf(const GgufFile &file);
+    void upload_gguf(const GgufSource &file);
     void finish_construction();
     int enqueue_step();
     ttl_stage_input layer_input(size_t layer, const float *norm_weight) const;

@@ -8,8 +8,8 @@
 //
 // `run` prefills the prompt, then generates as the reference's greedy / forward loop does
 // (the forwards run on the device in chunks) until the end-of-sequence id
-// (tokenizer.ggml.eos_token_id) or the generation limit, printing each generated id; the
-// timing lines on stderr have the reference's format.  `inspect` applies the model checks
+// (tokenizer.ggml.eos_token_id, required as in the reference) or the generation limit,
+// printing each generated id; the timing lines on stderr have the reference's format.  `inspect` applies the model checks
 // (model.cpp:64-206) without a device and prints the shape it found.  Errors print
 // "error: <message>" and exit 1, usage errors exit 2, as main.cpp does.  --loose admits
 // the small test models (check_gguf_model(file, false)).
@@ -146,11 +146,9 @@ int main(int argc, char **argv) {
         if (limit > context - prompt.size()) {
             throw std::runtime_error("prompt and generation exceed the model context");
         }
-        // main.cpp:373-411: the end-of-sequence id ends the generation (a file without the
-        // key generates to the limit)
-        const int64_t eos = file.find("tokenizer.ggml.eos_token_id")
-                                ? int64_t(file.integer("tokenizer.ggml.eos_token_id"))
-                                : -1;
+        // main.cpp:373-411: the end-of-sequence id ends the generation; like the
+        // reference, a file without the key is an error (GgufFile::integer throws)
+        const int32_t eos = int32_t(file.integer("tokenizer.ggml.eos_token_id"));
         ttlab::HipGptOssModel model(file, prompt.size() + limit, int(device), strict);
         const auto prefill_begin = std::chrono::steady_clock::now();
         const float *logits = model.prefill(prompt.data(), prompt.size());
@@ -159,11 +157,12 @@ int main(int argc, char **argv) {
         // in chunks: generate() feeds each step's argmax (the same first-maximum rule as
         // greedy) to the next step without a host round trip, and the chunk's tokens are
         // then printed, stopping at the end-of-sequence id as the reference does.  Steps a
-        // chunk runs past that id are discarded and not counted.
+        // chunk runs past that id are discarded and neither counted nor timed: each
+        // counted forward adds its chunk's time divided by the chunk's steps.
         constexpr size_t kChunk = 32;
         std::vector<int32_t> pending{model.greedy(logits)};
         size_t next_index = 0, generated = 0, evaluations = 0;
-        double decode_seconds = 0.0;
+        double decode_seconds = 0.0, step_seconds = 0.0;
         int32_t last = -1;
         for (size_t i = 0; i < limit; ++i) {
             if (next_index == pending.size()) {
@@ -171,12 +170,13 @@ int main(int argc, char **argv) {
                 const size_t steps = std::min(kChunk, limit - i);
                 const auto begin = std::chrono::steady_clock::now();
                 pending = model.generate(last, prompt.size() + i - 1, steps);
-                decode_seconds += seconds(begin, std::chrono::steady_clock::now());
+                step_seconds = seconds(begin, std::chrono::steady_clock::now()) / double(steps);
                 next_index = 0;
             }
             const int32_t next = pending[next_index++];
             if (i > 0) {
                 ++evaluations;  // the forward that produced this token (main.cpp counts it)
+                decode_seconds += step_seconds;
             }
             if (next == eos) {
                 break;
