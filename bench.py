@@ -13,7 +13,9 @@ back on the device) and value = tokens/s.
 roofline: the MXFP4 gate/up + SwiGLU expert kernel (the path's dominant kernel),
 timed live with HIP events around a graph of the 24 layers' launches; bytes per
 launch are the 4 selected experts' gate and up rows, their biases, x and the
-SwiGLU output.
+SwiGLU output.  The line's
+"matvec" field is config 0 (one 5760x2880 MXFP4 matvec over 1.13 GB of rotated
+matrices), measured in the same run: the metric's "MXFP4 matvec GB/s".
 
 cpu_baseline: the CPU oracle's restatement of the reference's forward
 (model.cpp:557-602) on one host core, over a bounded sample: one sliding-window
@@ -49,6 +51,9 @@ SEED = 0x77000003
 # Algorithmic bytes of one gate/up+SwiGLU launch: 4 experts x (gate + up) x 2880 rows x
 # 1530 B, their f32 biases, x (f32 2880) read, hidden (f32 4x2880) written.
 GATEUP_BYTES = USED * 2 * N * 1530 + USED * 2 * N * 4 + N * 4 + USED * N * 4
+# Algorithmic bytes of the step's one-launch gate/up + down: the 4 experts' gate, up and
+# down rows and biases, x, and the down outputs (the hidden stays inside the launch).
+GATEUP_DOWN_BYTES = USED * 3 * N * 1530 + USED * 3 * N * 4 + N * 4 + USED * N * 4
 Q8_ROW_2880, Q8_ROW_4096 = 90 * 34, 128 * 34
 # The committed rocprofv3 summary the measured HBM bytes per launch come from
 # (FETCH_SIZE and WRITE_SIZE runs, scaled on a known-size copy).
@@ -84,6 +89,8 @@ def step_kernel_bytes(kind, position, experts, vocab):
         return experts * N * 4 + experts * 4 + 2 * N * 4
     if kind in ("gateup_routed", "gateup_given"):
         return GATEUP_BYTES
+    if kind == "gateup_down":
+        return GATEUP_DOWN_BYTES
     if kind == "down":  # 4 experts' down rows and biases, hidden in, 4 outputs
         return USED * N * 1530 + 3 * USED * N * 4
     if kind == "logits":  # bf16 unembedding; residual, 4 down outputs, norm; logits out
@@ -148,9 +155,14 @@ def gpu_decode(args):
     model_bytes = model.device_bytes
     log(f"model resident: {model_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
     t0 = time.time()
-    filled = model.generate(1, 0, context)
-    log(f"KV caches filled to {context} positions by decoding ({time.time() - t0:.1f} s)")
-    token = int(filled[-1])
+    if args.kv_fill == "synthetic":
+        model.fill_kv_synthetic(context)
+        token = 1
+        log(f"KV caches filled to {context} positions with synthetic values ({time.time() - t0:.1f} s)")
+    else:
+        filled = model.generate(1, 0, context)
+        log(f"KV caches filled to {context} positions by decoding ({time.time() - t0:.1f} s)")
+        token = int(filled[-1])
     ms = model.time_decode(token, context, args.warmup, args.steps)
     tok_s = 1000.0 / ms
     mid = context + args.warmup + args.steps // 2
@@ -169,7 +181,9 @@ def gpu_decode(args):
         gbs = nbytes / (us_k * 1e-6) / 1e9
         kernels[kind] = {"us": round(us_k, 3), "launches_per_step": n, "bytes_per_launch": nbytes,
                          "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-        if kind != "gateup_given":
+        # the step runs gate/up with its ranking (routed) and down as two launches; gate/up
+        # with the indices given and the one-launch gate/up + down are timed for comparison
+        if kind not in ("gateup_given", "gateup_down"):
             total_us += us_k * n
         log(f"{kind:17s} {n:3d} launches x {us_k:7.2f} us, {gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
     log(f"sum of the step's kernels timed one kind at a time: {total_us / 1000:.4f} ms (step {ms:.4f} ms)")
@@ -179,8 +193,16 @@ def gpu_decode(args):
     us_read = read_ceiling(GATEUP_BYTES, args.layers)
     log(f"plain read of the same {GATEUP_BYTES / 1e6:.1f} MB per launch: {us_read:.2f} us, "
         f"{GATEUP_BYTES / (us_read * 1e-6) / 1e9:.0f} GB/s")
-    given = kernels["gateup_given"]
+    given, fused = kernels["gateup_given"], kernels["gateup_down"]
+    if args.table:
+        write_table(args.table, args, ms, step_bytes, kernels, total_us, us_read)
+    # the metric's second half: config 0's standalone MXFP4 matvec, in the same run
+    mv_us, mv_gbs, mv_read = measure_matvec(args)
+    matvec = {"workload": MATVEC_WORKLOAD, "kernel": "matvec_kernel", "bytes_per_launch": MATVEC_BYTES,
+              "launch_us": round(mv_us, 3), "GBps": round(mv_gbs, 1), "frac": round(mv_gbs / HBM_PEAK_GBS, 4),
+              "read_ceiling": ceiling_entry(mv_gbs, MATVEC_BYTES, mv_read)}
     return {
+        "matvec": matvec,
         "value": tok_s,
         "unit": "tok/s",
         "ms_per_step": ms,
@@ -205,8 +227,32 @@ def gpu_decode(args):
                      "bytes_per_launch": GATEUP_BYTES, "launch_us": round(us, 3),
                      "given_indices": {"kernel": "gateup_swiglu_kernel<1, false, 3>", "launch_us": given["us"],
                                        "GBps": given["GBps"], "frac": given["frac"]},
+                     "one_launch_with_down": {"kernel": "gateup_down_kernel<0, true, 1> (not the step's: its "
+                                                        "in-launch handoff costs more than the kernel boundary)",
+                                              "bytes_per_launch": GATEUP_DOWN_BYTES, "launch_us": fused["us"],
+                                              "GBps": fused["GBps"], "frac": fused["frac"]},
                      "read_ceiling": ceiling_entry(achieved, GATEUP_BYTES, us_read)},
     }
+
+
+def write_table(path, args, ms, step_bytes, kernels, total_us, us_read):
+    """The decode run's per-kind kernel table (HIP events around graph replays of every
+    launch of one kind in a step), as text, for committing beside a rocprof summary
+    of the same invocation."""
+    mode = "eager launches" if args.eager else "graph replays"
+    lines = [f"# bench.py per-kind decode kernel table (HIP events, {mode}): config {args.config}, "
+             f"{args.layers} layers, KV context {args.context}",
+             f"#   command: python3 bench.py {' '.join(sys.argv[1:])}",
+             f"#   step: {ms:.4f} ms per token, {1000.0 / ms:.1f} tok/s, {step_bytes / 1e9:.3f} GB algorithmic",
+             f"# {'kind':17s} {'launches':>8s} {'us':>8s} {'bytes':>12s} {'GB/s':>8s} {'frac':>7s}"]
+    for kind, k in kernels.items():
+        lines.append(f"  {kind:17s} {k['launches_per_step']:8d} {k['us']:8.3f} {k['bytes_per_launch']:12d} "
+                     f"{k['GBps']:8.1f} {k['frac']:7.4f}")
+    lines.append(f"# sum of the step's kernels (gateup_given and gateup_down, timed for comparison, excluded): "
+                 f"{total_us / 1000:.4f} ms")
+    lines.append(f"# stream_read_kernel of {GATEUP_BYTES} B (the gate/up launch's bytes): {us_read:.3f} us")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
 
 
 def gpu_moe(args):
@@ -294,7 +340,10 @@ MATVEC_BYTES = 2 * N * 1530 + N * 4 + 2 * N * 4  # W, x, y: 8,847,360
 MATVEC_FLOP = 2 * 2 * N * N
 
 
-def gpu_matvec(args):
+def measure_matvec(args):
+    """Config 0 on the device: microseconds per launch of one 5760x2880 MXFP4 matvec over
+    MATVEC_COPIES distinct resident matrices replayed in rotation (1.13 GB, beyond every
+    cache), and of a plain read of the same bytes per launch."""
     import ttlab_amd
 
     dev = ttlab_amd.Device(0)
@@ -326,17 +375,26 @@ def gpu_matvec(args):
         graph.free()
     for w in mats:
         w.free()
+    for b in (x, y):
+        b.free()
     dev.close()
     us_read = read_ceiling(MATVEC_BYTES, MATVEC_COPIES)
     log(f"plain read of the same {MATVEC_BYTES / 1e6:.2f} MB per launch: {us_read:.2f} us, "
         f"{MATVEC_BYTES / (us_read * 1e-6) / 1e9:.0f} GB/s")
+    return us, gbs, us_read
+
+
+MATVEC_WORKLOAD = ("config 0: one 5760x2880 MXFP4 matvec (gate|up stacked) per launch; "
+                   f"{MATVEC_COPIES} distinct resident matrices (1.13 GB) replayed in rotation; step = one launch")
+
+
+def gpu_matvec(args):
+    us, gbs, us_read = measure_matvec(args)
     return {
         "value": gbs,
         "unit": "GB/s",
         "ms_per_step": us * 1e-3,
-        "config": {"workload": "config 0: one 5760x2880 MXFP4 matvec (gate|up stacked) per launch; "
-                               f"{MATVEC_COPIES} distinct resident matrices (1.13 GB) replayed in rotation; "
-                               "step = one launch",
+        "config": {"workload": MATVEC_WORKLOAD,
                    "rows": 2 * N, "cols": N, "bytes_per_launch": MATVEC_BYTES,
                    "matvec_GFLOPs": round(MATVEC_FLOP / (us * 1e-6) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -691,6 +749,11 @@ def main():
                     help="KV positions filled before timing (default: 2048 for config 3, 4096 for config 4)")
     ap.add_argument("--layers", type=int, default=None,
                     help="decoder layers (default 24 / 36; fewer only for counter probes)")
+    ap.add_argument("--kv-fill", choices=["decode", "synthetic"], default="decode",
+                    help="decode workload: fill the KV caches by decoding (the benchmark) or with synthetic "
+                         "values (counter runs, whose profilers serialize every launch)")
+    ap.add_argument("--table", default=None,
+                    help="decode workload: also write the per-kind kernel table (text) to this path")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device once, a known-size reference "
                          "dispatch for scaling hardware byte counters")
@@ -741,6 +804,8 @@ def main():
         "roofline": res["roofline"],
         "cpu_baseline": base,
     }
+    if "matvec" in res:
+        line["matvec"] = res["matvec"]
     print(json.dumps(line), flush=True)
 
 

@@ -226,6 +226,29 @@ int ttl_moe_route_gateup_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const 
                                 int32_t *indices_dev, float *weights_dev, uint32_t stages);
 int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_dev, const int32_t *indices_dev,
                  float *down_dev);
+/* GptOssModel::moe up to the combine (model.cpp:293-333) in two launches: the router
+ * rows (TTL_ROUTE_ROWS, as above), then gate/up + SwiGLU and the `used` experts' down
+ * rows + bias in one launch (TTL_ROUTE_GATEUP_DOWN): hidden_dev f32 [used][2880],
+ * indices_dev int32 [used], weights_dev f32 [used], down_dev f32 [used][hidden].  Each
+ * down workgroup issues its weight loads before waiting for its expert's hidden from the
+ * gate/up workgroups of the same launch, so the down weights stream while gate/up ends.
+ * The single launch needs its whole grid (used x 180 workgroups of 512 threads)
+ * resident at once; where the occupancy does not allow it, gate/up and down run as two
+ * launches with the same results (ttl_moe_gateup_down_fused says which).  The down sums
+ * are the same products as ttl_moe_down's in another order.  Slower than the two-launch
+ * form on MI355X (46.8 against 10.4 + 5.8 us at the gpt-oss-20b shape: the waits inside
+ * the launch cost more than a kernel boundary), so the model's decode step does not use
+ * it; kept for callers that cannot launch twice and as the measurement of that choice.
+ * No reference counterpart as one call. */
+#define TTL_ROUTE_GATEUP_DOWN 4u
+int ttl_moe_route_gateup_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                              int32_t *indices_dev, float *weights_dev, float *down_dev, uint32_t stages);
+/* *fused = 1 if ttl_moe_route_gateup_down runs gate/up and down as one launch for this
+ * layer shape on this device, 0 if as two. */
+int ttl_moe_gateup_down_fused(ttl_ctx *ctx, const ttl_moe_layer *layer, int *fused);
+/* Waits of the one-launch gate/up + down that ended at their bound since the context was
+ * created (their down rows are NaN); 0 unless a workgroup of the grid was not resident. */
+int ttl_moe_handoff_give_ups(ttl_ctx *ctx, uint64_t *count);
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,
                     float *out_dev);
 /* down + combine + residual add in one launch (for used == 4; other counts run the

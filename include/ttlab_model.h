@@ -84,6 +84,8 @@ int ttlm_time_expert_kernel(ttlm_model *model, uint32_t reps, double *us_per_lau
 #define TTLM_KERNEL_GATEUP_GIVEN 6u      /* the same with the indices given                      */
 #define TTLM_KERNEL_DOWN 7u              /* the 4 experts' down projections + bias (down_kernel) */
 #define TTLM_KERNEL_LOGITS 8u            /* unembedding + per-workgroup argmax                   */
+#define TTLM_KERNEL_GATEUP_DOWN 9u       /* gate/up and down in one launch (gateup_down_kernel; the
+                                          * step runs them as two, which is faster)               */
 int ttlm_time_kernel(ttlm_model *model, uint32_t kind, uint32_t position, uint32_t reps, double *us_per_launch,
                      uint32_t *launches);
 
@@ -101,6 +103,12 @@ int ttlm_layer_state(ttlm_model *model, uint32_t layer, float *x_in, float *resi
 int ttlm_final_state(ttlm_model *model, float *x_final);
 /* Key and value caches of `layer`, positions [0, positions): f32 [positions][8][64] each. */
 int ttlm_kv_cache(ttlm_model *model, uint32_t layer, uint32_t positions, float *keys, float *values);
+/* Fills positions [0, positions) of every layer's key and value caches with N(0, 1)
+ * values from the synthetic generator (stream = seed-derived, per layer), as if that
+ * many tokens had been decoded: a decode step at `positions` then attends over a full
+ * context without decoding it first (hardware counter runs, whose profilers serialize
+ * every launch).  No reference counterpart. */
+int ttlm_fill_kv_synthetic(ttlm_model *model, uint32_t positions, uint64_t seed);
 /* Bytes of device memory the model holds. */
 size_t ttlm_device_bytes(const ttlm_model *model);
 /* Algorithmic bytes one decode step reads and writes at this position (weights actually

@@ -161,3 +161,19 @@ def test_eager_launches_match_graph_replay(models):
         for u, v in zip(g if isinstance(g, tuple) else (g,), e if isinstance(e, tuple) else (e,)):
             assert np.array_equal(u, v)
     assert us > 0.0
+
+
+def test_synthetic_kv_fill_then_decode(models):
+    """ttlm_fill_kv_synthetic writes the generator's N(0, 1) values (per layer, keys on
+    stream 2l, values on 2l + 1) into positions [0, n) of every cache; a decode step at
+    position n then matches the oracle over that context, layer by layer.  (Last in the
+    module: it overwrites the caches the other tests built.)"""
+    gpu, host = models
+    position, seed = 40, 0x78000300
+    gpu.fill_kv_synthetic(position, seed)
+    for l in (0, LAYERS - 1):
+        keys, values = gpu.kv_cache(l, position)
+        assert np.array_equal(keys, O.synth_normal(seed, 2 * l, position * 512))
+        assert np.array_equal(values, O.synth_normal(seed, 2 * l + 1, position * 512))
+    gpu.forward(5, position)
+    check_layers(gpu, host, position)

@@ -265,3 +265,57 @@ def test_down_combine_adds_residual_in_reference_order(dev, used):
     for b in (xb, rb, ib, wb, hidden, ref_down, got_down, out):
         b.free()
     device.free()
+
+
+@pytest.mark.parametrize("experts,norm", [(32, True), (32, False), (128, True)])
+def test_gateup_and_down_in_one_launch(dev, experts, norm):
+    """ttl_moe_route_gateup_down, the decode step's MoE: gate/up (the ranking at its head)
+    and the four experts' down rows in one launch, the down workgroups waiting inside it
+    for their expert's hidden.  Against the two-launch form (ttl_moe_route_gateup, then
+    ttl_moe_down): the routing and the hidden bit for bit, the down rows to f32 rounding
+    (the same products summed in another order); the down rows against the oracle's
+    matvec on that hidden within 1e-5 (model.cpp:326-333).  Five tokens back to back
+    (the in-launch counts reset between launches), with and without the layer's input
+    norm (the step's form: the router rows leave the normalized input for gate/up); no
+    wait may end at its bound."""
+    host = HostLayer(experts, 4, biases=True, seed=0x77000910 + experts, fill_experts=[])
+    device = DeviceLayer(dev, host)
+    nb = None
+    if norm:
+        nb = dev.upload(O.synth_normal(0x77000911, 0, N, sigma=0.05, mean=1.0))
+        device.desc.input_norm = nb.ptr
+        device.desc.input_norm_epsilon = 1e-5
+    assert dev.moe_gateup_down_fused(device.desc), "the grid should be resident at once on gfx950"
+    before = dev.handoff_give_ups()
+    bufs = [dev.alloc(4 * N * 4) for _ in range(4)] + [dev.alloc(16) for _ in range(4)]
+    hid_a, down_a, hid_b, down_b, ia, wa, ib, wb = bufs
+    checked = set()
+    for token in range(5):
+        x = O.synth_normal(X_SEED, 900 + token, N)
+        xb = dev.upload(x)
+        dev.moe_route_gateup(device.desc, xb, hid_a, ia, wa)
+        dev.moe_down(device.desc, hid_a, ia, down_a)
+        dev.moe_route_gateup_down(device.desc, xb, hid_b, ib, wb, down_b)
+        idx = ia.download(np.int32)
+        assert np.array_equal(ib.download(np.int32), idx)
+        assert np.array_equal(wb.download(np.uint32), wa.download(np.uint32))
+        h_a, h_b = hid_a.download(np.float32), hid_b.download(np.float32)
+        assert np.array_equal(h_b.view(np.uint32), h_a.view(np.uint32))
+        d_a = down_a.download(np.float32).reshape(4, N)
+        d_b = down_b.download(np.float32).reshape(4, N)
+        for r in range(4):
+            assert O.rel_l2(d_b[r], d_a[r]) <= 1e-6, (token, r)
+            e = int(idx[r])
+            if e not in checked:  # the host matrices of an expert are generated once
+                checked.add(e)
+                host_down = O.synth_mxfp4(host.seed, 3000 + e, N * 90)
+                ref = O.mxfp4_matvec(host_down, host.down_b[e * N:(e + 1) * N], N, N, h_a.reshape(4, N)[r],
+                                     body=O.BODY_DEFAULT)
+                assert O.rel_l2(d_b[r], ref) <= TOL, (token, r, e)
+        xb.free()
+    assert dev.handoff_give_ups() == before
+    for b in bufs:
+        b.free()
+    if nb:
+        nb.free()
+    device.free()

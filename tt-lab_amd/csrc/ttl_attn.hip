@@ -250,7 +250,12 @@ __global__ __launch_bounds__(kWinThreads) void attn_window_kernel(const float *_
     __shared__ float sq[4][kWindow];
     __shared__ float stat[4];
     __shared__ float part[kWinThreads / kHead][kHead];
-    const uint32_t head = blockIdx.x, kvh = head / kGroup, t = threadIdx.x;
+    // Workgroups are dealt to the 8 XCDs in turn (workgroup b to XCD b % 8), each XCD with
+    // its own L2: workgroup b takes query head 8 (b % 8) + b / 8, so the 8 heads that read
+    // one kv head's window run on one XCD and share its L2 (with head = b the window was
+    // fetched once per XCD, 7.6 times its bytes).
+    const uint32_t head = (blockIdx.x % kKvHeads) * kGroup + blockIdx.x / kKvHeads, kvh = head / kGroup;
+    const uint32_t t = threadIdx.x;
     // q and the sink first (one of q's 16 float4 per thread), then the position, then the
     // window's K and V rows (positions past n re-read the last): two round trips
     const float4 qv = reinterpret_cast<const float4 *>(q + size_t(head) * kHead)[t % (kHead / 4)];

@@ -898,6 +898,200 @@ __global__ __launch_bounds__(kSplit * 64) void down_kernel(
     }
 }
 
+// ---- gate/up + SwiGLU and down in one launch (the decode step) -----------------------
+//
+// Workgroup (slot, tile) runs gateup_swiglu_kernel's work for its 16 hidden rows, then
+// the down rows of the same tile index for the same slot.  Down needs all 2880 hidden
+// values of its slot, written by the slot's 180 gate/up tiles, so the tiles hand them
+// over inside the launch:
+//  - a gate/up tile writes its 16 values with agent-scope stores (written through to
+//    the memory side, past this XCD's L2), waits until they are complete (s_waitcnt)
+//    and adds one to its slot's arrival count;
+//  - every workgroup issues its down tile's weight loads as soon as its gate/up work
+//    is done (they depend only on the routing), then waits, boundedly, for its slot's
+//    count to reach the tile count, and reads the hidden with agent-scope loads;
+//  - the last workgroup past its wait resets the counts for the next launch.
+// No release fence: on this chip an agent-scope release writes back the whole L2 of
+// the XCD.  Every workgroup must be resident at once (a waiting workgroup holds its CU);
+// the host launches this form only when the occupancy allows the whole grid, and a wait
+// that reaches its bound counts a give-up and leaves NaN rows instead of hanging.
+// The down rows are split over the 8 waves (3 iterations each; down_kernel splits 4
+// ways): the same products, summed in another order.
+// Measured on config 3 (MI355X): 46.8 us per launch, against 10.4 + 5.8 us for
+// gateup_swiglu_kernel and down_kernel as two launches, so the decode step keeps the
+// two.  Per-workgroup timestamps (s_memrealtime) show every workgroup resident within
+// 0.6 us and the gate/up tiles counted by 9-13 us, but the 180 waiters of a slot seeing
+// the full count one after another, about 90 ns apart (12 to 28 us for slot 0): reads
+// and atomics that bypass the L2 serialize on the few lines they share.  Eight count
+// lines per slot shortened those waits, but reading the hidden through the L2 after an
+// agent-scope acquire (which invalidates the XCD's L2, once per workgroup) then took
+// about 30 us.  A kernel boundary makes the hidden visible with one writeback per XCD.
+constexpr unsigned kHandoffSpinLimit = 1u << 21;
+constexpr int kDownPer = 3;  // down iterations per wave: 8 x 3 = 24 >= 23
+static_assert(kDownPer * 2 * kSplit * mx::lanes_k <= GateUpSplit::x_blocks, "the staged hidden covers the split");
+
+struct Handoff {
+    uint32_t arrived[kMaxUsed * 16];  // per slot (one 64-byte line each): gate/up tiles written
+    uint32_t departed;                // workgroups past their wait
+    uint32_t give_ups;                // waits that ended at the spin limit (their rows are NaN)
+};
+
+struct DownArgs {
+    const uint8_t *codes, *scales;
+    const float *bias;
+    uint32_t rows, tiles;  // down rows (the hidden size) and their 16-row tiles
+    float *down;           // [used][rows]
+    Handoff *handoff;
+};
+
+template <int MODE, bool ROUTE, int PL = kPerLane>
+__global__ __launch_bounds__(kGateUpThreads) void gateup_down_kernel(GateUpArgs a, DownArgs d) {
+    __shared__ __attribute__((aligned(16))) float xs[GateUpSplit::x_floats];
+    __shared__ float red[stage::red_floats(GateUpSplit::x_blocks)];
+    __shared__ float part[2 * kSplit][mx::tile_rows];
+    __shared__ int waited;
+    const uint32_t slot = blockIdx.x / a.tiles, tile = blockIdx.x % a.tiles;
+    const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const uint32_t which = wave / kSplit, w = wave % kSplit;  // which: 0 gate, 1 up
+
+    // ---- gate/up + SwiGLU, as gateup_swiglu_kernel ----
+    RouteRows<PL> rows;
+    if constexpr (ROUTE) {
+        load_route_rows<PL>(a.experts, a.scratch, rows);
+    }
+    stage::Pending<mx::cols, GateUpSplit::x_blocks, kGateUpThreads, MODE> pending;
+    stage::stage_load(a.in, pending);
+    int32_t e;
+    bool staged = false;
+    if constexpr (ROUTE) {
+        __shared__ RouteLds rl;
+        const bool first = blockIdx.x == 0;
+        float *logits = first ? a.logits_out : nullptr;
+        route_certified_wave<PL>(a.experts, a.k, false, rows, rl, logits, first);
+        if (!rl.certified) {
+            stage::stage_finish(a.in, pending, xs, red);
+            route_exact_serial(a.router_weight, a.router_bias, a.experts, a.k, xs, a.scratch, rl, logits);
+            staged = true;
+        }
+        e = rl.indices[slot];
+        if (first && threadIdx.x < a.k) {
+            a.indices_out[threadIdx.x] = rl.indices[threadIdx.x];
+            a.weights_out[threadIdx.x] = rl.weights[threadIdx.x];
+        }
+    } else {
+        e = a.expert_ids[slot];
+    }
+    const bool valid = e >= 0 && uint32_t(e) < a.experts;
+    const uint32_t e_safe = valid ? uint32_t(e) : 0u;
+    const uint32_t row = tile * mx::tile_rows + lane % mx::tile_rows;
+    const size_t brow = size_t(e_safe) * a.rows + row;
+    const float gb = a.gate_bias ? a.gate_bias[brow] : 0.0f;
+    const float ub = a.up_bias ? a.up_bias[brow] : 0.0f;
+    {
+        mxt::SplitRegs<kSplit> regs;
+        mxt::split_load<kSplit>(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales,
+                                size_t(e_safe) * a.tiles + tile, w, lane, regs);
+        if (!staged) {
+            stage::stage_finish(a.in, pending, xs, red);
+        }
+        const float acc = mxt::split_compute<kSplit>(regs, xs, w, lane);
+        if (lane < mx::tile_rows) {
+            part[which * kSplit + w][lane] = acc;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        if (lane < mx::tile_rows) {
+            const float g = sum_parts<kSplit>(part, lane), u = sum_parts<kSplit>(part + kSplit, lane);
+            const float h =
+                valid ? clamped_swiglu(a.gate_bias ? g + gb : g, a.up_bias ? u + ub : u) : __builtin_nanf("");
+            __hip_atomic_store(&a.hidden[size_t(slot) * a.rows + row], h, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // the 16 stores are this wave's: once they are complete, count the tile
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane == 0) {
+            __hip_atomic_fetch_add(&d.handoff->arrived[slot * 16], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    // ---- down: the weight loads first, then the wait for the slot's hidden ----
+    const uint32_t kl = lane / mx::tile_rows;
+    const size_t dtile = size_t(e_safe) * d.tiles + tile;
+    const uint32_t drow = tile * mx::tile_rows + lane % mx::tile_rows;
+    const float db = d.bias ? d.bias[size_t(e_safe) * d.rows + drow] : 0.0f;
+    uint4 q[kDownPer];
+    uint32_t sc[kDownPer];
+    {
+        const uint8_t *rec = d.scales + dtile * mx::tile_scale_bytes + size_t(lane) * mx::scale_pad;
+        const uint4 *tc = reinterpret_cast<const uint4 *>(d.codes) + dtile * mx::blocks * mx::tile_rows +
+                          lane % mx::tile_rows;
+#pragma unroll
+        for (int j = 0; j < kDownPer; ++j) {
+            sc[j] = rec[wave * kDownPer + j];  // iteration 23: the record's pad byte (scale 2^0)
+        }
+#pragma unroll
+        for (int j = 0; j < kDownPer; ++j) {
+            const uint32_t kb = min(uint32_t(4 * (wave * kDownPer + j)) + kl, uint32_t(mx::blocks - 1));
+            q[j] = ttl::load_stream(tc + size_t(kb) * mx::tile_rows);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (threadIdx.x == 0) {
+        unsigned spins = 0;
+        while (__hip_atomic_load(&d.handoff->arrived[slot * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                   a.tiles &&
+               spins < kHandoffSpinLimit) {
+            __builtin_amdgcn_s_sleep(1);
+            ++spins;
+        }
+        waited = spins < kHandoffSpinLimit ? 1 : 0;
+    }
+    __syncthreads();
+    // the slot's hidden, read past this XCD's L2, into the padded layout (blocks 90.. zero)
+    float *hs = a.hidden + size_t(slot) * a.rows;
+    for (uint32_t i = threadIdx.x; i < uint32_t(GateUpSplit::x_blocks) * 32; i += kGateUpThreads) {
+        const float v = i < uint32_t(mx::cols) ? __hip_atomic_load(&hs[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                               : 0.0f;
+        xs[(i / 32) * mxt::x_stride + i % 32] = v;
+    }
+    __syncthreads();
+    {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kDownPer; ++j) {
+            const uint32_t kb = 4 * (wave * kDownPer + j) + kl;
+            acc += __builtin_amdgcn_ldexpf(mxt::block_dot(q[j], xs + kb * mxt::x_stride), int(sc[j]) - 127);
+        }
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+        if (lane < mx::tile_rows) {
+            part[wave][lane] = acc;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < mx::tile_rows) {
+        const float sum = sum_parts<2 * kSplit>(part, threadIdx.x);
+        d.down[size_t(slot) * d.rows + drow] =
+            (!valid || !waited) ? __builtin_nanf("") : (d.bias ? sum + db : sum);
+    }
+    if (threadIdx.x == 0) {
+        if (!waited) {
+            __hip_atomic_fetch_add(&d.handoff->give_ups, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // the last workgroup past its wait opens the next launch
+        if (__hip_atomic_fetch_add(&d.handoff->departed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            gridDim.x - 1) {
+            for (uint32_t r = 0; r < a.k; ++r) {
+                __hip_atomic_store(&d.handoff->arrived[r * 16], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __hip_atomic_store(&d.handoff->departed, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 // down + combine + residual for used == 4: one workgroup per 16-row tile holds all
 // four slots (16 waves: slot = wave / 4, K split over wave % 4), so it can finish
 // the rows: out = residual + (0 + w_0 d_0 + w_1 d_1 + w_2 d_2 + w_3 d_3), the
@@ -1006,6 +1200,7 @@ struct MoeWorkspace {
     alignas(256) float normed[2880];  // the router rows' normalized input, for the routed gate/up
     alignas(256) float hidden[kMaxUsed * 2880];
     alignas(256) float down[kMaxUsed * 2880];
+    alignas(256) Handoff handoff;  // gateup_down_kernel's counts (zero between launches)
 };
 
 size_t moe_workspace_bytes() {
@@ -1190,6 +1385,78 @@ int launch_gateup(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, const in
     return TTL_OK;
 }
 
+// The fused gate/up + down launch of the decode step: its grid (4 slots x 180 tiles of
+// 512 threads) must be resident at once.  Returns false, launching nothing, when the
+// occupancy does not allow that; the caller then runs gate/up and down as two launches.
+template <class Kernel>
+bool fits_resident(ttl_ctx *ctx, Kernel kernel, uint32_t grid) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGateUpThreads, 0) != hipSuccess) {
+        return false;
+    }
+    return uint64_t(per_cu) * uint64_t(ctx->compute_units) >= grid;
+}
+
+int launch_gateup_down(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, float *hidden, int32_t *indices,
+                       float *weights, float *down, bool *fused) {
+    GateUpArgs a{};
+    a.gate_codes = L.gate->codes;
+    a.gate_scales = L.gate->scales;
+    a.gate_bias = L.gate_bias;
+    a.up_codes = L.up->codes;
+    a.up_scales = L.up->scales;
+    a.up_bias = L.up_bias;
+    a.rows = L.expert_hidden;
+    a.tiles = L.expert_hidden / mx::tile_rows;
+    a.experts = L.experts;
+    a.k = L.used;
+    a.in = layer_input(L, x);
+    if (L.input_norm) {
+        a.in.base = workspace(ctx)->normed;  // left there by the router rows launch
+        a.in.norm_w = nullptr;
+    }
+    a.expert_ids = nullptr;
+    a.hidden = hidden;
+    a.router_weight = L.router_weight;
+    a.router_bias = L.router_bias;
+    a.scratch = &workspace(ctx)->router;
+    a.indices_out = indices;
+    a.weights_out = weights;
+    a.logits_out = workspace(ctx)->logits;
+    DownArgs d{};
+    d.codes = L.down->codes;
+    d.scales = L.down->scales;
+    d.bias = L.down_bias;
+    d.rows = L.hidden;
+    d.tiles = L.hidden / mx::tile_rows;
+    d.down = down;
+    d.handoff = &workspace(ctx)->handoff;
+    const uint32_t grid = a.tiles * L.used;
+    *fused = false;
+    // the tile index of gate/up and of down is the same (both 180), so one grid covers both
+    if (d.tiles != a.tiles) {
+        return TTL_OK;
+    }
+    stage::with_mode(a.in, [&](auto mode) {
+        constexpr int M = decltype(mode)::value;
+        auto go = [&](auto kernel) {
+            if (fits_resident(ctx, kernel, grid)) {
+                kernel<<<grid, kGateUpThreads, 0, ctx->stream>>>(a, d);
+                *fused = true;
+            }
+        };
+        if (L.experts <= 64) {
+            go(gateup_down_kernel<M, true, 1>);
+        } else if (L.experts <= 128) {
+            go(gateup_down_kernel<M, true, 2>);
+        } else {
+            go(gateup_down_kernel<M, true, kPerLane>);
+        }
+    });
+    TTL_LAUNCHED("gateup_down_kernel");
+    return TTL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1273,6 +1540,60 @@ int ttl_moe_route_gateup_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const 
 int ttl_moe_route_gateup(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
                          int32_t *indices_dev, float *weights_dev) {
     return ttl_moe_route_gateup_stages(ctx, layer, x_dev, hidden_dev, indices_dev, weights_dev, TTL_ROUTE_ALL);
+}
+
+int ttl_moe_route_gateup_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
+                              int32_t *indices_dev, float *weights_dev, float *down_dev, uint32_t stages) {
+    TTL_REQUIRE(ctx && x_dev && hidden_dev && indices_dev && weights_dev && down_dev, TTL_ERR_INVALID,
+                "ttl_moe_route_gateup_down: null argument");
+    TTL_REQUIRE((stages & ~uint32_t(TTL_ROUTE_ROWS | TTL_ROUTE_GATEUP_DOWN)) == 0, TTL_ERR_INVALID,
+                "ttl_moe_route_gateup_down: unknown stage bits 0x%x", stages);
+    int rc = check_layer(layer, "ttl_moe_route_gateup_down");
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    const ttl_moe_layer &L = *layer;
+    rc = check_router(L.router_weight, L.router_bias, L.experts, L.hidden, x_dev, L.used);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    if (stages & TTL_ROUTE_ROWS) {
+        launch_router_rows(ctx, L, layer_input(L, x_dev));
+        TTL_LAUNCHED("router_rows_kernel");
+    }
+    if (stages & TTL_ROUTE_GATEUP_DOWN) {
+        bool fused = false;
+        rc = launch_gateup_down(ctx, L, x_dev, hidden_dev, indices_dev, weights_dev, down_dev, &fused);
+        if (rc != TTL_OK || fused) {
+            return rc;
+        }
+        // the grid cannot be resident at once: gate/up and down as two launches
+        rc = launch_gateup(ctx, L, x_dev, nullptr, hidden_dev, indices_dev, weights_dev);
+        if (rc == TTL_OK) {
+            rc = ttl_moe_down(ctx, layer, hidden_dev, indices_dev, down_dev);
+        }
+    }
+    return rc;
+}
+
+int ttl_moe_gateup_down_fused(ttl_ctx *ctx, const ttl_moe_layer *layer, int *fused) {
+    TTL_REQUIRE(ctx && layer && fused, TTL_ERR_INVALID, "ttl_moe_gateup_down_fused: null argument");
+    const uint32_t tiles = layer->expert_hidden / mx::tile_rows, grid = tiles * layer->used;
+    const auto kernel = layer->experts <= 64    ? gateup_down_kernel<stage::kPlain, true, 1>
+                        : layer->experts <= 128 ? gateup_down_kernel<stage::kPlain, true, 2>
+                                                : gateup_down_kernel<stage::kPlain, true, kPerLane>;
+    *fused = (layer->hidden == layer->expert_hidden && fits_resident(ctx, kernel, grid)) ? 1 : 0;
+    return TTL_OK;
+}
+
+int ttl_moe_handoff_give_ups(ttl_ctx *ctx, uint64_t *count) {
+    TTL_REQUIRE(ctx && count, TTL_ERR_INVALID, "ttl_moe_handoff_give_ups: null argument");
+    uint32_t value = 0;
+    TTL_HIP(hipMemcpyAsync(&value, &workspace(ctx)->handoff.give_ups, sizeof(value), hipMemcpyDeviceToHost,
+                           ctx->stream));
+    TTL_HIP(hipStreamSynchronize(ctx->stream));
+    *count = value;
+    return TTL_OK;
 }
 
 int ttl_moe_combine(ttl_ctx *ctx, const float *down_dev, const float *weights_dev, uint32_t k, uint32_t n,

@@ -360,7 +360,9 @@ int HipGptOssModel::enqueue_step() {
         }
         if (status == TTL_OK) {
             // the four experts' down projections (+ bias), one workgroup per (slot, tile);
-            // the combine and the residual add run in the next consumer's staging
+            // the combine and the residual add run in the next consumer's staging.  (One
+            // launch for gate/up and down, ttl_moe_route_gateup_down, is slower: its
+            // in-launch handoff costs more than this kernel boundary.)
             status = ttl_moe_down(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, down_ + l * kUsed * kHidden);
         }
     }
@@ -644,6 +646,7 @@ double HipGptOssModel::time_kernel(uint32_t kind, size_t position, size_t reps, 
         float *kc = kind == kKernelQkv ? static_cast<float *>(take(cache_bytes)) : nullptr;
         float *vc = kind == kKernelQkv ? static_cast<float *>(take(cache_bytes)) : nullptr;
         float *vec = static_cast<float *>(take(sizeof(float) * kUsed * kHidden));
+        float *vec2 = kind == kKernelGateUpDown ? static_cast<float *>(take(sizeof(float) * kUsed * kHidden)) : nullptr;
         int32_t *idx = static_cast<int32_t *>(take(sizeof(int32_t) * kUsed));
         float *w = static_cast<float *>(take(sizeof(float) * kUsed));
         float *logits = kind == kKernelLogits ? static_cast<float *>(take(sizeof(float) * spec_.vocab)) : nullptr;
@@ -700,6 +703,11 @@ double HipGptOssModel::time_kernel(uint32_t kind, size_t position, size_t reps, 
                     break;
                 case kKernelDown:
                     status = ttl_moe_down(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, vec);
+                    ++count;
+                    break;
+                case kKernelGateUpDown:
+                    status = ttl_moe_route_gateup_down(ctx_, &layer.moe, residual_ + l * kHidden, vec, idx, w, vec2,
+                                                       TTL_ROUTE_GATEUP_DOWN);
                     ++count;
                     break;
                 }
@@ -769,6 +777,18 @@ void HipGptOssModel::kv_cache(size_t layer, size_t positions, float *keys, float
     const size_t bytes = sizeof(float) * positions * kKvWidth;
     check(ttl_memcpy_d2h(ctx_, keys, layers_[layer].key_cache, bytes), "ttl_memcpy_d2h");
     check(ttl_memcpy_d2h(ctx_, values, layers_[layer].value_cache, bytes), "ttl_memcpy_d2h");
+}
+
+void HipGptOssModel::fill_kv_synthetic(size_t positions, uint64_t seed) {
+    if (positions > spec_.capacity) {
+        throw std::runtime_error("positions exceed the token capacity");
+    }
+    const size_t n = positions * kKvWidth;
+    for (size_t l = 0; l < layers_.size(); ++l) {
+        check(ttl_synth_normal(ctx_, seed, 2 * l, 0, n, 0.0f, 1.0f, layers_[l].key_cache), "ttl_synth_normal");
+        check(ttl_synth_normal(ctx_, seed, 2 * l + 1, 0, n, 0.0f, 1.0f, layers_[l].value_cache), "ttl_synth_normal");
+    }
+    check(ttl_sync(ctx_), "ttl_sync");
 }
 
 double HipGptOssModel::step_bytes(size_t position) const {

@@ -134,7 +134,8 @@ class HipGptOssModel {
         kKernelGateUpGiven = 6,      // the same kernel with the indices given
         kKernelDown = 7,             // the four experts' down projections (+ bias)
         kKernelLogits = 8,
-        kKernelKinds = 9,
+        kKernelGateUpDown = 9,       // gate/up (ranking) and down in one launch; not the step's
+        kKernelKinds = 10,
     };
     // Microseconds per launch (for kKernelAttentionFull: per partials + combine pair) of
     // every launch of `kind` one step at `position` makes, with the last step's inputs
@@ -159,6 +160,8 @@ class HipGptOssModel {
     }
     void final_state(float *x_final) const;
     void kv_cache(size_t layer, size_t positions, float *keys, float *values) const;
+    // Positions [0, positions) of every layer's caches filled with N(0, 1) values.
+    void fill_kv_synthetic(size_t positions, uint64_t seed);
     size_t device_bytes() const {
         return device_bytes_;
     }

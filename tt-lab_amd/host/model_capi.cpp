@@ -165,6 +165,10 @@ int ttlm_kv_cache(ttlm_model *model, uint32_t layer, uint32_t positions, float *
     return guarded([&] { model->model->kv_cache(layer, positions, keys, values); });
 }
 
+int ttlm_fill_kv_synthetic(ttlm_model *model, uint32_t positions, uint64_t seed) {
+    return guarded([&] { model->model->fill_kv_synthetic(positions, seed); });
+}
+
 size_t ttlm_device_bytes(const ttlm_model *model) {
     return model ? model->model->device_bytes() : 0;
 }

@@ -86,7 +86,7 @@ def load_model_library():
     if not os.path.exists(MODEL_LIB_PATH):
         raise TtlError(f"{MODEL_LIB_PATH} is missing: run __graft_entry__.build()")
     lib = C.CDLL(MODEL_LIB_PATH)
-    vp, u32, i32 = C.c_void_p, C.c_uint32, C.c_int
+    vp, u32, u64, i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
     sigs = {
         "ttlm_create_synthetic": (i32, [i32, u32, u32, u32, u32, C.c_uint64, C.POINTER(vp)]),
         "ttlm_destroy": (None, [vp]),
@@ -101,6 +101,7 @@ def load_model_library():
         "ttlm_layer_state": (i32, [vp, u32, vp, vp, vp, vp]),
         "ttlm_final_state": (i32, [vp, vp]),
         "ttlm_kv_cache": (i32, [vp, u32, u32, vp, vp]),
+        "ttlm_fill_kv_synthetic": (i32, [vp, u32, u64]),
         "ttlm_device_bytes": (C.c_size_t, [vp]),
         "ttlm_step_bytes": (C.c_double, [vp, u32]),
         "ttlm_prefill_state": (i32, [vp, u32, u32, vp]),
@@ -184,6 +185,10 @@ class Model:
     def prefill_batch(self):
         return int(self.lib.ttlm_prefill_batch(self.h))
 
+    def fill_kv_synthetic(self, positions, seed=0x78000300):
+        """KV caches of every layer filled with N(0, 1) values for positions [0, positions)."""
+        _mcheck(self.lib.ttlm_fill_kv_synthetic(self.h, positions, seed), "ttlm_fill_kv_synthetic")
+
     def generate(self, token, position, steps):
         out = np.empty(steps, np.int32)
         _mcheck(self.lib.ttlm_generate(self.h, token, position, steps, out.ctypes.data), "ttlm_generate")
@@ -203,7 +208,7 @@ class Model:
         _mcheck(self.lib.ttlm_set_graph_replay(self.h, 1 if enabled else 0), "ttlm_set_graph_replay")
 
     KERNELS = ("qkv", "attention_window", "attention_full", "output", "router_rows", "gateup_routed",
-               "gateup_given", "down", "logits")
+               "gateup_given", "down", "logits", "gateup_down")
 
     def time_kernel(self, kind, position, reps):
         """Microseconds per launch of one kind of the step's kernels (KERNELS names them), and
@@ -286,6 +291,9 @@ def load_library():
         "ttl_moe_combine": (i32, [vp, vp, vp, u32, u32, vp]),
         "ttl_moe_down_combine": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
         "ttl_moe_route_gateup": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp, vp]),
+        "ttl_moe_route_gateup_down": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp, vp, vp, u32]),
+        "ttl_moe_gateup_down_fused": (i32, [vp, C.POINTER(MoeLayerDesc), C.POINTER(C.c_int)]),
+        "ttl_moe_handoff_give_ups": (i32, [vp, C.POINTER(C.c_uint64)]),
         "ttl_synth_bf16": (i32, [vp, u64, u64, sz, sz, vp]),
         "ttl_q8_upload": (i32, [vp, vp, u32, u32, vp, u32, C.POINTER(vp)]),
         "ttl_q8_upload_dev": (i32, [vp, vp, u32, u32, vp, C.POINTER(vp)]),
@@ -589,6 +597,25 @@ class Device:
     def moe_gateup_swiglu(self, layer, x, indices, hidden):
         _check(self.lib.ttl_moe_gateup_swiglu(self.ctx, C.byref(layer), x.ptr, indices.ptr, hidden.ptr),
                "ttl_moe_gateup_swiglu")
+
+    def moe_route_gateup(self, layer, x, hidden, indices, weights):
+        _check(self.lib.ttl_moe_route_gateup(self.ctx, C.byref(layer), x.ptr, hidden.ptr, indices.ptr, weights.ptr),
+               "ttl_moe_route_gateup")
+
+    def moe_route_gateup_down(self, layer, x, hidden, indices, weights, down, stages=5):
+        """Router rows (stage 1), then gate/up + down in one launch (stage 4)."""
+        _check(self.lib.ttl_moe_route_gateup_down(self.ctx, C.byref(layer), x.ptr, hidden.ptr, indices.ptr,
+                                                  weights.ptr, down.ptr, stages), "ttl_moe_route_gateup_down")
+
+    def moe_gateup_down_fused(self, layer):
+        f = C.c_int()
+        _check(self.lib.ttl_moe_gateup_down_fused(self.ctx, C.byref(layer), C.byref(f)), "ttl_moe_gateup_down_fused")
+        return bool(f.value)
+
+    def handoff_give_ups(self):
+        c = C.c_uint64()
+        _check(self.lib.ttl_moe_handoff_give_ups(self.ctx, C.byref(c)), "ttl_moe_handoff_give_ups")
+        return c.value
 
     def moe_down(self, layer, hidden, indices, down):
         _check(self.lib.ttl_moe_down(self.ctx, C.byref(layer), hidden.ptr, indices.ptr, down.ptr), "ttl_moe_down")
