@@ -70,6 +70,18 @@ int ttl_fill_bytes(ttl_ctx *ctx, void *dst_dev, uint8_t value, size_t bytes);
  * words equals a fixed constant. */
 int ttl_stream_read(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *sink_dev);
 
+/* ttl_stream_read with ordinary loads instead of non-temporal ones (the kernels mark
+ * their streamed weights non-temporal; this is the comparison).  Measurement only. */
+int ttl_stream_read_plain(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *sink_dev);
+
+/* The cost of a kernel boundary: a graph of `launches` dependent kernels (blocks
+ * workgroups of `threads` threads each), each reading in every workgroup a word the
+ * previous kernel wrote, replayed 20 times; *us_per_kernel is the time per launch,
+ * *wrong 1 if the chain's count came out wrong.  Measurement only, with no counterpart
+ * in the reference: the fixed cost every kernel of the decode step pays. */
+int ttl_measure_boundary(ttl_ctx *ctx, uint32_t launches, uint32_t blocks, uint32_t threads, float *us_per_kernel,
+                         uint32_t *wrong);
+
 /* The cost of handing 2880 floats from 180 producer workgroups to 32 consumer
  * workgroups, each consumer needing all of them: mode 0 across a kernel boundary (a
  * producer launch, then a consumer launch), mode 1 inside one launch (release fence and

@@ -56,6 +56,45 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const uint4 *
         *sink = acc;
     }
 }
+// The same read with ordinary (temporal) loads, for the comparison the weight streams
+// are tuned on: the kernels mark their streamed weights non-temporal.
+__global__ __launch_bounds__(kReadThreads) void stream_read_plain_kernel(const uint4 *__restrict__ src, size_t n,
+                                                                         uint32_t *__restrict__ sink) {
+    const size_t stride = size_t(gridDim.x) * kReadThreads * kReadPerThread;
+    uint32_t acc = 0;
+    for (size_t base = size_t(blockIdx.x) * kReadThreads * kReadPerThread + threadIdx.x; base < n; base += stride) {
+        uint4 v[kReadPerThread];
+#pragma unroll
+        for (int k = 0; k < kReadPerThread; ++k) {
+            const size_t i = base + size_t(k) * kReadThreads;
+            v[k] = src[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < kReadPerThread; ++k) {
+            acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+        }
+    }
+    if (acc == 0x9e3779b9u) {
+        *sink = acc;
+    }
+}
+
+// ---- the cost of a kernel boundary: a chain of launches that each depend on the last ----
+//
+// Kernel i of a chain reads word[i % 2], which kernel i - 1 wrote, in every workgroup
+// (the shape of a decode step, whose every kernel starts by reading what the previous
+// one wrote), and workgroup 0 writes word[(i + 1) % 2] = that value + 1.  Nothing else
+// is done, so the time per launch in a replayed graph is the boundary alone.
+__global__ void boundary_kernel(uint32_t *word, uint32_t i, uint32_t *sink) {
+    const uint32_t v = word[i % 2];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        word[(i + 1) % 2] = v + 1;
+    }
+    if (v == 0xffffffffu) {  // never: keeps every workgroup's load live
+        *sink = v;
+    }
+}
+
 // ---- a device-wide handoff: a kernel boundary against a barrier inside one kernel ----
 //
 // 180 producer workgroups each write 16 floats (the shape of the 16-row matvec tiles);
@@ -333,6 +372,84 @@ int ttl_stream_read(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *s
     stream_read_kernel<<<unsigned(blocks), kReadThreads, 0, ctx->stream>>>(static_cast<const uint4 *>(src_dev), words,
                                                                        sink_dev);
     TTL_LAUNCHED("stream_read_kernel");
+    return TTL_OK;
+}
+
+int ttl_stream_read_plain(ttl_ctx *ctx, const void *src_dev, size_t bytes, uint32_t *sink_dev) {
+    TTL_REQUIRE(ctx && src_dev && sink_dev, TTL_ERR_INVALID, "ttl_stream_read_plain: null argument");
+    TTL_REQUIRE(bytes >= 16 && bytes % 16 == 0, TTL_ERR_SHAPE,
+                "ttl_stream_read_plain: bytes must be a positive multiple of 16");
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(src_dev) & 15) == 0, TTL_ERR_INVALID,
+                "ttl_stream_read_plain: source must be 16-byte aligned");
+    const size_t words = bytes / 16;
+    const size_t per_block = size_t(kReadThreads) * kReadPerThread;
+    const size_t blocks = std::min((words + per_block - 1) / per_block, size_t(kReadBlocks));
+    stream_read_plain_kernel<<<unsigned(blocks), kReadThreads, 0, ctx->stream>>>(static_cast<const uint4 *>(src_dev),
+                                                                             words, sink_dev);
+    TTL_LAUNCHED("stream_read_plain_kernel");
+    return TTL_OK;
+}
+
+int ttl_measure_boundary(ttl_ctx *ctx, uint32_t launches, uint32_t blocks, uint32_t threads, float *us_per_kernel,
+                         uint32_t *wrong) {
+    TTL_REQUIRE(ctx && us_per_kernel && wrong, TTL_ERR_INVALID, "ttl_measure_boundary: null argument");
+    TTL_REQUIRE(launches >= 2 && launches <= 1000, TTL_ERR_INVALID, "ttl_measure_boundary: 2..1000 launches");
+    TTL_REQUIRE(blocks >= 1 && blocks <= 65536 && threads >= 64 && threads <= 1024 && threads % 64 == 0,
+                TTL_ERR_INVALID, "ttl_measure_boundary: 1..65536 workgroups of 64..1024 threads (a multiple of 64)");
+    uint32_t *words = nullptr;
+    TTL_HIP(hipMalloc(&words, 4 * sizeof(uint32_t)));
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int rc = TTL_OK;
+    const auto fail = [&](hipError_t err, const char *what) {
+        if (rc == TTL_OK && err != hipSuccess) {
+            rc = ttl::hip_fail(err, what);
+        }
+    };
+    fail(hipMemsetAsync(words, 0, 4 * sizeof(uint32_t), ctx->stream), "hipMemsetAsync");
+    fail(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (rc == TTL_OK) {
+        fail(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        // an even chain, so every replay starts from word[0]
+        const uint32_t n = launches + launches % 2;
+        for (uint32_t i = 0; i < n && rc == TTL_OK; ++i) {
+            boundary_kernel<<<blocks, threads, 0, ctx->stream>>>(words, i, words + 2);
+        }
+        fail(hipStreamEndCapture(ctx->stream, &graph), "hipStreamEndCapture");
+        launches = n;
+    }
+    if (rc == TTL_OK) {
+        fail(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+    constexpr int kReps = 20;
+    float ms = 0.0f;
+    if (rc == TTL_OK) {
+        fail(hipGraphLaunch(exec, ctx->stream), "hipGraphLaunch");
+        fail(hipEventRecord(ctx->timer_start, ctx->stream), "hipEventRecord");
+        for (int r = 0; r < kReps && rc == TTL_OK; ++r) {
+            fail(hipGraphLaunch(exec, ctx->stream), "hipGraphLaunch");
+        }
+        fail(hipEventRecord(ctx->timer_stop, ctx->stream), "hipEventRecord");
+        fail(hipEventSynchronize(ctx->timer_stop), "hipEventSynchronize");
+        fail(hipEventElapsedTime(&ms, ctx->timer_start, ctx->timer_stop), "hipEventElapsedTime");
+    }
+    uint32_t host[4] = {0, 0, 0, 0};
+    if (rc == TTL_OK) {
+        fail(hipMemcpy(host, words, sizeof host, hipMemcpyDeviceToHost), "hipMemcpy");
+    }
+    if (exec) {
+        (void)hipGraphExecDestroy(exec);
+    }
+    if (graph) {
+        (void)hipGraphDestroy(graph);
+    }
+    (void)hipFree(words);
+    if (rc != TTL_OK) {
+        return rc;
+    }
+    // every kernel of every replay added one along the chain
+    *wrong = host[0] == launches * uint32_t(kReps + 1) ? 0u : 1u;
+    *us_per_kernel = ms * 1000.0f / float(kReps * launches);
     return TTL_OK;
 }
 

@@ -326,6 +326,8 @@ def load_library():
         "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
         "ttl_stream_read": (i32, [vp, vp, sz, vp]),
         "ttl_measure_handoff": (i32, [vp, i32, u32, C.POINTER(f32), C.POINTER(u32)]),
+        "ttl_measure_boundary": (i32, [vp, u32, u32, u32, C.POINTER(f32), C.POINTER(u32)]),
+        "ttl_stream_read_plain": (i32, [vp, vp, sz, vp]),
         "ttl_matmul_q8_0_workspace_bytes": (sz, [u32, u32]),
         "ttl_matmul_q8_0": (i32, [vp, vp, vp, vp, u32, vp, vp, vp, sz]),
         "ttl_capture_begin": (i32, [vp]),
@@ -550,6 +552,36 @@ class Device:
         _check(self.lib.ttl_measure_handoff(self.ctx, mode, launches, C.byref(us), C.byref(wrong)),
                "ttl_measure_handoff")
         return us.value, wrong.value
+
+    def measure_boundary(self, launches=200, blocks=1, threads=64):
+        """(microseconds per launch of a chain of dependent kernels, 1 if the chain's count
+        came out wrong): the fixed cost of a kernel boundary in a replayed graph."""
+        us, wrong = C.c_float(), C.c_uint32()
+        _check(self.lib.ttl_measure_boundary(self.ctx, launches, blocks, threads, C.byref(us), C.byref(wrong)),
+               "ttl_measure_boundary")
+        return us.value, wrong.value
+
+    def time_stream_read(self, buffers, nbytes, nontemporal=True, reps=20):
+        """Microseconds per launch of a plain read of nbytes (non-temporal or ordinary loads),
+        over the given buffers in turn, captured as one graph and replayed."""
+        sink = self.alloc(256)
+        fn = self.lib.ttl_stream_read if nontemporal else self.lib.ttl_stream_read_plain
+
+        def launches():
+            for b in buffers:
+                _check(fn(self.ctx, b.ptr, nbytes, sink.ptr), "stream read")
+
+        g = self.capture(launches)
+        for _ in range(3):
+            g.launch()
+        self.sync()
+        self.timer_start()
+        for _ in range(reps):
+            g.launch()
+        us = 1e3 * self.timer_stop() / (reps * len(buffers))
+        g.free()
+        sink.free()
+        return us
 
     # ---- synthetic inputs ----
     def synth_normal(self, buf, seed, stream, n, sigma=1.0, mean=0.0, offset=0):
