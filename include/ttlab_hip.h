@@ -85,7 +85,9 @@ int ttl_measure_boundary(ttl_ctx *ctx, uint32_t launches, uint32_t blocks, uint3
 /* The cost of handing 2880 floats from 180 producer workgroups to 32 consumer
  * workgroups, each consumer needing all of them: mode 0 across a kernel boundary (a
  * producer launch, then a consumer launch), mode 1 inside one launch (release fence and
- * a flag per producer, bounded polling, acquire fence).  `launches` handoffs are
+ * a flag per producer, bounded polling, acquire fence), mode 2 inside one launch without
+ * fences (values and flags written through with agent-scope stores after the values
+ * completed, polled and read with agent-scope loads).  `launches` handoffs are
  * captured into a graph and replayed; *us_per_handoff is the average, *wrong the
  * consumers that read a wrong sum or gave up polling (0 when the handoff worked).
  * Measurement only, with no counterpart in the reference: it is why the decode step

@@ -19,12 +19,15 @@ def test_handoff_across_a_boundary_and_inside_a_kernel():
     try:
         boundary, wrong_b = dev.measure_handoff(0, 50)
         inside, wrong_i = dev.measure_handoff(1, 50)
+        nofence, wrong_n = dev.measure_handoff(2, 50)
     finally:
         dev.close()
     print(f"handoff of 2880 floats, 180 producers -> 32 consumers: kernel boundary {boundary:.2f} us, "
-          f"inside one kernel (release/acquire fences, flags) {inside:.2f} us")
+          f"inside one kernel (release/acquire fences, flags) {inside:.2f} us, "
+          f"inside one kernel without fences (write-through stores, coherent loads) {nofence:.2f} us")
     assert wrong_b == 0
     assert wrong_i == 0
+    assert wrong_n == 0
 
 
 def test_kernel_boundary_cost_is_independent_of_the_grid():

@@ -67,29 +67,30 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(const float *__r
     __shared__ float4 qs[kThreads];
     __shared__ float e[kGroup][kChunk];
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
-    // The 8 query heads first (every thread loads one of their 128 float4), then the position,
-    // then the chunk's K and V rows of head kvh (16 float4 per row; positions past n
-    // re-read the last valid one): two round trips in all.
-    // No early exit (the compiler would sink the query loads below it): a workgroup
-    // past the span, or of a position past the capacity, computes chunk 0 of a valid
-    // span and stores nothing.
+    // Full-context layers only (their span starts at position 0), so the chunk's rows do
+    // not depend on the position: the 8 query heads (every thread loads one of their 128
+    // float4), the chunk's 64 K and V rows of head kvh (16 float4 per row; rows past
+    // the capacity re-read the last) and the position are requested together, one
+    // round trip.  Rows past the span's end are read but never used: their scores are
+    // masked and the weighted sum stops at the span's end.
+    // No early exit (the compiler would sink the loads below it): a workgroup past the
+    // span, or of a position past the capacity, computes with a valid count and stores
+    // nothing.
     const float4 qv = reinterpret_cast<const float4 *>(q + size_t(kvh) * kGroup * kHead)[t % (kGroup * kHead / 4)];
-    const uint32_t pos = uint32_t(*position);
-    const Span sp = span_of(pos < capacity ? pos : 0u, layer_index);
-    const bool live = pos < capacity && chunk * kChunk < sp.count;
-    const uint32_t c0 = live ? chunk * kChunk : 0u;
-    const uint32_t start = sp.first + c0;
-    const uint32_t n = min(uint32_t(kChunk), sp.count - c0);
-
     constexpr int kPer = kChunk * (kHead / 4) / kThreads;  // 4 float4 of K and of V per thread
     float4 kr[kPer], vr[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t f = t + uint32_t(k) * kThreads, p = f / (kHead / 4), d4 = f % (kHead / 4);
-        const size_t row = (size_t(start + (p < n ? p : n - 1)) * kKvHeads + kvh) * kHead;
+        const size_t row = (size_t(min(chunk * kChunk + p, capacity - 1)) * kKvHeads + kvh) * kHead;
         kr[k] = reinterpret_cast<const float4 *>(k_cache + row)[d4];
         vr[k] = reinterpret_cast<const float4 *>(v_cache + row)[d4];
     }
+    const uint32_t pos = uint32_t(*position);
+    const Span sp = span_of(pos < capacity ? pos : 0u, layer_index);
+    const bool live = pos < capacity && chunk * kChunk < sp.count;
+    const uint32_t c0 = live ? chunk * kChunk : 0u;
+    const uint32_t n = min(uint32_t(kChunk), sp.count - c0);
     qs[t] = qv;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {

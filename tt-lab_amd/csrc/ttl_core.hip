@@ -146,6 +146,69 @@ __global__ __launch_bounds__(kHandoffThreads) void handoff_consumers_kernel(Hand
     handoff_consume(st, blockIdx.x, true);
 }
 
+// Inside one launch without fences: each producer writes its values with agent-scope
+// stores (written through past its XCD's L2), waits for them to complete, then writes
+// its flag the same way; each consumer polls the flags and reads the values with
+// agent-scope loads (past its own L2), so no L2 is written back or invalidated.
+__global__ __launch_bounds__(kHandoffThreads) void handoff_in_kernel_nofence(HandoffState *st) {
+    const unsigned epoch = __hip_atomic_load(&st->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    if (blockIdx.x < uint32_t(kHandoffProducers)) {
+        if (threadIdx.x < 64) {
+            if (threadIdx.x < 16) {
+                const uint32_t i = blockIdx.x * 16 + threadIdx.x;
+                __hip_atomic_store(&st->data[i], float(i) * 0.5f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (threadIdx.x == 0) {
+                __hip_atomic_store(&st->flags[blockIdx.x * 16], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return;
+    }
+    __shared__ int all;
+    __shared__ float red[kHandoffThreads];
+    if (threadIdx.x == 0) {
+        all = 1;
+    }
+    __syncthreads();
+    if (threadIdx.x < uint32_t(kHandoffProducers)) {
+        unsigned spins = 0;
+        while (__hip_atomic_load(&st->flags[threadIdx.x * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch &&
+               spins < kHandoffMaxSpin) {
+            __builtin_amdgcn_s_sleep(1);
+            ++spins;
+        }
+        if (spins == kHandoffMaxSpin) {
+            all = 0;
+        }
+    }
+    __syncthreads();
+    const uint32_t consumer = blockIdx.x - kHandoffProducers;
+    float sum = 0.0f;
+    for (int i = int(threadIdx.x); i < kHandoffValues; i += kHandoffThreads) {
+        sum += __hip_atomic_load(&st->data[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    red[threadIdx.x] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float a = 0.0f;
+        for (int i = 0; i < kHandoffThreads; ++i) {
+            a += red[i];
+        }
+        st->out[consumer] = all ? a : -1.0f;
+        if (!all) {
+            __hip_atomic_fetch_add(&st->failures, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const unsigned d = __hip_atomic_fetch_add(&st->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == unsigned(kHandoffConsumers - 1)) {
+            __hip_atomic_store(&st->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&st->epoch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 __global__ __launch_bounds__(kHandoffThreads) void handoff_in_kernel(HandoffState *st) {
     const unsigned epoch = __hip_atomic_load(&st->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
     if (blockIdx.x < uint32_t(kHandoffProducers)) {
@@ -455,7 +518,7 @@ int ttl_measure_boundary(ttl_ctx *ctx, uint32_t launches, uint32_t blocks, uint3
 
 int ttl_measure_handoff(ttl_ctx *ctx, int mode, uint32_t launches, float *us_per_handoff, uint32_t *wrong) {
     TTL_REQUIRE(ctx && us_per_handoff && wrong, TTL_ERR_INVALID, "ttl_measure_handoff: null argument");
-    TTL_REQUIRE(mode == 0 || mode == 1, TTL_ERR_INVALID, "ttl_measure_handoff: mode must be 0 or 1");
+    TTL_REQUIRE(mode >= 0 && mode <= 2, TTL_ERR_INVALID, "ttl_measure_handoff: mode must be 0, 1 or 2");
     TTL_REQUIRE(launches >= 1 && launches <= 1000, TTL_ERR_INVALID, "ttl_measure_handoff: 1..1000 launches");
     TTL_REQUIRE(ctx->compute_units >= kHandoffProducers + kHandoffConsumers, TTL_ERR_SHAPE,
                 "ttl_measure_handoff: needs %d resident workgroups", kHandoffProducers + kHandoffConsumers);
@@ -478,8 +541,11 @@ int ttl_measure_handoff(ttl_ctx *ctx, int mode, uint32_t launches, float *us_per
             if (mode == 0) {
                 handoff_producers_kernel<<<kHandoffProducers, kHandoffThreads, 0, ctx->stream>>>(st);
                 handoff_consumers_kernel<<<kHandoffConsumers, kHandoffThreads, 0, ctx->stream>>>(st);
-            } else {
+            } else if (mode == 1) {
                 handoff_in_kernel<<<kHandoffProducers + kHandoffConsumers, kHandoffThreads, 0, ctx->stream>>>(st);
+            } else {
+                handoff_in_kernel_nofence<<<kHandoffProducers + kHandoffConsumers, kHandoffThreads, 0,
+                                            ctx->stream>>>(st);
             }
         }
         fail(hipStreamEndCapture(ctx->stream, &graph), "hipStreamEndCapture");
