@@ -227,8 +227,8 @@ def gpu_decode(args):
                      "bytes_per_launch": GATEUP_BYTES, "launch_us": round(us, 3),
                      "given_indices": {"kernel": "gateup_swiglu_kernel<1, false, 3>", "launch_us": given["us"],
                                        "GBps": given["GBps"], "frac": given["frac"]},
-                     "one_launch_with_down": {"kernel": "gateup_down_kernel<0, true, 1> (not the step's: its "
-                                                        "in-launch handoff costs more than the kernel boundary)",
+                     "one_launch_with_down": {"kernel": "gateup_down_kernel<0, true, 1> (not the step's: level with "
+                                                        "the two launches alone, slower in the step)",
                                               "bytes_per_launch": GATEUP_DOWN_BYTES, "launch_us": fused["us"],
                                               "GBps": fused["GBps"], "frac": fused["frac"]},
                      "read_ceiling": ceiling_entry(achieved, GATEUP_BYTES, us_read)},

@@ -249,11 +249,11 @@ int ttl_moe_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *hidden_d
  * The single launch needs its whole grid (used x 180 workgroups of 512 threads)
  * resident at once; where the occupancy does not allow it, gate/up and down run as two
  * launches with the same results (ttl_moe_gateup_down_fused says which).  The down sums
- * are the same products as ttl_moe_down's in another order.  Slower than the two-launch
- * form on MI355X (46.8 against 10.4 + 5.8 us at the gpt-oss-20b shape: the waits inside
- * the launch cost more than a kernel boundary), so the model's decode step does not use
- * it; kept for callers that cannot launch twice and as the measurement of that choice.
- * No reference counterpart as one call. */
+ * are the same products as ttl_moe_down's in another order.  Level with the two-launch
+ * form on MI355X (16.7 against 10.5 + 5.8 us at the gpt-oss-20b shape) and slightly
+ * slower in the decode step (1.207 against 1.193 ms per token), so the model's step does
+ * not use it; kept for callers that cannot launch twice and as the measurement of that
+ * choice.  No reference counterpart as one call. */
 #define TTL_ROUTE_GATEUP_DOWN 4u
 int ttl_moe_route_gateup_down(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, float *hidden_dev,
                               int32_t *indices_dev, float *weights_dev, float *down_dev, uint32_t stages);

@@ -2,7 +2,10 @@
 
 - ttl_measure_handoff: 2880 floats from 180 producer workgroups to 32 consumers that
   each need all of them, across a kernel boundary and inside one kernel (agent-scope
-  release and acquire fences, bounded polling); both forms must deliver every value;
+  release and acquire fences, or none: agent-scope stores and loads past the L2s;
+  bounded polling); every form must deliver every value.  The fence-free form is the
+  cheapest here, where the producers do nothing else; merged into the step's own
+  launches (the O projection with the router rows, gate/up with down) it did not gain;
 - ttl_measure_boundary: the fixed cost of a kernel boundary in a replayed graph;
 - ttl_stream_read / ttl_stream_read_plain: non-temporal against ordinary loads on a
   stream beyond every cache.

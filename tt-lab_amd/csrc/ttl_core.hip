@@ -186,9 +186,19 @@ __global__ __launch_bounds__(kHandoffThreads) void handoff_in_kernel_nofence(Han
     }
     __syncthreads();
     const uint32_t consumer = blockIdx.x - kHandoffProducers;
+    // all of a thread's loads requested before the first is used: as a loop of loads
+    // each added to the sum, every load waited for the one before (a round trip each)
+    constexpr int kPer = (kHandoffValues + kHandoffThreads - 1) / kHandoffThreads;
+    float v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = min(int(threadIdx.x) + k * kHandoffThreads, kHandoffValues - 1);
+        v[k] = __hip_atomic_load(&st->data[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     float sum = 0.0f;
-    for (int i = int(threadIdx.x); i < kHandoffValues; i += kHandoffThreads) {
-        sum += __hip_atomic_load(&st->data[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        sum += int(threadIdx.x) + k * kHandoffThreads < kHandoffValues ? v[k] : 0.0f;
     }
     red[threadIdx.x] = sum;
     __syncthreads();

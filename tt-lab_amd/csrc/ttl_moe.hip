@@ -904,36 +904,53 @@ __global__ __launch_bounds__(kSplit * 64) void down_kernel(
 // the down rows of the same tile index for the same slot.  Down needs all 2880 hidden
 // values of its slot, written by the slot's 180 gate/up tiles, so the tiles hand them
 // over inside the launch:
-//  - a gate/up tile writes its 16 values with agent-scope stores (written through to
-//    the memory side, past this XCD's L2), waits until they are complete (s_waitcnt)
-//    and adds one to its slot's arrival count;
+//  - a gate/up tile writes its 16 values into its own 128-byte mailbox line with
+//    agent-scope stores (written through to the memory side), waits until they are
+//    complete (s_waitcnt), then raises its flag in 8 replicas, one per XCD, each in a
+//    line of its own: the launch's epoch, one more than the tile's flag of the launch
+//    before (every launch runs every tile, so the tiles agree on it without a count);
 //  - every workgroup issues its down tile's weight loads as soon as its gate/up work
-//    is done (they depend only on the routing), then waits, boundedly, for its slot's
-//    count to reach the tile count, and reads the hidden with agent-scope loads;
-//  - the last workgroup past its wait resets the counts for the next launch.
-// No release fence: on this chip an agent-scope release writes back the whole L2 of
-// the XCD.  Every workgroup must be resident at once (a waiting workgroup holds its CU);
-// the host launches this form only when the occupancy allows the whole grid, and a wait
-// that reaches its bound counts a give-up and leaves NaN rows instead of hanging.
-// The down rows are split over the 8 waves (3 iterations each; down_kernel splits 4
-// ways): the same products, summed in another order.
-// Measured on config 3 (MI355X): 46.8 us per launch, against 10.4 + 5.8 us for
-// gateup_swiglu_kernel and down_kernel as two launches, so the decode step keeps the
-// two.  Per-workgroup timestamps (s_memrealtime) show every workgroup resident within
-// 0.6 us and the gate/up tiles counted by 9-13 us, but the 180 waiters of a slot seeing
-// the full count one after another, about 90 ns apart (12 to 28 us for slot 0): reads
-// and atomics that bypass the L2 serialize on the few lines they share.  Eight count
-// lines per slot shortened those waits, but reading the hidden through the L2 after an
-// agent-scope acquire (which invalidates the XCD's L2, once per workgroup) then took
-// about 30 us.  A kernel boundary makes the hidden visible with one writeback per XCD.
+//    is done (they depend only on the routing), then polls its slot's 180 flags in its
+//    own XCD's replica, one lane each, boundedly, and reads the mailbox with ordinary
+//    loads: no mailbox line is in an L2 when a launch starts (kernel boundaries write
+//    the L2s back and invalidate them) and each line has one writer whose values are in
+//    memory before its flag, so the first reader on an XCD fetches a line and the others
+//    find it in that XCD's L2.
+// No release or acquire fence: on this chip an agent-scope release writes back the
+// XCD's whole L2 and an acquire invalidates it.  Every workgroup must be resident at
+// once (a waiting workgroup holds its CU); the host launches this form only when the
+// occupancy allows the whole grid, and a wait that reaches its bound counts a give-up
+// and leaves NaN rows instead of hanging.  The down rows are split over the 8 waves
+// (3 iterations each; down_kernel splits 4 ways): the same products in another order.
+// Measured on config 3 (MI355X), graph replays: 16.7 us per launch against 10.5 + 5.8 us
+// for gateup_swiglu_kernel and down_kernel, and the decode step 1.207 against 1.193 ms
+// per token with it, so the step keeps the two launches.  Per-workgroup timestamps
+// (s_memrealtime): every workgroup resident within 0.5 us, the gate/up tiles done at
+// 5.4-10.2 us, each slot's waiters released 0.5-2.8 us after its last tile, the mailbox
+// staged about 1 us later and the down rows 1 us after that (the last at 13.7 us).
+// Earlier forms and what they cost: one arrival count per slot, polled by all 180 of
+// the slot's workgroups and read past the L2, 46.8 us (the waiters saw the full count
+// one after another, about 90 ns apart: accesses that bypass the L2 serialize on the
+// line they share); the same with eight count lines per slot and the hidden read
+// through the L2 after an agent-scope acquire (which invalidates the XCD's L2, once per
+// workgroup), about 30 us; per-XCD flags with a global count of departed workgroups to
+// advance the epoch, 22.7 us (720 atomics on one line at the end of every launch).
 constexpr unsigned kHandoffSpinLimit = 1u << 21;
 constexpr int kDownPer = 3;  // down iterations per wave: 8 x 3 = 24 >= 23
 static_assert(kDownPer * 2 * kSplit * mx::lanes_k <= GateUpSplit::x_blocks, "the staged hidden covers the split");
 
+constexpr uint32_t kHoMaxTiles = 180;  // 16-row tiles of a 2880-row gate/up matrix
+constexpr uint32_t kHoXcds = 8;        // one flag replica per XCD (workgroup b runs on XCD b % 8)
+
 struct Handoff {
-    uint32_t arrived[kMaxUsed * 16];  // per slot (one 64-byte line each): gate/up tiles written
-    uint32_t departed;                // workgroups past their wait
-    uint32_t give_ups;                // waits that ended at the spin limit (their rows are NaN)
+    // per (slot, XCD, gate/up tile), one 128-byte line each: the launch in which the tile
+    // published its hidden values (a consumer on XCD x polls replica x only, so each line
+    // has the slot's waiters of one XCD, not all of them)
+    uint32_t flags[kMaxUsed][kHoXcds][kHoMaxTiles][32];
+    // per (slot, tile), one 128-byte line each: the tile's 16 hidden values (one writer
+    // per line, so an XCD's L2 holds no part of another workgroup's line)
+    float mailbox[kMaxUsed][kHoMaxTiles][32];
+    uint32_t give_ups;  // waits that ended at the spin limit (their rows are NaN)
 };
 
 struct DownArgs {
@@ -987,10 +1004,18 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_down_kernel(GateUpArgs 
     const size_t brow = size_t(e_safe) * a.rows + row;
     const float gb = a.gate_bias ? a.gate_bias[brow] : 0.0f;
     const float ub = a.up_bias ? a.up_bias[brow] : 0.0f;
+    uint32_t epoch;
     {
         mxt::SplitRegs<kSplit> regs;
         mxt::split_load<kSplit>(which == 0 ? a.gate_codes : a.up_codes, which == 0 ? a.gate_scales : a.up_scales,
                                 size_t(e_safe) * a.tiles + tile, w, lane, regs);
+        // the launch's epoch: one more than the value this (slot, tile) published in the
+        // launch before, which every tile of the slot also published (each launch runs all
+        // of them), so no workgroup counts the launches for the others (720 atomics on one
+        // line at the end of a launch took about 7 us); requested once the weight loads
+        // are, as it is first needed at the end of gate/up
+        epoch = __hip_atomic_load(&d.handoff->flags[slot][0][tile][0], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) + 1u;
         if (!staged) {
             stage::stage_finish(a.in, pending, xs, red);
         }
@@ -1005,15 +1030,17 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_down_kernel(GateUpArgs 
             const float g = sum_parts<kSplit>(part, lane), u = sum_parts<kSplit>(part + kSplit, lane);
             const float h =
                 valid ? clamped_swiglu(a.gate_bias ? g + gb : g, a.up_bias ? u + ub : u) : __builtin_nanf("");
-            __hip_atomic_store(&a.hidden[size_t(slot) * a.rows + row], h, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            a.hidden[size_t(slot) * a.rows + row] = h;  // the caller's copy (read after the launch)
+            __hip_atomic_store(&d.handoff->mailbox[slot][tile][lane], h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        // the 16 stores are this wave's: once they are complete, count the tile
+        // the mailbox stores are this wave's: once they are complete, raise the tile's
+        // flag in every XCD's replica
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (lane == 0) {
-            __hip_atomic_fetch_add(&d.handoff->arrived[slot * 16], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane < kHoXcds) {
+            __hip_atomic_store(&d.handoff->flags[slot][lane][tile][0], epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 
@@ -1040,22 +1067,44 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_down_kernel(GateUpArgs 
         }
     }
     if (threadIdx.x == 0) {
+        waited = 1;
+    }
+    __syncthreads();
+    // one lane per gate/up tile of the slot polls its flag in this XCD's replica
+    if (threadIdx.x < a.tiles) {
+        const uint32_t *flag = &d.handoff->flags[slot][blockIdx.x % kHoXcds][threadIdx.x][0];
         unsigned spins = 0;
-        while (__hip_atomic_load(&d.handoff->arrived[slot * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                   a.tiles &&
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch &&
                spins < kHandoffSpinLimit) {
             __builtin_amdgcn_s_sleep(1);
             ++spins;
         }
-        waited = spins < kHandoffSpinLimit ? 1 : 0;
+        if (spins == kHandoffSpinLimit) {
+            waited = 0;  // gave up: counted below, never waits longer
+        }
     }
     __syncthreads();
-    // the slot's hidden, read past this XCD's L2, into the padded layout (blocks 90.. zero)
-    float *hs = a.hidden + size_t(slot) * a.rows;
-    for (uint32_t i = threadIdx.x; i < uint32_t(GateUpSplit::x_blocks) * 32; i += kGateUpThreads) {
-        const float v = i < uint32_t(mx::cols) ? __hip_atomic_load(&hs[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                               : 0.0f;
-        xs[(i / 32) * mxt::x_stride + i % 32] = v;
+    // the slot's hidden from the mailbox, into the padded layout (blocks 90.. zero), with
+    // ordinary loads: no part of a mailbox line is in any L2 at the start of a launch
+    // (kernel boundaries write the L2s back and invalidate them) and each line has one
+    // writer, whose values are in memory before its flag, so the first reader on an XCD
+    // fetches the line from memory and the others find it in that XCD's L2.  All of a
+    // thread's loads are requested before the first is used.
+    const float(*mb)[32] = d.handoff->mailbox[slot];
+    constexpr uint32_t kStaged = uint32_t(GateUpSplit::x_blocks) * 32;
+    constexpr int kHiddenPer = int((kStaged + kGateUpThreads - 1) / kGateUpThreads);
+    float hv[kHiddenPer];
+#pragma unroll
+    for (int k = 0; k < kHiddenPer; ++k) {
+        const uint32_t i = min(threadIdx.x + uint32_t(k) * kGateUpThreads, uint32_t(mx::cols) - 1);
+        hv[k] = mb[i / mx::tile_rows][i % mx::tile_rows];
+    }
+#pragma unroll
+    for (int k = 0; k < kHiddenPer; ++k) {
+        const uint32_t i = threadIdx.x + uint32_t(k) * kGateUpThreads;
+        if (i < kStaged) {
+            xs[(i / 32) * mxt::x_stride + i % 32] = i < uint32_t(mx::cols) ? hv[k] : 0.0f;
+        }
     }
     __syncthreads();
     {
@@ -1080,14 +1129,6 @@ __global__ __launch_bounds__(kGateUpThreads) void gateup_down_kernel(GateUpArgs 
     if (threadIdx.x == 0) {
         if (!waited) {
             __hip_atomic_fetch_add(&d.handoff->give_ups, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        // the last workgroup past its wait opens the next launch
-        if (__hip_atomic_fetch_add(&d.handoff->departed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            gridDim.x - 1) {
-            for (uint32_t r = 0; r < a.k; ++r) {
-                __hip_atomic_store(&d.handoff->arrived[r * 16], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __hip_atomic_store(&d.handoff->departed, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -1434,7 +1475,7 @@ int launch_gateup_down(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, flo
     const uint32_t grid = a.tiles * L.used;
     *fused = false;
     // the tile index of gate/up and of down is the same (both 180), so one grid covers both
-    if (d.tiles != a.tiles) {
+    if (d.tiles != a.tiles || a.tiles > kHoMaxTiles || L.used > kMaxUsed) {
         return TTL_OK;
     }
     stage::with_mode(a.in, [&](auto mode) {

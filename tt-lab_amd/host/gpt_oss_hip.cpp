@@ -361,8 +361,9 @@ int HipGptOssModel::enqueue_step() {
         if (status == TTL_OK) {
             // the four experts' down projections (+ bias), one workgroup per (slot, tile);
             // the combine and the residual add run in the next consumer's staging.  (One
-            // launch for gate/up and down, ttl_moe_route_gateup_down, is slower: its
-            // in-launch handoff costs more than this kernel boundary.)
+            // launch for gate/up and down, ttl_moe_route_gateup_down, made the step
+            // slightly slower: its in-launch handoff costs about what this kernel
+            // boundary does.)
             status = ttl_moe_down(ctx_, &layer.moe, hidden_, indices_ + l * kUsed, down_ + l * kUsed * kHidden);
         }
     }
