@@ -24,6 +24,7 @@
 
 #include <cmath>
 #include <type_traits>
+#include <utility>
 
 namespace {
 
@@ -174,99 +175,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_rows_kernel(const float
         // u = 2^-24; 1.001 covers second-order terms (n u < 2e-4); the 1e-12 term
         // covers the f64 rounding of the exact sums; 1e-37 covers subnormal steps.
         scratch->bound[row] = 1.001 * 0x1p-24 * (abs_partials + abs_products) + 1e-12 * abs_products + 1e-37;
-    }
-}
-
-// Router rows of a batch (prefill): the same exact values and bounds as
-// router_rows_kernel, for kRbTokens tokens x kRbExperts experts per workgroup.  The
-// tokens are staged once; each wave takes kRbExperts / 4 experts, loads a row once and
-// runs it against every staged token.  Lane j < 60 holds columns 48j .. 48j+47, so a
-// row's scan over the columns stays within the wave (no barriers between pairs).
-constexpr int kRbTokens = 4;
-constexpr int kRbExperts = 8;
-constexpr int kRbLanes = 60;
-constexpr int kRbCols = kRouterCols / kRbLanes;  // 48
-static_assert(kRbLanes * kRbCols == kRouterCols && kRbCols % 4 == 0, "whole float4 per lane");
-
-template <int MODE>
-__global__ __launch_bounds__(256) void router_rows_batch_kernel(const float *__restrict__ weight,
-                                                                const float *__restrict__ bias, stage::Input in,
-                                                                RouterScratch *scratch, uint32_t x_stride,
-                                                                uint32_t count, uint32_t experts) {
-    __shared__ __attribute__((aligned(16))) float xs[kRbTokens][mxt::x_floats];
-    __shared__ float red[stage::red_floats(mxt::x_blocks)];
-    const uint32_t t = threadIdx.x, lane = t % 64, wave = t / 64;
-    const uint32_t token0 = blockIdx.x * kRbTokens;
-    const uint32_t tokens = min(uint32_t(kRbTokens), count - token0);
-#pragma unroll 1
-    for (uint32_t k = 0; k < uint32_t(kRbTokens); ++k) {
-        stage::Input ik = in;
-        ik.base += size_t(token0 + min(k, tokens - 1)) * x_stride;  // past the batch: a stand-in
-        stage::stage<kRouterCols, mxt::x_blocks, 256, MODE>(ik, xs[k], red);
-    }
-    __syncthreads();
-    const bool active = lane < uint32_t(kRbLanes);
-    const uint32_t c0 = (active ? lane : 0) * kRbCols;
-    auto xat = [&](uint32_t k, uint32_t c) __attribute__((always_inline)) {
-        return *reinterpret_cast<const float4 *>(xs[k] + (c / 32) * mxt::x_stride + c % 32);
-    };
-#pragma unroll 1
-    for (uint32_t r = 0; r < uint32_t(kRbExperts / 4); ++r) {
-        const uint32_t row = blockIdx.y * kRbExperts + wave * (kRbExperts / 4) + r;
-        if (row >= experts) {
-            break;
-        }
-        float4 w[kRbCols / 4];
-        const float4 *w4 = reinterpret_cast<const float4 *>(weight + size_t(row) * kRouterCols + c0);
-#pragma unroll
-        for (int i = 0; i < kRbCols / 4; ++i) {
-            w[i] = w4[i];
-        }
-        const double b = double(bias[row]);
-#pragma unroll 1
-        for (uint32_t k = 0; k < tokens; ++k) {
-            // the lane's products (exact in f64: fma(w, x, s) rounds only the sum, as
-            // s + w x would), their sum and absolute sum
-            double local = 0.0, abs_products = 0.0;
-#pragma unroll
-            for (int i = 0; i < kRbCols / 4; ++i) {
-                const float4 x = xat(k, c0 + 4 * i);
-                const float wa[4] = {w[i].x, w[i].y, w[i].z, w[i].w}, xa[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    local = fma(double(wa[e]), double(xa[e]), local);
-                    abs_products = fma(fabs(double(wa[e])), fabs(double(xa[e])), abs_products);
-                }
-            }
-            if (!active) {
-                local = 0.0;
-                abs_products = 0.0;
-            }
-            const double incl = wave_inclusive_scan(local, lane);
-            // the partial sums S_c of the reference's order, from the bias
-            double running = b + (incl - local), abs_partials = 0.0;
-#pragma unroll
-            for (int i = 0; i < kRbCols / 4; ++i) {
-                const float4 x = xat(k, c0 + 4 * i);
-                const float wa[4] = {w[i].x, w[i].y, w[i].z, w[i].w}, xa[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    running = fma(double(wa[e]), double(xa[e]), running);
-                    abs_partials += fabs(running);
-                }
-            }
-            if (!active) {
-                abs_partials = 0.0;
-            }
-            const double total = __shfl(incl, 63);
-            const double s_partials = wave_sum(abs_partials), s_products = wave_sum(abs_products);
-            if (lane == 0 && k < tokens) {
-                RouterScratch *sk = scratch + token0 + k;
-                sk->exact[row] = b + total;
-                // the bound of router_rows_kernel
-                sk->bound[row] = 1.001 * 0x1p-24 * (s_partials + s_products) + 1e-12 * s_products + 1e-37;
-            }
-        }
     }
 }
 
@@ -751,6 +659,200 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float *__restr
     if (threadIdx.x < k) {
         indices[threadIdx.x] = lds.indices[threadIdx.x];
         weights_out[threadIdx.x] = lds.weights[threadIdx.x];
+    }
+}
+
+// Router logits of a batch in the reference's own order (matmul_add_f32,
+// tensor.cpp:498-527: sum = bias, then sum = sum + w[c] * x[c] for c = 0..2879,
+// every product and every sum rounded to f32).  Each logit is one chain of 2880
+// dependent adds, so a batch is as many chains as (token, expert) pairs: lane l of
+// wave w runs token blockIdx.x * 64 + l against expert blockIdx.y * W + w.  The
+// workgroup's 64 token rows are staged a tile of kRcCols columns at a time into one
+// of two LDS buffers, the next tile's loads in flight while the waves run the
+// current one (one barrier per tile); a lane reads its token's columns 16 bytes at
+// a time.  The expert's weights reach the products through DPP: for each 64-column
+// group g of the tile, lane l holds columns 64 g + 4 (l % 16) .. + 3 (each 16-lane
+// row the same), and the product of column 64 g + 4 j + i takes component i from
+// lane j of its row (row_newbcast), so the broadcast costs no instruction.  One wave
+// per SIMD (W <= 4): a wave's two VALU operations per column (product, sum) are the
+// chain's issue rate.  Logits go to logits[token * experts + expert]; past the
+// batch or the experts, a lane reads a stand-in row and stores nothing.
+constexpr int kRcTokens = 64;
+constexpr int kRcGroups = 3;                 // 64-column groups per tile
+constexpr int kRcCols = 64 * kRcGroups;      // 15 tiles
+constexpr int kRcStride = kRcCols + 4;       // floats; stride / 4 odd: the lanes' b128 reads miss each other's banks
+constexpr int kRcQuads = kRcCols / 4;
+static_assert(kRouterCols % kRcCols == 0 && (kRcStride / 4) % 2 == 1, "whole tiles, conflict-free rows");
+
+// lane j of the caller's 16-lane row (row_newbcast:j)
+template <int J>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xf, 0xf, true));
+}
+
+// f(std::integral_constant<int, 0>) .. f(std::integral_constant<int, N - 1>), in order
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int W>
+__global__ __launch_bounds__(64 * W) void router_chain_batch_kernel(const float *__restrict__ weight,
+                                                                    const float *__restrict__ bias,
+                                                                    const float *__restrict__ x, uint32_t x_stride,
+                                                                    uint32_t count, uint32_t experts,
+                                                                    float *__restrict__ logits) {
+    constexpr int kTiles = kRouterCols / kRcCols;
+    constexpr int kPer = kRcTokens * kRcQuads / (64 * W);  // token pieces (16 bytes) per thread and tile
+    constexpr int kChunk = 4;                              // float4 of x per LDS read batch
+    constexpr int kChunks = kRcQuads / kChunk;
+    static_assert(kRcTokens * kRcQuads % (64 * W) == 0 && 16 % kChunk == 0, "whole pieces, chunks within a group");
+    constexpr int kStaged = (kPer + kChunks - 1) / kChunks;  // staged pieces per chunk
+    static_assert(kTiles % 2 == 1, "tile pairs, then the last tile");
+    // a native vector (not HIP's float4 struct), so the staged pieces stay in registers
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) float xs[2][kRcTokens * kRcStride];
+    const uint32_t t = threadIdx.x, lane = t % 64;
+    const uint32_t wave = uint32_t(__builtin_amdgcn_readfirstlane(int(t / 64)));
+    const uint32_t token0 = blockIdx.x * kRcTokens;
+    const uint32_t last = count - 1 - token0;  // the grid covers the batch: token0 < count
+    const uint32_t expert = blockIdx.y * W + wave;
+    const f4 *wsrc =
+        reinterpret_cast<const f4 *>(weight + size_t(min(expert, experts - 1)) * kRouterCols) + lane % 16;
+    // token piece i of a tile: token (t + 64 W i) / kRcQuads (clamped to the batch),
+    // float4 (t + 64 W i) % kRcQuads
+    const float *xg = x + size_t(token0) * x_stride;
+    uint32_t src[kPer], dst[kPer];  // float offsets from xg, from the LDS buffer
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t p = t + 64u * W * uint32_t(i);
+        src[i] = min(p / kRcQuads, last) * x_stride + 4 * (p % kRcQuads);
+        dst[i] = (p / kRcQuads) * kRcStride + 4 * (p % kRcQuads);
+    }
+    // Two register sets of a tile's token pieces: tile t + 1 is stored from set
+    // (t + 1) % 2 at tile t, which then loads tile t + 3, so a tile's loads have two
+    // tiles' time to land.  The weights are loaded a tile ahead.
+    f4 ra[kPer], rb[kPer], wt[kRcGroups], wn[kRcGroups];
+    auto load = [&](f4(&r)[kPer], int tile) __attribute__((always_inline)) {
+        const float *xt = xg + min(tile, kTiles - 1) * kRcCols;  // past the last tile: a re-read, unused
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            r[i] = *reinterpret_cast<const f4 *>(xt + src[i]);
+        }
+    };
+    auto load_w = [&](f4(&w)[kRcGroups], int tile) __attribute__((always_inline)) {
+        tile = min(tile, kTiles - 1);
+#pragma unroll
+        for (int g = 0; g < kRcGroups; ++g) {
+            w[g] = wsrc[tile * kRcQuads + 16 * g];
+        }
+    };
+    auto store = [&](const f4(&r)[kPer], int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            *reinterpret_cast<f4 *>(xs[buf] + dst[i]) = r[i];
+        }
+    };
+    load(ra, 0);
+    load_w(wt, 0);
+    store(ra, 0);
+    load(rb, 1);
+    load(ra, 2);
+    float sum = bias[min(expert, experts - 1)];
+    __syncthreads();
+    // tile `tile` from LDS buffer tile % 2 with the weights in wt; before chunk c,
+    // stage(i) for its kStaged pieces i (a staged piece's store and its next load,
+    // spread over the tile so a wave never waits to issue a burst of loads)
+    auto compute = [&](int buf, auto &&stage) __attribute__((always_inline)) {
+        const f4 *row = reinterpret_cast<const f4 *>(xs[buf] + lane * kRcStride);
+        f4 xa[kChunk], xb[kChunk];
+#pragma unroll
+        for (int q = 0; q < kChunk; ++q) {
+            xa[q] = row[q];
+        }
+        static_for<kChunks>([&](auto cc) __attribute__((always_inline)) {
+            constexpr int c = decltype(cc)::value;
+            f4(&xc)[kChunk] = c % 2 == 0 ? xa : xb;
+            f4(&xn)[kChunk] = c % 2 == 0 ? xb : xa;
+            if constexpr (c + 1 < kChunks) {
+#pragma unroll
+                for (int q = 0; q < kChunk; ++q) {
+                    xn[q] = row[(c + 1) * kChunk + q];
+                }
+            }
+            static_for<kStaged>([&](auto kk) __attribute__((always_inline)) {
+                constexpr int i = c * kStaged + decltype(kk)::value;
+                if constexpr (i < kPer) {
+                    stage(std::integral_constant<int, i>{});
+                }
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            const f4 w = wt[c * kChunk / 16];
+            static_for<kChunk>([&](auto kk) __attribute__((always_inline)) {
+#pragma clang fp contract(off)
+                constexpr int J = (c * kChunk) % 16 + decltype(kk)::value;
+                const f4 xq = xc[decltype(kk)::value];
+                const float p0 = row_bcast<J>(w.x) * xq.x, p1 = row_bcast<J>(w.y) * xq.y;
+                const float p2 = row_bcast<J>(w.z) * xq.z, p3 = row_bcast<J>(w.w) * xq.w;
+                sum = sum + p0;
+                sum = sum + p1;
+                sum = sum + p2;
+                sum = sum + p3;
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    // one tile: tile + 1 into LDS buffer (tile + 1) % 2 (last read before the previous
+    // barrier) from the set S holding it, which then loads tile + 3; the weights of
+    // tile + 1 are loaded meanwhile and move to wt after this tile's products
+    auto step = [&](auto s_, int tile) __attribute__((always_inline)) {
+        constexpr int S = decltype(s_)::value;  // (tile + 1) % 2
+        f4(&r)[kPer] = S == 1 ? rb : ra;
+        load_w(wn, tile + 1);
+        const float *xt = xg + min(tile + 3, kTiles - 1) * kRcCols;  // past the last tile: a re-read, unused
+        compute(S ^ 1, [&](auto i_) __attribute__((always_inline)) {
+            constexpr int i = decltype(i_)::value;
+            *reinterpret_cast<f4 *>(xs[S] + dst[i]) = r[i];
+            r[i] = *reinterpret_cast<const f4 *>(xt + src[i]);
+        });
+#pragma unroll
+        for (int g = 0; g < kRcGroups; ++g) {
+            wt[g] = wn[g];
+        }
+        __syncthreads();  // every wave is done with buffer tile % 2 before it is refilled
+    };
+#pragma unroll 1
+    for (int tile = 0; tile + 1 < kTiles; tile += 2) {
+        step(std::integral_constant<int, 1>{}, tile);
+        step(std::integral_constant<int, 0>{}, tile + 1);
+    }
+    compute((kTiles - 1) % 2, [](auto) {});
+    if (lane <= last && expert < experts) {
+        logits[size_t(token0 + lane) * experts + expert] = sum;
+    }
+}
+
+// The reference's selection sort and softmax (model.cpp:350-377) on a batch's exact
+// logits: one 64-thread workgroup per token.
+__global__ __launch_bounds__(64) void router_select_logits_kernel(const float *__restrict__ logits,
+                                                                  uint32_t experts, uint32_t k,
+                                                                  int32_t *__restrict__ indices,
+                                                                  float *__restrict__ weights_out) {
+    __shared__ RouteLds lds;
+    const float *row = logits + size_t(blockIdx.x) * experts;
+    for (uint32_t c = threadIdx.x; c < experts; c += 64) {
+        lds.ref_logits[c] = row[c];
+        lds.order[c] = int32_t(c);
+    }
+    __syncthreads();
+    replay_selection(experts, k, nullptr, lds, false);
+    if (threadIdx.x < k) {
+        indices[size_t(blockIdx.x) * k + threadIdx.x] = lds.indices[threadIdx.x];
+        weights_out[size_t(blockIdx.x) * k + threadIdx.x] = lds.weights[threadIdx.x];
     }
 }
 
@@ -1346,9 +1448,10 @@ size_t router_scratch_bytes() {
 }
 
 // Routing of `count` tokens at once (GptOssModel::moe_batch's router and top-k,
-// model.cpp:341-377): token t's input is x + t * hidden (normalized by the layer's
-// input norm if it has one), its exact rows go to scratch[t], its indices and
-// weights to indices/weights + t * used.
+// model.cpp:341-377): token t's input is x + t * hidden (already normalized), its
+// logits in the reference's order go to the scratch (count * experts floats), its
+// indices and weights to indices/weights + t * used.  The logits are exact, so no
+// certificate and no fallback: a batch costs the same whatever its ties.
 int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, uint32_t count, void *scratch,
                         int32_t *indices, float *weights) {
     const int rc = check_router(L.router_weight, L.router_bias, L.experts, L.hidden, x, L.used);
@@ -1356,18 +1459,16 @@ int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, ui
         return rc;
     }
     TTL_REQUIRE(count < 65536, TTL_ERR_SHAPE, "moe_batch router: at most 65535 tokens per call");
-    RouterScratch *s = static_cast<RouterScratch *>(scratch);
-    const stage::Input in = layer_input(L, x);
-    stage::with_mode(in, [&](auto mode) {
-        constexpr int M = decltype(mode)::value;
-        router_rows_batch_kernel<M>
-            <<<dim3((count + kRbTokens - 1) / kRbTokens, (L.experts + kRbExperts - 1) / kRbExperts), 256, 0,
-               ctx->stream>>>(L.router_weight, L.router_bias, in, s, L.hidden, count, L.experts);
-        with_tile_cols(L.experts, [&](auto tc) {
-            router_select_kernel<M, decltype(tc)::value><<<count, 256, 0, ctx->stream>>>(
-                L.router_weight, L.router_bias, L.experts, in, L.used, 0u, s, nullptr, indices, weights, L.hidden);
-        });
-    });
+    TTL_REQUIRE(!L.input_norm, TTL_ERR_INVALID, "moe_batch router: x is the normalized router input");
+    // the logits in the reference's order (the scratch holds count * experts floats),
+    // then the selection
+    static_assert(sizeof(RouterScratch) >= 4 * kMaxExperts, "a token's scratch holds its logits");
+    float *logits = static_cast<float *>(scratch);
+    constexpr int W = 4;
+    router_chain_batch_kernel<W>
+        <<<dim3((count + kRcTokens - 1) / kRcTokens, (L.experts + W - 1) / W), 64 * W, 0, ctx->stream>>>(
+            L.router_weight, L.router_bias, x, L.hidden, count, L.experts, logits);
+    router_select_logits_kernel<<<count, 64, 0, ctx->stream>>>(logits, L.experts, L.used, indices, weights);
     TTL_LAUNCHED("moe_batch router kernels");
     return TTL_OK;
 }
