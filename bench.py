@@ -15,7 +15,10 @@ timed live with HIP events around a graph of the 24 layers' launches; bytes per
 launch are the 4 selected experts' gate and up rows, their biases, x and the
 SwiGLU output.  The line's
 "matvec" field is config 0 (one 5760x2880 MXFP4 matvec over 1.13 GB of rotated
-matrices), measured in the same run: the metric's "MXFP4 matvec GB/s".
+matrices), measured in the same run: the metric's "MXFP4 matvec GB/s".  The
+line's "other_configs" field holds configs 1, 2 (bf16 and scaled paths) and 4 from
+the same run, each its own workload below with fewer steps (--no-other-configs
+skips them).
 
 cpu_baseline: the CPU oracle's restatement of the reference's forward
 (model.cpp:557-602) on one host core, over a bounded sample: one sliding-window
@@ -197,10 +200,12 @@ def gpu_decode(args):
     if args.table:
         write_table(args.table, args, ms, step_bytes, kernels, total_us, us_read)
     # the metric's second half: config 0's standalone MXFP4 matvec, in the same run
-    mv_us, mv_gbs, mv_read = measure_matvec(args)
-    matvec = {"workload": MATVEC_WORKLOAD, "kernel": "matvec_kernel", "bytes_per_launch": MATVEC_BYTES,
-              "launch_us": round(mv_us, 3), "GBps": round(mv_gbs, 1), "frac": round(mv_gbs / HBM_PEAK_GBS, 4),
-              "read_ceiling": ceiling_entry(mv_gbs, MATVEC_BYTES, mv_read)}
+    matvec = None
+    if not getattr(args, "skip_matvec", False):
+        mv_us, mv_gbs, mv_read = measure_matvec(args)
+        matvec = {"workload": MATVEC_WORKLOAD, "kernel": "matvec_kernel", "bytes_per_launch": MATVEC_BYTES,
+                  "launch_us": round(mv_us, 3), "GBps": round(mv_gbs, 1), "frac": round(mv_gbs / HBM_PEAK_GBS, 4),
+                  "read_ceiling": ceiling_entry(mv_gbs, MATVEC_BYTES, mv_read)}
     return {
         "matvec": matvec,
         "value": tok_s,
@@ -728,6 +733,47 @@ def _cpu_baseline(seconds, workload, layers=LAYERS, context=CONTEXT):
                       f"(-O3 -ffp-contract=off -march=x86-64-v3)"}
 
 
+def _summary(res, kernel_keys=("kernel", "launch_us", "GBps", "achieved", "frac", "bytes_per_launch",
+                                 "mfma_algorithmic_TFLOPs", "mfma_peak_TFLOPs")):
+    roof = {k: v for k, v in res["roofline"].items() if k in kernel_keys}
+    ceiling = res["roofline"].get("read_ceiling")
+    if ceiling:
+        roof["read_ceiling_us"] = ceiling["launch_us"]
+        roof["kernel_frac_of_ceiling"] = ceiling["kernel_frac_of_ceiling"]
+    out = {"workload": res["config"]["workload"], "value": round(res["value"], 2), "unit": res["unit"],
+           "ms_per_step": round(res["ms_per_step"], 5), "roofline": roof}
+    if "dtype" in res:
+        out["dtype"] = res["dtype"]
+    return out
+
+
+def other_configs(args):
+    """Configs 1, 2 (both arithmetic paths) and 4 in the default run, so that the driver's
+    own run measures every BASELINE config: each is its own workload's measurement
+    (--workload moe / prefill / decode --config 4) with fewer steps, summarized."""
+    import copy
+
+    out = {}
+    a = copy.copy(args)
+    a.steps, a.warmup = 40, 5
+    t0 = time.time()
+    out["config1"] = _summary(gpu_moe(a))
+    log(f"config 1: {out['config1']['value']:.0f} token-layers/s ({time.time() - t0:.1f} s)")
+    for act in ("bf16", "mxfp8"):
+        t0 = time.time()
+        a = copy.copy(args)
+        a.steps, a.warmup, a.activations = 60, 3, act
+        out[f"config2_{act}"] = _summary(gpu_prefill(a))
+        log(f"config 2 ({act}): {out[f'config2_{act}']['value']:.0f} token-layers/s ({time.time() - t0:.1f} s)")
+    t0 = time.time()
+    a = copy.copy(args)
+    a.config, a.experts, a.layers, a.context = 4, 128, 36, 4096
+    a.steps, a.warmup, a.table, a.skip_matvec = 20, 5, None, True
+    out["config4"] = _summary(gpu_decode(a))
+    log(f"config 4: {out['config4']['value']:.1f} tok/s ({time.time() - t0:.1f} s)")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -754,6 +800,9 @@ def main():
                          "values (counter runs, whose profilers serialize every launch)")
     ap.add_argument("--table", default=None,
                     help="decode workload: also write the per-kind kernel table (text) to this path")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="decode workload: skip configs 1, 2 and 4, which the default run also measures "
+                         "(the line's other_configs field)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device once, a known-size reference "
                          "dispatch for scaling hardware byte counters")
@@ -804,8 +853,10 @@ def main():
         "roofline": res["roofline"],
         "cpu_baseline": base,
     }
-    if "matvec" in res:
+    if res.get("matvec"):
         line["matvec"] = res["matvec"]
+    if args.workload == "decode" and args.config == 3 and not args.no_other_configs:
+        line["other_configs"] = other_configs(args)
     print(json.dumps(line), flush=True)
 
 
