@@ -319,3 +319,49 @@ def test_gateup_and_down_in_one_launch(dev, experts, norm):
     if nb:
         nb.free()
     device.free()
+
+
+def test_gateup_swiglu_nonfinite_gates_follow_reference(dev):
+    """The clamped SwiGLU's non-finite cases (model.cpp:328-332): std::min(gate, 7) and
+    std::clamp(up, -7, 7) return a NaN argument as it is, so a NaN gate or up gives a NaN
+    hidden value; a gate of -inf gives -inf / (1 + exp(inf)) = NaN; a gate of +inf or of
+    1e30 clamps to 7 and an up of +-inf to +-7, finite.  Forced through the biases of the
+    routed experts' rows.  The hidden of ttl_moe_gateup_swiglu against the oracle's gate and
+    up matvecs and orc_swiglu: NaN exactly where the oracle has NaN, the finite entries
+    within 1e-5; the layer output through down is NaN wherever the oracle's is."""
+    host = HostLayer(32, 4, biases=True, seed=0x77000004)
+    x = O.synth_normal(X_SEED, 500, N)
+    _, _, idx, w = host.oracle_moe(x, O.BODY_V4)  # the routing does not read the gate/up biases
+    cases = [("gate", 5, np.nan), ("gate", 6, np.inf), ("gate", 7, -np.inf), ("gate", 8, 1e30),
+             ("up", 9, np.nan), ("up", 10, np.inf), ("up", 11, -np.inf), ("up", 12, -1e30)]
+    for slot, e in enumerate(idx):
+        for kind, row, value in cases:
+            bias = host.gate_b if kind == "gate" else host.up_b
+            bias[int(e) * N + row + 16 * slot] = value  # other rows in each slot
+    device = DeviceLayer(dev, host)
+    xb = dev.upload(x)
+    ib = dev.upload(np.asarray(idx, np.int32))
+    hidden = dev.alloc(4 * N * 4)
+    dev.moe_gateup_swiglu(device.desc, xb, ib, hidden)
+    got = hidden.download(np.float32).reshape(4, N)
+    for slot, e in enumerate(idx):
+        gate = O.mxfp4_matvec(host.gate, host.gate_b, N, N, x, int(e), O.BODY_V4)
+        up = O.mxfp4_matvec(host.up, host.up_b, N, N, x, int(e), O.BODY_V4)
+        ref = np.empty(N, np.float32)
+        O.lib.orc_swiglu(gate, up, N, ref)
+        nan = np.isnan(ref)
+        for kind, row, value in cases:
+            r = row + 16 * slot
+            expect_nan = (kind == "gate" and (np.isnan(value) or value == -np.inf)) or (kind == "up" and np.isnan(value))
+            assert bool(nan[r]) == expect_nan, (slot, kind, row, value)
+        assert np.array_equal(np.isnan(got[slot]), nan), slot
+        assert np.all(np.isfinite(got[slot][~nan]))
+        assert O.rel_l2(got[slot][~nan], ref[~nan]) <= TOL, slot
+    # through down and the combine: every output is NaN, as in the oracle
+    out = dev.alloc(N * 4)
+    dev.moe_decode(device.desc, xb, out)
+    ref_out, _, _, _ = host.oracle_moe(x, O.BODY_V4)
+    assert np.array_equal(np.isnan(out.download(np.float32)), np.isnan(ref_out))
+    for b in (xb, ib, hidden, out):
+        b.free()
+    device.free()
