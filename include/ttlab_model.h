@@ -115,6 +115,33 @@ size_t ttlm_device_bytes(const ttlm_model *model);
  * touched: 4 experts per layer, the attention span per layer, embedding row, unembedding). */
 double ttlm_step_bytes(const ttlm_model *model, uint32_t position);
 
+/* ---- text <-> tokens (ttlab::Tokenizer, tt-lab_amd/host/tokenizer.{hpp,cpp}) ----------
+ * The gpt-oss byte-level BPE of a GGUF file's tokenizer.ggml.* metadata, as the
+ * reference's Tokenizer (tokenizer.h:15-34, tokenizer.cpp:273-406); its constructor
+ * sets LC_CTYPE from the environment, as the reference's does, and the letter, digit and
+ * space classes of the pre-tokenizer follow that locale. */
+typedef struct ttlm_tokenizer ttlm_tokenizer;
+/* Tokenizer(file) (tokenizer.cpp:273-306): maps the file, checks the metadata. */
+int ttlm_tokenizer_open(const char *gguf_path, ttlm_tokenizer **out);
+void ttlm_tokenizer_free(ttlm_tokenizer *tokenizer);
+/* Tokenizer::encode (tokenizer.cpp:308-331) of text[0, length): *count = the number of ids;
+ * min(*count, capacity) of them are written to tokens. */
+int ttlm_tokenizer_encode(const ttlm_tokenizer *tokenizer, const char *text, size_t length, int32_t *tokens,
+                          size_t capacity, size_t *count);
+/* Tokenizer::decode_to (tokenizer.cpp:370-401): the bytes of `token` into out[0, capacity),
+ * *written of them; errors (an id out of range, a buffer too small) as the reference's. */
+int ttlm_tokenizer_decode(const ttlm_tokenizer *tokenizer, int32_t token, int render_special, char *out,
+                          size_t capacity, size_t *written);
+/* Vocabulary size (tokenizer.ggml.tokens). */
+size_t ttlm_tokenizer_vocabulary(const ttlm_tokenizer *tokenizer);
+/* The gpt-4o pre-tokenizer's pieces of text[0, length) under the current LC_CTYPE
+ * (tokenizer.cpp:112-237): *count pieces; ends[i] (i < capacity) is the byte offset where
+ * piece i ends.  No reference counterpart as an entry point (the reference's is internal). */
+int ttlm_pretokenize(const char *text, size_t length, size_t *ends, size_t capacity, size_t *count);
+/* harmony_prompt (tokenizer.cpp:404-406) of user[0, length) into out[0, capacity); returns
+ * the formatted length (the text is cut to capacity). */
+size_t ttlm_harmony_prompt(const char *user, size_t length, char *out, size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,3 +56,27 @@ def test_run_requires_the_end_of_sequence_id(tmp_path):
     done = cli("run", "-m", model_file(tmp_path), "--loose", "-t", "1,2", "-n", "2")
     assert done.returncode == 1
     assert done.stderr.strip() == "error: missing GGUF key: tokenizer.ggml.eos_token_id"
+
+
+def test_tokenize_prints_the_ids_of_the_text(tmp_path):
+    """`ttlab_run tokenize -m <file> -p <text>`: the reference's print_tokens format
+    (main.cpp:99-108, 286-289), the ids of ttlab::Tokenizer without the chat template,
+    equal to the tokenizer oracle's; usage errors as the reference's."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle"))
+    import tokenizer_oracle as T
+    from test_tokenizer import CORPUS, train_merges, write_tokenizer
+
+    path = str(tmp_path / "tok.gguf")
+    lists = write_tokenizer(path, train_merges(CORPUS, 300))
+    text = "Hello world, I'm here.<|end|> 12345"
+    done = cli("tokenize", "-m", path, "-p", text)
+    assert done.returncode == 0, done.stderr
+    ids = T.Tokenizer(*lists).encode(text.encode())
+    assert done.stdout == f"prompt: {text}\ntokens ({len(ids)}): [{', '.join(str(i) for i in ids)}]\n"
+    assert cli("tokenize", "-m", path).returncode == 2                       # no text
+    assert cli("tokenize", "-m", path, "-p", "x", "-n", "3").returncode == 2  # -n is for run
+    assert cli("inspect", "-m", path, "-p", "x").returncode == 2
+    assert cli("run", "-m", path, "-p", "x", "-t", "1").returncode == 2
+    bad = cli("tokenize", "-m", str(tmp_path / "none.gguf"), "-p", "x")
+    assert bad.returncode == 1 and bad.stderr.startswith("error: cannot open")

@@ -179,3 +179,55 @@ def test_command_line_stops_at_end_of_sequence(run):
     assert out == tokens[:tokens.index(eos)]
     # main.cpp counts the forward that produced the end-of-sequence id
     assert f"generated: {len(out)} tokens" in err and f"decode: {len(out)} evals" in err
+
+
+def test_command_line_text_prompt(run):
+    """`ttlab_run run -p <text>` (main.cpp:291-411): the prompt in the Harmony template,
+    encoded by ttlab::Tokenizer (its ids the tokenizer oracle's), generates what the same
+    ids given with -t generate, and prints the formatted prompt followed by each
+    generated token's bytes (decode_to, special tokens rendered)."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle"))
+    import tokenizer_oracle as T
+    from gguf_writer import ARRAY, I32, STRING
+    from test_tokenizer import CORPUS, SPECIALS, byte_chars, train_merges
+
+    tmp, _, _ = run
+    alpha = byte_chars()
+    merges = train_merges(CORPUS, 300)
+    tokens, seen = list(alpha), set(alpha)
+    for a, b in merges:
+        if a + b not in seen and len(tokens) < VOCAB - len(SPECIALS):
+            seen.add(a + b)
+            tokens.append(a + b)
+    k = 0
+    while len(tokens) < VOCAB - len(SPECIALS):  # filler ordinary tokens, two byte characters each
+        t = alpha[(k // 256) % 256] + alpha[k % 256]  # every pair in turn
+        k += 1
+        if t not in seen:
+            seen.add(t)
+            tokens.append(t)
+    types = [1] * len(tokens) + [3] * len(SPECIALS)
+    tokens += SPECIALS
+    merge_text = [f"{a} {b}" for a, b in merges]
+    md = gpt_oss_metadata(LAYERS, EXPERTS, overrides={"tokenizer.ggml.tokens": (ARRAY, (STRING, tokens))})
+    md += [("tokenizer.ggml.model", STRING, "gpt2"), ("tokenizer.ggml.pre", STRING, "gpt-4o"),
+           ("tokenizer.ggml.token_type", ARRAY, (I32, types)), ("tokenizer.ggml.merges", ARRAY, (STRING, merge_text)),
+           ("tokenizer.ggml.eos_token_id", U32, VOCAB)]
+    path = os.path.join(tmp, "gpt-oss-small-text.gguf")
+    write_gguf(path, md, gpt_oss_tensors(LAYERS, EXPERTS, VOCAB, generated, GGML_Q8_0))
+    oracle = T.Tokenizer(tokens, types, merge_text)
+    user = "Hello world, what's 2+2?"
+    formatted = T.harmony_prompt(user.encode())
+    ids = oracle.encode(formatted)
+    by_ids = subprocess.run([CLI, "run", "-m", path, "--loose", "-t", ",".join(str(t) for t in ids), "-n",
+                             str(LIMIT)], capture_output=True, timeout=300)
+    assert by_ids.returncode == 0, by_ids.stderr
+    out_ids = [int(v) for v in by_ids.stdout.split()]
+    assert len(out_ids) == LIMIT
+    by_text = subprocess.run([CLI, "run", "-m", path, "--loose", "-p", user, "-n", str(LIMIT)], capture_output=True,
+                             timeout=300)
+    print(by_text.stdout, by_text.stderr.decode())
+    assert by_text.returncode == 0, by_text.stderr
+    assert by_text.stdout == formatted + b"".join(oracle.decode(t) for t in out_ids) + b"\n"
+    assert f"prefill: {len(ids)} tokens".encode() in by_text.stderr

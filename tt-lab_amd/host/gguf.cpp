@@ -107,8 +107,8 @@ class HeaderParser {
     }
 
     // One metadata value of `kind`: scalars and arrays of scalars keep a pointer to
-    // their bytes in the mapping; strings a view; string arrays (the tokenizer's
-    // vocabulary) are walked over and not kept.
+    // their bytes in the mapping; strings and the elements of string arrays (the
+    // tokenizer's vocabulary and merges) views into it.
     GgufEntry value(GgufKind kind) {
         GgufEntry e;
         e.kind = kind;
@@ -126,8 +126,9 @@ class HeaderParser {
                 if (e.count > uint64_t(end_ - at_) / sizeof(uint64_t)) {
                     fail("GGUF string array is too large");
                 }
+                e.strings.reserve(size_t(e.count));
                 for (uint64_t i = 0; i < e.count; ++i) {
-                    text();
+                    e.strings.push_back(text());
                 }
             } else {
                 const uint64_t w = traits(e.element).width;

@@ -32,6 +32,7 @@ struct GgufEntry {
     uint64_t count = 1;          // arrays only
     const uint8_t *raw = nullptr;  // fixed-size value(s)
     std::string_view text;       // strings
+    std::vector<std::string_view> strings;  // arrays of strings (the tokenizer's vocabulary)
 };
 
 struct GgufTensorInfo {

@@ -1,14 +1,24 @@
 // C API of ttlab::HipGptOssModel (include/ttlab_model.h): exceptions become status codes.
 #include "gguf.hpp"
 #include "gpt_oss_hip.hpp"
+#include "tokenizer.hpp"
 #include "ttlab_model.h"
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <string>
+#include <string_view>
+#include <vector>
 
 struct ttlm_model {
     ttlab::HipGptOssModel *model;
+};
+
+struct ttlm_tokenizer {
+    ttlab::GgufFile file;  // the vocabulary and merges are views into its mapping
+    ttlab::Tokenizer tokenizer;
+    explicit ttlm_tokenizer(const char *path) : file(path), tokenizer(file) {}
 };
 
 namespace {
@@ -175,6 +185,68 @@ size_t ttlm_device_bytes(const ttlm_model *model) {
 
 double ttlm_step_bytes(const ttlm_model *model, uint32_t position) {
     return model ? model->model->step_bytes(position) : 0.0;
+}
+
+int ttlm_tokenizer_open(const char *gguf_path, ttlm_tokenizer **out) {
+    if (!out || !gguf_path) {
+        last_error = "ttlm_tokenizer_open: null argument";
+        return -1;
+    }
+    *out = nullptr;
+    return guarded([&] { *out = new ttlm_tokenizer(gguf_path); });
+}
+
+void ttlm_tokenizer_free(ttlm_tokenizer *tokenizer) {
+    delete tokenizer;
+}
+
+int ttlm_tokenizer_encode(const ttlm_tokenizer *tokenizer, const char *text, size_t length, int32_t *tokens,
+                          size_t capacity, size_t *count) {
+    if (!tokenizer || (!text && length) || (!tokens && capacity) || !count) {
+        last_error = "ttlm_tokenizer_encode: null argument";
+        return -1;
+    }
+    return guarded([&] {
+        const std::vector<int32_t> ids = tokenizer->tokenizer.encode(std::string_view(text ? text : "", length));
+        *count = ids.size();
+        std::memcpy(tokens, ids.data(), std::min(ids.size(), capacity) * sizeof(int32_t));
+    });
+}
+
+int ttlm_tokenizer_decode(const ttlm_tokenizer *tokenizer, int32_t token, int render_special, char *out,
+                          size_t capacity, size_t *written) {
+    if (!tokenizer || (!out && capacity) || !written) {
+        last_error = "ttlm_tokenizer_decode: null argument";
+        return -1;
+    }
+    return guarded([&] { *written = tokenizer->tokenizer.decode_to(token, out, capacity, render_special != 0); });
+}
+
+size_t ttlm_tokenizer_vocabulary(const ttlm_tokenizer *tokenizer) {
+    return tokenizer ? tokenizer->tokenizer.vocabulary_size() : 0;
+}
+
+int ttlm_pretokenize(const char *text, size_t length, size_t *ends, size_t capacity, size_t *count) {
+    if ((!text && length) || (!ends && capacity) || !count) {
+        last_error = "ttlm_pretokenize: null argument";
+        return -1;
+    }
+    return guarded([&] {
+        const std::string_view all(text ? text : "", length);
+        const std::vector<std::string_view> pieces = ttlab::pretokenize(all);
+        *count = pieces.size();
+        for (size_t i = 0; i < pieces.size() && i < capacity; ++i) {
+            ends[i] = size_t(pieces[i].data() - all.data()) + pieces[i].size();
+        }
+    });
+}
+
+size_t ttlm_harmony_prompt(const char *user, size_t length, char *out, size_t capacity) {
+    const std::string formatted = ttlab::harmony_prompt(std::string_view(user ? user : "", user ? length : 0));
+    if (out) {
+        std::memcpy(out, formatted.data(), std::min(formatted.size(), capacity));
+    }
+    return formatted.size();
 }
 
 }  // extern "C"

@@ -1,26 +1,32 @@
-// ttlab_run: the reference CLI's generation path (main.cpp:292-411, `tt-lab run`) on the
-// gfx950 backend.  The model, its checks and its decode loop are the reference's; the
-// prompt arrives as token ids (the tokenizer and the Harmony template stay on the
-// reference's side: `tt-lab tokenize` prints the ids of a formatted prompt).
+// ttlab_run: the reference CLI's generation path (main.cpp:275-411, `tt-lab run` and
+// `tt-lab tokenize`) on the gfx950 backend.  The model, its checks, its decode loop and the
+// tokenizer (ttlab::Tokenizer, the reference's Tokenizer restated) are the reference's.
 //
-//   ttlab_run run -m <model.gguf> -t <id,id,...> [-n <tokens>] [--device <ordinal>] [--loose]
+//   ttlab_run run -m <model.gguf> (-p <prompt> | -t <id,id,...>) [-n <tokens>] [--device <ordinal>] [--loose]
+//   ttlab_run tokenize -m <model.gguf> -p <text>
 //   ttlab_run inspect -m <model.gguf> [--loose]
 //
-// `run` prefills the prompt, then generates as the reference's greedy / forward loop does
-// (the forwards run on the device in chunks) until the end-of-sequence id
-// (tokenizer.ggml.eos_token_id, required as in the reference) or the generation limit,
-// printing each generated id; the timing lines on stderr have the reference's format.  `inspect` applies the model checks
-// (model.cpp:64-206) without a device and prints the shape it found.  Errors print
-// "error: <message>" and exit 1, usage errors exit 2, as main.cpp does.  --loose admits
-// the small test models (check_gguf_model(file, false)).
+// `run -p` formats the prompt with the Harmony template (harmony_prompt), encodes it,
+// prefills it, prints the formatted prompt and then each generated token's text, as the
+// reference does; `run -t` takes the prompt as token ids and prints the generated ids.
+// Generation follows the reference's greedy / forward loop (the forwards run on the device
+// in chunks) until the end-of-sequence id (tokenizer.ggml.eos_token_id, required as in the
+// reference) or the generation limit; the timing lines on stderr have the reference's
+// format.  `tokenize` prints the ids of the text as the reference's does (no template).
+// `inspect` applies the model checks (model.cpp:64-206) without a device and prints the
+// shape it found.  Errors print "error: <message>" and exit 1, usage errors exit 2, as
+// main.cpp does.  --loose admits the small test models (check_gguf_model(file, false)).
 #include "gguf.hpp"
 #include "gpt_oss_hip.hpp"
+#include "tokenizer.hpp"
 
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cstdio>
 #include <iostream>
 #include <limits>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -28,7 +34,9 @@
 namespace {
 
 void usage(const char *argv0) {
-    std::cerr << "usage: " << argv0 << " run -m <model.gguf> -t <id,id,...> [-n <tokens>] [--device <ordinal>] [--loose]\n"
+    std::cerr << "usage: " << argv0
+              << " run -m <model.gguf> (-p <prompt> | -t <id,id,...>) [-n <tokens>] [--device <ordinal>] [--loose]\n"
+              << "       " << argv0 << " tokenize -m <model.gguf> -p <text>\n"
               << "       " << argv0 << " inspect -m <model.gguf> [--loose]\n";
 }
 
@@ -81,7 +89,7 @@ int main(int argc, char **argv) {
         usage(argv[0]);
         return 0;
     }
-    if (command != "run" && command != "inspect") {
+    if (command != "run" && command != "inspect" && command != "tokenize") {
         std::cerr << "unknown command: " << command << '\n';
         usage(argv[0]);
         return 2;
@@ -89,6 +97,7 @@ int main(int argc, char **argv) {
     std::string model_path;
     std::vector<int32_t> prompt;
     bool tokens_set = false, predict_set = false, strict = true;
+    const char *text = nullptr;
     size_t predict = 0, device = 0;
     for (int i = 2; i < argc; ++i) {
         const std::string argument = argv[i];
@@ -100,6 +109,8 @@ int main(int argc, char **argv) {
                 return 2;
             }
             tokens_set = true;
+        } else if ((argument == "-p" || argument == "--prompt") && i + 1 < argc) {
+            text = argv[++i];
         } else if ((argument == "-n" || argument == "--predict" || argument == "--n-predict") && i + 1 < argc) {
             if (!parse_size(argv[++i], &predict)) {
                 std::cerr << "invalid generation limit: " << argv[i] << '\n';
@@ -119,24 +130,53 @@ int main(int argc, char **argv) {
             return 2;
         }
     }
-    if (model_path.empty() || (command == "run" && !tokens_set)) {
+    if (model_path.empty() || (command == "run" && !tokens_set && !text) || (command == "tokenize" && !text)) {
         usage(argv[0]);
         return 2;
     }
-    if (command == "inspect" && (tokens_set || predict_set)) {
+    if (command == "run" && tokens_set && text) {
+        std::cerr << "-p and -t are mutually exclusive\n";
+        usage(argv[0]);
+        return 2;
+    }
+    if (command != "run" && (tokens_set || predict_set)) {
         std::cerr << "-t and -n are only valid for 'run'\n";
+        usage(argv[0]);
+        return 2;
+    }
+    if (command == "inspect" && text) {
+        std::cerr << "-p/--prompt is not valid for 'inspect'\n";
         usage(argv[0]);
         return 2;
     }
 
     try {
         const ttlab::GgufFile file(model_path);
+        if (command == "tokenize") {
+            // main.cpp:99-108, 286-289: the text's ids, without the chat template
+            const ttlab::Tokenizer tokenizer(file);
+            const std::vector<int32_t> ids = tokenizer.encode(text);
+            std::cout << "prompt: " << text << "\ntokens (" << ids.size() << "): [";
+            for (size_t k = 0; k < ids.size(); ++k) {
+                std::cout << (k ? ", " : "") << ids[k];
+            }
+            std::cout << "]\n";
+            return 0;
+        }
         const ttlab::GgufModelShape shape = ttlab::check_gguf_model(file, strict);
         if (command == "inspect") {
             std::cout << "gpt-oss model: " << shape.layers << " layers, " << shape.experts
                       << " experts, vocabulary " << shape.vocab << ", output.weight type " << shape.output_type
                       << '\n';
             return 0;
+        }
+        // main.cpp:291-294: a text prompt in the Harmony template, encoded
+        std::unique_ptr<ttlab::Tokenizer> tokenizer;
+        std::string formatted;
+        if (text) {
+            tokenizer = std::make_unique<ttlab::Tokenizer>(file);
+            formatted = ttlab::harmony_prompt(text);
+            prompt = tokenizer->encode(formatted);
         }
         constexpr size_t context = ttlab::HipGptOssModel::context_length;
         if (prompt.size() > context) {
@@ -153,6 +193,10 @@ int main(int argc, char **argv) {
         const auto prefill_begin = std::chrono::steady_clock::now();
         const float *logits = model.prefill(prompt.data(), prompt.size());
         const auto prefill_end = std::chrono::steady_clock::now();
+        if (tokenizer) {
+            std::cout << formatted << std::flush;
+        }
+        std::array<char, 8192> decoded;
         // The reference's loop (greedy, print, forward) with the forwards run on the device
         // in chunks: generate() feeds each step's argmax (the same first-maximum rule as
         // greedy) to the next step without a host round trip, and the chunk's tokens are
@@ -182,7 +226,13 @@ int main(int argc, char **argv) {
                 break;
             }
             ++generated;
-            std::cout << (generated > 1 ? " " : "") << next << std::flush;
+            if (tokenizer) {
+                const size_t n = tokenizer->decode_to(next, decoded.data(), decoded.size(), true);
+                std::cout.write(decoded.data(), std::streamsize(n));
+                std::cout << std::flush;
+            } else {
+                std::cout << (generated > 1 ? " " : "") << next << std::flush;
+            }
             last = next;
         }
         std::cout << '\n' << std::flush;

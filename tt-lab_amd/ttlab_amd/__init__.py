@@ -108,6 +108,13 @@ def load_model_library():
         "ttlm_prefill_batch": (u32, [vp]),
         "ttlm_gguf_inspect": (i32, [C.c_char_p, i32, C.POINTER(GgufInfo)]),
         "ttlm_create_from_gguf": (i32, [C.c_char_p, i32, u32, i32, C.POINTER(vp)]),
+        "ttlm_tokenizer_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+        "ttlm_tokenizer_free": (None, [vp]),
+        "ttlm_tokenizer_encode": (i32, [vp, C.c_char_p, C.c_size_t, vp, C.c_size_t, C.POINTER(C.c_size_t)]),
+        "ttlm_tokenizer_decode": (i32, [vp, C.c_int32, i32, vp, C.c_size_t, C.POINTER(C.c_size_t)]),
+        "ttlm_tokenizer_vocabulary": (C.c_size_t, [vp]),
+        "ttlm_pretokenize": (i32, [C.c_char_p, C.c_size_t, vp, C.c_size_t, C.POINTER(C.c_size_t)]),
+        "ttlm_harmony_prompt": (C.c_size_t, [C.c_char_p, C.c_size_t, vp, C.c_size_t]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -121,6 +128,67 @@ def _mcheck(rc, what):
     if rc != 0:
         msg = load_model_library().ttlm_last_error()
         raise TtlError(f"{what} failed: {msg.decode() if msg else ''}")
+
+
+class Tokenizer:
+    """ttlab::Tokenizer (include/ttlab_model.h, ttlm_tokenizer_*): the gpt-oss BPE of a
+    GGUF file's tokenizer.ggml.* metadata, as the reference's Tokenizer."""
+
+    def __init__(self, path):
+        self.lib = load_model_library()
+        h = C.c_void_p()
+        _mcheck(self.lib.ttlm_tokenizer_open(os.fsencode(path), C.byref(h)), "ttlm_tokenizer_open")
+        self.handle = h
+
+    def encode(self, text):
+        data = text.encode() if isinstance(text, str) else bytes(text)
+        count = C.c_size_t()
+        cap = 4 * len(data) + 16
+        out = (C.c_int32 * cap)()
+        _mcheck(self.lib.ttlm_tokenizer_encode(self.handle, data, len(data), out, cap, C.byref(count)),
+                "ttlm_tokenizer_encode")
+        assert count.value <= cap
+        return list(out[:count.value])
+
+    def decode(self, token, render_special=True, capacity=1024):
+        """The token's bytes (bytes object); raises TtlError as the reference throws."""
+        buf = C.create_string_buffer(max(capacity, 1))
+        n = C.c_size_t()
+        _mcheck(self.lib.ttlm_tokenizer_decode(self.handle, token, 1 if render_special else 0, buf, capacity,
+                                               C.byref(n)), "ttlm_tokenizer_decode")
+        return buf.raw[:n.value]
+
+    def vocabulary(self):
+        return self.lib.ttlm_tokenizer_vocabulary(self.handle)
+
+    def close(self):
+        if self.handle:
+            self.lib.ttlm_tokenizer_free(self.handle)
+            self.handle = None
+
+
+def pretokenize(text):
+    """The gpt-4o pre-tokenizer's pieces (bytes) under the process's LC_CTYPE."""
+    lib = load_model_library()
+    data = text.encode() if isinstance(text, str) else bytes(text)
+    cap = len(data) + 1
+    ends = (C.c_size_t * cap)()
+    count = C.c_size_t()
+    _mcheck(lib.ttlm_pretokenize(data, len(data), ends, cap, C.byref(count)), "ttlm_pretokenize")
+    pieces, start = [], 0
+    for k in range(count.value):
+        pieces.append(data[start:ends[k]])
+        start = ends[k]
+    return pieces
+
+
+def harmony_prompt(user):
+    lib = load_model_library()
+    data = user.encode() if isinstance(user, str) else bytes(user)
+    n = lib.ttlm_harmony_prompt(data, len(data), None, 0)
+    buf = C.create_string_buffer(n + 1)
+    lib.ttlm_harmony_prompt(data, len(data), buf, n)
+    return buf.raw[:n]
 
 
 class GgufInfo(C.Structure):
