@@ -61,7 +61,8 @@ CORPUS = (
 
 def train_merges(corpus, count):
     """Greedy BPE over the raw corpus (no pre-split): the most frequent adjacent pair,
-    first seen first on ties, merged `count` times."""
+    first seen first on ties, merged `count` times (pairs seen once too, so long merges
+    across the pattern's cuts exist)."""
     alpha = byte_chars()
     seq = [alpha[b] for b in corpus.encode()]
     merges = []
@@ -74,8 +75,6 @@ def train_merges(corpus, count):
         if not freq:
             break
         best = max(freq, key=lambda p: (freq[p], -first[p]))
-        if freq[best] < 2:
-            break
         merges.append(best)
         out, i = [], 0
         while i < len(seq):
