@@ -145,6 +145,12 @@ size_t ttl_mxfp4_bytes(const ttl_mxfp4 *tensor);
  * ttl_moe_prefill* such a tensor with TTL_ERR_SHAPE; HipGptOssModel then runs prefill
  * as decode steps. */
 int ttl_mxfp4_edge_scales(const ttl_mxfp4 *tensor);
+/* 1 if every block with a code of nonzero magnitude has E8M0 scale 114..140, so that every
+ * weight E2M1 x 2^(e-127) is a normal f16, else 0 (negative: error).  Then the exact
+ * prefill path (ttl_moe_prefill*) runs the down GEMM on f16 MFMA, with the SwiGLU hidden
+ * as two f16 planes; otherwise on bf16 MFMA with the hidden as three bf16 planes.  No
+ * reference counterpart (a property of this backend's kernels). */
+int ttl_mxfp4_f16_exact(const ttl_mxfp4 *tensor);
 
 /* Decodes expert `expert` to f32 [rows][cols] on the device (out_dev).
  * mode 0: the reference's table, weight = 2^(e-128) * int(code) (tensor.cpp:34-74).

@@ -21,8 +21,11 @@ class HostLayer:
     matrices generated to those experts; the others stay zero (for oracle runs that
     only read the listed experts)."""
 
-    def __init__(self, experts=32, used=4, biases=False, seed=W_SEED, fill_experts=None):
+    def __init__(self, experts=32, used=4, biases=False, seed=W_SEED, fill_experts=None, scales=None):
+        """scales: optional {"gate"|"up"|"down": (emin, emax)} E8M0 ranges (default 119..125)."""
         self.experts, self.used, self.seed = experts, used, seed
+        self.scales = {k: (119, 125) for k in ("gate", "up", "down")}
+        self.scales.update(scales or {})
         self.router_w = O.synth_normal_bf16(seed, ROUTER_STREAM, experts * N, 0.02)
         if biases:
             self.router_b = O.synth_normal(seed, BIAS_STREAM, experts, sigma=0.1)
@@ -39,7 +42,7 @@ class HostLayer:
         for name, stream in (("gate", GATE_STREAM), ("up", UP_STREAM), ("down", DOWN_STREAM)):
             arr = np.zeros(experts * per, np.uint8)
             for e in fill:
-                arr[e * per:(e + 1) * per] = O.synth_mxfp4(seed, stream + e, N * 90)
+                arr[e * per:(e + 1) * per] = O.synth_mxfp4(seed, stream + e, N * 90, *self.scales[name])
             setattr(self, name, arr)
 
     def oracle_struct(self):
@@ -71,9 +74,9 @@ class DeviceLayer:
         import ttlab_amd
         self.dev, self.host = dev, host
         E = host.experts
-        self.gate = dev.mxfp4_synthetic(N, N, E, host.seed, GATE_STREAM)
-        self.up = dev.mxfp4_synthetic(N, N, E, host.seed, UP_STREAM)
-        self.down = dev.mxfp4_synthetic(N, N, E, host.seed, DOWN_STREAM)
+        self.gate = dev.mxfp4_synthetic(N, N, E, host.seed, GATE_STREAM, *host.scales["gate"])
+        self.up = dev.mxfp4_synthetic(N, N, E, host.seed, UP_STREAM, *host.scales["up"])
+        self.down = dev.mxfp4_synthetic(N, N, E, host.seed, DOWN_STREAM, *host.scales["down"])
         self.bufs = [dev.upload(a) for a in (host.router_w, host.router_b, host.gate_b, host.up_b, host.down_b)]
         d = ttlab_amd.MoeLayerDesc()
         d.hidden, d.expert_hidden, d.experts, d.used = N, N, E, host.used

@@ -271,6 +271,31 @@ def test_mfma_entry_points_refuse_edge_scales(dev):
         b.free()
 
 
+def test_f16_exact_flag_at_upload(dev):
+    """ttl_mxfp4_f16_exact: 1 when every block with a code of nonzero magnitude has E8M0
+    scale 114..140 (every weight a normal f16), the range of the f16 down GEMM; a block of
+    zero codes does not count, whatever its scale."""
+    rows = 64
+    base = O.synth_mxfp4(0x77000000, 10, rows * 90)
+    t = dev.mxfp4_upload(base, rows, N, 1)
+    assert t.f16_exact
+    t.free()
+    for e, zero_codes, exact in ((113, False, False), (141, False, False), (114, False, True), (140, False, True),
+                                 (113, True, True), (200, True, True)):
+        blocks = base.copy()
+        blocks[17 * 777] = e
+        if zero_codes:
+            blocks[17 * 777 + 1:17 * 778] = 0x88 if e == 200 else 0  # +0 and -0 codes
+        t = dev.mxfp4_upload(blocks, rows, N, 1)
+        assert t.f16_exact == exact, (e, zero_codes)
+        assert not t.edge_scales
+        t.free()
+    for emin, emax, exact in ((114, 140, True), (113, 125, False), (119, 141, False)):
+        syn = dev.mxfp4_synthetic(rows, N, 2, 1, 1, emin=emin, emax=emax)
+        assert syn.f16_exact == exact, (emin, emax)
+        syn.free()
+
+
 def test_config0_as_one_5760_row_matrix(dev):
     """The {2880, 2880, 2} bytes uploaded as one 5760-row matrix (the bench's config-0
     launch) give bitwise the two experts' rows, and the oracle's values."""

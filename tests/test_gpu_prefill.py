@@ -178,6 +178,55 @@ def test_moe_prefill_intermediates_exact_path(dev, layer8):
             b.free()
 
 
+@pytest.mark.parametrize("down_scales,f16", [((119, 125), True), ((110, 125), False), ((126, 145), False)])
+def test_moe_prefill_down_decode_paths(dev, down_scales, f16):
+    """The exact path's down GEMM: with every down scale in E8M0 114..140 the hidden is two
+    f16 planes of h x 2^8 against f16 weights, else three bf16 planes against bf16 weights
+    (ttl_mxfp4_f16_exact says which).  Both against the oracle within 1e-5 per token, for
+    f32 and bf16 tokens; the hidden the down GEMM reads (ttl_moe_prefill_intermediates)
+    against orc_swiglu of the oracle's gate and up, and the down rows against the oracle's
+    matvec on that hidden, within 1e-5."""
+    host = HostLayer(8, 4, biases=True, seed=0x77000140, scales={"down": down_scales})
+    device = DeviceLayer(dev, host)
+    count, used = 24, 4
+    try:
+        assert device.down.f16_exact == f16
+        idx, w = balanced_routing(count, 8, used, 31)
+        for dtype in (ttlab_amd.TTL_DTYPE_F32, ttlab_amd.TTL_DTYPE_BF16):
+            if dtype == ttlab_amd.TTL_DTYPE_BF16:
+                x = O.synth_normal_bf16(0x78000140, 1, count * N, 1.0).reshape(count, N)
+            else:
+                x = O.synth_normal(0x78000140, 2, count * N).reshape(count, N)
+            got = run_prefill(dev, device, x, idx, w, dtype)
+            ref = oracle_prefill(host, x, idx, w)
+            for p in range(count):
+                assert O.rel_l2(got[p], ref[p]) <= TOL, (dtype, p)
+        dtype = ttlab_amd.TTL_DTYPE_F32
+        x = O.synth_normal(0x78000140, 3, count * N).reshape(count, N)
+        xb, ib, wb = dev.upload(x), dev.upload(idx), dev.upload(w)
+        ws = dev.alloc(dev.moe_prefill_workspace_bytes(count, 8, used, dtype))
+        out, hid, dwn = dev.alloc(count * N * 4), dev.alloc(count * used * N * 4), dev.alloc(count * used * N * 4)
+        try:
+            dev.moe_prefill_experts(device.desc, xb, dtype, count, ib, wb, out, ws)
+            dev.moe_prefill_intermediates(device.desc, dtype, count, ws, hid, dwn)
+            hidden = hid.download(np.float32).reshape(count, used, N)
+            down = dwn.download(np.float32).reshape(count, used, N)
+            for p, r in ((0, 0), (9, 3), (23, 1)):
+                e = int(idx[p, r])
+                gate = O.mxfp4_matvec(host.gate, host.gate_b, N, N, x[p], expert=e, body=O.BODY_DEFAULT)
+                up = O.mxfp4_matvec(host.up, host.up_b, N, N, x[p], expert=e, body=O.BODY_DEFAULT)
+                h = np.empty(N, np.float32)
+                O.lib.orc_swiglu(gate, up, N, h)
+                assert O.rel_l2(hidden[p, r], h) <= TOL, (p, r)
+                d = O.mxfp4_matvec(host.down, host.down_b, N, N, hidden[p, r], expert=e, body=O.BODY_DEFAULT)
+                assert O.rel_l2(down[p, r], d) <= TOL, (p, r)
+        finally:
+            for b in (xb, ib, wb, ws, out, hid, dwn):
+                b.free()
+    finally:
+        device.free()
+
+
 def test_moe_prefill_uneven_buckets_and_invalid_index(dev, layer8):
     # experts with 0, 1, 2 and 70 (two tiles) tokens; one pair with an index out of range
     host, device = layer8

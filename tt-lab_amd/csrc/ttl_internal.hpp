@@ -48,6 +48,21 @@ struct ttl_mxfp4 {
         }
         return false;
     }
+    // Per expert: some block with a nonzero code has an E8M0 scale outside 114..140, where
+    // E2M1 times the scale is not always a normal f16 (the f16 decode of the prefill's down
+    // GEMM is exact only inside; such tensors take the bf16 decode).
+    std::vector<uint8_t> f16_inexact_experts;
+    bool f16_exact() const {
+        if (f16_inexact_experts.size() != experts) {
+            return false;  // not computed for this tensor
+        }
+        for (uint8_t f : f16_inexact_experts) {
+            if (f) {
+                return false;
+            }
+        }
+        return true;
+    }
 };
 
 // Q8_0 tensor in the repacked layout (see q8:: constants in ttl_q8_tile.hpp): rows of
@@ -137,8 +152,9 @@ constexpr int scale_pad = 24;                                 // per-lane scale 
 constexpr size_t tile_code_bytes = size_t(blocks) * tile_rows * 16;          // 23040
 constexpr size_t tile_scale_bytes = size_t(lanes_k) * tile_rows * scale_pad; // 1536
 constexpr uint8_t pad_scale = 127;                            // scale of padding blocks
-// One 32-bit word per expert after the scale plane, set by the repack for the edge
-// scales (ttl_mxfp4::edge_experts).
+// One 32-bit word per expert after the scale plane, set by the repack: bit 0 for the edge
+// scales (ttl_mxfp4::edge_experts), bit 1 for scales outside the f16 decode's range
+// (ttl_mxfp4::f16_inexact_experts).
 inline size_t edge_flag_bytes(uint32_t experts) {
     return (size_t(experts) * 4 + 15) / 16 * 16;
 }

@@ -93,6 +93,67 @@ __device__ inline void split_planes(const float (&v)[8], uint4 (&out)[P]) {
     }
 }
 
+// ---- f16 operands (the prefill's hidden as two planes) ------------------------------------
+//
+// v_mfma_f32_16x16x32_f16 has the bf16 instruction's operand layout and rate.  Its use
+// here: the SwiGLU hidden, an f32 vector of magnitude at most 7 x 8 = 56 (the clamps of
+// model.cpp:328-332), as two f16 planes against weights decoded to f16.  The weights'
+// products stay exact where every E2M1 value times its E8M0 scale is a normal f16, E8M0
+// f16_scale_min..f16_scale_max; the hidden's two planes hold 22 of its 24 bits (hi rounded
+// to nearest, lo the rounded remainder).
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// 0.5 x 2^(e-127) >= 2^-14 and 6 x 2^(e-127) <= 65504
+constexpr uint32_t f16_scale_min = 114, f16_scale_max = 140;
+// The hidden is scaled by 2^kHiddenF16Shift before its split (56 x 2^8 = 14336 < 65504), so
+// its low plane stays a normal f16 down to |h| = 2^-11.
+constexpr int kHiddenF16Shift = 8;
+
+__device__ inline f32x4 mfma(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// decode_step with f16 weights (exact for E8M0 f16_scale_min..f16_scale_max).
+__device__ inline f16x8 decode_step_f16(uint32_t word, float scale) {
+    const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, scale, 0);
+    const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, scale, 1);
+    const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, scale, 2);
+    const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, scale, 3);
+    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// The decode of operand type V (bf16x8 or f16x8).
+template <class V>
+__device__ inline V decode_as(uint32_t word, float scale);
+template <>
+__device__ inline bf16x8 decode_as<bf16x8>(uint32_t word, float scale) {
+    return decode_step(word, scale);
+}
+template <>
+__device__ inline f16x8 decode_as<f16x8>(uint32_t word, float scale) {
+    return decode_step_f16(word, scale);
+}
+
+// Two f16 planes of 8 f32 values times 2^SHIFT, packed as the MFMA fragments are (value
+// 2k in the low half of dword k).  A non-finite value stays in the first plane (a NaN a
+// NaN) and the second is zero.
+template <int SHIFT>
+__device__ inline void split_f16x2(const float (&v)[8], uint4 (&out)[2]) {
+    uint32_t hi[8], lo[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float s = __builtin_amdgcn_ldexpf(v[j], SHIFT);
+        const _Float16 h = _Float16(s);
+        const _Float16 l = isfinite(s) ? _Float16(s - float(h)) : _Float16(0.0f);
+        hi[j] = __builtin_bit_cast(uint16_t, h);
+        lo[j] = __builtin_bit_cast(uint16_t, l);
+    }
+    out[0] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16));
+    out[1] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16));
+}
+
 }  // namespace mf
 
 // The scaled path: v_mfma_scale_f32_16x16x128_f8f6f4 with MXFP4 weights as A and

@@ -39,10 +39,13 @@ __global__ void repack_kernel(const uint8_t *__restrict__ gguf, uint32_t rows, u
     const uint8_t e8 = src[0];
     scales[mx::scale_offset(tile_index, block, row % mx::tile_rows)] = e8;
     // E8M0 255, or 0 with a code of nonzero magnitude (zero codes decode to 0 at any
-    // finite scale): the bf16 MFMA decode cannot represent the block
+    // finite scale): the bf16 MFMA decode cannot represent the block (bit 0); a nonzero
+    // block outside the f16 decode's exact range (bit 1)
     const bool nonzero = ((w[0] | w[1] | w[2] | w[3]) & 0x77777777u) != 0;
-    if (e8 == 255 || (e8 == 0 && nonzero)) {
-        edge_flag[e] = 1u;  // every writer stores the same value
+    const uint32_t flags = ((e8 == 255 || (e8 == 0 && nonzero)) ? 1u : 0u) |
+                           ((nonzero && (e8 < mf::f16_scale_min || e8 > mf::f16_scale_max)) ? 2u : 0u);
+    if (flags) {
+        atomicOr(&edge_flag[e], flags);
     }
 }
 
@@ -260,7 +263,12 @@ int ttl_mxfp4_upload_dev(ttl_ctx *ctx, const void *gguf_blocks_dev, uint32_t row
         *out = nullptr;
         return ttl::hip_fail(err, "ttl_mxfp4_upload_dev: repack_kernel");
     }
-    t->edge_experts.assign(edge.begin(), edge.end());
+    t->edge_experts.resize(experts);
+    t->f16_inexact_experts.resize(experts);
+    for (uint32_t e = 0; e < experts; ++e) {
+        t->edge_experts[e] = uint8_t(edge[e] & 1u);
+        t->f16_inexact_experts[e] = uint8_t((edge[e] >> 1) & 1u);
+    }
     return TTL_OK;
 }
 
@@ -289,12 +297,18 @@ int ttl_mxfp4_synthetic(ttl_ctx *ctx, uint32_t rows, uint32_t cols, uint32_t exp
     }
     // every expert then holds such blocks (a block of 32 zero codes has odds 2^-128)
     (*out)->edge_experts.assign(experts, emin == 0 || emax == 255 ? 1 : 0);
+    (*out)->f16_inexact_experts.assign(experts, emin < mf::f16_scale_min || emax > mf::f16_scale_max ? 1 : 0);
     return ttl::synth_mxfp4_repacked(ctx, *out, seed, stream, emin, emax);
 }
 
 int ttl_mxfp4_edge_scales(const ttl_mxfp4 *t) {
     TTL_REQUIRE(t, TTL_ERR_INVALID, "ttl_mxfp4_edge_scales: null tensor");
     return t->edge_scales() ? 1 : 0;
+}
+
+int ttl_mxfp4_f16_exact(const ttl_mxfp4 *t) {
+    TTL_REQUIRE(t, TTL_ERR_INVALID, "ttl_mxfp4_f16_exact: null tensor");
+    return t->f16_exact() ? 1 : 0;
 }
 
 int ttl_mxfp4_download(ttl_ctx *ctx, const ttl_mxfp4 *t, void *gguf_blocks) {

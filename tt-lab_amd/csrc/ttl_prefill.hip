@@ -545,7 +545,7 @@ struct AOperand {
 // decode(s, w) fills the M A fragments of step s of the quad; stage_end(stage)
 // runs after the last MFMA of each stage (publishes the next one).  Only the first
 // NC column tiles are multiplied (narrow tiles leave the others unread).
-template <int P, int M, int LOOK, int NC, class Decode, class StageEnd>
+template <int P, int M, int LOOK, int NC, class V = bf16x8, class Decode, class StageEnd>
 __device__ __attribute__((always_inline)) inline void quad_mfma(const mf::u32x4 *buf0, const mf::u32x4 *buf1,
                                                                 int i, uint32_t lane, Decode &&decode,
                                                                 StageEnd &&stage_end, f32x4 (&acc)[M][NC]) {
@@ -560,17 +560,17 @@ __device__ __attribute__((always_inline)) inline void quad_mfma(const mf::u32x4 
         const mf::u32x4 *buf = (stage % 2) ? buf1 : buf0;
         auto frag = [&](int f) __attribute__((always_inline)) {
             const int ls = f / FPS, c = (f % FPS) / P, p = f % P;
-            return mf::as_bf16x8v(buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
+            return __builtin_bit_cast(V, buf[((p * SS::steps + ls) * mf::col_tiles + c) * 64 + lane]);
         };
-        bf16x8 ring[D];
+        V ring[D];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             ring[d] = frag(d);
         }
-        bf16x8 w[M];
+        V w[M];
 #pragma unroll
         for (int f = 0; f < SF; ++f) {
-            const bf16x8 b = ring[f % D];
+            const V b = ring[f % D];
             if (f + D < SF) {
                 ring[f % D] = frag(f + D);
             }
@@ -648,7 +648,9 @@ __device__ inline bool tile_of_workgroup(const PlanHeader *header, uint32_t &til
 
 // Accumulators: [matrix (gate 0/1, up 2/3)][column tile]; NC column tiles (the plan's
 // wide tiles with all of them, or its narrow ones with kNarrowCols).
-template <int PX, int NC>
+// F16H: the hidden as two f16 planes of h x 2^kHiddenF16Shift (for the f16 down GEMM),
+// else three exact bf16 planes.
+template <int PX, int NC, bool F16H>
 __device__ __attribute__((always_inline)) inline void gateup_tile(
     const GateUpArgs &a, uint32_t tile, uint32_t row_group,
     mf::u32x4 (*lds)[Stager<PX, kGuWaves * 64>::lds_chunks]) {
@@ -762,25 +764,30 @@ __device__ __attribute__((always_inline)) inline void gateup_tile(
             h[2 * i] = moe_math::clamped_swiglu(acc[0][c][i], acc[2][c][i]);
             h[2 * i + 1] = moe_math::clamped_swiglu(acc[1][c][i], acc[3][c][i]);
         }
-        uint4 planes[kHiddenPlanes];
-        mf::split_planes<kHiddenPlanes>(h, planes);
+        constexpr int HP = F16H ? 2 : kHiddenPlanes;
+        uint4 planes[HP];
+        if constexpr (F16H) {
+            mf::split_f16x2<mf::kHiddenF16Shift>(h, planes);
+        } else {
+            mf::split_planes<HP>(h, planes);
+        }
         const size_t off = ((size_t(quad) * 4 + g) * mf::col_tiles + c) * mf::frag_bytes + (gb * 16 + n16) * 16;
 #pragma unroll
-        for (int p = 0; p < kHiddenPlanes; ++p) {
+        for (int p = 0; p < HP; ++p) {
             *reinterpret_cast<uint4 *>(hb + size_t(p) * mf::plane_bytes + off) = planes[p];
         }
         // blocks 90 and 91 (quad 22, lane groups 2 and 3) hold no rows: zero
         if (beta + 2 >= uint32_t(mx::blocks) && beta < uint32_t(mx::blocks)) {
             const size_t zoff = off + 2 * 16 * 16;
 #pragma unroll
-            for (int p = 0; p < kHiddenPlanes; ++p) {
+            for (int p = 0; p < HP; ++p) {
                 *reinterpret_cast<uint4 *>(hb + size_t(p) * mf::plane_bytes + zoff) = make_uint4(0, 0, 0, 0);
             }
         }
     }
 }
 
-template <int PX>
+template <int PX, bool F16H>
 __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void gateup_kernel(GateUpArgs a) {
     __shared__ mf::u32x4 lds[2][Stager<PX, kGuWaves * 64>::lds_chunks];
     uint32_t tile, row_group;
@@ -789,9 +796,9 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
         return;
     }
     if (narrow) {
-        gateup_tile<PX, kNarrowCols>(a, tile, row_group, lds);
+        gateup_tile<PX, kNarrowCols, F16H>(a, tile, row_group, lds);
     } else {
-        gateup_tile<PX, mf::col_tiles>(a, tile, row_group, lds);
+        gateup_tile<PX, mf::col_tiles, F16H>(a, tile, row_group, lds);
     }
 }
 
@@ -801,13 +808,17 @@ struct MatmulArgs {
     const uint8_t *codes, *scales;
     const float *bias;  // [experts][rows] or null
     uint32_t rows, tiles_per_expert;
-    const uint8_t *frags;  // [tile][P][plane_bytes]
+    const uint8_t *frags;  // [tile][tile_planes][plane_bytes], the GEMM reading the first P planes
+    uint32_t tile_planes;
     Plan plan;
     float *out;          // SCATTER: [x_rows][rows] by token; else [slots][rows] by slot
     uint32_t out_rows;   // SCATTER: rows of out (tokens beyond are skipped)
 };
 
-template <int P, bool SCATTER, int NC>
+// V: the operand type (bf16x8, or f16x8 for the hidden's two f16 planes); the B operand
+// then holds its values times 2^SHIFT, so the accumulator starts at bias x 2^SHIFT and is
+// scaled back at the store (powers of two: exact).
+template <int P, bool SCATTER, int NC, class V, int SHIFT>
 __device__ __attribute__((always_inline)) inline void matmul_tile(const MatmulArgs &a, uint32_t tile,
                                                                   uint32_t row_group,
                                                                   mf::u32x4 (*lds)[Stager<P, kMmWaves * 64>::lds_chunks]) {
@@ -819,7 +830,7 @@ __device__ __attribute__((always_inline)) inline void matmul_tile(const MatmulAr
     const bool rows_ok = row0 < a.rows;  // waves past the last row only help stage
     const uint32_t row_base = rows_ok ? row0 : 0;
     const size_t tile0 = size_t(expert) * a.tiles_per_expert + row_base / 16;
-    const uint8_t *frags = a.frags + size_t(tile) * P * mf::plane_bytes;
+    const uint8_t *frags = a.frags + size_t(tile) * a.tile_planes * mf::plane_bytes;
 
     AOperand<kMmTiles> wa;
     size_t ti[kMmTiles];
@@ -839,6 +850,12 @@ __device__ __attribute__((always_inline)) inline void matmul_tile(const MatmulAr
                 const float4 v =
                     *reinterpret_cast<const float4 *>(a.bias + size_t(expert) * a.rows + row_base + 16 * m + 4 * g);
                 b = f32x4{v.x, v.y, v.z, v.w};
+                if constexpr (SHIFT != 0) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        b[k] = __builtin_amdgcn_ldexpf(b[k], SHIFT);
+                    }
+                }
             }
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
@@ -875,14 +892,14 @@ __device__ __attribute__((always_inline)) inline void matmul_tile(const MatmulAr
             sc[m] = wa.scale(m);
         }
         wa.next_quad();
-        auto decode = [&](int s, bf16x8(&w)[kMmTiles]) __attribute__((always_inline)) {
+        auto decode = [&](int s, V(&w)[kMmTiles]) __attribute__((always_inline)) {
 #pragma unroll
             for (int m = 0; m < kMmTiles; ++m) {
                 const uint32_t word = s == 0 ? q[m].x : (s == 1 ? q[m].y : (s == 2 ? q[m].z : q[m].w));
-                w[m] = mf::decode_step(word, sc[m]);
+                w[m] = mf::decode_as<V>(word, sc[m]);
             }
         };
-        quad_mfma<P, kMmTiles, 4, NC>(lds[0], lds[1], i, lane, decode, stage_end, acc);
+        quad_mfma<P, kMmTiles, 4, NC, V>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
     for (int i = 0; i < mf::quads; i += 3) {
@@ -925,13 +942,19 @@ __device__ __attribute__((always_inline)) inline void matmul_tile(const MatmulAr
         float *dst = a.out + out_row * a.rows + row0 + 4 * g;
 #pragma unroll
         for (int m = 0; m < kMmTiles; ++m) {
-            *reinterpret_cast<float4 *>(dst + 16 * m) = make_float4(acc[m][c][0], acc[m][c][1], acc[m][c][2],
-                                                                    acc[m][c][3]);
+            f32x4 v = acc[m][c];
+            if constexpr (SHIFT != 0) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[k] = __builtin_amdgcn_ldexpf(v[k], -SHIFT);
+                }
+            }
+            *reinterpret_cast<float4 *>(dst + 16 * m) = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
 }
 
-template <int P, bool SCATTER>
+template <int P, bool SCATTER, class V = bf16x8, int SHIFT = 0>
 __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
     __shared__ mf::u32x4 lds[2][Stager<P, kMmWaves * 64>::lds_chunks];
     uint32_t tile, row_group;
@@ -940,9 +963,9 @@ __global__ __launch_bounds__(kMmWaves * 64) void matmul_kernel(MatmulArgs a) {
         return;
     }
     if (narrow) {
-        matmul_tile<P, SCATTER, kNarrowCols>(a, tile, row_group, lds);
+        matmul_tile<P, SCATTER, kNarrowCols, V, SHIFT>(a, tile, row_group, lds);
     } else {
-        matmul_tile<P, SCATTER, mf::col_tiles>(a, tile, row_group, lds);
+        matmul_tile<P, SCATTER, mf::col_tiles, V, SHIFT>(a, tile, row_group, lds);
     }
 }
 
@@ -1437,11 +1460,12 @@ __global__ __launch_bounds__(256) void mx8_dequantize_kernel(const void *__restr
 // ---- the intermediates, read back for inspection -----------------------------------------
 
 // One workgroup per (token, rank) pair p: the pair's SwiGLU hidden as the down GEMM
-// reads it (the MXFP8 codes times their E8M0 scale on the scaled path, the sum of the
-// three bf16 planes otherwise) and its down row (bias included, before the routing
+// reads it (the MXFP8 codes times their E8M0 scale on the scaled path; the sum of the
+// three bf16 planes, or of the two f16 planes scaled back by 2^-kHiddenF16Shift, on the
+// exact one) and its down row (bias included, before the routing
 // weight), from the workspace a full prefill left.  A pair without a slot (invalid
 // expert index) gets NaN rows.  The slot's tile is found by a scan of the plan's tiles.
-template <bool SCALED>
+template <bool SCALED, bool F16H>
 __global__ __launch_bounds__(256) void prefill_intermediates_kernel(Plan plan, uint32_t rows,
                                                                     float *__restrict__ hidden_out,
                                                                     float *__restrict__ down_out,
@@ -1482,16 +1506,24 @@ __global__ __launch_bounds__(256) void prefill_intermediates_kernel(Plan plan, u
             }
         } else {
             // element e of block beta: K step 4 quad + (e % 16) / 4, lane (beta % 4, n16),
-            // bf16 2 (e % 4) + e / 16 of the lane's 8
+            // value 2 (e % 4) + e / 16 of the lane's 8
             const uint8_t *hb = plan.hb + size_t(tile) * kHiddenPlanes * mf::plane_bytes;
             const size_t off = ((size_t(quad) * 4 + (e % 16) / 4) * mf::col_tiles + c) * mf::frag_bytes +
                                (g * 16 + n16) * 16 + 2 * (2 * (e % 4) + e / 16);
-            v = 0.0f;
+            auto half = [&](int pl) __attribute__((always_inline)) {
+                return *reinterpret_cast<const uint16_t *>(hb + size_t(pl) * mf::plane_bytes + off);
+            };
+            if (F16H) {
+                // the two f16 planes of h x 2^kHiddenF16Shift: their sum is exact in f32
+                v = __builtin_amdgcn_ldexpf(float(__builtin_bit_cast(_Float16, half(0))) +
+                                                float(__builtin_bit_cast(_Float16, half(1))),
+                                            -mf::kHiddenF16Shift);
+            } else {
+                v = 0.0f;
 #pragma unroll
-            for (int pl = 0; pl < kHiddenPlanes; ++pl) {
-                v += __uint_as_float(uint32_t(*reinterpret_cast<const uint16_t *>(hb + size_t(pl) * mf::plane_bytes +
-                                                                                  off))
-                                     << 16);
+                for (int pl = 0; pl < kHiddenPlanes; ++pl) {
+                    v += __uint_as_float(uint32_t(half(pl)) << 16);
+                }
             }
         }
         h[k] = v;
@@ -1573,6 +1605,13 @@ void combine_for(uint32_t used, const Plan &plan, uint32_t count, uint32_t rows,
 
 // The MFMA kernels take weights as bf16 = E2M1 x 2^(e-127), exact for E8M0 1..254
 // (and for zero codes at E8M0 0) only.  expert < 0: every expert of the tensor.
+// The exact path's hidden between gate/up and down: two f16 planes (down decoded to f16,
+// two thirds of the three-plane MFMAs) when every down expert's scales keep its f16
+// decode exact, else three bf16 planes.
+bool hidden_f16(const ttl_moe_layer &L) {
+    return L.down->f16_exact();
+}
+
 int check_bf16_scales(const ttl_mxfp4 *w, int64_t expert, const char *who) {
     const bool edge = expert < 0 ? w->edge_scales() : w->edge_experts[size_t(expert)] != 0;
     TTL_REQUIRE(!edge, TTL_ERR_SHAPE,
@@ -1639,6 +1678,7 @@ int ttl_matmul_mxfp4_selected(ttl_ctx *ctx, const ttl_mxfp4 *w, const float *bia
     m.rows = w->rows;
     m.tiles_per_expert = w->tiles;
     m.frags = plan.xb;
+    m.tile_planes = 3;
     m.plan = plan;
     m.out = out_dev;
     m.out_rows = x_rows;
@@ -1694,6 +1734,7 @@ int ttl_matmul_mxfp4_selected_mxfp8(ttl_ctx *ctx, const ttl_mxfp4 *w, const floa
     m.rows = w->rows;
     m.tiles_per_expert = w->tiles;
     m.frags = plan.xb;
+    m.tile_planes = 1;
     m.plan = plan;
     m.out = out_dev;
     m.out_rows = x_rows;
@@ -1765,6 +1806,7 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     const uint32_t pairs = count * L.used;
     const bool scaled = x_dtype == TTL_DTYPE_F32_AS_MXFP8 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
     const bool bf16 = x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
+    const bool f16h = !scaled && hidden_f16(L);
     const Layout lay = make_layout(pairs, L.experts, (bf16 || scaled) ? 1 : 3, true, L.hidden);
     TTL_REQUIRE(workspace_bytes >= lay.total, TTL_ERR_SHAPE,
                 "ttl_moe_prefill_experts: workspace of %zu bytes, %zu needed for this count and x_dtype",
@@ -1812,10 +1854,14 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         mx8_gateup_kernel<<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         TTL_LAUNCHED("mx8_gateup_kernel");
     } else if (stages & TTL_PREFILL_GATEUP) {
-        if (bf16) {
-            gateup_kernel<1><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        if (bf16 && f16h) {
+            gateup_kernel<1, true><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        } else if (bf16) {
+            gateup_kernel<1, false><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        } else if (f16h) {
+            gateup_kernel<3, true><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         } else {
-            gateup_kernel<3><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+            gateup_kernel<3, false><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         }
         TTL_LAUNCHED("gateup_kernel");
     }
@@ -1827,12 +1873,17 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     m.rows = L.hidden;
     m.tiles_per_expert = L.down->tiles;
     m.frags = plan.hb;
+    m.tile_planes = kHiddenPlanes;
     m.plan = plan;
     m.out = plan.down;
     m.out_rows = 0;
     if ((stages & TTL_PREFILL_DOWN) && scaled) {
         mx8_matmul_kernel<false><<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
         TTL_LAUNCHED("mx8_matmul_kernel");
+    } else if ((stages & TTL_PREFILL_DOWN) && f16h) {
+        matmul_kernel<2, false, mf::f16x8, mf::kHiddenF16Shift>
+            <<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
+        TTL_LAUNCHED("matmul_kernel");
     } else if (stages & TTL_PREFILL_DOWN) {
         matmul_kernel<kHiddenPlanes, false><<<dim3(L.hidden / kMmRows, lay.tmax), kMmWaves * 64, 0, ctx->stream>>>(m);
         TTL_LAUNCHED("matmul_kernel");
@@ -1847,7 +1898,7 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
 int ttl_moe_prefill_intermediates(ttl_ctx *ctx, const ttl_moe_layer *layer, int x_dtype, uint32_t count,
                                   const void *workspace_dev, size_t workspace_bytes, float *hidden_dev,
                                   float *down_dev, uint8_t *hidden_scales_dev) {
-    TTL_REQUIRE(ctx && layer && workspace_dev && hidden_dev && down_dev, TTL_ERR_INVALID,
+    TTL_REQUIRE(ctx && layer && layer->down && workspace_dev && hidden_dev && down_dev, TTL_ERR_INVALID,
                 "ttl_moe_prefill_intermediates: null argument");
     TTL_REQUIRE(x_dtype == TTL_DTYPE_F32 || x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_F32_AS_MXFP8 ||
                     x_dtype == TTL_DTYPE_BF16_AS_MXFP8,
@@ -1873,11 +1924,14 @@ int ttl_moe_prefill_intermediates(ttl_ctx *ctx, const ttl_moe_layer *layer, int 
                 workspace_bytes, lay.total);
     const Plan plan = plan_at(const_cast<void *>(workspace_dev), lay);
     if (scaled) {
-        prefill_intermediates_kernel<true><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
-                                                                            down_dev, hidden_scales_dev);
+        prefill_intermediates_kernel<true, false><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
+                                                                                   down_dev, hidden_scales_dev);
+    } else if (hidden_f16(*layer)) {
+        prefill_intermediates_kernel<false, true><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
+                                                                                   down_dev, hidden_scales_dev);
     } else {
-        prefill_intermediates_kernel<false><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
-                                                                             down_dev, hidden_scales_dev);
+        prefill_intermediates_kernel<false, false><<<pairs, 256, 0, ctx->stream>>>(plan, layer->hidden, hidden_dev,
+                                                                                    down_dev, hidden_scales_dev);
     }
     TTL_LAUNCHED("prefill_intermediates_kernel");
     return TTL_OK;

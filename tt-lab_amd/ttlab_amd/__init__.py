@@ -348,6 +348,7 @@ def load_library():
         "ttl_mxfp4_shape": (i32, [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(u32)]),
         "ttl_mxfp4_bytes": (sz, [vp]),
         "ttl_mxfp4_edge_scales": (i32, [vp]),
+        "ttl_mxfp4_f16_exact": (i32, [vp]),
         "ttl_mxfp4_dequantize": (i32, [vp, vp, u32, i32, vp]),
         "ttl_matvec_mxfp4": (i32, [vp, vp, vp, vp, vp, u32]),
         "ttl_matvec_mxfp4_experts": (i32, [vp, vp, vp, vp, u32, vp, u32, vp]),
@@ -510,6 +511,14 @@ class Mxfp4:
         rc = self.dev.lib.ttl_mxfp4_edge_scales(self.handle)
         if rc < 0:
             _check(rc, "ttl_mxfp4_edge_scales")
+        return bool(rc)
+
+    @property
+    def f16_exact(self):
+        """True if every nonzero block's E8M0 scale is 114..140 (the f16 down GEMM's range)."""
+        rc = self.dev.lib.ttl_mxfp4_f16_exact(self.handle)
+        if rc < 0:
+            _check(rc, "ttl_mxfp4_f16_exact")
         return bool(rc)
 
     def download_gguf(self):
