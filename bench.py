@@ -29,8 +29,10 @@ is 12 of each plus the unembedding.
 distinct resident layers, value = token-layers/s.
 
 --workload prefill runs benchmark config 2: the batched prefill experts of one MoE
-layer for 512 bf16 tokens with balanced given routing (bf16 MFMA; with
---activations mxfp8 the scaled fp8 x fp4 MFMA path), value = token-layers/s;
+layer for 512 bf16 tokens with balanced given routing (bf16 MFMA, the down GEMM
+on f16 MFMA over the hidden's two f16 planes where the down weights' E8M0 scales
+keep their f16 decode exact; with --activations mxfp8 the scaled fp8 x fp4 MFMA
+path), value = token-layers/s;
 roofline on the larger of the gate/up and down GEMM launches.
 
 --workload model-prefill runs the full synthetic gpt-oss-20b model's layer-major
@@ -449,6 +451,8 @@ def gpu_prefill(args):
         d.gate, d.up, d.down = gate.handle, up.handle, down.handle
         keep += [gate, up, down]
         descs.append(d)
+    # the down GEMM runs on the hidden's two f16 planes when every down expert's scales allow
+    hidden_f16 = all(t.f16_exact for t in keep[2::3])
     xs = np.random.RandomState(0x78000002).randn(PREFILL_TOKENS * N).astype(np.float32)
     x = dev.upload(ttlab_amd.bf16_bits(xs))
     idx, w = ttlab_amd.balanced_routing(PREFILL_TOKENS, EXPERTS, USED, 0x79000002)
@@ -512,7 +516,10 @@ def gpu_prefill(args):
         "unit": "token-layers/s",
         "ms_per_step": ms,
         "dtype": ("MXFP8 activations and hidden x MXFP4 weights, f32 accumulate (scaled fp8/fp4 MFMA)" if scaled
-                  else "bf16 activations x MXFP4 weights, f32 accumulate (bf16 MFMA)"),
+                  else "bf16 activations x MXFP4 weights, f32 accumulate (bf16 MFMA; down on f16 MFMA over "
+                       "the hidden's two f16 planes)" if hidden_f16
+                  else "bf16 activations x MXFP4 weights, f32 accumulate (bf16 MFMA; down over the hidden's "
+                       "three bf16 planes)"),
         "config": {"workload": "config 2: batched prefill experts of one gpt-oss-20b MoE layer, 512 bf16 tokens, "
                                "top-4 of 32 experts, balanced given routing (64 tokens per expert); step = one layer "
                                f"(plan, gather, gate/up+SwiGLU, down, combine) over {PREFILL_LAYERS} distinct "
@@ -560,7 +567,8 @@ def gpu_model_prefill(args):
         "value": PROMPT_TOKENS / (ms * 1e-3),
         "unit": "prompt tok/s",
         "ms_per_step": ms,
-        "dtype": "bf16 MFMA, exact products (f32 activations as three bf16 planes), f32 accumulate",
+        "dtype": "bf16 MFMA, exact products (f32 activations as three bf16 planes), f32 accumulate; the "
+                 "MoE down GEMM on f16 MFMA over the SwiGLU hidden's two f16 planes where the down scales allow",
         "config": {"workload": f"full synthetic gpt-oss-{'20b' if args.config == 3 else '120b'} layer-major prefill "
                                f"of a {PROMPT_TOKENS}-token prompt (GptOssModel::prefill); step = one prefill "
                                "(host tokens in, last-token logits out)",
