@@ -178,19 +178,24 @@ def test_moe_prefill_intermediates_exact_path(dev, layer8):
             b.free()
 
 
-@pytest.mark.parametrize("down_scales,f16", [((119, 125), True), ((110, 125), False), ((126, 145), False)])
-def test_moe_prefill_down_decode_paths(dev, down_scales, f16):
-    """The exact path's down GEMM: with every down scale in E8M0 114..140 the hidden is two
-    f16 planes of h x 2^8 against f16 weights, else three bf16 planes against bf16 weights
-    (ttl_mxfp4_f16_exact says which).  Both against the oracle within 1e-5 per token, for
-    f32 and bf16 tokens; the hidden the down GEMM reads (ttl_moe_prefill_intermediates)
-    against orc_swiglu of the oracle's gate and up, and the down rows against the oracle's
-    matvec on that hidden, within 1e-5."""
-    host = HostLayer(8, 4, biases=True, seed=0x77000140, scales={"down": down_scales})
+@pytest.mark.parametrize("scales,f16", [({}, (True, True, True)),
+                                        ({"down": (110, 125)}, (True, True, False)),
+                                        ({"down": (126, 145)}, (True, True, False)),
+                                        ({"gate": (110, 125)}, (False, True, True)),
+                                        ({"up": (126, 145)}, (True, False, True))])
+def test_moe_prefill_decode_paths(dev, scales, f16):
+    """The unscaled path's operands: with every gate and up scale in E8M0 114..140, f32
+    tokens are two f16 planes of x 2^k (k per token) against f16 weights, else three bf16
+    planes; with every down scale in that range the hidden is two f16 planes of h x 2^8,
+    else three bf16 planes (ttl_mxfp4_f16_exact says which).  All against the oracle within
+    1e-5 per token, for f32 and bf16 tokens; the hidden the down GEMM reads
+    (ttl_moe_prefill_intermediates) against orc_swiglu of the oracle's gate and up, and the
+    down rows against the oracle's matvec on that hidden, within 1e-5."""
+    host = HostLayer(8, 4, biases=True, seed=0x77000140, scales=scales)
     device = DeviceLayer(dev, host)
     count, used = 24, 4
     try:
-        assert device.down.f16_exact == f16
+        assert (device.gate.f16_exact, device.up.f16_exact, device.down.f16_exact) == f16
         idx, w = balanced_routing(count, 8, used, 31)
         for dtype in (ttlab_amd.TTL_DTYPE_F32, ttlab_amd.TTL_DTYPE_BF16):
             if dtype == ttlab_amd.TTL_DTYPE_BF16:
@@ -225,6 +230,38 @@ def test_moe_prefill_down_decode_paths(dev, down_scales, f16):
                 b.free()
     finally:
         device.free()
+
+
+def test_moe_prefill_f32_token_magnitudes(dev, layer8):
+    """f32 tokens as two f16 planes, each token scaled by its own power of two: tokens
+    scaled by 2^-100 .. 2^100, one whose values span 2^-40 .. 2^40, a zero token and tokens
+    holding infinities or a NaN, against the oracle: finite tokens within 1e-5, the others
+    NaN and infinite where the oracle's are."""
+    host, device = layer8
+    assert device.gate.f16_exact and device.up.f16_exact
+    count, used = 12, 4
+    rs = np.random.RandomState(0x78000150)
+    x = rs.standard_normal((count, N)).astype(np.float32)
+    x *= np.array([2.0 ** -100, 2.0 ** 100, 2.0 ** -30, 2.0 ** 30] + [1.0] * 8, np.float32)[:, None]
+    x[4] *= np.exp2(rs.randint(-40, 41, N)).astype(np.float32)
+    x[5] = 0.0
+    x[6, 17] = np.inf
+    x[7, 2000] = np.nan
+    x[8, 100] = -np.inf
+    x[9] *= np.float32(2.0 ** -60)
+    x[9, 5] = 1.0
+    idx, w = balanced_routing(count, 8, used, 41)
+    got = run_prefill(dev, device, x, idx, w, ttlab_amd.TTL_DTYPE_F32)
+    with np.errstate(all="ignore"):
+        ref = oracle_prefill(host, x, idx, w)
+    for p in range(count):
+        if np.all(np.isfinite(ref[p])):
+            assert O.rel_l2(got[p], ref[p]) <= TOL, p
+        else:
+            assert np.array_equal(np.isnan(got[p]), np.isnan(ref[p])), p
+            inf = np.isinf(ref[p])
+            assert np.array_equal(got[p][inf], ref[p][inf]), p
+    assert not np.all(np.isfinite(ref[[6, 7, 8]]))
 
 
 def test_moe_prefill_uneven_buckets_and_invalid_index(dev, layer8):

@@ -1,7 +1,8 @@
 """GPU parity of the batched Q8_0 matmul (ttl_matmul_q8_0, MFMA) against the oracle's
 matmul_add_q8_0 (tensor.cpp:529-566) and against an f64 product of the dequantized
-weights.  Tolerance: relative L2 <= 1e-5 per token (the MFMA sums the same exact
-products in f32 in another order)."""
+weights.  Tolerance: relative L2 <= 1e-5 per token (the MFMA sums products of the
+exact weights and the activations held to 2^-22 of themselves, in f32 in another
+order)."""
 import numpy as np
 import pytest
 
@@ -86,3 +87,63 @@ def test_q8_matmul_rejects_small_workspace(dev):
     for b in (xb, ob, ws):
         b.free()
     t.free()
+
+
+def magnitude_rows(seed, tokens, cols):
+    """Token rows for the per-token shift of the f16 planes: scaled by 2^-100 .. 2^100, a row
+    whose values span 2^-40 .. 2^40, one large value among values 2^-60 of it, a zero row,
+    rows holding +inf, -inf or a NaN, and one value of 1e30 among values near 1."""
+    rs = np.random.RandomState(seed)
+    x = rs.standard_normal((tokens, cols)).astype(np.float32)
+    scale = [2.0 ** -100, 2.0 ** 100, 2.0 ** -30, 2.0 ** 30, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 2.0 ** -7]
+    x *= np.array(scale[:tokens], np.float32)[:, None]
+    x[4] *= np.exp2(rs.randint(-40, 41, cols)).astype(np.float32)
+    x[5] *= np.float32(2.0 ** -60)
+    x[5, 5] = 1.0
+    x[6] = 0.0
+    x[7, 17] = np.inf
+    x[8, 2000] = np.nan
+    x[9, 100] = -np.inf
+    x[10, 3] = np.float32(1.0e30)
+    return x
+
+
+def assert_matches_with_nonfinite(got, ref, tokens):
+    for p in range(tokens):
+        bad = ~np.isfinite(ref[p])
+        if not bad.any():
+            assert O.rel_l2(got[p], ref[p]) <= TOL, p
+            continue
+        assert np.array_equal(np.isnan(got[p]), np.isnan(ref[p])), p
+        inf = np.isinf(ref[p])
+        assert np.array_equal(got[p][inf], ref[p][inf]), p
+        ok = np.isfinite(ref[p])
+        if ok.any():
+            assert O.rel_l2(got[p][ok], ref[p][ok]) <= TOL, p
+
+
+@pytest.mark.parametrize("cols", [2880, 4096])
+def test_q8_matmul_token_magnitudes_and_nonfinite(dev, cols):
+    """Each token is scaled by its own power of two before its two f16 planes, and its sums
+    are scaled back before the bias: tokens of very different magnitudes, a zero token and
+    tokens holding infinities or a NaN against the oracle (finite results within 1e-5 per
+    token; NaN and infinite outputs where the oracle's are, with its signs)."""
+    rows, tokens = 48, 12
+    blocks = O.synth_q8_0(31, cols, rows * cols // 32)
+    x = magnitude_rows(32 + cols, tokens, cols)
+    bias = O.synth_normal(33, cols, rows, sigma=0.1)
+    t = dev.q8_upload(blocks, rows, cols)
+    xb, bb, ob = dev.upload(x), dev.upload(bias), dev.alloc(tokens * rows * 4)
+    try:
+        dev.matmul_q8_0(t, bb, xb, tokens, None, ob)
+        got = ob.download(np.float32).reshape(tokens, rows)
+        with np.errstate(all="ignore"):
+            ref = oracle_matmul(blocks, bias, rows, cols, x, tokens)
+        assert np.all(np.isfinite(ref[[0, 1, 2, 3, 4, 5, 6, 11]]))
+        assert not np.all(np.isfinite(ref[[7, 8, 9]]))
+        assert_matches_with_nonfinite(got, ref, tokens)
+        assert np.array_equal(got[6], bias)  # a zero token: the bias alone
+    finally:
+        for b in (xb, bb, ob):
+            b.free()
+        t.free()

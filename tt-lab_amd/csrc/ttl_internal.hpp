@@ -90,6 +90,12 @@ size_t router_scratch_bytes();
 int launch_router_batch(ttl_ctx *ctx, const ttl_moe_layer &L, const float *x, uint32_t count, void *scratch,
                         int32_t *indices, float *weights);
 
+// The shift k of each of `rows` f32 rows (`cols` values each, a multiple of 4 and at most
+// 4096, rows `stride` floats apart, 16-byte aligned) for their two f16 planes: k of the
+// row's largest finite magnitude (mf::row_shift), into shift[rows] (ttl_prefill.hip).
+int launch_row_shifts(hipStream_t stream, const float *x, uint32_t stride, uint32_t rows, uint32_t cols,
+                       int32_t *shift);
+
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t err, const char *what);
 

@@ -95,12 +95,16 @@ __device__ inline void split_planes(const float (&v)[8], uint4 (&out)[P]) {
 
 // ---- f16 operands (the prefill's hidden as two planes) ------------------------------------
 //
-// v_mfma_f32_16x16x32_f16 has the bf16 instruction's operand layout and rate.  Its use
-// here: the SwiGLU hidden, an f32 vector of magnitude at most 7 x 8 = 56 (the clamps of
-// model.cpp:328-332), as two f16 planes against weights decoded to f16.  The weights'
-// products stay exact where every E2M1 value times its E8M0 scale is a normal f16, E8M0
-// f16_scale_min..f16_scale_max; the hidden's two planes hold 22 of its 24 bits (hi rounded
-// to nearest, lo the rounded remainder).
+// v_mfma_f32_16x16x32_f16 has the bf16 instruction's operand layout and rate.  Its uses
+// here: f32 vectors as two f16 planes, each scaled by a power of two 2^k first, against
+// weights decoded to f16 (MXFP4) or taken as f16 (Q8_0 codes, exact).  MXFP4 products stay
+// exact where every E2M1 value times its E8M0 scale is a normal f16, E8M0
+// f16_scale_min..f16_scale_max; the two planes hold 22 of a value's 24 bits (hi rounded to
+// nearest, lo the rounded remainder).  The scale keeps hi within the f16 range and lo a
+// normal f16 for values down to 2^-17 of the largest: the SwiGLU hidden, of magnitude at
+// most 7 x 8 = 56 (the clamps of model.cpp:328-332), takes the fixed k = kHiddenF16Shift;
+// a token row takes its own k = row_shift(max |x|), applied back to the GEMM's sums (a
+// power of two, exact) before anything else (a bias) is added to them.
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -136,15 +140,14 @@ __device__ inline f16x8 decode_as<f16x8>(uint32_t word, float scale) {
     return decode_step_f16(word, scale);
 }
 
-// Two f16 planes of 8 f32 values times 2^SHIFT, packed as the MFMA fragments are (value
+// Two f16 planes of 8 f32 values times 2^shift, packed as the MFMA fragments are (value
 // 2k in the low half of dword k).  A non-finite value stays in the first plane (a NaN a
 // NaN) and the second is zero.
-template <int SHIFT>
-__device__ inline void split_f16x2(const float (&v)[8], uint4 (&out)[2]) {
+__device__ inline void split_f16x2(const float (&v)[8], int shift, uint4 (&out)[2]) {
     uint32_t hi[8], lo[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const float s = __builtin_amdgcn_ldexpf(v[j], SHIFT);
+        const float s = __builtin_amdgcn_ldexpf(v[j], shift);
         const _Float16 h = _Float16(s);
         const _Float16 l = isfinite(s) ? _Float16(s - float(h)) : _Float16(0.0f);
         hi[j] = __builtin_bit_cast(uint16_t, h);
@@ -152,6 +155,23 @@ __device__ inline void split_f16x2(const float (&v)[8], uint4 (&out)[2]) {
     }
     out[0] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16));
     out[1] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16));
+}
+
+// The shift k of a token row whose largest finite magnitude is m: m x 2^k in [2^14, 2^15),
+// so every finite value's hi plane is at most 32768 (< 65504) and the GEMM's sums of the
+// scaled values stay far from the f32 range (k runs from -112 for m near 2^127 to 163 for
+// m = 2^-149; consumers scale their sums back before adding anything unscaled, such as a
+// bias).  0 for a row with no nonzero finite value.  Non-finite values are left out of m:
+// they stay non-finite in hi.
+__device__ inline int row_shift(float m) {
+    // m = f x 2^e with f in [0.5, 1) (subnormal m included): m x 2^(15 - e) in [2^14, 2^15)
+    return m > 0.0f ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+}
+
+// The largest finite |x| of this lane's values (NaN and infinities left out).
+__device__ inline float finite_max(float m, float x) {
+    const float a = __builtin_fabsf(x);
+    return a <= 3.40282347e38f ? __builtin_fmaxf(m, a) : m;
 }
 
 }  // namespace mf

@@ -84,10 +84,13 @@ struct Plan {
     uint8_t *xb;            // [tmax][x planes][plane_bytes]
     uint8_t *hb;            // [tmax][hidden planes][plane_bytes]
     float *down;            // [S][rows]
+    int32_t *token_shift;   // [tokens] k of each token row (f16 token planes hold x 2^k)
+    int32_t *tile_shift;    // [tmax][64] k of each tile column (0 past the tile's slots)
 };
 
 struct Layout {
-    size_t header, tile_expert, tile_first, tile_count, slot_token, slot_weight, pair_slot, xb, hb, down, total;
+    size_t header, tile_expert, tile_first, tile_count, slot_token, slot_weight, pair_slot, xb, hb, down,
+        token_shift, tile_shift, total;
     uint32_t tmax;
 };
 
@@ -102,7 +105,9 @@ uint32_t max_tiles(uint32_t pairs, uint32_t experts) {
     return uint32_t((uint64_t(pairs) + uint64_t(mf::tile_slots - 1) * nonempty) / mf::tile_slots) + 1;
 }
 
-Layout make_layout(uint32_t pairs, uint32_t experts, int x_planes, bool with_hidden, uint32_t rows) {
+// tokens > 0: room for the token and tile shifts of f16 token planes.
+Layout make_layout(uint32_t pairs, uint32_t experts, int x_planes, bool with_hidden, uint32_t rows,
+                   uint32_t tokens = 0) {
     Layout L{};
     L.tmax = max_tiles(pairs, experts);
     size_t o = 0;
@@ -130,6 +135,13 @@ Layout make_layout(uint32_t pairs, uint32_t experts, int x_planes, bool with_hid
     if (with_hidden) {
         o = align256(o + 4ull * pairs * rows);
     }
+    L.token_shift = o;
+    L.tile_shift = o;
+    if (tokens > 0) {
+        o = align256(o + 4ull * tokens);
+        L.tile_shift = o;
+        o = align256(o + 4ull * L.tmax * mf::tile_slots);
+    }
     L.total = o;
     return L;
 }
@@ -147,6 +159,8 @@ Plan plan_at(void *workspace, const Layout &L) {
     p.xb = w + L.xb;
     p.hb = w + L.hb;
     p.down = reinterpret_cast<float *>(w + L.down);
+    p.token_shift = reinterpret_cast<int32_t *>(w + L.token_shift);
+    p.tile_shift = reinterpret_cast<int32_t *>(w + L.tile_shift);
     return p;
 }
 
@@ -355,16 +369,55 @@ __global__ void plan_selected_kernel(const int32_t *__restrict__ tokens, uint32_
 
 // ---- activation fragments ------------------------------------------------------------
 
+// Row shifts (ttl::launch_row_shifts): one wave per row, four rows per workgroup; each
+// lane requests its (at most 16) float4 of the row at once, clamped to the row's last
+// (a repeated value leaves the maximum unchanged).
+constexpr uint32_t kShiftRowsPerBlock = 4;
+constexpr uint32_t kShiftMaxCols = 4096;
+
+__global__ __launch_bounds__(kShiftRowsPerBlock * 64) void row_shift_kernel(const float *__restrict__ x,
+                                                                            uint32_t stride, uint32_t rows,
+                                                                            uint32_t cols,
+                                                                            int32_t *__restrict__ shift) {
+    const uint32_t row = blockIdx.x * kShiftRowsPerBlock + threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (row >= rows) {
+        return;
+    }
+    const float4 *p = reinterpret_cast<const float4 *>(x + size_t(row) * stride);
+    const uint32_t n4 = cols / 4;
+    constexpr int kPer = kShiftMaxCols / 4 / 64;
+    float4 v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        v[j] = p[min(lane + 64u * j, n4 - 1)];
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        m = mf::finite_max(mf::finite_max(mf::finite_max(mf::finite_max(m, v[j].x), v[j].y), v[j].z), v[j].w);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        m = __builtin_fmaxf(m, __shfl_xor(m, d));
+    }
+    if (lane == 0) {
+        shift[row] = mf::row_shift(m);
+    }
+}
+
 // One workgroup per (quad, token tile); thread (column tile, lane) takes slot
 // 16 ct + lane % 16 and K-block 4 quad + lane / 16, i.e. the 8 activations of that B
 // fragment lane in each of the quad's four K steps: one 128-byte run of the row (f32;
 // 64 bytes for bf16), converted to P bf16 planes per step.  The tile's metadata and
 // the early exit are requested together, then the slot's token, then its row
 // (unconditional requests at clamped addresses, masked after).  Slots past the tile's
-// count, and blocks 90/91, are zero; a token out of range is NaN.
-template <bool BF16_IN, int P>
+// count, and blocks 90/91, are zero; a token out of range is NaN.  F16X (f32 rows, P = 2):
+// the planes are two f16 of x 2^k with the token's k from plan.token_shift, and the quad-0
+// workgroups record each column's k in plan.tile_shift (0 for an empty or NaN column).
+template <bool BF16_IN, int P, bool F16X = false>
 __global__ __launch_bounds__(mf::col_tiles * 64) void gather_kernel(const void *__restrict__ x, uint32_t x_stride,
                                                                     uint32_t x_rows, Plan plan) {
+    static_assert(!F16X || (P == 2 && !BF16_IN), "f16 token planes are two, from f32 rows");
     const uint32_t tile = blockIdx.y, quad = blockIdx.x;
     // (tile < the layout's tmax: its metadata words exist, stale past the plan's tiles)
     const uint32_t tiles = plan.header->tiles, cnt = plan.tile_count[tile], first = plan.tile_first[tile];
@@ -414,6 +467,14 @@ __global__ __launch_bounds__(mf::col_tiles * 64) void gather_kernel(const void *
     }
     const float fill = (live && !token_ok) ? __builtin_nanf("") : 0.0f;
     const bool keep = live && token_ok;
+    int k = 0;
+    if constexpr (F16X) {
+        const int kt = plan.token_shift[token_ok ? token : 0u];
+        k = keep ? kt : 0;
+        if (quad == 0 && lane < 16) {
+            plan.tile_shift[size_t(tile) * mf::tile_slots + n] = k;
+        }
+    }
     uint8_t *dst = plan.xb + size_t(tile) * P * mf::plane_bytes + size_t(ct) * mf::frag_bytes + lane * 16;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -425,7 +486,11 @@ __global__ __launch_bounds__(mf::col_tiles * 64) void gather_kernel(const void *
             v[2 * k + 1] = keep ? e[16 + 4 * s + k] : fill;
         }
         uint4 out[P];
-        mf::split_planes<P>(v, out);
+        if constexpr (F16X) {
+            mf::split_f16x2(v, k, out);
+        } else {
+            mf::split_planes<P>(v, out);
+        }
         const size_t step = size_t(quad) * 4 + size_t(s);
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -649,11 +714,16 @@ __device__ inline bool tile_of_workgroup(const PlanHeader *header, uint32_t &til
 // Accumulators: [matrix (gate 0/1, up 2/3)][column tile]; NC column tiles (the plan's
 // wide tiles with all of them, or its narrow ones with kNarrowCols).
 // F16H: the hidden as two f16 planes of h x 2^kHiddenF16Shift (for the f16 down GEMM),
-// else three exact bf16 planes.
-template <int PX, int NC, bool F16H>
+// else three exact bf16 planes.  VX: the token operand, bf16x8 (PX exact planes; the
+// accumulators start at the bias) or f16x8 (two planes of x 2^k per column, k from
+// plan.tile_shift; the weights decoded to f16): then the accumulators start at zero, and
+// the sums are scaled back by 2^-k and the bias added before the SwiGLU.
+template <int PX, int NC, bool F16H, class VX>
 __device__ __attribute__((always_inline)) inline void gateup_tile(
     const GateUpArgs &a, uint32_t tile, uint32_t row_group,
     mf::u32x4 (*lds)[Stager<PX, kGuWaves * 64>::lds_chunks]) {
+    constexpr bool XS = __is_same(VX, mf::f16x8);
+    static_assert(!XS || PX == 2, "f16 token operands are two planes");
     using SS = StageShape<PX>;
     constexpr int kThreads = kGuWaves * 64;
     const uint32_t t = threadIdx.x, wave = t / 64, lane = t % 64;
@@ -671,22 +741,33 @@ __device__ __attribute__((always_inline)) inline void gateup_tile(
     ga.init(a.gate_codes, a.gate_scales, ti, lane);
     ua.init(a.up_codes, a.up_scales, ti, lane);
 
+    // the bias of the lane's D rows 4g..4g+3 of matrix m (gate 0/1, up 2/3)
+    auto bias_of = [&](int m) __attribute__((always_inline)) {
+        const float *bias = m < 2 ? a.gate_bias : a.up_bias;
+        f32x4 b = {0.f, 0.f, 0.f, 0.f};
+        if (bias) {
+            const float4 v = *reinterpret_cast<const float4 *>(bias + size_t(expert) * a.rows + row_base +
+                                                               16 * (m % 2) + 4 * (lane / 16));
+            b = f32x4{v.x, v.y, v.z, v.w};
+        }
+        return b;
+    };
     f32x4 acc[4][NC];
-    {
-        const uint32_t g = lane / 16;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const float *bias = m < 2 ? a.gate_bias : a.up_bias;
-            f32x4 b = {0.f, 0.f, 0.f, 0.f};
-            if (bias) {
-                const float4 v = *reinterpret_cast<const float4 *>(bias + size_t(expert) * a.rows + row_base +
-                                                                   16 * (m % 2) + 4 * g);
-                b = f32x4{v.x, v.y, v.z, v.w};
-            }
+    for (int m = 0; m < 4; ++m) {
+        f32x4 b;
+        if constexpr (XS) {
+            // a zero the compiler cannot see: starting the MFMA chains from a known
+            // zero made it keep extra registers through the loop (34 spilled)
+            float z;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+            b = f32x4{z, z, z, z};
+        } else {
+            b = bias_of(m);
+        }
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                acc[m][c] = b;
-            }
+        for (int c = 0; c < NC; ++c) {
+            acc[m][c] = b;
         }
     }
 
@@ -733,16 +814,16 @@ __device__ __attribute__((always_inline)) inline void gateup_tile(
         sc[3] = ua.scale(1);
         ga.next_quad();
         ua.next_quad();
-        auto decode = [&](int s, bf16x8(&w)[4]) __attribute__((always_inline)) {
+        auto decode = [&](int s, VX(&w)[4]) __attribute__((always_inline)) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const uint32_t word = s == 0 ? q[m].x : (s == 1 ? q[m].y : (s == 2 ? q[m].z : q[m].w));
-                w[m] = mf::decode_step(word, sc[m]);
+                w[m] = mf::decode_as<VX>(word, sc[m]);
             }
         };
         // B fragments four ahead of their MFMAs for one plane and for three (with three
         // planes this fits the 256 registers of two waves per SIMD without spilling)
-        quad_mfma<PX, 4, 4, NC>(lds[0], lds[1], i, lane, decode, stage_end, acc);
+        quad_mfma<PX, 4, 4, NC, VX>(lds[0], lds[1], i, lane, decode, stage_end, acc);
     };
 
     rotate_quads(qa, load_quad, compute_quad);
@@ -758,6 +839,18 @@ __device__ __attribute__((always_inline)) inline void gateup_tile(
     uint8_t *hb = a.plan.hb + size_t(tile) * kHiddenPlanes * mf::plane_bytes;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+        if constexpr (XS) {
+            // the column's sums scaled back, then the bias
+            const int k = a.plan.tile_shift[size_t(tile) * mf::tile_slots + c * 16 + n16];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 b = bias_of(m);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[m][c][i] = b[i] + __builtin_amdgcn_ldexpf(acc[m][c][i], -k);
+                }
+            }
+        }
         float h[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -767,7 +860,7 @@ __device__ __attribute__((always_inline)) inline void gateup_tile(
         constexpr int HP = F16H ? 2 : kHiddenPlanes;
         uint4 planes[HP];
         if constexpr (F16H) {
-            mf::split_f16x2<mf::kHiddenF16Shift>(h, planes);
+            mf::split_f16x2(h, mf::kHiddenF16Shift, planes);
         } else {
             mf::split_planes<HP>(h, planes);
         }
@@ -787,7 +880,7 @@ __device__ __attribute__((always_inline)) inline void gateup_tile(
     }
 }
 
-template <int PX, bool F16H>
+template <int PX, bool F16H, class VX = bf16x8>
 __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void gateup_kernel(GateUpArgs a) {
     __shared__ mf::u32x4 lds[2][Stager<PX, kGuWaves * 64>::lds_chunks];
     uint32_t tile, row_group;
@@ -796,9 +889,9 @@ __global__ __launch_bounds__(kGuWaves * 64) __attribute__((amdgpu_waves_per_eu(2
         return;
     }
     if (narrow) {
-        gateup_tile<PX, kNarrowCols, F16H>(a, tile, row_group, lds);
+        gateup_tile<PX, kNarrowCols, F16H, VX>(a, tile, row_group, lds);
     } else {
-        gateup_tile<PX, mf::col_tiles, F16H>(a, tile, row_group, lds);
+        gateup_tile<PX, mf::col_tiles, F16H, VX>(a, tile, row_group, lds);
     }
 }
 
@@ -1629,6 +1722,24 @@ int check_mxfp4(const ttl_mxfp4 *w, const char *who) {
 
 }  // namespace
 
+namespace ttl {
+
+int launch_row_shifts(hipStream_t stream, const float *x, uint32_t stride, uint32_t rows, uint32_t cols,
+                      int32_t *shift) {
+    TTL_REQUIRE(cols > 0 && cols <= kShiftMaxCols && cols % 4 == 0 && stride % 4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(x) & 15) == 0,
+                TTL_ERR_SHAPE, "row shifts: rows of %u values, %u apart", cols, stride);
+    if (rows == 0) {
+        return TTL_OK;
+    }
+    row_shift_kernel<<<ttl::blocks_for(rows, kShiftRowsPerBlock), kShiftRowsPerBlock * 64, 0, stream>>>(
+        x, stride, rows, cols, shift);
+    TTL_LAUNCHED("row_shift_kernel");
+    return TTL_OK;
+}
+
+}  // namespace ttl
+
 extern "C" {
 
 size_t ttl_matmul_mxfp4_selected_workspace_bytes(uint32_t count) {
@@ -1761,8 +1872,9 @@ int ttl_mxfp8_dequantize(ttl_ctx *ctx, const void *x_dev, int x_dtype, uint32_t 
 }
 
 size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used, int x_dtype) {
-    const int planes = x_dtype == TTL_DTYPE_F32 ? 3 : 1;  // bf16, or the MXFP8 fragments (one plane's room)
-    return make_layout(count * used, experts, planes, true, uint32_t(mx::cols)).total;
+    const bool f32 = x_dtype == TTL_DTYPE_F32;
+    const int planes = f32 ? 3 : 1;  // bf16, or the MXFP8 fragments (one plane's room)
+    return make_layout(count * used, experts, planes, true, uint32_t(mx::cols), f32 ? count : 0).total;
 }
 
 int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
@@ -1807,7 +1919,11 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
     const bool scaled = x_dtype == TTL_DTYPE_F32_AS_MXFP8 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
     const bool bf16 = x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
     const bool f16h = !scaled && hidden_f16(L);
-    const Layout lay = make_layout(pairs, L.experts, (bf16 || scaled) ? 1 : 3, true, L.hidden);
+    // f32 tokens as two f16 planes of x 2^k (k per token) when the gate and up weights'
+    // scales keep their f16 decode exact, else three exact bf16 planes
+    const bool f32 = x_dtype == TTL_DTYPE_F32;
+    const bool f16x = f32 && L.gate->f16_exact() && L.up->f16_exact();
+    const Layout lay = make_layout(pairs, L.experts, (bf16 || scaled) ? 1 : 3, true, L.hidden, f32 ? count : 0);
     TTL_REQUIRE(workspace_bytes >= lay.total, TTL_ERR_SHAPE,
                 "ttl_moe_prefill_experts: workspace of %zu bytes, %zu needed for this count and x_dtype",
                 workspace_bytes, lay.total);
@@ -1827,10 +1943,18 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         }
         TTL_LAUNCHED("gather_mx8_kernel");
     } else if (stages & TTL_PREFILL_GATHER) {
+        const dim3 grid(mf::quads, lay.tmax);
         if (bf16) {
-            gather_kernel<true, 1><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<true, 1><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+        } else if (f16x) {
+            const int rc = ttl::launch_row_shifts(ctx->stream, static_cast<const float *>(x_dev), L.hidden, count,
+                                                  L.hidden, plan.token_shift);
+            if (rc != TTL_OK) {
+                return rc;
+            }
+            gather_kernel<false, 2, true><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         } else {
-            gather_kernel<false, 3><<<dim3(mf::quads, lay.tmax), mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<false, 3><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         }
         TTL_LAUNCHED("gather_kernel");
     }
@@ -1858,6 +1982,10 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
             gateup_kernel<1, true><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         } else if (bf16) {
             gateup_kernel<1, false><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        } else if (f16x && f16h) {
+            gateup_kernel<2, true, mf::f16x8><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
+        } else if (f16x) {
+            gateup_kernel<2, false, mf::f16x8><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         } else if (f16h) {
             gateup_kernel<3, true><<<gu_grid, kGuWaves * 64, 0, ctx->stream>>>(g);
         } else {
@@ -1918,7 +2046,8 @@ int ttl_moe_prefill_intermediates(ttl_ctx *ctx, const ttl_moe_layer *layer, int 
     const uint32_t pairs = count * layer->used;
     const bool scaled = x_dtype == TTL_DTYPE_F32_AS_MXFP8 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
     const bool bf16 = x_dtype == TTL_DTYPE_BF16 || x_dtype == TTL_DTYPE_BF16_AS_MXFP8;
-    const Layout lay = make_layout(pairs, layer->experts, (bf16 || scaled) ? 1 : 3, true, layer->hidden);
+    const Layout lay = make_layout(pairs, layer->experts, (bf16 || scaled) ? 1 : 3, true, layer->hidden,
+                                   x_dtype == TTL_DTYPE_F32 ? count : 0);
     TTL_REQUIRE(workspace_bytes >= lay.total, TTL_ERR_SHAPE,
                 "ttl_moe_prefill_intermediates: workspace of %zu bytes, %zu needed for this count and x_dtype",
                 workspace_bytes, lay.total);

@@ -2,33 +2,36 @@
 // tokens, as GptOssModel::prefill runs the attention projections (model.cpp:493-498,
 // 519-520).
 //
-// Operands of v_mfma_f32_16x16x32_bf16 (D = A B + C; lane l holds 8 bf16 of A row
+// Operands of v_mfma_f32_16x16x32_f16 (D = A B + C; lane l holds 8 f16 of A row
 // l%16 and of B column l%16 for the K offsets of lane group g = l/16, and receives D
 // rows 4g..4g+3 of column l%16):
 //  - one K step is one Q8_0 block of 32 columns; lane group g holds offsets 8g..8g+7;
-//  - A is 16 tokens: the f32 activations split into three bf16 planes whose sum is
-//    each value exactly (mf::split_planes), staged through LDS;
-//  - B is 16 weight rows: the int8 codes, exact in bf16 (at most 8 significant bits);
+//  - A is 16 tokens: token t's f32 activations times 2^k_t as two f16 planes
+//    (mf::split_f16x2, k_t = mf::row_shift of the row's largest finite |x|), staged
+//    through LDS;
+//  - B is 16 weight rows: the int8 codes, exact in f16 (|q| <= 128 < 2^11);
 //  - D[token][row]: a lane holds four tokens of one row, so the block's fp16 scale is
-//    one value per lane, applied after the block: acc += d * (A0 B + A1 B + A2 B).
+//    one value per lane, applied after the block: acc += d * (A0 B + A1 B).
 // Every product q x is exact; the MFMA sums a block's products in f32 and d times that
-// sum is added to the accumulator.  The reference sums the same products
-// sequentially from the bias (d q rounds to nothing: it has at most 19 significant
-// bits), so results agree to f32 rounding, not bit for bit.
+// sum is added to the accumulator, all times 2^k_t, which the store takes back (powers
+// of two: the same roundings as unscaled).  The two planes hold each activation to
+// 2^-22 of itself (to 2^-39 of the row's largest below 2^-17 of it).  The reference sums
+// the products sequentially from the bias (d q rounds to nothing: it has at most 19
+// significant bits), so results agree to f32 rounding, not bit for bit.
 //
-// Token fragments: [token tile of 64][plane][step][16-token sub-tile][lane][16 B];
-// steps past the last block (K = 2880 has 90 blocks, padded to 92) hold zero tokens,
-// and their row scales are zero.
+// Workspace: token fragments [token tile of 64][plane][step][16-token sub-tile][lane][16 B]
+// (steps past the last block -- K = 2880 has 90 blocks, padded to 92 -- hold zero tokens,
+// and their row scales are zero), then the tokens' shifts k_t [tiles x 64] (int32).
 #include "ttl_mfma.hpp"
 
 #include <hip/hip_fp16.h>
 
 namespace {
 
-using mf::bf16x8;
+using mf::f16x8;
 using mf::f32x4;
 
-constexpr int kPlanes = 3;
+constexpr int kPlanes = 2;
 constexpr int kSub = 4;  // 16-token sub-tiles per 64-token tile
 constexpr int kTileTokens = 16 * kSub;
 constexpr int kStageSteps = 2;  // K steps per LDS stage
@@ -52,14 +55,17 @@ struct Shape {
 };
 
 // Token fragments of one (step, tile): thread (sub-tile m, lane (t, g)) converts
-// x[64 tile + 16 m + t][32 step + 8 g .. + 7] (zero past the tokens or the row end).
+// x[64 tile + 16 m + t][32 step + 8 g .. + 7] times 2^shift[token] (zero past the tokens
+// or the row end).
 template <int K>
 __global__ __launch_bounds__(kSub * 64) void q8_gather_kernel(const float *__restrict__ x, uint32_t tokens,
+                                                              const int32_t *__restrict__ shift,
                                                               uint8_t *__restrict__ frags) {
     using S = Shape<K>;
     const uint32_t step = blockIdx.x, tile = blockIdx.y;
     const uint32_t m = threadIdx.x / 64, lane = threadIdx.x % 64, g = lane / 16;
     const uint32_t token = tile * kTileTokens + m * 16 + lane % 16;
+    const int k = shift[token < tokens ? token : 0];
     float v[8];
     if (token < tokens && step < uint32_t(S::blocks)) {
         const float4 *p = reinterpret_cast<const float4 *>(x + size_t(token) * K + step * 32 + 8 * g);
@@ -79,7 +85,7 @@ __global__ __launch_bounds__(kSub * 64) void q8_gather_kernel(const float *__res
         }
     }
     uint4 out[kPlanes];
-    mf::split_planes<kPlanes>(v, out);
+    mf::split_f16x2(v, k, out);
     uint8_t *dst = frags + size_t(tile) * S::tile_bytes + (size_t(step) * kSub + m) * mf::frag_bytes + lane * 16;
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) {
@@ -87,18 +93,23 @@ __global__ __launch_bounds__(kSub * 64) void q8_gather_kernel(const float *__res
     }
 }
 
-// 8 int8 codes (K order) as bf16: exact, so the bf16 bits are the f32's top half.
-__device__ inline bf16x8 int8_bf16(uint2 c) {
-    mf::u32x4 r;
+// 8 int8 codes (K order) as f16, exact: code q's byte with its top bit flipped is
+// u = q + 128, and the f16 with bits 0x6400 | u is 1024 + u, so (1024 + u) - 1152 = q
+// (an exact f16 subtraction).  Dword k holds codes 2k (low half) and 2k + 1.
+__device__ inline f16x8 int8_f16(uint2 c) {
+    typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+    const f16x2v bias = {_Float16(1152.0f), _Float16(1152.0f)};
+    f16x8 r;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t w = k < 2 ? c.x : c.y;
-        const uint32_t sh = 16 * (k % 2);
-        const float f0 = float(int32_t(w << (24 - sh)) >> 24);
-        const float f1 = float(int32_t(w << (16 - sh)) >> 24);
-        r[k] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+        const uint32_t w = (k < 2 ? c.x : c.y) ^ 0x80808080u;
+        const uint32_t b = k % 2 == 0 ? w : w >> 16;  // the two codes in bytes 0 and 1
+        const uint32_t h = (b & 0xffu) | ((b & 0xff00u) << 8) | 0x64006400u;
+        const f16x2v v = __builtin_bit_cast(f16x2v, h) - bias;
+        r[2 * k] = v[0];
+        r[2 * k + 1] = v[1];
     }
-    return mf::as_bf16x8v(r);
+    return r;
 }
 
 struct GemmArgs {
@@ -108,6 +119,7 @@ struct GemmArgs {
     const float *residual;       // [tokens][rows] or null
     float *out;                  // [tokens][rows]
     const uint8_t *frags;        // token fragments
+    const int32_t *shift;        // [tiles x 64] the tokens' k (fragments hold x 2^k)
     uint32_t rows, row_tiles, tokens;
 };
 
@@ -210,17 +222,17 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
             // MFMAs are independent, so consecutive MFMAs never wait on each other)
             auto frag = [&](int f) __attribute__((always_inline)) {
                 const int ls = f / (kSub * kPlanes), p = (f / kSub) % kPlanes, m = f % kSub;
-                return mf::as_bf16x8v(buf[((p * kStageSteps + ls) * kSub + m) * 64 + lane]);
+                return __builtin_bit_cast(f16x8, buf[((p * kStageSteps + ls) * kSub + m) * 64 + lane]);
             };
-            bf16x8 ring[kLook];
+            f16x8 ring[kLook];
 #pragma unroll
             for (int d = 0; d < kLook; ++d) {
                 ring[d] = frag(d);
             }
-            bf16x8 w[kRowTiles];
+            f16x8 w[kRowTiles];
 #pragma unroll
             for (int f = 0; f < SF; ++f) {
-                const bf16x8 av = ring[f % kLook];
+                const f16x8 av = ring[f % kLook];
                 if (f + kLook < SF) {
                     ring[f % kLook] = frag(f + kLook);
                 }
@@ -229,7 +241,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
                 if (f % (kSub * kPlanes) == 0) {
 #pragma unroll
                     for (int j = 0; j < kRowTiles; ++j) {
-                        w[j] = int8_bf16(c[j][k]);
+                        w[j] = int8_f16(c[j][k]);
                         const uint32_t word = k < 2 ? s[j].x : s[j].y;
                         pend_d[j] = dcur[j];
                         dcur[j] = __half2float(__ushort_as_half(uint16_t(word >> (16 * (k % 2)))));
@@ -288,6 +300,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
     }
 
     // D rows 4g..4g+3 of sub-tile m are tokens; the lane's column is row[j]
+    int4 ks[kSub];  // the shifts of the lane's 16 tokens (within the shift array's tiles)
+#pragma unroll
+    for (int m = 0; m < kSub; ++m) {
+        ks[m] = *reinterpret_cast<const int4 *>(a.shift + tile * kTileTokens + m * 16 + 4 * g);
+    }
 #pragma unroll
     for (int j = 0; j < kRowTiles; ++j) {
         if (!ok[j]) {
@@ -296,12 +313,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
         const float bv = a.bias ? a.bias[row[j]] : 0.0f;
 #pragma unroll
         for (int m = 0; m < kSub; ++m) {
+            const int kk[4] = {ks[m].x, ks[m].y, ks[m].z, ks[m].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t token = tile * kTileTokens + m * 16 + 4 * g + e;
                 if (token < a.tokens) {
                     const size_t o = size_t(token) * a.rows + row[j];
-                    float v = a.bias ? bv + acc[m][j][e] : acc[m][j][e];
+                    const float sum = __builtin_amdgcn_ldexpf(acc[m][j][e], -kk[e]);
+                    float v = a.bias ? bv + sum : sum;
                     if (a.residual) {
                         v = a.residual[o] + v;
                     }
@@ -313,8 +332,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
 }
 
 template <int K>
+size_t frag_bytes_for(uint32_t tokens) {
+    return (size_t((tokens + kTileTokens - 1) / kTileTokens) * Shape<K>::tile_bytes + 255) & ~size_t(255);
+}
+
+template <int K>
 size_t workspace_for(uint32_t tokens) {
-    return size_t((tokens + kTileTokens - 1) / kTileTokens) * Shape<K>::tile_bytes;
+    return frag_bytes_for<K>(tokens) + size_t((tokens + kTileTokens - 1) / kTileTokens) * kTileTokens * 4;
 }
 
 }  // namespace
@@ -347,17 +371,27 @@ int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
     a.residual = residual_dev;
     a.out = out_dev;
     a.frags = static_cast<const uint8_t *>(workspace_dev);
+    int32_t *shift = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(workspace_dev) +
+                                                 (w->cols == 2880 ? frag_bytes_for<2880>(tokens)
+                                                                  : frag_bytes_for<4096>(tokens)));
+    a.shift = shift;
     a.rows = w->rows;
     a.row_tiles = w->tiles;
     a.tokens = tokens;
     const uint32_t group = uint32_t(kWaves * kRowTiles);
     const dim3 grid((w->tiles + group - 1) / group, tiles);
     uint8_t *frags = static_cast<uint8_t *>(workspace_dev);
+    const int rc = ttl::launch_row_shifts(ctx->stream, x_dev, w->cols, tokens, w->cols, shift);
+    if (rc != TTL_OK) {
+        return rc;
+    }
     if (w->cols == 2880) {
-        q8_gather_kernel<2880><<<dim3(Shape<2880>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, frags);
+        q8_gather_kernel<2880><<<dim3(Shape<2880>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, shift,
+                                                                                               frags);
         q8_gemm_kernel<2880><<<grid, kWaves * 64, 0, ctx->stream>>>(a);
     } else {
-        q8_gather_kernel<4096><<<dim3(Shape<4096>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, frags);
+        q8_gather_kernel<4096><<<dim3(Shape<4096>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, shift,
+                                                                                               frags);
         q8_gemm_kernel<4096><<<grid, kWaves * 64, 0, ctx->stream>>>(a);
     }
     TTL_LAUNCHED("q8 gemm kernels");
