@@ -567,8 +567,9 @@ def gpu_model_prefill(args):
         "value": PROMPT_TOKENS / (ms * 1e-3),
         "unit": "prompt tok/s",
         "ms_per_step": ms,
-        "dtype": "bf16 MFMA, exact products (f32 activations as three bf16 planes), f32 accumulate; the "
-                 "MoE down GEMM on f16 MFMA over the SwiGLU hidden's two f16 planes where the down scales allow",
+        "dtype": "f16 MFMA, f32 accumulate: f32 activations (and the SwiGLU hidden) as two f16 planes "
+                 "scaled by a power of two per token, exact weights (three exact bf16 planes on bf16 MFMA "
+                 "where MXFP4 scales leave the f16 range)",
         "config": {"workload": f"full synthetic gpt-oss-{'20b' if args.config == 3 else '120b'} layer-major prefill "
                                f"of a {PROMPT_TOKENS}-token prompt (GptOssModel::prefill); step = one prefill "
                                "(host tokens in, last-token logits out)",
