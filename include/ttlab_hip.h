@@ -146,10 +146,11 @@ size_t ttl_mxfp4_bytes(const ttl_mxfp4 *tensor);
  * as decode steps. */
 int ttl_mxfp4_edge_scales(const ttl_mxfp4 *tensor);
 /* 1 if every block with a code of nonzero magnitude has E8M0 scale 114..140, so that every
- * weight E2M1 x 2^(e-127) is a normal f16, else 0 (negative: error).  Then the exact
- * prefill path (ttl_moe_prefill*) runs the down GEMM on f16 MFMA, with the SwiGLU hidden
- * as two f16 planes; otherwise on bf16 MFMA with the hidden as three bf16 planes.  No
- * reference counterpart (a property of this backend's kernels). */
+ * weight E2M1 x 2^(e-127) is a normal f16, else 0 (negative: error).  Then the unscaled
+ * prefill path (ttl_moe_prefill*) runs that tensor's GEMM on f16 MFMA with its f32 operand
+ * (the down GEMM's SwiGLU hidden; gate/up's f32 tokens when both gate and up qualify) as
+ * two f16 planes; otherwise on bf16 MFMA with it as three bf16 planes.  No reference
+ * counterpart (a property of this backend's kernels). */
 int ttl_mxfp4_f16_exact(const ttl_mxfp4 *tensor);
 
 /* Decodes expert `expert` to f32 [rows][cols] on the device (out_dev).
@@ -281,10 +282,14 @@ int ttl_moe_down_combine(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *
                          float *out_dev, float *down_dev);
 
 /* ---- batched prefill on MFMA (benchmark config 2) ------------------------------------ *
- * bf16 MFMA with f32 accumulation.  Every product is exact: the weights E2M1 x
- * 2^(e-127) are bf16 values for E8M0 e in 1..254, and f32 activations are split
- * into three bf16 planes that sum to them exactly.  Results therefore agree with
- * the reference's f32 sums to rounding (relative L2 <= 1e-5), not bit for bit.
+ * bf16 or f16 MFMA with f32 accumulation.  The weights E2M1 x 2^(e-127) are exact
+ * bf16 values for E8M0 e in 1..254 (exact f16 values for e in 114..140, see
+ * ttl_mxfp4_f16_exact); bf16 activations are one exact plane.  An f32 operand (f32
+ * tokens, the SwiGLU hidden) is two f16 planes of x 2^k (k a power-of-two scale per
+ * token, or 8 for the hidden; 22 of the value's 24 bits) where the tensor's scales
+ * allow f16, else three bf16 planes that sum to it exactly; the sums are scaled back
+ * by 2^-k before the bias.  Results agree with the reference's f32 sums to rounding
+ * (relative L2 <= 1e-5), not bit for bit.
  * workspace_dev is caller-owned device memory, 256-byte aligned, of at least the
  * size the matching *_workspace_bytes function returns (workspace_bytes says how
  * much the caller holds; a smaller workspace is an error); calls sharing a
@@ -440,8 +445,9 @@ int ttl_matvec_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
  * out[t][r] = bias[r] + sum_k W[r][k] x[t][k] (+ residual[t][r] when residual_dev is
  * non-NULL, the residual add of model.cpp:521-529).  x_dev f32 [tokens][cols] (cols
  * 2880 or 4096), out_dev f32 [tokens][rows] in the tensor's row order; bias_dev may
- * be NULL.  bf16 MFMA with exact products (int8 codes; the activations as three bf16
- * planes) and the block scale applied per block: results agree with the reference to
+ * be NULL.  f16 MFMA (int8 codes, exact; each token's activations times a power of two
+ * 2^k as two f16 planes, 22 of their 24 bits, the sums scaled back by 2^-k before the
+ * bias) and the block scale applied per block: results agree with the reference to
  * f32 rounding.  workspace_dev (16-byte aligned) holds
  * ttl_matmul_q8_0_workspace_bytes(tokens, cols). */
 size_t ttl_matmul_q8_0_workspace_bytes(uint32_t tokens, uint32_t cols);
