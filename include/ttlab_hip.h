@@ -366,6 +366,15 @@ int ttl_moe_prefill_experts(ttl_ctx *ctx, const ttl_moe_layer *layer, const void
  * so layer->input_norm must be NULL; indices_dev / weights_dev (int32 / f32
  * [count][used]) may be NULL, else they receive the routing. */
 size_t ttl_moe_prefill_batch_workspace_bytes(uint32_t count, uint32_t experts, uint32_t used);
+/* ttl_moe_prefill with two of the layer loop's neighbouring steps folded in:
+ * x_shift_dev (int32 [count], or NULL) holds the f16-plane shifts of the rows of x as
+ * ttl_rms_norm_rows_shifts writes them, so no launch computes them again; residual_dev
+ * (f32 [count][2880], 16-byte aligned, or NULL) makes out = residual + the MoE output,
+ * the residual add of model.cpp:545-551 (ttl_add of the two, bit for bit).  No reference
+ * counterpart as one entry point. */
+int ttl_moe_prefill_fused(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, const int32_t *x_shift_dev,
+                          const float *residual_dev, uint32_t count, float *out_dev, int32_t *indices_dev,
+                          float *weights_dev, void *workspace_dev, size_t workspace_bytes);
 int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, uint32_t count, float *out_dev,
                     int32_t *indices_dev, float *weights_dev, void *workspace_dev, size_t workspace_bytes);
 
@@ -453,6 +462,12 @@ int ttl_matvec_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
 size_t ttl_matmul_q8_0_workspace_bytes(uint32_t tokens, uint32_t cols);
 int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev, uint32_t tokens,
                     const float *residual_dev, float *out_dev, void *workspace_dev, size_t workspace_bytes);
+/* ttl_matmul_q8_0 with the tokens' f16-plane shifts given: shift_dev int32 [tokens] as
+ * ttl_rms_norm_rows_shifts writes them for x, so no launch computes them again (the same
+ * results, bit for bit).  No reference counterpart as an entry point. */
+int ttl_matmul_q8_0_shifted(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev,
+                            const int32_t *shift_dev, uint32_t tokens, const float *residual_dev, float *out_dev,
+                            void *workspace_dev, size_t workspace_bytes);
 
 /* The row order ttl_attn_qkv expects of its 5120-row tensor: rows of attn_q (0..4095),
  * attn_k (4096..4607) and attn_v (4608..5119) stacked, reordered so each RoPE pair
@@ -505,6 +520,14 @@ int ttl_attention_prefill(ttl_ctx *ctx, const float *q_dev, const float *k_cache
  * 524-526), in the decode kernels' summation order. */
 int ttl_rms_norm_rows(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev, float epsilon,
                       float *out_dev);
+/* ttl_rms_norm_rows that also writes each normalized row's f16-plane shift into
+ * shift_dev (int32 [rows]; NULL: none): k = 15 - e for the row's largest finite
+ * magnitude m = f 2^e, f in [0.5, 1) (0 for a row with no nonzero finite value), the
+ * shift with which ttl_matmul_q8_0 and ttl_moe_prefill split a row into two f16
+ * planes.  For ttl_matmul_q8_0_shifted and ttl_moe_prefill_fused; no reference
+ * counterpart. */
+int ttl_rms_norm_rows_shifts(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev,
+                             float epsilon, float *out_dev, int32_t *shift_dev);
 /* The bias, RoPE and KV-cache store of model.cpp:499-507 for `tokens` tokens at
  * positions first_position .. : qkv_dev f32 [tokens][5120] is the output of
  * ttl_matmul_q8_0 on a tensor in ttl_qkv_row_source order without its bias; bias_dev

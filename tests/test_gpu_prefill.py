@@ -377,6 +377,33 @@ def test_moe_prefill_router_and_experts_match_oracle(dev, layer8):
     assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
 
 
+def test_moe_prefill_fused_matches_unfused(dev, layer8):
+    """ttl_moe_prefill_fused, as the layer loop calls it: the normalized rows with the
+    f16-plane shifts ttl_rms_norm_rows_shifts wrote for them, and the residual add in the
+    combine, gives the bits of ttl_moe_prefill followed by the f32 add residual + moe."""
+    host, device = layer8
+    count, used = 40, 4
+    raw = O.synth_normal(0x78000160, 0, count * N, sigma=3.0).reshape(count, N)
+    raw[9] = 0.0
+    norm_w = O.synth_normal(0x78000160, 1, N, sigma=1.0)
+    resid = O.synth_normal(0x78000160, 2, count * N).reshape(count, N)
+    rb, nb, resb = dev.upload(raw), dev.upload(norm_w), dev.upload(resid)
+    xb, sh = dev.alloc(count * N * 4), dev.alloc(count * 4)
+    oa, ob = dev.alloc(count * N * 4), dev.alloc(count * N * 4)
+    ia, wa, ib2, wb2 = (dev.alloc(count * used * 4) for _ in range(4))
+    try:
+        dev.rms_norm_rows(rb, count, nb, 1e-5, xb, shifts=sh)
+        dev.moe_prefill(device.desc, xb, count, oa, ia, wa)
+        dev.moe_prefill(device.desc, xb, count, ob, ib2, wb2, shifts=sh, residual=resb)
+        moe = oa.download(np.float32).reshape(count, N)
+        fused = ob.download(np.float32).reshape(count, N)
+        assert np.array_equal(ia.download(np.int32), ib2.download(np.int32))
+        assert np.array_equal((resid + moe).view(np.uint32), fused.view(np.uint32))
+    finally:
+        for b in (rb, nb, resb, xb, sh, oa, ob, ia, wa, ib2, wb2):
+            b.free()
+
+
 def test_moe_prefill_config2_router(dev):
     # 32 experts, 256 f32 tokens: the oracle on a sample of tokens, routing for all
     count = 256

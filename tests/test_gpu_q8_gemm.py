@@ -147,3 +147,46 @@ def test_q8_matmul_token_magnitudes_and_nonfinite(dev, cols):
         for b in (xb, bb, ob):
             b.free()
         t.free()
+
+
+def expected_shifts(x):
+    """The f16-plane shift of each row: 15 - e for its largest finite magnitude m = f 2^e,
+    f in [0.5, 1); 0 for a row with no nonzero finite value."""
+    a = np.where(np.isfinite(x), np.abs(x), 0.0).max(axis=1)
+    return np.where(a > 0, 15 - np.frexp(a)[1], 0).astype(np.int32)
+
+
+def test_q8_matmul_shifted_matches_unshifted(dev):
+    """ttl_rms_norm_rows_shifts writes the rows of ttl_rms_norm_rows, bit for bit, and
+    each row's f16-plane shift; ttl_matmul_q8_0_shifted on those shifts gives the bits of
+    ttl_matmul_q8_0, which computes them itself."""
+    rows, cols, tokens = 64, 2880, 70
+    raw = O.synth_normal(61, 0, tokens * cols, sigma=3.0).reshape(tokens, cols)
+    raw[9] = 0.0
+    norm_w = O.synth_normal(61, 1, cols, sigma=1.0)
+    norm_w[:100] *= np.float32(2.0 ** 12)  # some rows' largest value from these columns
+    blocks = O.synth_q8_0(62, cols, rows * cols // 32)
+    bias = O.synth_normal(63, cols, rows, sigma=0.1)
+    t = dev.q8_upload(blocks, rows, cols)
+    rb, nb, bb = dev.upload(raw), dev.upload(norm_w), dev.upload(bias)
+    xa, xs, sh = dev.alloc(tokens * cols * 4), dev.alloc(tokens * cols * 4), dev.alloc(tokens * 4)
+    oa, os_ = dev.alloc(tokens * rows * 4), dev.alloc(tokens * rows * 4)
+    try:
+        dev.rms_norm_rows(rb, tokens, nb, 1e-5, xa)
+        dev.rms_norm_rows(rb, tokens, nb, 1e-5, xs, shifts=sh)
+        x = xa.download(np.float32).reshape(tokens, cols)
+        assert np.array_equal(x.view(np.uint32), xs.download(np.float32).reshape(tokens, cols).view(np.uint32))
+        shifts = sh.download(np.int32)
+        assert np.array_equal(shifts, expected_shifts(x))
+        assert shifts[9] == 0 and len(set(shifts.tolist())) > 1
+        dev.matmul_q8_0(t, bb, xa, tokens, None, oa)
+        dev.matmul_q8_0(t, bb, xa, tokens, None, os_, shifts=sh)
+        a, b = oa.download(np.float32), os_.download(np.float32)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        ref = oracle_matmul(blocks, bias, rows, cols, x, tokens)
+        for p in range(tokens):
+            assert O.rel_l2(b.reshape(tokens, rows)[p], ref[p]) <= TOL, p
+    finally:
+        for buf in (rb, nb, bb, xa, xs, sh, oa, os_):
+            buf.free()
+        t.free()

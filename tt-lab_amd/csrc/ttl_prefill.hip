@@ -1634,7 +1634,7 @@ __global__ __launch_bounds__(256) void prefill_intermediates_kernel(Plan plan, u
 // USED is the pairs per token (the sort is a fixed network over USED registers).
 template <int USED>
 __global__ __launch_bounds__(256) void combine_kernel(Plan plan, uint32_t count, uint32_t rows,
-                                                      float *__restrict__ out) {
+                                                      const float *__restrict__ residual, float *__restrict__ out) {
 #pragma clang fp contract(off)
     const uint32_t quads_per_row = rows / 4;
     const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1675,23 +1675,30 @@ __global__ __launch_bounds__(256) void combine_kernel(Plan plan, uint32_t count,
             acc.w = acc.w + w * d.w;
         }
     }
+    if (residual) {
+        // model.cpp:545-551: x = residual + moe
+        const float4 r = reinterpret_cast<const float4 *>(residual + size_t(p) * rows)[q];
+        acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+    }
     reinterpret_cast<float4 *>(out + size_t(p) * rows)[q] = acc;
 }
 
 template <int USED>
-void launch_combine(const Plan &plan, uint32_t count, uint32_t rows, float *out, hipStream_t stream) {
+void launch_combine(const Plan &plan, uint32_t count, uint32_t rows, const float *residual, float *out,
+                    hipStream_t stream) {
     const size_t threads = size_t(count) * (rows / 4);
-    combine_kernel<USED><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(plan, count, rows, out);
+    combine_kernel<USED><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(plan, count, rows, residual, out);
 }
 
 // Dispatches the combine on the number of pairs per token (1..16).
 template <int U = 1>
-void combine_for(uint32_t used, const Plan &plan, uint32_t count, uint32_t rows, float *out, hipStream_t stream) {
+void combine_for(uint32_t used, const Plan &plan, uint32_t count, uint32_t rows, const float *residual, float *out,
+                 hipStream_t stream) {
     if constexpr (U <= int(kMaxUsed)) {
         if (used == uint32_t(U)) {
-            launch_combine<U>(plan, count, rows, out, stream);
+            launch_combine<U>(plan, count, rows, residual, out, stream);
         } else {
-            combine_for<U + 1>(used, plan, count, rows, out, stream);
+            combine_for<U + 1>(used, plan, count, rows, residual, out, stream);
         }
     }
 }
@@ -1877,9 +1884,16 @@ size_t ttl_moe_prefill_workspace_bytes(uint32_t count, uint32_t experts, uint32_
     return make_layout(count * used, experts, planes, true, uint32_t(mx::cols), f32 ? count : 0).total;
 }
 
-int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
-                           uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
-                           void *workspace_dev, size_t workspace_bytes, uint32_t stages) {
+}  // extern "C"
+
+namespace {
+
+// ttl_moe_prefill_stages with, for f32 tokens, their f16-plane shifts given (x_shift_dev,
+// int32 [count], as ttl::launch_row_shifts computes them; else computed here) and the
+// combine's residual add (residual_dev f32 [count][hidden], or null).
+int moe_prefill_run(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype, uint32_t count,
+                    const int32_t *indices_dev, const float *weights_dev, float *out_dev, void *workspace_dev,
+                    size_t workspace_bytes, uint32_t stages, const int32_t *x_shift_dev, const float *residual_dev) {
     TTL_REQUIRE(ctx && layer && x_dev && indices_dev && weights_dev && out_dev && workspace_dev, TTL_ERR_INVALID,
                 "ttl_moe_prefill_experts: null argument");
     TTL_REQUIRE((stages & ~uint32_t(TTL_PREFILL_ALL)) == 0, TTL_ERR_INVALID,
@@ -1947,12 +1961,17 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         if (bf16) {
             gather_kernel<true, 1><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         } else if (f16x) {
-            const int rc = ttl::launch_row_shifts(ctx->stream, static_cast<const float *>(x_dev), L.hidden, count,
-                                                  L.hidden, plan.token_shift);
-            if (rc != TTL_OK) {
-                return rc;
+            Plan p = plan;
+            if (x_shift_dev) {
+                p.token_shift = const_cast<int32_t *>(x_shift_dev);
+            } else {
+                const int rc = ttl::launch_row_shifts(ctx->stream, static_cast<const float *>(x_dev), L.hidden,
+                                                      count, L.hidden, plan.token_shift);
+                if (rc != TTL_OK) {
+                    return rc;
+                }
             }
-            gather_kernel<false, 2, true><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
+            gather_kernel<false, 2, true><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, p);
         } else {
             gather_kernel<false, 3><<<grid, mf::col_tiles * 64, 0, ctx->stream>>>(x_dev, L.hidden, count, plan);
         }
@@ -2017,10 +2036,21 @@ int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void 
         TTL_LAUNCHED("matmul_kernel");
     }
     if (stages & TTL_PREFILL_COMBINE) {
-        combine_for(L.used, plan, count, L.hidden, out_dev, ctx->stream);
+        combine_for(L.used, plan, count, L.hidden, residual_dev, out_dev, ctx->stream);
         TTL_LAUNCHED("combine_kernel");
     }
     return TTL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ttl_moe_prefill_stages(ttl_ctx *ctx, const ttl_moe_layer *layer, const void *x_dev, int x_dtype,
+                           uint32_t count, const int32_t *indices_dev, const float *weights_dev, float *out_dev,
+                           void *workspace_dev, size_t workspace_bytes, uint32_t stages) {
+    return moe_prefill_run(ctx, layer, x_dev, x_dtype, count, indices_dev, weights_dev, out_dev, workspace_dev,
+                           workspace_bytes, stages, nullptr, nullptr);
 }
 
 int ttl_moe_prefill_intermediates(ttl_ctx *ctx, const ttl_moe_layer *layer, int x_dtype, uint32_t count,
@@ -2078,8 +2108,9 @@ size_t ttl_moe_prefill_batch_workspace_bytes(uint32_t count, uint32_t experts, u
     return routing + ttl_moe_prefill_workspace_bytes(count, experts, used, TTL_DTYPE_F32);
 }
 
-int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, uint32_t count, float *out_dev,
-                    int32_t *indices_dev, float *weights_dev, void *workspace_dev, size_t workspace_bytes) {
+int ttl_moe_prefill_fused(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, const int32_t *x_shift_dev,
+                          const float *residual_dev, uint32_t count, float *out_dev, int32_t *indices_dev,
+                          float *weights_dev, void *workspace_dev, size_t workspace_bytes) {
     TTL_REQUIRE(ctx && layer && x_dev && out_dev && workspace_dev, TTL_ERR_INVALID, "ttl_moe_prefill: null argument");
     TTL_REQUIRE(layer->gate && layer->up && layer->down, TTL_ERR_INVALID, "ttl_moe_prefill: null expert tensor");
     for (const ttl_mxfp4 *t : {layer->gate, layer->up, layer->down}) {
@@ -2090,6 +2121,8 @@ int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev
     }
     TTL_REQUIRE(!layer->input_norm, TTL_ERR_INVALID,
                 "ttl_moe_prefill: x is the normalized MoE input (model.cpp:549-551); the layer's input_norm must be NULL");
+    TTL_REQUIRE((reinterpret_cast<uintptr_t>(residual_dev) & 15) == 0, TTL_ERR_INVALID,
+                "ttl_moe_prefill: the residual must be 16-byte aligned");
     TTL_REQUIRE(layer->used >= 1 && layer->used <= kMaxUsed, TTL_ERR_SHAPE, "ttl_moe_prefill: used must be 1..%u",
                 kMaxUsed);
     TTL_REQUIRE(workspace_bytes >= ttl_moe_prefill_batch_workspace_bytes(count, layer->experts, layer->used),
@@ -2113,8 +2146,15 @@ int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev
     if (rc != TTL_OK) {
         return rc;
     }
-    return ttl_moe_prefill_experts(ctx, layer, x_dev, TTL_DTYPE_F32, count, indices_dev ? indices_dev : indices,
-                                   weights_dev ? weights_dev : weights, out_dev, w, rest);
+    return moe_prefill_run(ctx, layer, x_dev, TTL_DTYPE_F32, count, indices_dev ? indices_dev : indices,
+                           weights_dev ? weights_dev : weights, out_dev, w, rest, TTL_PREFILL_ALL, x_shift_dev,
+                           residual_dev);
+}
+
+int ttl_moe_prefill(ttl_ctx *ctx, const ttl_moe_layer *layer, const float *x_dev, uint32_t count, float *out_dev,
+                    int32_t *indices_dev, float *weights_dev, void *workspace_dev, size_t workspace_bytes) {
+    return ttl_moe_prefill_fused(ctx, layer, x_dev, nullptr, nullptr, count, out_dev, indices_dev, weights_dev,
+                                 workspace_dev, workspace_bytes);
 }
 
 }  // extern "C"

@@ -6,6 +6,7 @@
 //   - output projection + residual add       model.cpp:584-588
 #include <hip/hip_fp16.h>
 
+#include "ttl_mfma.hpp"
 #include "ttl_q8_tile.hpp"
 
 namespace {
@@ -276,19 +277,40 @@ __global__ __launch_bounds__(256) void qkv_rope_store_kernel(const float *__rest
 
 // rms_norm (tensor.cpp:568-580) of row blockIdx.x of x [rows][2880], in the staging's
 // canonical order (so a row normalizes to the same bits as in the decode kernels).
+// shift, if not null, receives the normalized row's f16-plane shift (mf::row_shift of
+// its largest finite magnitude), as ttl::launch_row_shifts would compute it.
 __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                            float eps, float *__restrict__ out) {
+                                                            float eps, float *__restrict__ out,
+                                                            int32_t *__restrict__ shift) {
     using S = q8::Shape<2880>;
     __shared__ __attribute__((aligned(16))) float xs[S::x_blocks * stage::x_stride];
     __shared__ float red[stage::red_floats(S::x_blocks)];
+    __shared__ float wave_m[4];
     stage::Input in{};
     in.base = x + size_t(blockIdx.x) * 2880;
     in.norm_w = w;
     in.eps = eps;
     stage::stage<2880, S::x_blocks, 256, stage::kNorm>(in, xs, red);
     float *o = out + size_t(blockIdx.x) * 2880;
+    float m = 0.0f;
     for (uint32_t c = threadIdx.x; c < 2880u; c += 256) {
-        o[c] = xs[(c / 32) * stage::x_stride + c % 32];
+        const float v = xs[(c / 32) * stage::x_stride + c % 32];
+        o[c] = v;
+        m = mf::finite_max(m, v);
+    }
+    if (shift) {
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            m = __builtin_fmaxf(m, __shfl_xor(m, d));
+        }
+        if (threadIdx.x % 64 == 0) {
+            wave_m[threadIdx.x / 64] = m;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const float mm = __builtin_fmaxf(__builtin_fmaxf(wave_m[0], wave_m[1]), __builtin_fmaxf(wave_m[2], wave_m[3]));
+            shift[blockIdx.x] = mf::row_shift(mm);
+        }
     }
 }
 
@@ -511,8 +533,8 @@ int ttl_qkv_rope_store(ttl_ctx *ctx, const float *qkv_dev, uint32_t tokens, uint
     return TTL_OK;
 }
 
-int ttl_rms_norm_rows(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev, float epsilon,
-                      float *out_dev) {
+int ttl_rms_norm_rows_shifts(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev,
+                             float epsilon, float *out_dev, int32_t *shift_dev) {
     TTL_REQUIRE(ctx && x_dev && weight_dev && out_dev, TTL_ERR_INVALID, "ttl_rms_norm_rows: null argument");
     TTL_REQUIRE(((uintptr_t)x_dev & 15) == 0 && ((uintptr_t)weight_dev & 15) == 0, TTL_ERR_INVALID,
                 "ttl_rms_norm_rows: x and weight must be 16-byte aligned");
@@ -520,9 +542,14 @@ int ttl_rms_norm_rows(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const flo
     if (rows == 0) {
         return TTL_OK;
     }
-    rms_norm_rows_kernel<<<rows, 256, 0, ctx->stream>>>(x_dev, weight_dev, epsilon, out_dev);
+    rms_norm_rows_kernel<<<rows, 256, 0, ctx->stream>>>(x_dev, weight_dev, epsilon, out_dev, shift_dev);
     TTL_LAUNCHED("rms_norm_rows_kernel");
     return TTL_OK;
+}
+
+int ttl_rms_norm_rows(ttl_ctx *ctx, const float *x_dev, uint32_t rows, const float *weight_dev, float epsilon,
+                      float *out_dev) {
+    return ttl_rms_norm_rows_shifts(ctx, x_dev, rows, weight_dev, epsilon, out_dev, nullptr);
 }
 
 int ttl_add(ttl_ctx *ctx, const float *a_dev, const float *b_dev, size_t n, float *out_dev) {

@@ -21,7 +21,8 @@
 //
 // Workspace: token fragments [token tile of 64][plane][step][16-token sub-tile][lane][16 B]
 // (steps past the last block -- K = 2880 has 90 blocks, padded to 92 -- hold zero tokens,
-// and their row scales are zero), then the tokens' shifts k_t [tiles x 64] (int32).
+// and their row scales are zero), then the tokens' shifts k_t [tiles x 64] (int32), unless
+// the caller passes them (ttl_matmul_q8_0_shifted).
 #include "ttl_mfma.hpp"
 
 #include <hip/hip_fp16.h>
@@ -119,7 +120,7 @@ struct GemmArgs {
     const float *residual;       // [tokens][rows] or null
     float *out;                  // [tokens][rows]
     const uint8_t *frags;        // token fragments
-    const int32_t *shift;        // [tiles x 64] the tokens' k (fragments hold x 2^k)
+    const int32_t *shift;        // [tokens] the tokens' k (fragments hold x 2^k)
     uint32_t rows, row_tiles, tokens;
 };
 
@@ -300,10 +301,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
     }
 
     // D rows 4g..4g+3 of sub-tile m are tokens; the lane's column is row[j]
-    int4 ks[kSub];  // the shifts of the lane's 16 tokens (within the shift array's tiles)
+    int ks[kSub][4];  // the shifts of the lane's 16 tokens (tokens past the count read token 0's)
 #pragma unroll
     for (int m = 0; m < kSub; ++m) {
-        ks[m] = *reinterpret_cast<const int4 *>(a.shift + tile * kTileTokens + m * 16 + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t token = tile * kTileTokens + m * 16 + 4 * g + e;
+            ks[m][e] = a.shift[token < a.tokens ? token : 0u];
+        }
     }
 #pragma unroll
     for (int j = 0; j < kRowTiles; ++j) {
@@ -313,13 +318,12 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2))
         const float bv = a.bias ? a.bias[row[j]] : 0.0f;
 #pragma unroll
         for (int m = 0; m < kSub; ++m) {
-            const int kk[4] = {ks[m].x, ks[m].y, ks[m].z, ks[m].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t token = tile * kTileTokens + m * 16 + 4 * g + e;
                 if (token < a.tokens) {
                     const size_t o = size_t(token) * a.rows + row[j];
-                    const float sum = __builtin_amdgcn_ldexpf(acc[m][j][e], -kk[e]);
+                    const float sum = __builtin_amdgcn_ldexpf(acc[m][j][e], -ks[m][e]);
                     float v = a.bias ? bv + sum : sum;
                     if (a.residual) {
                         v = a.residual[o] + v;
@@ -341,25 +345,18 @@ size_t workspace_for(uint32_t tokens) {
     return frag_bytes_for<K>(tokens) + size_t((tokens + kTileTokens - 1) / kTileTokens) * kTileTokens * 4;
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t ttl_matmul_q8_0_workspace_bytes(uint32_t tokens, uint32_t cols) {
-    return cols == 4096 ? workspace_for<4096>(tokens) : workspace_for<2880>(tokens);
-}
-
-int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev, uint32_t tokens,
-                    const float *residual_dev, float *out_dev, void *workspace_dev, size_t workspace_bytes) {
+int matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev, const int32_t *shift_dev,
+                uint32_t tokens, const float *residual_dev, float *out_dev, void *workspace_dev,
+                size_t workspace_bytes, const char *who) {
     TTL_REQUIRE(ctx && w && w->codes && w->row_scales && x_dev && out_dev && workspace_dev, TTL_ERR_INVALID,
-                "ttl_matmul_q8_0: null argument");
-    TTL_REQUIRE(w->cols == 2880 || w->cols == 4096, TTL_ERR_SHAPE, "ttl_matmul_q8_0: cols must be 2880 or 4096");
-    TTL_REQUIRE(tokens < (1u << 20), TTL_ERR_SHAPE, "ttl_matmul_q8_0: at most %u tokens per call", (1u << 20) - 1);
+                "%s: null argument", who);
+    TTL_REQUIRE(w->cols == 2880 || w->cols == 4096, TTL_ERR_SHAPE, "%s: cols must be 2880 or 4096", who);
+    TTL_REQUIRE(tokens < (1u << 20), TTL_ERR_SHAPE, "%s: at most %u tokens per call", who, (1u << 20) - 1);
     const size_t need = ttl_matmul_q8_0_workspace_bytes(tokens, w->cols);
-    TTL_REQUIRE(workspace_bytes >= need, TTL_ERR_SHAPE, "ttl_matmul_q8_0: workspace of %zu bytes, %zu needed",
+    TTL_REQUIRE(workspace_bytes >= need, TTL_ERR_SHAPE, "%s: workspace of %zu bytes, %zu needed", who,
                 workspace_bytes, need);
     TTL_REQUIRE((reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace_dev) & 15) == 0,
-                TTL_ERR_INVALID, "ttl_matmul_q8_0: x and the workspace must be 16-byte aligned");
+                TTL_ERR_INVALID, "%s: x and the workspace must be 16-byte aligned", who);
     if (tokens == 0) {
         return TTL_OK;
     }
@@ -374,28 +371,54 @@ int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const 
     int32_t *shift = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(workspace_dev) +
                                                  (w->cols == 2880 ? frag_bytes_for<2880>(tokens)
                                                                   : frag_bytes_for<4096>(tokens)));
-    a.shift = shift;
+    if (shift_dev) {
+        a.shift = shift_dev;
+    } else {
+        const int rc = ttl::launch_row_shifts(ctx->stream, x_dev, w->cols, tokens, w->cols, shift);
+        if (rc != TTL_OK) {
+            return rc;
+        }
+        a.shift = shift;
+    }
     a.rows = w->rows;
     a.row_tiles = w->tiles;
     a.tokens = tokens;
     const uint32_t group = uint32_t(kWaves * kRowTiles);
     const dim3 grid((w->tiles + group - 1) / group, tiles);
     uint8_t *frags = static_cast<uint8_t *>(workspace_dev);
-    const int rc = ttl::launch_row_shifts(ctx->stream, x_dev, w->cols, tokens, w->cols, shift);
-    if (rc != TTL_OK) {
-        return rc;
-    }
     if (w->cols == 2880) {
-        q8_gather_kernel<2880><<<dim3(Shape<2880>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, shift,
+        q8_gather_kernel<2880><<<dim3(Shape<2880>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, a.shift,
                                                                                                frags);
         q8_gemm_kernel<2880><<<grid, kWaves * 64, 0, ctx->stream>>>(a);
     } else {
-        q8_gather_kernel<4096><<<dim3(Shape<4096>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, shift,
+        q8_gather_kernel<4096><<<dim3(Shape<4096>::steps, tiles), kSub * 64, 0, ctx->stream>>>(x_dev, tokens, a.shift,
                                                                                                frags);
         q8_gemm_kernel<4096><<<grid, kWaves * 64, 0, ctx->stream>>>(a);
     }
     TTL_LAUNCHED("q8 gemm kernels");
     return TTL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ttl_matmul_q8_0_workspace_bytes(uint32_t tokens, uint32_t cols) {
+    return cols == 4096 ? workspace_for<4096>(tokens) : workspace_for<2880>(tokens);
+}
+
+int ttl_matmul_q8_0(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev, uint32_t tokens,
+                    const float *residual_dev, float *out_dev, void *workspace_dev, size_t workspace_bytes) {
+    return matmul_q8_0(ctx, w, bias_dev, x_dev, nullptr, tokens, residual_dev, out_dev, workspace_dev,
+                       workspace_bytes, "ttl_matmul_q8_0");
+}
+
+int ttl_matmul_q8_0_shifted(ttl_ctx *ctx, const ttl_q8 *w, const float *bias_dev, const float *x_dev,
+                            const int32_t *shift_dev, uint32_t tokens, const float *residual_dev, float *out_dev,
+                            void *workspace_dev, size_t workspace_bytes) {
+    TTL_REQUIRE(shift_dev, TTL_ERR_INVALID, "ttl_matmul_q8_0_shifted: null shifts");
+    return matmul_q8_0(ctx, w, bias_dev, x_dev, shift_dev, tokens, residual_dev, out_dev, workspace_dev,
+                       workspace_bytes, "ttl_matmul_q8_0_shifted");
 }
 
 }  // extern "C"

@@ -167,7 +167,7 @@ void HipGptOssModel::finish_construction() {
         q_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kQueryWidth));
         attended_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kQueryWidth));
         residual_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kHidden));
-        moe_seq_ = static_cast<float *>(alloc(sizeof(float) * B * kHidden));
+        shift_seq_ = static_cast<int32_t *>(alloc(sizeof(int32_t) * B));
         gemm_workspace_bytes_ = std::max(ttl_matmul_q8_0_workspace_bytes(uint32_t(B), 2880),
                                          ttl_matmul_q8_0_workspace_bytes(uint32_t(B), 4096));
         gemm_workspace_ = alloc(gemm_workspace_bytes_);
@@ -436,10 +436,11 @@ int HipGptOssModel::enqueue_prefill_chunk(size_t first, size_t count) {
         Layer &layer = layers_[l];
         const float *x_in = x_seq_ + l * B * kHidden;
         float *x_out = x_seq_ + (l + 1) * B * kHidden;
-        status = ttl_rms_norm_rows(ctx_, x_in, n, layer.attn_norm, norm_epsilon, norm_seq_);
+        // the normalized rows' f16-plane shifts come with the norm, for the GEMM after it
+        status = ttl_rms_norm_rows_shifts(ctx_, x_in, n, layer.attn_norm, norm_epsilon, norm_seq_, shift_seq_);
         if (status == TTL_OK) {
-            status = ttl_matmul_q8_0(ctx_, layer.qkv, nullptr, norm_seq_, n, nullptr, qkv_seq_, gemm_workspace_,
-                                     gemm_workspace_bytes_);
+            status = ttl_matmul_q8_0_shifted(ctx_, layer.qkv, nullptr, norm_seq_, shift_seq_, n, nullptr, qkv_seq_,
+                                             gemm_workspace_, gemm_workspace_bytes_);
         }
         if (status == TTL_OK) {
             status = ttl_qkv_rope_store(ctx_, qkv_seq_, n, uint32_t(first), layer.qkv_bias, rope_,
@@ -455,16 +456,15 @@ int HipGptOssModel::enqueue_prefill_chunk(size_t first, size_t count) {
                                      residual_seq_, gemm_workspace_, gemm_workspace_bytes_);
         }
         if (status == TTL_OK) {
-            status = ttl_rms_norm_rows(ctx_, residual_seq_, n, layer.post_norm, norm_epsilon, norm_seq_);
+            status = ttl_rms_norm_rows_shifts(ctx_, residual_seq_, n, layer.post_norm, norm_epsilon, norm_seq_,
+                                              shift_seq_);
         }
         if (status == TTL_OK) {
             ttl_moe_layer moe = layer.moe;
             moe.input_norm = nullptr;  // moe_batch receives the normalized sequence (model.cpp:531)
-            status = ttl_moe_prefill(ctx_, &moe, norm_seq_, n, moe_seq_, nullptr, nullptr, moe_workspace_,
-                                     moe_workspace_bytes_);
-        }
-        if (status == TTL_OK) {
-            status = ttl_add(ctx_, residual_seq_, moe_seq_, size_t(n) * kHidden, x_out);
+            // x_{l+1} = residual + moe (model.cpp:545-553), the add in the MoE's combine
+            status = ttl_moe_prefill_fused(ctx_, &moe, norm_seq_, shift_seq_, residual_seq_, n, x_out, nullptr,
+                                           nullptr, moe_workspace_, moe_workspace_bytes_);
         }
     }
     if (status == TTL_OK) {

@@ -229,7 +229,8 @@ class HipGptOssModel {
     int32_t *prefill_tokens_ = nullptr;
     float *x_seq_ = nullptr;         // [layers + 1][batch][2880]
     float *norm_seq_ = nullptr, *qkv_seq_ = nullptr, *q_seq_ = nullptr, *attended_seq_ = nullptr;
-    float *residual_seq_ = nullptr, *moe_seq_ = nullptr;
+    float *residual_seq_ = nullptr;
+    int32_t *shift_seq_ = nullptr;   // [batch] f16-plane shifts of the normalized rows
     void *gemm_workspace_ = nullptr, *moe_workspace_ = nullptr;
     size_t gemm_workspace_bytes_ = 0, moe_workspace_bytes_ = 0;
 };

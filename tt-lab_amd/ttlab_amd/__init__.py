@@ -392,6 +392,9 @@ def load_library():
         "ttl_moe_prefill_intermediates": (i32, [vp, C.POINTER(MoeLayerDesc), i32, u32, vp, sz, vp, vp, vp]),
         "ttl_moe_prefill_batch_workspace_bytes": (sz, [u32, u32, u32]),
         "ttl_moe_prefill": (i32, [vp, C.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp, vp, sz]),
+        "ttl_moe_prefill_fused": (i32, [vp, C.POINTER(MoeLayerDesc), vp, vp, vp, u32, vp, vp, vp, vp, sz]),
+        "ttl_rms_norm_rows": (i32, [vp, vp, u32, vp, f32, vp]),
+        "ttl_rms_norm_rows_shifts": (i32, [vp, vp, u32, vp, f32, vp, vp]),
         "ttl_logits_q8_0": (i32, [vp, vp, u32, C.POINTER(StageInput), vp, vp]),
         "ttl_stream_read": (i32, [vp, vp, sz, vp]),
         "ttl_measure_handoff": (i32, [vp, i32, u32, C.POINTER(f32), C.POINTER(u32)]),
@@ -399,6 +402,7 @@ def load_library():
         "ttl_stream_read_plain": (i32, [vp, vp, sz, vp]),
         "ttl_matmul_q8_0_workspace_bytes": (sz, [u32, u32]),
         "ttl_matmul_q8_0": (i32, [vp, vp, vp, vp, u32, vp, vp, vp, sz]),
+        "ttl_matmul_q8_0_shifted": (i32, [vp, vp, vp, vp, vp, u32, vp, vp, vp, sz]),
         "ttl_capture_begin": (i32, [vp]),
         "ttl_capture_end": (i32, [vp, C.POINTER(vp)]),
         "ttl_graph_launch": (i32, [vp, vp]),
@@ -750,16 +754,32 @@ class Device:
         _check(self.lib.ttl_matvec_q8_0(self.ctx, w.handle, bias.ptr if bias else None, C.byref(stage),
                                         residual.ptr if residual else None, y.ptr), "ttl_matvec_q8_0")
 
-    def matmul_q8_0(self, w, bias, x, tokens, residual, out):
-        """matmul_add_q8_0 for `tokens` rows of x on the device; allocates its workspace."""
+    def matmul_q8_0(self, w, bias, x, tokens, residual, out, shifts=None):
+        """matmul_add_q8_0 for `tokens` rows of x on the device; allocates its workspace.
+        shifts: the rows' f16-plane shifts (from rms_norm_rows), for ttl_matmul_q8_0_shifted."""
         ws = self.alloc(max(16, self.lib.ttl_matmul_q8_0_workspace_bytes(tokens, w.cols)))
         try:
-            _check(self.lib.ttl_matmul_q8_0(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, tokens,
-                                            residual.ptr if residual else None, out.ptr, ws.ptr, ws.nbytes),
-                   "ttl_matmul_q8_0")
+            if shifts is None:
+                _check(self.lib.ttl_matmul_q8_0(self.ctx, w.handle, bias.ptr if bias else None, x.ptr, tokens,
+                                                residual.ptr if residual else None, out.ptr, ws.ptr, ws.nbytes),
+                       "ttl_matmul_q8_0")
+            else:
+                _check(self.lib.ttl_matmul_q8_0_shifted(self.ctx, w.handle, bias.ptr if bias else None, x.ptr,
+                                                        shifts.ptr, tokens, residual.ptr if residual else None,
+                                                        out.ptr, ws.ptr, ws.nbytes), "ttl_matmul_q8_0_shifted")
             self.sync()
         finally:
             ws.free()
+
+    def rms_norm_rows(self, x, rows, weight, epsilon, out, shifts=None):
+        """rms_norm of each of `rows` rows of 2880; shifts (int32 [rows]) receives their
+        f16-plane shifts (ttl_rms_norm_rows_shifts)."""
+        if shifts is None:
+            _check(self.lib.ttl_rms_norm_rows(self.ctx, x.ptr, rows, weight.ptr, epsilon, out.ptr),
+                   "ttl_rms_norm_rows")
+        else:
+            _check(self.lib.ttl_rms_norm_rows_shifts(self.ctx, x.ptr, rows, weight.ptr, epsilon, out.ptr,
+                                                     shifts.ptr), "ttl_rms_norm_rows_shifts")
 
     def attn_qkv(self, qkv, bias, stage, rope, position, capacity, q, kc, vc):
         _check(self.lib.ttl_attn_qkv(self.ctx, qkv.handle, bias.ptr, C.byref(stage), rope.ptr, position.ptr, capacity,
@@ -846,13 +866,23 @@ class Device:
                                                       hidden_scales.ptr if hidden_scales is not None else None),
                "ttl_moe_prefill_intermediates")
 
-    def moe_prefill(self, layer, x, count, out, indices=None, weights=None):
-        """GptOssModel::moe_batch on the device (router + experts); allocates its workspace."""
+    def moe_prefill(self, layer, x, count, out, indices=None, weights=None, shifts=None, residual=None):
+        """GptOssModel::moe_batch on the device (router + experts); allocates its workspace.
+        shifts (x's f16-plane shifts) and residual (out = residual + moe) select
+        ttl_moe_prefill_fused."""
         ws = self.alloc(self.lib.ttl_moe_prefill_batch_workspace_bytes(count, layer.experts, layer.used))
         try:
-            _check(self.lib.ttl_moe_prefill(self.ctx, C.byref(layer), x.ptr, count, out.ptr,
-                                            indices.ptr if indices else None, weights.ptr if weights else None,
-                                            ws.ptr, ws.nbytes), "ttl_moe_prefill")
+            if shifts is None and residual is None:
+                _check(self.lib.ttl_moe_prefill(self.ctx, C.byref(layer), x.ptr, count, out.ptr,
+                                                indices.ptr if indices else None, weights.ptr if weights else None,
+                                                ws.ptr, ws.nbytes), "ttl_moe_prefill")
+            else:
+                _check(self.lib.ttl_moe_prefill_fused(self.ctx, C.byref(layer), x.ptr,
+                                                      shifts.ptr if shifts else None,
+                                                      residual.ptr if residual else None, count, out.ptr,
+                                                      indices.ptr if indices else None,
+                                                      weights.ptr if weights else None, ws.ptr, ws.nbytes),
+                       "ttl_moe_prefill_fused")
             self.sync()
         finally:
             ws.free()
