@@ -404,6 +404,22 @@ def test_moe_prefill_fused_matches_unfused(dev, layer8):
             b.free()
 
 
+def test_moe_prefill_fused_rejects_misaligned_residual(dev, layer8):
+    host, device = layer8
+    count = 4
+    xb, out = dev.alloc(count * N * 4), dev.alloc(count * N * 4)
+    resid = dev.alloc(count * N * 4 + 16)
+    ws = dev.alloc(dev.lib.ttl_moe_prefill_batch_workspace_bytes(count, 8, 4))
+    try:
+        with pytest.raises(ttlab_amd.TtlError, match="16-byte aligned"):
+            ttlab_amd._check(dev.lib.ttl_moe_prefill_fused(dev.ctx, C.byref(device.desc), xb.ptr, None,
+                                                           C.c_void_p(resid.ptr + 4), count, out.ptr, None, None,
+                                                           ws.ptr, ws.nbytes), "ttl_moe_prefill_fused")
+    finally:
+        for b in (xb, out, resid, ws):
+            b.free()
+
+
 def test_moe_prefill_config2_router(dev):
     # 32 experts, 256 f32 tokens: the oracle on a sample of tokens, routing for all
     count = 256

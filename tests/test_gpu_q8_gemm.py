@@ -190,3 +190,19 @@ def test_q8_matmul_shifted_matches_unshifted(dev):
         for buf in (rb, nb, bb, xa, xs, sh, oa, os_):
             buf.free()
         t.free()
+
+
+def test_q8_matmul_shifted_rejects_null_shifts(dev):
+    import ttlab_amd
+    rows, cols, tokens = 16, 2880, 3
+    t = dev.q8_upload(O.synth_q8_0(64, 1, rows * cols // 32), rows, cols)
+    xb, ob = dev.alloc(tokens * cols * 4), dev.alloc(tokens * rows * 4)
+    ws = dev.alloc(dev.lib.ttl_matmul_q8_0_workspace_bytes(tokens, cols))
+    try:
+        with pytest.raises(ttlab_amd.TtlError, match="null shifts"):
+            ttlab_amd._check(dev.lib.ttl_matmul_q8_0_shifted(dev.ctx, t.handle, None, xb.ptr, None, tokens, None,
+                                                             ob.ptr, ws.ptr, ws.nbytes), "ttl_matmul_q8_0_shifted")
+    finally:
+        for b in (xb, ob, ws):
+            b.free()
+        t.free()
